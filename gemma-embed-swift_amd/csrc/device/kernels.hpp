@@ -1,0 +1,72 @@
+// Host-side launchers of the gfx950 kernels. Every launcher checks the shapes its kernel
+// assumes and returns hipErrorInvalidValue instead of launching when they do not hold.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstdint>
+
+namespace ge {
+
+// One block of query rows of one packed sequence (AttentionWork, Shaders/Common.metal:75-79).
+struct AttnWork {
+    uint32_t seq_start;
+    uint32_t seq_len;
+    uint32_t q0;
+};
+
+struct SeqRange {
+    uint32_t start;
+    uint32_t length;
+};
+
+// Query rows per attention work item.
+constexpr int kAttnQueries = 32;
+// Rows of slack every activation buffer keeps past its last token, so tile loads of the last
+// GEMM row block and of the last attention query/key block stay inside the allocation.
+constexpr int kRowSlack = 256;
+
+// A repacked Q8_0 matrix in device memory: quants [rows][cols] int8 and scales
+// [rows][cols / 32] fp16 (raw bits).
+struct Q8Dev {
+    int rows = 0, cols = 0;
+    int8_t* q = nullptr;
+    uint16_t* s = nullptr;
+};
+
+enum GemmEpilogue { kEpiF32 = 0, kEpiF16 = 1, kEpiGeglu = 2 };
+
+// y[M][N] = (x[M][K] (fp16) * W[N][K]^T (Q8_0)) * out_scale. kEpiGeglu expects W's rows
+// interleaved in 32-row gate/up groups and writes fp16 act[M][N / 2] = gelu_tanh(gate) * up *
+// out_scale. out_scale is a power of two wherever the forward uses it, so it is exact.
+hipError_t launch_gemm_q8(hipStream_t s, const Q8Dev& w, const uint16_t* x, int M, void* y, GemmEpilogue epi,
+                          float out_scale = 1.0f);
+
+// x = table[id] * scale (fp32 [T][d]), h = rmsnorm(x) * w (fp16 [T][d]).
+hipError_t launch_embed_norm(hipStream_t s, const Q8Dev& table, const int32_t* tokens, int T, float scale,
+                             const float* norm_w, float eps, float* x, uint16_t* h);
+
+// x = (x + rmsnorm(t) * w) * out_scale; if next_w: h = rmsnorm(x) * next_w (fp16).
+hipError_t launch_residual_norm(hipStream_t s, float* x, const float* t, const float* w, float out_scale,
+                                const float* next_w, float eps, int T, int d, uint16_t* h);
+
+// qkv fp32 [T][(H + 2 KV) hd] -> q fp16 [T][H][hd], k, v fp16 [T][KV][hd]: weighted RMSNorm and
+// NeoX RoPE on q and k, unweighted RMSNorm on v.
+hipError_t launch_qk_norm_rope(hipStream_t s, const float* qkv, int T, int H, int KV, int hd, const float* q_norm,
+                               const float* k_norm, float eps, const int32_t* positions, const float* rope_table,
+                               uint16_t* q, uint16_t* k, uint16_t* v);
+
+// Flash-style bidirectional attention over packed sequences.
+hipError_t launch_attention(hipStream_t s, const uint16_t* q, const uint16_t* k, const uint16_t* v, uint16_t* o,
+                            const AttnWork* work, int n_work, int H, int KV, int hd, int half_window, float scale);
+
+// pooled[s] = mean of the sequence's rows of x [*][width].
+hipError_t launch_mean_pool(hipStream_t s, const float* x, const SeqRange* seqs, int n_seqs, int width, float* pooled);
+
+// Per-device kernel attributes (dynamic LDS limits); call once per device before launching.
+hipError_t configure_kernels();
+
+hipError_t launch_f32_to_f16(hipStream_t s, const float* src, uint16_t* dst, size_t n);
+hipError_t launch_f16_to_f32(hipStream_t s, const uint16_t* src, float* dst, size_t n);
+
+}  // namespace ge

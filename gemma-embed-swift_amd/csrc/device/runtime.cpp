@@ -1,0 +1,1033 @@
+// Device runtime behind the C-ABI: context, weight upload with Q8_0 repacking, grow-only
+// workspace, the per-layer forward encode, named-tensor tracing, HIP-event profiling and the
+// per-op entry points. Replaces Sources/GemmaEmbed/Metal/MetalContext.swift and
+// Metal/MetalForward.swift (execute :310-360, encode :364-423, Kernels :427-759).
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <cmath>
+#include <cstdarg>
+#include <cstdio>
+#include <cstring>
+#include <map>
+#include <memory>
+#include <string>
+#include <vector>
+
+#include "gemmaembed.h"
+#include "kernels.hpp"
+
+namespace ge {
+namespace {
+
+struct Fail {
+    int code;
+    std::string msg;
+};
+
+[[noreturn]] void fail(int code, const char* fmt, ...) {
+    char buf[512];
+    va_list ap;
+    va_start(ap, fmt);
+    std::vsnprintf(buf, sizeof(buf), fmt, ap);
+    va_end(ap);
+    throw Fail{code, buf};
+}
+
+void hip_check(hipError_t e, const char* what) {
+    if (e != hipSuccess) fail(GE_ERR_GPU, "GPU execution failed: %s: %s", what, hipGetErrorString(e));
+}
+
+uint16_t host_f2h(float f);
+float host_h2f(uint16_t h);
+
+// ---------------------------------------------------------------- half conversion (host)
+float host_h2f(uint16_t h) {
+    const uint32_t sign = uint32_t(h & 0x8000u) << 16;
+    uint32_t exp = (h >> 10) & 0x1fu, man = h & 0x3ffu, bits;
+    if (exp == 0) {
+        if (man == 0) {
+            bits = sign;
+        } else {
+            int e = -1;
+            do {
+                man <<= 1;
+                e++;
+            } while (!(man & 0x400u));
+            bits = sign | (uint32_t(127 - 15 - e) << 23) | ((man & 0x3ffu) << 13);
+        }
+    } else if (exp == 31) {
+        bits = sign | 0x7f800000u | (man << 13);
+    } else {
+        bits = sign | ((exp + 112) << 23) | (man << 13);
+    }
+    float f;
+    std::memcpy(&f, &bits, 4);
+    return f;
+}
+
+// ---------------------------------------------------------------- device model
+
+struct DevLayer {
+    bool sliding = false;
+    int kv_heads = 0, head_dim = 0, qd = 0, kvd = 0;
+    float rope_base = 0, out_scale = 1;
+    // act is stored in fp16 as gelu(gate) * up * act_scale; the down projection multiplies by
+    // 1 / act_scale. Both are powers of two, so the round trip is exact.
+    float act_scale = 1, down_scale = 1;
+    Q8Dev wqkv, wo, wgu, wd;  // wqkv rows: q | k | v; wgu rows: gate/up interleaved in 32-row groups
+    float *attn_norm = nullptr, *q_norm = nullptr, *k_norm = nullptr, *post_attn = nullptr, *ffn_norm = nullptr,
+          *post_ffw = nullptr;
+    const float* rope = nullptr;
+};
+
+struct DevModel {
+    int layers = 0, hidden = 0, heads = 0, ff = 0, out_dims = 0, pl = 0, vocab = 0, window = 0, max_tokens = 8192;
+    float eps = 1e-6f, emb_scale = 1, pl_scale = 1;
+    Q8Dev tok_embd, output;
+    float* out_norm = nullptr;
+    std::vector<DevLayer> layer;
+    int max_qd = 0, max_kvd = 0, max_qkv = 0;
+};
+
+struct Workspace {
+    int rows = 0;  // capacity in rows, slack included
+    float *x = nullptr, *qkv = nullptr, *t = nullptr, *out = nullptr;
+    uint16_t *h = nullptr, *q = nullptr, *k = nullptr, *v = nullptr, *attn = nullptr, *act = nullptr;
+    int32_t *tokens = nullptr, *positions = nullptr;
+    int seq_cap = 0, work_cap = 0;
+    SeqRange* seqs = nullptr;
+    AttnWork* work = nullptr;
+    float* pooled = nullptr;
+};
+
+struct ProfStat {
+    int64_t launches = 0;
+    double ms = 0;
+};
+
+struct PendingEvent {
+    std::string name;
+    hipEvent_t a, b;
+};
+
+struct StopPoint {
+    std::string name;
+    int layer = -1;
+    bool hit = false;
+};
+
+}  // namespace
+}  // namespace ge
+
+struct ge_q8_matrix {
+    ge::Q8Dev m;
+};
+
+struct ge_ctx {
+    int device = 0;
+    hipStream_t stream = nullptr;
+    hipEvent_t ev_start = nullptr, ev_stop = nullptr;
+    std::string err, name;
+    bool has_model = false;
+    ge::DevModel model;
+    std::vector<void*> weight_allocs;
+    std::map<std::pair<int, float>, float*> rope_tables;
+    ge::Workspace ws;
+    // staged batch
+    int staged_tokens = -1, staged_seqs = 0, staged_work = 0;
+    // profiling
+    bool prof = false;
+    std::string prof_prefix;
+    std::vector<std::pair<std::string, ge::ProfStat>> prof_stats;
+    std::vector<ge::PendingEvent> prof_pending;
+    std::vector<hipEvent_t> event_pool;
+};
+
+namespace ge {
+namespace {
+
+thread_local std::string g_create_error;
+
+int set_error(ge_ctx* c, const Fail& f) {
+    if (c) c->err = f.msg;
+    return f.code;
+}
+
+template <typename F>
+int guarded(ge_ctx* c, F&& f) {
+    if (!c) return GE_ERR_INVALID;
+    try {
+        hipError_t e = hipSetDevice(c->device);
+        if (e != hipSuccess) fail(GE_ERR_GPU, "GPU execution failed: hipSetDevice: %s", hipGetErrorString(e));
+        f();
+        return GE_OK;
+    } catch (const Fail& fl) {
+        return set_error(c, fl);
+    } catch (const std::bad_alloc&) {
+        c->err = "out of host memory";
+        return GE_ERR_GPU;
+    } catch (const std::exception& ex) {
+        c->err = ex.what();
+        return GE_ERR_INVALID;
+    }
+}
+
+void* dev_alloc(size_t bytes, const char* what) {
+    void* p = nullptr;
+    if (bytes == 0) bytes = 16;
+    hipError_t e = hipMalloc(&p, bytes);
+    if (e != hipSuccess) fail(GE_ERR_GPU, "GPU execution failed: hipMalloc(%zu) for %s: %s", bytes, what, hipGetErrorString(e));
+    return p;
+}
+
+// ---------------------------------------------------------------- profiling
+
+hipEvent_t take_event(ge_ctx* c) {
+    if (!c->event_pool.empty()) {
+        hipEvent_t e = c->event_pool.back();
+        c->event_pool.pop_back();
+        return e;
+    }
+    hipEvent_t e;
+    hip_check(hipEventCreate(&e), "hipEventCreate");
+    return e;
+}
+
+void resolve_profile(ge_ctx* c) {
+    for (auto& p : c->prof_pending) {
+        hip_check(hipEventSynchronize(p.b), "hipEventSynchronize");
+        float ms = 0;
+        hip_check(hipEventElapsedTime(&ms, p.a, p.b), "hipEventElapsedTime");
+        auto it = std::find_if(c->prof_stats.begin(), c->prof_stats.end(), [&](auto& s) { return s.first == p.name; });
+        if (it == c->prof_stats.end()) {
+            c->prof_stats.push_back({p.name, ProfStat{}});
+            it = c->prof_stats.end() - 1;
+        }
+        it->second.launches++;
+        it->second.ms += ms;
+        c->event_pool.push_back(p.a);
+        c->event_pool.push_back(p.b);
+    }
+    c->prof_pending.clear();
+}
+
+// Runs one launch, bracketed by events when profiling covers `name`.
+template <typename F>
+void launch(ge_ctx* c, const char* name, F&& f) {
+    const bool prof = c->prof && std::strncmp(name, c->prof_prefix.c_str(), c->prof_prefix.size()) == 0;
+    hipEvent_t a = nullptr, b = nullptr;
+    if (prof) {
+        a = take_event(c);
+        b = take_event(c);
+        hip_check(hipEventRecord(a, c->stream), "hipEventRecord");
+    }
+    hipError_t e = f();
+    if (e != hipSuccess) fail(e == hipErrorInvalidValue ? GE_ERR_INVALID : GE_ERR_GPU, "GPU execution failed: %s: %s", name, hipGetErrorString(e));
+    if (prof) {
+        hip_check(hipEventRecord(b, c->stream), "hipEventRecord");
+        c->prof_pending.push_back({name, a, b});
+    }
+}
+
+// ---------------------------------------------------------------- upload
+
+const ge_tensor_desc* find(const ge_model_desc* d, const std::string& name, bool optional = false) {
+    for (int i = 0; i < d->n_tensors; i++)
+        if (d->tensors[i].name && name == d->tensors[i].name) return &d->tensors[i];
+    if (!optional) fail(GE_ERR_MODEL, "weight file lacks tensor %s", name.c_str());
+    return nullptr;
+}
+
+int64_t tensor_rows(const ge_tensor_desc* t) {
+    int64_t r = 1;
+    for (int i = 1; i < t->ndim; i++) r *= t->shape[i];
+    return r;
+}
+
+size_t tensor_bytes(const ge_tensor_desc* t) {
+    const int64_t n = t->shape[0] * tensor_rows(t);
+    switch (t->type) {
+    case GE_TYPE_F32: return size_t(n) * 4;
+    case GE_TYPE_F16:
+    case GE_TYPE_BF16: return size_t(n) * 2;
+    case GE_TYPE_Q8_0: return size_t(n) / 32 * 34;
+    default: return 0;
+    }
+}
+
+const uint8_t* tensor_ptr(const ge_tensor_desc* t, const void* base, size_t len) {
+    const size_t b = tensor_bytes(t);
+    if (b == 0) fail(GE_ERR_MODEL, "tensor %s uses unsupported storage type %d", t->name, t->type);
+    if (t->offset > len || b > len - t->offset) fail(GE_ERR_GGUF, "invalid GGUF file: tensor %s extends past the end of the file", t->name);
+    return static_cast<const uint8_t*>(base) + t->offset;
+}
+
+void check_shape(const ge_tensor_desc* t, int64_t cols, int64_t rows) {
+    if (t->shape[0] != cols || tensor_rows(t) != rows)
+        fail(GE_ERR_MODEL, "tensor %s has shape [%lld, %lld], expected [%lld, %lld]", t->name, (long long)t->shape[0],
+             (long long)tensor_rows(t), (long long)cols, (long long)rows);
+}
+
+// A Q8_0 matrix's rows, split into an int8 quant plane and an fp16 scale plane.
+struct HostQ8 {
+    int rows = 0, cols = 0;
+    std::vector<int8_t> q;
+    std::vector<uint16_t> s;
+};
+
+void repack_rows(const uint8_t* src, int rows, int cols, HostQ8* dst, int dst_row0) {
+    const int kb = cols / 32;
+    for (int r = 0; r < rows; r++) {
+        const uint8_t* row = src + (size_t)r * kb * 34;
+        int8_t* q = dst->q.data() + (size_t)(dst_row0 + r) * cols;
+        uint16_t* s = dst->s.data() + (size_t)(dst_row0 + r) * kb;
+        for (int b = 0; b < kb; b++) {
+            s[b] = uint16_t(row[b * 34] | (row[b * 34 + 1] << 8));
+            std::memcpy(q + b * 32, row + b * 34 + 2, 32);
+        }
+    }
+}
+
+HostQ8 host_q8(int rows, int cols) {
+    HostQ8 h;
+    h.rows = rows;
+    h.cols = cols;
+    h.q.resize((size_t)rows * cols);
+    h.s.resize((size_t)rows * (cols / 32));
+    return h;
+}
+
+Q8Dev upload_q8(ge_ctx* c, const HostQ8& h, const char* what) {
+    Q8Dev d;
+    d.rows = h.rows;
+    d.cols = h.cols;
+    d.q = static_cast<int8_t*>(dev_alloc(h.q.size(), what));
+    c->weight_allocs.push_back(d.q);
+    d.s = static_cast<uint16_t*>(dev_alloc(h.s.size() * 2, what));
+    c->weight_allocs.push_back(d.s);
+    hip_check(hipMemcpy(d.q, h.q.data(), h.q.size(), hipMemcpyHostToDevice), "hipMemcpy weights");
+    hip_check(hipMemcpy(d.s, h.s.data(), h.s.size() * 2, hipMemcpyHostToDevice), "hipMemcpy weights");
+    return d;
+}
+
+const uint8_t* q8_tensor(const ge_model_desc* d, const std::string& name, int64_t cols, int64_t rows, const void* base,
+                         size_t len) {
+    const ge_tensor_desc* t = find(d, name);
+    check_shape(t, cols, rows);
+    if (t->type != GE_TYPE_Q8_0)
+        fail(GE_ERR_MODEL, "tensor %s uses storage type %d; the MI355X GEMMs take Q8_0 projection weights", t->name, t->type);
+    if (cols % 32) fail(GE_ERR_MODEL, "tensor %s: Q8_0 rows must be a multiple of 32 wide", t->name);
+    return tensor_ptr(t, base, len);
+}
+
+float* upload_f32(ge_ctx* c, const ge_model_desc* d, const std::string& name, int64_t n, const void* base, size_t len) {
+    const ge_tensor_desc* t = find(d, name);
+    check_shape(t, n, 1);
+    if (t->type != GE_TYPE_F32) fail(GE_ERR_MODEL, "tensor %s uses unsupported storage type %d", t->name, t->type);
+    const uint8_t* p = tensor_ptr(t, base, len);
+    float* dptr = static_cast<float*>(dev_alloc(size_t(n) * 4, t->name));
+    c->weight_allocs.push_back(dptr);
+    hip_check(hipMemcpy(dptr, p, size_t(n) * 4, hipMemcpyHostToDevice), "hipMemcpy norm");
+    return dptr;
+}
+
+// RopeTable (Model/RopeTable.swift:16-31): cos/sin of pos * base^(-2i/hd) in fp64, stored fp32.
+const float* rope_table(ge_ctx* c, int hd, float base, int positions) {
+    auto key = std::make_pair(hd, base);
+    auto it = c->rope_tables.find(key);
+    if (it != c->rope_tables.end()) return it->second;
+    const int pairs = hd / 2;
+    std::vector<float> t((size_t)positions * pairs * 2);
+    for (int i = 0; i < pairs; i++) {
+        const double inv = std::pow(double(base), -2.0 * double(i) / double(hd));
+        for (int p = 0; p < positions; p++) {
+            const double th = double(p) * inv;
+            t[((size_t)p * pairs + i) * 2] = float(std::cos(th));
+            t[((size_t)p * pairs + i) * 2 + 1] = float(std::sin(th));
+        }
+    }
+    float* dptr = static_cast<float*>(dev_alloc(t.size() * 4, "rope table"));
+    c->weight_allocs.push_back(dptr);
+    hip_check(hipMemcpy(dptr, t.data(), t.size() * 4, hipMemcpyHostToDevice), "hipMemcpy rope");
+    c->rope_tables[key] = dptr;
+    return dptr;
+}
+
+// Bounds |act| = |gelu_tanh(h . g_j) * (h . u_j)| <= |h . g_j| |h . u_j| over any input: h is an
+// RMS-normalised row times the ffn_norm weight, so ||h||_2 <= sqrt(d) max|w|, and by Cauchy-Schwarz
+// |act_j| <= d max|w|^2 ||g_j||_2 ||u_j||_2. The shift keeps that bound under 2^15, half of fp16's
+// largest finite value, leaving room for the fp16 rounding of h and of the dequantised weights.
+void choose_act_scale(ge_ctx*, const ge_model_desc* d, const std::string& b, const uint8_t* g, const uint8_t* u, int D,
+                      int ff, const void* base, size_t len, DevLayer* L) {
+    const ge_tensor_desc* nt = find(d, b + "ffn_norm.weight");
+    check_shape(nt, D, 1);
+    const float* w = reinterpret_cast<const float*>(tensor_ptr(nt, base, len));
+    double wmax = 0;
+    for (int i = 0; i < D; i++) wmax = std::max(wmax, double(std::fabs(w[i])));
+    const size_t rb = size_t(D / 32) * 34;
+    double worst = 0;
+    for (int j = 0; j < ff; j++) {
+        double gg = 0, uu = 0;
+        for (int blk = 0; blk < D / 32; blk++) {
+            const uint8_t* gp = g + (size_t)j * rb + (size_t)blk * 34;
+            const uint8_t* up = u + (size_t)j * rb + (size_t)blk * 34;
+            const double gd = host_h2f(uint16_t(gp[0] | (gp[1] << 8))), ud = host_h2f(uint16_t(up[0] | (up[1] << 8)));
+            double gs = 0, us = 0;
+            for (int e = 0; e < 32; e++) {
+                gs += double(int8_t(gp[2 + e])) * int8_t(gp[2 + e]);
+                us += double(int8_t(up[2 + e])) * int8_t(up[2 + e]);
+            }
+            gg += gd * gd * gs;
+            uu += ud * ud * us;
+        }
+        worst = std::max(worst, std::sqrt(gg * uu));
+    }
+    const double bound = double(D) * wmax * wmax * worst;
+    int shift = 0;
+    while (bound * std::ldexp(1.0, -shift) > 32768.0 && shift < 60) shift++;
+    L->act_scale = float(std::ldexp(1.0, -shift));
+    L->down_scale = float(std::ldexp(1.0, shift));
+}
+
+void free_model(ge_ctx* c) {
+    for (void* p : c->weight_allocs) (void)hipFree(p);
+    c->weight_allocs.clear();
+    c->rope_tables.clear();
+    c->model = DevModel{};
+    c->has_model = false;
+}
+
+void free_workspace(ge_ctx* c) {
+    Workspace& w = c->ws;
+    void* ps[] = {w.x, w.qkv, w.t, w.out, w.h, w.q, w.k, w.v, w.attn, w.act, w.tokens, w.positions, w.seqs, w.work, w.pooled};
+    for (void* p : ps)
+        if (p) (void)hipFree(p);
+    c->ws = Workspace{};
+    c->staged_tokens = -1;
+}
+
+void upload(ge_ctx* c, const ge_model_desc* d, const void* base, size_t len) {
+    if (!d || !base) fail(GE_ERR_INVALID, "null model descriptor or file base");
+    if (d->layers <= 0 || d->hidden <= 0 || d->heads <= 0 || d->feed_forward <= 0 || d->out_dims <= 0 || d->vocab <= 0)
+        fail(GE_ERR_MODEL, "model descriptor has a non-positive size");
+    if (d->per_layer_input > 0)
+        fail(GE_ERR_MODEL, "the per-layer-input branch (per_layer_model_proj) is not supported on the GPU path yet");
+    if (d->hidden % 64 || d->hidden > 1024) fail(GE_ERR_MODEL, "hidden size %d: the kernels need a multiple of 64 up to 1024", d->hidden);
+    if (d->feed_forward % 32) fail(GE_ERR_MODEL, "feed_forward_length %d is not a multiple of 32", d->feed_forward);
+    if (d->out_dims % 64) fail(GE_ERR_MODEL, "embedding_length_out %d is not a multiple of 64", d->out_dims);
+    free_model(c);
+    free_workspace(c);
+    DevModel& m = c->model;
+    m.layers = d->layers;
+    m.hidden = d->hidden;
+    m.heads = d->heads;
+    m.ff = d->feed_forward;
+    m.out_dims = d->out_dims;
+    m.pl = d->per_layer_input;
+    m.vocab = d->vocab;
+    m.window = d->sliding_window;
+    m.max_tokens = d->max_tokens > 0 ? d->max_tokens : 8192;
+    m.eps = d->eps;
+    m.emb_scale = d->embedding_scale;
+    m.pl_scale = d->per_layer_scale;
+    const int D = m.hidden;
+
+    {
+        HostQ8 h = host_q8(m.vocab, D);
+        repack_rows(q8_tensor(d, "token_embd.weight", D, m.vocab, base, len), m.vocab, D, &h, 0);
+        m.tok_embd = upload_q8(c, h, "token_embd");
+    }
+    {
+        HostQ8 h = host_q8(m.out_dims, D);
+        repack_rows(q8_tensor(d, "output.weight", D, m.out_dims, base, len), m.out_dims, D, &h, 0);
+        m.output = upload_q8(c, h, "output");
+    }
+    m.out_norm = upload_f32(c, d, "output_norm.weight", D, base, len);
+    for (int i = 0; i < m.layers; i++) {
+        DevLayer L;
+        L.sliding = d->sliding[i] != 0;
+        L.kv_heads = d->kv_heads[i];
+        L.head_dim = d->head_dim[i];
+        L.rope_base = d->rope_base[i];
+        L.out_scale = d->out_scale ? d->out_scale[i] : 1.0f;
+        const int hd = L.head_dim;
+        if (L.kv_heads <= 0 || m.heads % L.kv_heads || m.heads / L.kv_heads > 4)
+            fail(GE_ERR_MODEL, "layer %d: %d query heads over %d KV heads (the attention kernel takes groups of 1 to 4)", i, m.heads, L.kv_heads);
+        if (hd != 128 && hd != 256 && hd != 512) fail(GE_ERR_MODEL, "layer %d: head dim %d (supported: 128, 256, 512)", i, hd);
+        L.qd = m.heads * hd;
+        L.kvd = L.kv_heads * hd;
+        const std::string b = "blk." + std::to_string(i) + ".";
+        {
+            const int n = L.qd + 2 * L.kvd;
+            HostQ8 h = host_q8(n, D);
+            repack_rows(q8_tensor(d, b + "attn_q.weight", D, L.qd, base, len), L.qd, D, &h, 0);
+            repack_rows(q8_tensor(d, b + "attn_k.weight", D, L.kvd, base, len), L.kvd, D, &h, L.qd);
+            repack_rows(q8_tensor(d, b + "attn_v.weight", D, L.kvd, base, len), L.kvd, D, &h, L.qd + L.kvd);
+            L.wqkv = upload_q8(c, h, "attn_qkv");
+        }
+        {
+            HostQ8 h = host_q8(D, L.qd);
+            repack_rows(q8_tensor(d, b + "attn_output.weight", L.qd, D, base, len), D, L.qd, &h, 0);
+            L.wo = upload_q8(c, h, "attn_output");
+        }
+        {
+            HostQ8 h = host_q8(2 * m.ff, D);
+            const uint8_t* g = q8_tensor(d, b + "ffn_gate.weight", D, m.ff, base, len);
+            const uint8_t* u = q8_tensor(d, b + "ffn_up.weight", D, m.ff, base, len);
+            const size_t rb = size_t(D / 32) * 34;
+            for (int jb = 0; jb < m.ff / 32; jb++) {
+                repack_rows(g + (size_t)jb * 32 * rb, 32, D, &h, jb * 64);
+                repack_rows(u + (size_t)jb * 32 * rb, 32, D, &h, jb * 64 + 32);
+            }
+            L.wgu = upload_q8(c, h, "ffn_gate_up");
+            choose_act_scale(c, d, b, g, u, D, m.ff, base, len, &L);
+        }
+        {
+            HostQ8 h = host_q8(D, m.ff);
+            repack_rows(q8_tensor(d, b + "ffn_down.weight", m.ff, D, base, len), D, m.ff, &h, 0);
+            L.wd = upload_q8(c, h, "ffn_down");
+        }
+        L.attn_norm = upload_f32(c, d, b + "attn_norm.weight", D, base, len);
+        L.q_norm = upload_f32(c, d, b + "attn_q_norm.weight", hd, base, len);
+        L.k_norm = upload_f32(c, d, b + "attn_k_norm.weight", hd, base, len);
+        L.post_attn = upload_f32(c, d, b + "post_attention_norm.weight", D, base, len);
+        L.ffn_norm = upload_f32(c, d, b + "ffn_norm.weight", D, base, len);
+        L.post_ffw = upload_f32(c, d, b + "post_ffw_norm.weight", D, base, len);
+        L.rope = rope_table(c, hd, L.rope_base, m.max_tokens);
+        m.max_qd = std::max(m.max_qd, L.qd);
+        m.max_kvd = std::max(m.max_kvd, L.kvd);
+        m.max_qkv = std::max(m.max_qkv, L.qd + 2 * L.kvd);
+        m.layer.push_back(L);
+    }
+    c->has_model = true;
+}
+
+// ---------------------------------------------------------------- workspace
+
+template <typename T>
+T* ws_alloc(size_t rows, size_t width, const char* what) {
+    const size_t bytes = rows * width * sizeof(T);
+    void* p = dev_alloc(bytes, what);
+    hip_check(hipMemset(p, 0, bytes), "hipMemset workspace");
+    return static_cast<T*>(p);
+}
+
+void ensure_workspace(ge_ctx* c, int tokens, int seqs, int work) {
+    Workspace& w = c->ws;
+    const DevModel& m = c->model;
+    const int rows = (tokens + 63) / 64 * 64 + kRowSlack;
+    if (rows > w.rows) {
+        const int keep_seq = w.seq_cap, keep_work = w.work_cap;
+        free_workspace(c);
+        w.seq_cap = keep_seq;
+        w.work_cap = keep_work;
+        w.rows = rows;
+        w.x = ws_alloc<float>(rows, m.hidden, "x");
+        w.h = ws_alloc<uint16_t>(rows, m.hidden, "h");
+        w.qkv = ws_alloc<float>(rows, m.max_qkv, "qkv");
+        w.q = ws_alloc<uint16_t>(rows, m.max_qd, "q");
+        w.k = ws_alloc<uint16_t>(rows, m.max_kvd, "k");
+        w.v = ws_alloc<uint16_t>(rows, m.max_kvd, "v");
+        w.attn = ws_alloc<uint16_t>(rows, m.max_qd, "attn");
+        w.t = ws_alloc<float>(rows, m.hidden, "t");
+        w.act = ws_alloc<uint16_t>(rows, m.ff, "act");
+        w.out = ws_alloc<float>(rows, m.out_dims, "out");
+        w.tokens = ws_alloc<int32_t>(rows, 1, "tokens");
+        w.positions = ws_alloc<int32_t>(rows, 1, "positions");
+        w.seqs = nullptr;
+        w.work = nullptr;
+        w.pooled = nullptr;
+        w.seq_cap = 0;
+        w.work_cap = 0;
+    }
+    if (seqs > w.seq_cap || !w.seqs) {
+        if (w.seqs) (void)hipFree(w.seqs);
+        if (w.pooled) (void)hipFree(w.pooled);
+        w.seq_cap = std::max(seqs, 1);
+        w.seqs = ws_alloc<SeqRange>(w.seq_cap, 1, "sequences");
+        w.pooled = ws_alloc<float>(w.seq_cap, m.out_dims, "pooled");
+    }
+    if (work > w.work_cap || !w.work) {
+        if (w.work) (void)hipFree(w.work);
+        w.work_cap = std::max(work, 1);
+        w.work = ws_alloc<AttnWork>(w.work_cap, 1, "attention work");
+    }
+}
+
+// ---------------------------------------------------------------- batch staging
+
+// Validates a packed batch and uploads it with its attention work list (PackedBatch and
+// AttentionWork.items, Metal/MetalForward.swift:8-58; execute :326-334).
+void stage(ge_ctx* c, const int32_t* tokens, const int32_t* positions, int n, const ge_seq* seqs, int n_seqs) {
+    if (!c->has_model) fail(GE_ERR_STATE, "no model has been uploaded");
+    if (n <= 0 || !tokens || !positions) fail(GE_ERR_INVALID, "a batch needs at least one token");
+    if (n_seqs <= 0 || !seqs) fail(GE_ERR_INVALID, "a batch needs at least one sequence");
+    const DevModel& m = c->model;
+    for (int i = 0; i < n; i++) {
+        if (tokens[i] < 0 || tokens[i] >= m.vocab)
+            fail(GE_ERR_INVALID, "token %d at row %d is outside the vocabulary [0, %d)", tokens[i], i, m.vocab);
+        if (positions[i] < 0 || positions[i] >= m.max_tokens)
+            fail(GE_ERR_INVALID, "position %d at row %d is outside [0, %d)", positions[i], i, m.max_tokens);
+    }
+    std::vector<AttnWork> work;
+    std::vector<SeqRange> sr((size_t)n_seqs);
+    for (int s = 0; s < n_seqs; s++) {
+        const uint64_t end = uint64_t(seqs[s].start) + seqs[s].length;
+        if (end > uint64_t(n)) fail(GE_ERR_INVALID, "sequence %d [%u, +%u) runs past the %d tokens", s, seqs[s].start, seqs[s].length, n);
+        if (seqs[s].length > uint32_t(m.max_tokens)) fail(GE_ERR_INVALID, "sequence %d has %u tokens, more than %d", s, seqs[s].length, m.max_tokens);
+        sr[s] = SeqRange{seqs[s].start, seqs[s].length};
+        for (uint32_t q0 = 0; q0 < seqs[s].length; q0 += kAttnQueries) work.push_back(AttnWork{seqs[s].start, seqs[s].length, q0});
+    }
+    ensure_workspace(c, n, n_seqs, int(work.size()));
+    Workspace& w = c->ws;
+    hip_check(hipMemcpyAsync(w.tokens, tokens, size_t(n) * 4, hipMemcpyHostToDevice, c->stream), "upload tokens");
+    hip_check(hipMemcpyAsync(w.positions, positions, size_t(n) * 4, hipMemcpyHostToDevice, c->stream), "upload positions");
+    hip_check(hipMemcpyAsync(w.seqs, sr.data(), sr.size() * sizeof(SeqRange), hipMemcpyHostToDevice, c->stream), "upload sequences");
+    if (!work.empty())
+        hip_check(hipMemcpyAsync(w.work, work.data(), work.size() * sizeof(AttnWork), hipMemcpyHostToDevice, c->stream), "upload work");
+    hip_check(hipStreamSynchronize(c->stream), "hipStreamSynchronize");
+    c->staged_tokens = n;
+    c->staged_seqs = n_seqs;
+    c->staged_work = int(work.size());
+}
+
+// ---------------------------------------------------------------- forward
+
+bool at(StopPoint* sp, const char* name, int layer) {
+    if (!sp || sp->hit) return false;
+    if (sp->name == name && sp->layer == layer) {
+        sp->hit = true;
+        return true;
+    }
+    return false;
+}
+
+// MetalForward.encode (Metal/MetalForward.swift:364-423) for the text path without the
+// per-layer-input branch: 7 launches per layer. Returns early after the op producing the stop point.
+void encode(ge_ctx* c, StopPoint* sp) {
+    const DevModel& m = c->model;
+    Workspace& w = c->ws;
+    const int T = c->staged_tokens;
+    hipStream_t s = c->stream;
+    const int D = m.hidden;
+    launch(c, "embed_norm", [&] {
+        return launch_embed_norm(s, m.tok_embd, w.tokens, T, m.emb_scale, m.layer[0].attn_norm, m.eps, w.x, w.h);
+    });
+    if (at(sp, "inp_scaled", -1) || at(sp, "attn_norm", 0)) return;
+    for (int l = 0; l < m.layers; l++) {
+        const DevLayer& L = m.layer[size_t(l)];
+        launch(c, "gemm_qkv", [&] { return launch_gemm_q8(s, L.wqkv, w.h, T, w.qkv, kEpiF32); });
+        if (at(sp, "Qcur", l) || at(sp, "Kcur", l) || at(sp, "Vcur", l)) return;
+        launch(c, "qk_norm_rope", [&] {
+            return launch_qk_norm_rope(s, w.qkv, T, m.heads, L.kv_heads, L.head_dim, L.q_norm, L.k_norm, m.eps, w.positions,
+                                       L.rope, w.q, w.k, w.v);
+        });
+        if (at(sp, "Qcur_pos", l) || at(sp, "Kcur_pos", l) || at(sp, "Vcur_normed", l)) return;
+        const int hw = L.sliding ? m.window / 2 : 0;  // halfWindow = slidingWindow / 2 (MetalForward.swift:399)
+        launch(c, "attention", [&] {
+            return launch_attention(s, w.q, w.k, w.v, w.attn, w.work, c->staged_work, m.heads, L.kv_heads, L.head_dim, hw, 1.0f);
+        });
+        if (at(sp, "kqv_out", l)) return;
+        launch(c, "gemm_o", [&] { return launch_gemm_q8(s, L.wo, w.attn, T, w.t, kEpiF32); });
+        launch(c, "residual_norm", [&] {
+            return launch_residual_norm(s, w.x, w.t, L.post_attn, 1.0f, L.ffn_norm, m.eps, T, D, w.h);
+        });
+        if (at(sp, "attn_out", l) || at(sp, "ffn_norm", l)) return;
+        launch(c, "gemm_gate_up", [&] { return launch_gemm_q8(s, L.wgu, w.h, T, w.act, kEpiGeglu, L.act_scale); });
+        if (at(sp, "ffn_geglu", l)) return;
+        launch(c, "gemm_down", [&] { return launch_gemm_q8(s, L.wd, w.act, T, w.t, kEpiF32, L.down_scale); });
+        if (at(sp, "ffn_out", l)) return;
+        const float* next = l + 1 < m.layers ? m.layer[size_t(l) + 1].attn_norm : m.out_norm;
+        launch(c, "residual_norm", [&] {
+            return launch_residual_norm(s, w.x, w.t, L.post_ffw, L.out_scale, next, m.eps, T, D, w.h);
+        });
+        if (at(sp, "pe_in", l) || at(sp, "l_out", l) || at(sp, "attn_norm", l + 1)) return;
+    }
+    if (at(sp, "result_norm", -1)) return;
+    launch(c, "gemm_output", [&] { return launch_gemm_q8(s, m.output, w.h, T, w.out, kEpiF32); });
+    if (at(sp, "result_embd", -1)) return;
+    launch(c, "mean_pool", [&] { return launch_mean_pool(s, w.out, w.seqs, c->staged_seqs, m.out_dims, w.pooled); });
+}
+
+void run_forward(ge_ctx* c, double* gpu_seconds) {
+    if (c->staged_tokens < 0) fail(GE_ERR_STATE, "no batch is staged");
+    hip_check(hipEventRecord(c->ev_start, c->stream), "hipEventRecord");
+    encode(c, nullptr);
+    hip_check(hipEventRecord(c->ev_stop, c->stream), "hipEventRecord");
+    if (gpu_seconds) {
+        hip_check(hipEventSynchronize(c->ev_stop), "hipEventSynchronize");
+        float ms = 0;
+        hip_check(hipEventElapsedTime(&ms, c->ev_start, c->ev_stop), "hipEventElapsedTime");
+        *gpu_seconds = ms * 1e-3;
+    }
+}
+
+void read_pooled(ge_ctx* c, float* out) {
+    hip_check(hipStreamSynchronize(c->stream), "hipStreamSynchronize");
+    if (c->prof) resolve_profile(c);
+    hip_check(hipMemcpy(out, c->ws.pooled, size_t(c->staged_seqs) * c->model.out_dims * 4, hipMemcpyDeviceToHost), "read pooled");
+}
+
+// Copies `rows` x `width` of a device buffer (fp32 or fp16, row stride `stride`) starting at
+// column `col0` into out as fp32.
+void copy_out(ge_ctx* c, const void* src, bool f16, int rows, int stride, int col0, int width, float* out) {
+    hip_check(hipStreamSynchronize(c->stream), "hipStreamSynchronize");
+    const size_t es = f16 ? 2 : 4;
+    std::vector<uint8_t> host((size_t)rows * stride * es);
+    hip_check(hipMemcpy(host.data(), src, host.size(), hipMemcpyDeviceToHost), "trace copy");
+    for (int r = 0; r < rows; r++)
+        for (int i = 0; i < width; i++) {
+            const size_t idx = (size_t)r * stride + col0 + i;
+            float v;
+            if (f16) {
+                uint16_t h;
+                std::memcpy(&h, host.data() + idx * 2, 2);
+                v = host_h2f(h);
+            } else {
+                std::memcpy(&v, host.data() + idx * 4, 4);
+            }
+            out[(size_t)r * width + i] = v;
+        }
+}
+
+void trace(ge_ctx* c, const char* name, int layer, float* out, size_t cap, size_t* needed) {
+    const DevModel& m = c->model;
+    const Workspace& w = c->ws;
+    const int T = c->staged_tokens;
+    if (!name) fail(GE_ERR_INVALID, "null tensor name");
+    if (layer < -1 || layer >= m.layers) fail(GE_ERR_INVALID, "layer %d out of range", layer);
+    const DevLayer* L = layer >= 0 ? &m.layer[size_t(layer)] : nullptr;
+    const std::string n = name;
+    // Which buffer holds the tensor, its element type, row stride, column range.
+    const void* buf = nullptr;
+    bool f16 = false;
+    int stride = 0, col0 = 0, width = 0;
+    auto need_layer = [&] {
+        if (!L) fail(GE_ERR_INVALID, "tensor %s needs a layer index", name);
+    };
+    if (n == "inp_scaled" || n == "attn_out" || n == "pe_in" || n == "l_out") {
+        if (n != "inp_scaled") need_layer();
+        buf = w.x; stride = width = m.hidden;
+    } else if (n == "attn_norm" || n == "ffn_norm" || n == "result_norm") {
+        if (n != "result_norm") need_layer();
+        buf = w.h; f16 = true; stride = width = m.hidden;
+    } else if (n == "Qcur" || n == "Kcur" || n == "Vcur") {
+        need_layer();
+        buf = w.qkv; stride = L->qd + 2 * L->kvd;
+        if (n == "Qcur") { col0 = 0; width = L->qd; }
+        else if (n == "Kcur") { col0 = L->qd; width = L->kvd; }
+        else { col0 = L->qd + L->kvd; width = L->kvd; }
+    } else if (n == "Qcur_pos") {
+        need_layer();
+        buf = w.q; f16 = true; stride = width = L->qd;
+    } else if (n == "Kcur_pos" || n == "Vcur_normed") {
+        need_layer();
+        buf = n == "Kcur_pos" ? w.k : w.v; f16 = true; stride = width = L->kvd;
+    } else if (n == "kqv_out") {
+        need_layer();
+        buf = w.attn; f16 = true; stride = width = L->qd;
+    } else if (n == "ffn_geglu") {
+        need_layer();
+        buf = w.act; f16 = true; stride = width = m.ff;
+    } else if (n == "ffn_out") {
+        need_layer();
+        buf = w.t; stride = width = m.hidden;
+    } else if (n == "result_embd") {
+        buf = w.out; stride = width = m.out_dims;
+    } else {
+        fail(GE_ERR_INVALID, "unknown trace tensor %s", name);
+    }
+    const size_t count = (size_t)T * width;
+    if (needed) *needed = count;
+    if (!out) return;
+    if (cap < count) fail(GE_ERR_INVALID, "trace buffer holds %zu floats, %s needs %zu", cap, name, count);
+    StopPoint sp{n, (n == "inp_scaled" || n == "result_norm" || n == "result_embd") ? -1 : layer, false};
+    encode(c, &sp);
+    if (!sp.hit) fail(GE_ERR_INVALID, "tensor %s at layer %d is not produced by this forward", name, layer);
+    copy_out(c, buf, f16, T, stride, col0, width, out);
+}
+
+}  // namespace
+}  // namespace ge
+
+using ge::Fail;
+using ge::fail;
+using ge::guarded;
+
+extern "C" {
+
+int ge_create(int device, ge_ctx** out) {
+    if (!out) return GE_ERR_INVALID;
+    *out = nullptr;
+    int count = 0;
+    hipError_t e = hipGetDeviceCount(&count);
+    if (e != hipSuccess || count == 0) {
+        ge::g_create_error = std::string("no HIP device is available: ") + hipGetErrorString(e);
+        return GE_ERR_NO_DEVICE;
+    }
+    if (device < 0 || device >= count) {
+        ge::g_create_error = "device " + std::to_string(device) + " does not exist (" + std::to_string(count) + " present)";
+        return GE_ERR_INVALID;
+    }
+    std::unique_ptr<ge_ctx> c(new ge_ctx);
+    c->device = device;
+    int rc = guarded(c.get(), [&] {
+        ge::hip_check(hipStreamCreateWithFlags(&c->stream, hipStreamNonBlocking), "hipStreamCreate");
+        ge::hip_check(hipEventCreate(&c->ev_start), "hipEventCreate");
+        ge::hip_check(hipEventCreate(&c->ev_stop), "hipEventCreate");
+        hipDeviceProp_t prop;
+        ge::hip_check(hipGetDeviceProperties(&prop, device), "hipGetDeviceProperties");
+        c->name = std::string(prop.name) + " (" + prop.gcnArchName + ")";
+        if (std::strncmp(prop.gcnArchName, "gfx950", 6) != 0)
+            fail(GE_ERR_NO_DEVICE, "device %d is %s; this library is built for gfx950 (MI355X)", device, prop.gcnArchName);
+        ge::hip_check(ge::configure_kernels(), "configure kernels");
+    });
+    if (rc != GE_OK) {
+        ge::g_create_error = c->err;
+        if (c->stream) (void)hipStreamDestroy(c->stream);
+        return rc;
+    }
+    *out = c.release();
+    return GE_OK;
+}
+
+void ge_destroy(ge_ctx* c) {
+    if (!c) return;
+    (void)hipSetDevice(c->device);
+    if (c->stream) (void)hipStreamSynchronize(c->stream);
+    ge::free_workspace(c);
+    ge::free_model(c);
+    for (auto& p : c->prof_pending) {
+        (void)hipEventDestroy(p.a);
+        (void)hipEventDestroy(p.b);
+    }
+    for (auto e : c->event_pool) (void)hipEventDestroy(e);
+    if (c->ev_start) (void)hipEventDestroy(c->ev_start);
+    if (c->ev_stop) (void)hipEventDestroy(c->ev_stop);
+    if (c->stream) (void)hipStreamDestroy(c->stream);
+    delete c;
+}
+
+const char* ge_last_error(const ge_ctx* c) { return c ? c->err.c_str() : "null context"; }
+const char* ge_create_error(void) { return ge::g_create_error.c_str(); }
+const char* ge_device_name(const ge_ctx* c) { return c ? c->name.c_str() : ""; }
+
+int ge_upload_model(ge_ctx* c, const ge_model_desc* desc, const void* base, size_t len) {
+    return guarded(c, [&] {
+        try {
+            ge::upload(c, desc, base, len);
+        } catch (...) {
+            ge::free_model(c);
+            throw;
+        }
+    });
+}
+
+int ge_forward(ge_ctx* c, const int32_t* tokens, const int32_t* positions, int32_t n, const ge_seq* seqs, int32_t n_seqs,
+               float* pooled, double* gpu_seconds) {
+    return guarded(c, [&] {
+        if (!pooled) fail(GE_ERR_INVALID, "null output");
+        ge::stage(c, tokens, positions, n, seqs, n_seqs);
+        ge::run_forward(c, gpu_seconds);
+        ge::read_pooled(c, pooled);
+    });
+}
+
+int ge_forward_trace(ge_ctx* c, const int32_t* tokens, const int32_t* positions, int32_t n, const ge_seq* seqs,
+                     int32_t n_seqs, const char* name, int32_t layer, float* out, size_t cap, size_t* needed) {
+    return guarded(c, [&] {
+        ge::stage(c, tokens, positions, n, seqs, n_seqs);
+        ge::trace(c, name, layer, out, cap, needed);
+    });
+}
+
+int ge_batch_stage(ge_ctx* c, const int32_t* tokens, const int32_t* positions, int32_t n, const ge_seq* seqs, int32_t n_seqs) {
+    return guarded(c, [&] { ge::stage(c, tokens, positions, n, seqs, n_seqs); });
+}
+
+int ge_batch_run(ge_ctx* c) {
+    return guarded(c, [&] { ge::run_forward(c, nullptr); });
+}
+
+int ge_batch_read(ge_ctx* c, float* pooled) {
+    return guarded(c, [&] {
+        if (!pooled) fail(GE_ERR_INVALID, "null output");
+        if (c->staged_tokens < 0) fail(GE_ERR_STATE, "no batch is staged");
+        ge::read_pooled(c, pooled);
+    });
+}
+
+int ge_sync(ge_ctx* c) {
+    return guarded(c, [&] {
+        ge::hip_check(hipStreamSynchronize(c->stream), "hipStreamSynchronize");
+        if (c->prof) ge::resolve_profile(c);
+    });
+}
+
+int ge_profile_enable(ge_ctx* c, const char* prefix) {
+    return guarded(c, [&] {
+        c->prof = true;
+        c->prof_prefix = prefix ? prefix : "";
+    });
+}
+
+int ge_profile_disable(ge_ctx* c) {
+    return guarded(c, [&] {
+        ge::hip_check(hipStreamSynchronize(c->stream), "hipStreamSynchronize");
+        ge::resolve_profile(c);
+        c->prof = false;
+    });
+}
+
+int ge_profile_reset(ge_ctx* c) {
+    return guarded(c, [&] {
+        ge::hip_check(hipStreamSynchronize(c->stream), "hipStreamSynchronize");
+        ge::resolve_profile(c);
+        c->prof_stats.clear();
+    });
+}
+
+int ge_profile_get(ge_ctx* c, int32_t i, const char** name, int64_t* launches, double* total_ms) {
+    return guarded(c, [&] {
+        ge::hip_check(hipStreamSynchronize(c->stream), "hipStreamSynchronize");
+        ge::resolve_profile(c);
+        if (i < 0 || size_t(i) >= c->prof_stats.size()) fail(GE_ERR_INVALID, "no kernel class %d", i);
+        if (name) *name = c->prof_stats[size_t(i)].first.c_str();
+        if (launches) *launches = c->prof_stats[size_t(i)].second.launches;
+        if (total_ms) *total_ms = c->prof_stats[size_t(i)].second.ms;
+    });
+}
+
+void* ge_dev_alloc(ge_ctx* c, size_t bytes) {
+    void* p = nullptr;
+    int rc = guarded(c, [&] {
+        p = ge::dev_alloc(bytes, "ge_dev_alloc");
+        ge::hip_check(hipMemset(p, 0, bytes ? bytes : 16), "hipMemset");
+    });
+    return rc == GE_OK ? p : nullptr;
+}
+
+int ge_dev_free(ge_ctx* c, void* p) {
+    return guarded(c, [&] { ge::hip_check(hipFree(p), "hipFree"); });
+}
+
+int ge_dev_upload(ge_ctx* c, void* dst, const void* src, size_t bytes) {
+    return guarded(c, [&] { ge::hip_check(hipMemcpy(dst, src, bytes, hipMemcpyHostToDevice), "hipMemcpy H2D"); });
+}
+
+int ge_dev_download(ge_ctx* c, void* dst, const void* src, size_t bytes) {
+    return guarded(c, [&] {
+        ge::hip_check(hipStreamSynchronize(c->stream), "hipStreamSynchronize");
+        ge::hip_check(hipMemcpy(dst, src, bytes, hipMemcpyDeviceToHost), "hipMemcpy D2H");
+    });
+}
+
+int ge_op_f32_to_f16(ge_ctx* c, const void* src, void* dst, size_t n) {
+    return guarded(c, [&] {
+        ge::launch(c, "f32_to_f16", [&] { return ge::launch_f32_to_f16(c->stream, static_cast<const float*>(src), static_cast<uint16_t*>(dst), n); });
+        ge::hip_check(hipStreamSynchronize(c->stream), "hipStreamSynchronize");
+    });
+}
+
+int ge_op_f16_to_f32(ge_ctx* c, const void* src, void* dst, size_t n) {
+    return guarded(c, [&] {
+        ge::launch(c, "f16_to_f32", [&] { return ge::launch_f16_to_f32(c->stream, static_cast<const uint16_t*>(src), static_cast<float*>(dst), n); });
+        ge::hip_check(hipStreamSynchronize(c->stream), "hipStreamSynchronize");
+    });
+}
+
+int ge_op_q8_create(ge_ctx* c, const void* rows_q8, int32_t rows, int32_t cols, ge_q8_matrix** out) {
+    if (out) *out = nullptr;
+    std::unique_ptr<ge_q8_matrix> m(new ge_q8_matrix);
+    int rc = guarded(c, [&] {
+        if (!rows_q8 || !out || rows <= 0 || cols <= 0 || cols % 32) fail(GE_ERR_INVALID, "Q8_0 matrix needs rows > 0 and cols a multiple of 32");
+        ge::HostQ8 h = ge::host_q8(rows, cols);
+        ge::repack_rows(static_cast<const uint8_t*>(rows_q8), rows, cols, &h, 0);
+        m->m.rows = rows;
+        m->m.cols = cols;
+        m->m.q = static_cast<int8_t*>(ge::dev_alloc(h.q.size(), "q8 matrix"));
+        m->m.s = static_cast<uint16_t*>(ge::dev_alloc(h.s.size() * 2, "q8 matrix"));
+        ge::hip_check(hipMemcpy(m->m.q, h.q.data(), h.q.size(), hipMemcpyHostToDevice), "hipMemcpy");
+        ge::hip_check(hipMemcpy(m->m.s, h.s.data(), h.s.size() * 2, hipMemcpyHostToDevice), "hipMemcpy");
+    });
+    if (rc != GE_OK) {
+        if (m->m.q) (void)hipFree(m->m.q);
+        if (m->m.s) (void)hipFree(m->m.s);
+        return rc;
+    }
+    *out = m.release();
+    return GE_OK;
+}
+
+int ge_op_q8_destroy(ge_ctx* c, ge_q8_matrix* m) {
+    if (!m) return GE_OK;
+    int rc = guarded(c, [&] {
+        ge::hip_check(hipFree(m->m.q), "hipFree");
+        ge::hip_check(hipFree(m->m.s), "hipFree");
+    });
+    delete m;
+    return rc;
+}
+
+int ge_op_gemm_q8(ge_ctx* c, const ge_q8_matrix* w, const void* x, int32_t m, void* y, int32_t y_f16) {
+    return guarded(c, [&] {
+        if (!w) fail(GE_ERR_INVALID, "null matrix");
+        ge::launch(c, "gemm", [&] {
+            return ge::launch_gemm_q8(c->stream, w->m, static_cast<const uint16_t*>(x), m, y, y_f16 ? ge::kEpiF16 : ge::kEpiF32);
+        });
+        ge::hip_check(hipStreamSynchronize(c->stream), "hipStreamSynchronize");
+    });
+}
+
+int ge_op_gemm_q8_geglu(ge_ctx* c, const ge_q8_matrix* gate, const ge_q8_matrix* up, const void* x, int32_t m, void* act) {
+    return guarded(c, [&] {
+        if (!gate || !up) fail(GE_ERR_INVALID, "null matrix");
+        if (gate->m.rows != up->m.rows || gate->m.cols != up->m.cols || gate->m.rows % 32)
+            fail(GE_ERR_INVALID, "gate and up must have the same shape, rows a multiple of 32");
+        // Interleave the two matrices' rows in 32-row groups on the device.
+        const int F = gate->m.rows, K = gate->m.cols;
+        ge::Q8Dev gu;
+        gu.rows = 2 * F;
+        gu.cols = K;
+        gu.q = static_cast<int8_t*>(ge::dev_alloc((size_t)gu.rows * K, "geglu"));
+        gu.s = static_cast<uint16_t*>(ge::dev_alloc((size_t)gu.rows * (K / 32) * 2, "geglu"));
+        struct Free {
+            ge::Q8Dev* p;
+            ~Free() {
+                (void)hipFree(p->q);
+                (void)hipFree(p->s);
+            }
+        } guard{&gu};
+        for (int jb = 0; jb < F / 32; jb++) {
+            for (int half = 0; half < 2; half++) {
+                const ge::Q8Dev& src = half ? up->m : gate->m;
+                ge::hip_check(hipMemcpyAsync(gu.q + (size_t)(jb * 64 + half * 32) * K, src.q + (size_t)jb * 32 * K, (size_t)32 * K,
+                                             hipMemcpyDeviceToDevice, c->stream), "hipMemcpy");
+                ge::hip_check(hipMemcpyAsync(gu.s + (size_t)(jb * 64 + half * 32) * (K / 32), src.s + (size_t)jb * 32 * (K / 32),
+                                             (size_t)32 * (K / 32) * 2, hipMemcpyDeviceToDevice, c->stream), "hipMemcpy");
+            }
+        }
+        ge::launch(c, "gemm_geglu", [&] {
+            return ge::launch_gemm_q8(c->stream, gu, static_cast<const uint16_t*>(x), m, act, ge::kEpiGeglu);
+        });
+        ge::hip_check(hipStreamSynchronize(c->stream), "hipStreamSynchronize");
+    });
+}
+
+int32_t ge_attention_queries(void) { return ge::kAttnQueries; }
+
+int ge_op_attention(ge_ctx* c, const void* q, const void* k, const void* v, void* out, const void* work, int32_t n_work,
+                    int32_t heads, int32_t kv_heads, int32_t head_dim, int32_t half_window, float scale) {
+    return guarded(c, [&] {
+        ge::launch(c, "attention", [&] {
+            return ge::launch_attention(c->stream, static_cast<const uint16_t*>(q), static_cast<const uint16_t*>(k),
+                                        static_cast<const uint16_t*>(v), static_cast<uint16_t*>(out),
+                                        static_cast<const ge::AttnWork*>(work), n_work, heads, kv_heads, head_dim,
+                                        half_window, scale);
+        });
+        ge::hip_check(hipStreamSynchronize(c->stream), "hipStreamSynchronize");
+    });
+}
+
+}  // extern "C"

@@ -1,0 +1,258 @@
+// Host mirror of the reference's public text API, over the device C-ABI:
+// EmbeddingModel.load / embed / embedTokens / batches / finish
+// (Sources/GemmaEmbed/EmbeddingModel.swift:40-289) with EmbedOptions / LoadOptions
+// (EmbedOptions.swift:35-56, :172-203). Token ids come in already tokenized: the task prefix
+// and the BPE tokenizer run before this boundary.
+#include <algorithm>
+#include <cmath>
+#include <cstdio>
+#include <cstring>
+#include <memory>
+#include <string>
+#include <vector>
+
+#include "gemmaembed.h"
+#include "gguf.hpp"
+
+struct ge_model {
+    std::unique_ptr<ge::GGUFFile> file;
+    ge::ModelConfig cfg;
+    ge_ctx* ctx = nullptr;
+    int budget = 8192;
+    std::string err;
+    std::string device_name;
+    ~ge_model() {
+        if (ctx) ge_destroy(ctx);
+    }
+};
+
+namespace ge {
+namespace {
+
+const int kAllowedDimensions[] = {768, 512, 256, 128};  // EmbedOptions.allowedDimensions (:55)
+
+// EmbeddingModel.batches (EmbeddingModel.swift:200-215).
+std::vector<int> plan_batches(const int32_t* costs, int n, const int32_t* budgets, int nb, int batch_size) {
+    std::vector<int> starts;
+    int start = 0;
+    std::vector<int64_t> totals(size_t(nb), 0);
+    for (int i = 0; i < n; i++) {
+        bool full = false;
+        if (batch_size > 0) {
+            full = i - start >= batch_size;
+        } else {
+            for (int b = 0; b < nb; b++)
+                if (totals[size_t(b)] + costs[size_t(i) * nb + b] > budgets[b]) full = true;
+        }
+        if (i > start && full) {
+            starts.push_back(start);
+            start = i;
+            std::fill(totals.begin(), totals.end(), 0);
+        }
+        for (int b = 0; b < nb; b++) totals[size_t(b)] += costs[size_t(i) * nb + b];
+    }
+    if (start < n) starts.push_back(start);
+    starts.push_back(n);
+    return starts;
+}
+
+// EmbeddingModel.finish (EmbeddingModel.swift:260-267).
+void finish(const float* v, int dims, bool normalise, float* out) {
+    for (int i = 0; i < dims; i++) out[i] = v[i];
+    if (normalise) {
+        float ss = 0;
+        for (int i = 0; i < dims; i++) ss += out[i] * out[i];
+        const float norm = std::sqrt(ss);
+        if (norm > 0)
+            for (int i = 0; i < dims; i++) out[i] /= norm;
+    }
+}
+
+int model_fail(ge_model* m, int code, const std::string& msg) {
+    m->err = msg;
+    return code;
+}
+
+// Runs one packed batch through the device (PackedBatch.append restarts positions at 0 per
+// sequence, Metal/MetalForward.swift:17-21).
+int run_batch(ge_model* m, const std::vector<std::vector<int32_t>>& seqs, std::vector<float>* pooled) {
+    std::vector<int32_t> tokens, positions;
+    std::vector<ge_seq> ranges;
+    for (const auto& s : seqs) {
+        ranges.push_back(ge_seq{uint32_t(tokens.size()), uint32_t(s.size())});
+        for (size_t i = 0; i < s.size(); i++) {
+            tokens.push_back(s[i]);
+            positions.push_back(int32_t(i));
+        }
+    }
+    pooled->assign(seqs.size() * size_t(m->cfg.out_dims), 0.0f);
+    int rc = ge_forward(m->ctx, tokens.data(), positions.data(), int32_t(tokens.size()), ranges.data(),
+                        int32_t(ranges.size()), pooled->data(), nullptr);
+    if (rc != GE_OK) m->err = ge_last_error(m->ctx);
+    return rc;
+}
+
+}  // namespace
+}  // namespace ge
+
+extern "C" {
+
+int ge_model_load(const char* path, const ge_load_options* options, ge_model** out, char* err, size_t errlen) {
+    auto report = [&](int code, const std::string& msg) {
+        if (err && errlen) std::snprintf(err, errlen, "%s", msg.c_str());
+        return code;
+    };
+    if (!path || !out) return report(GE_ERR_INVALID, "null argument");
+    *out = nullptr;
+    ge_load_options opt{0, 8192, 1};
+    if (options) opt = *options;
+    std::unique_ptr<ge_model> m(new ge_model);
+    try {
+        m->file.reset(new ge::GGUFFile(path));
+        m->cfg = ge::read_config(*m->file);
+    } catch (const ge::Error& e) {
+        return report(e.code, e.what());
+    }
+    int rc = ge_create(opt.device, &m->ctx);
+    if (rc != GE_OK) return report(rc, ge_create_error());
+    m->device_name = ge_device_name(m->ctx);
+    ge::UploadDesc u;
+    ge::make_upload_desc(*m->file, m->cfg, &u);
+    rc = ge_upload_model(m->ctx, &u.desc, m->file->base(), m->file->size());
+    if (rc != GE_OK) return report(rc, ge_last_error(m->ctx));
+    m->budget = opt.batch_token_budget > 0 ? std::max(64, opt.batch_token_budget) : 8192;
+    if (opt.warm_up) {
+        // EmbeddingModel.swift:111-114: one small forward before the first request.
+        std::vector<std::vector<int32_t>> warm{{m->cfg.bos_id, 2 < m->cfg.vocab ? 2 : 0, m->cfg.eos_id}};
+        std::vector<float> pooled;
+        rc = ge::run_batch(m.get(), warm, &pooled);
+        if (rc != GE_OK) return report(rc, m->err);
+    }
+    *out = m.release();
+    return GE_OK;
+}
+
+void ge_model_free(ge_model* m) { delete m; }
+
+const char* ge_model_last_error(const ge_model* m) { return m ? m->err.c_str() : "null model"; }
+
+ge_ctx* ge_model_context(ge_model* m) { return m ? m->ctx : nullptr; }
+
+int ge_model_get_info(const ge_model* m, ge_model_info* info) {
+    if (!m || !info) return GE_ERR_INVALID;
+    std::memset(info, 0, sizeof(*info));
+    std::snprintf(info->architecture, sizeof(info->architecture), "%s", m->cfg.architecture.c_str());
+    std::snprintf(info->name, sizeof(info->name), "%s", m->cfg.name.c_str());
+    std::snprintf(info->quantization, sizeof(info->quantization), "%s", m->cfg.quantization.c_str());
+    std::snprintf(info->device_name, sizeof(info->device_name), "%s", m->device_name.c_str());
+    info->layers = m->cfg.layers;
+    info->hidden = m->cfg.hidden;
+    info->out_dims = m->cfg.out_dims;
+    info->feed_forward = m->cfg.feed_forward;
+    info->per_layer_input = m->cfg.per_layer_input;
+    info->heads = m->cfg.heads;
+    info->vocab = m->cfg.vocab;
+    info->sliding_window = m->cfg.sliding_window;
+    info->max_tokens = m->cfg.max_tokens;
+    info->eps = m->cfg.eps;
+    info->file_size = int64_t(m->file->size());
+    info->bos_id = m->cfg.bos_id;
+    info->eos_id = m->cfg.eos_id;
+    return GE_OK;
+}
+
+int ge_plan_batches(const int32_t* costs, int32_t n, const int32_t* budgets, int32_t nb, int32_t batch_size,
+                    int32_t* starts, int32_t* n_ranges) {
+    if (n < 0 || nb <= 0 || !budgets || !starts || !n_ranges || (n > 0 && !costs)) return GE_ERR_INVALID;
+    std::vector<int> s = ge::plan_batches(costs, n, budgets, nb, batch_size);
+    for (size_t i = 0; i < s.size(); i++) starts[i] = s[i];
+    *n_ranges = int32_t(s.size()) - 1;
+    return GE_OK;
+}
+
+int ge_finish(const float* v, int32_t width, int32_t dims, int32_t normalise, float* out) {
+    if (!v || !out || dims <= 0 || dims > width) return GE_ERR_INVALID;
+    ge::finish(v, dims, normalise != 0, out);
+    return GE_OK;
+}
+
+int ge_model_embed(ge_model* m, const int32_t* tokens, const int32_t* lengths, int32_t n, const ge_embed_options* options,
+                   float* out, int32_t* token_counts, uint8_t* truncated, ge_progress_fn progress, void* user) {
+    if (!m) return GE_ERR_INVALID;
+    ge_embed_options opt{2048, 768, 1, 0};
+    if (options) opt = *options;
+    bool allowed = false;
+    for (int d : ge::kAllowedDimensions) allowed |= opt.dimensions == d;
+    if (!allowed) return ge::model_fail(m, GE_ERR_OPTIONS, "invalid options: dimensions must be one of [768, 512, 256, 128]");
+    if (opt.dimensions > m->cfg.out_dims)
+        return ge::model_fail(m, GE_ERR_OPTIONS, "invalid options: dimensions exceed the model's " + std::to_string(m->cfg.out_dims));
+    if (opt.max_tokens < 2 || opt.max_tokens > m->cfg.max_tokens)
+        return ge::model_fail(m, GE_ERR_OPTIONS, "invalid options: maxTokens must be between 2 and " + std::to_string(m->cfg.max_tokens));
+    if (opt.batch_size < 0) return ge::model_fail(m, GE_ERR_OPTIONS, "invalid options: batchSize must be at least 1");
+    if (n < 0 || (n > 0 && (!tokens || !lengths || !out))) return ge::model_fail(m, GE_ERR_INVALID, "null argument");
+    if (n == 0) return GE_OK;
+
+    // prepare (EmbeddingModel.swift:189-196): keep the first maxTokens - 1 ids and end with EOS.
+    std::vector<std::vector<int32_t>> prepared{size_t(n)};
+    std::vector<uint8_t> cut(static_cast<size_t>(n), 0);
+    size_t off = 0;
+    for (int i = 0; i < n; i++) {
+        if (lengths[i] < 0) return ge::model_fail(m, GE_ERR_INVALID, "negative length");
+        const int32_t* ids = tokens + off;
+        off += size_t(lengths[i]);
+        if (lengths[i] > opt.max_tokens) {
+            prepared[size_t(i)].assign(ids, ids + opt.max_tokens - 1);
+            prepared[size_t(i)].push_back(m->cfg.eos_id);
+            cut[size_t(i)] = 1;
+        } else {
+            prepared[size_t(i)].assign(ids, ids + lengths[i]);
+        }
+        if (prepared[size_t(i)].empty()) return ge::model_fail(m, GE_ERR_INVALID, "text " + std::to_string(i) + " has no tokens");
+    }
+    std::vector<int32_t> costs(static_cast<size_t>(n));
+    for (int i = 0; i < n; i++) costs[size_t(i)] = int32_t(prepared[size_t(i)].size());
+    const int32_t budget = m->budget;
+    std::vector<int> starts = ge::plan_batches(costs.data(), n, &budget, 1, opt.batch_size);
+    int completed_texts = 0;
+    int64_t completed_tokens = 0;
+    std::vector<float> pooled;
+    for (size_t r = 0; r + 1 < starts.size(); r++) {
+        std::vector<std::vector<int32_t>> batch(prepared.begin() + starts[r], prepared.begin() + starts[r + 1]);
+        int rc = ge::run_batch(m, batch, &pooled);
+        if (rc != GE_OK) return rc;
+        for (int i = starts[r]; i < starts[r + 1]; i++) {
+            const size_t j = size_t(i - starts[r]);
+            ge::finish(pooled.data() + j * size_t(m->cfg.out_dims), opt.dimensions, opt.normalise != 0,
+                       out + size_t(i) * size_t(opt.dimensions));
+            if (token_counts) token_counts[i] = costs[size_t(i)];
+            if (truncated) truncated[i] = cut[size_t(i)];
+            completed_tokens += costs[size_t(i)];
+        }
+        completed_texts = starts[r + 1];
+        // EmbeddingProgress after every batch; a non-zero return cancels before the next one
+        // (Task.checkCancellation, EmbeddingModel.swift:162).
+        if (progress && progress(user, completed_texts, n, completed_tokens) != 0 && r + 2 < starts.size())
+            return ge::model_fail(m, GE_ERR_CANCELLED, "embedding was cancelled");
+    }
+    return GE_OK;
+}
+
+int ge_model_embed_tokens(ge_model* m, const int32_t* tokens, const int32_t* lengths, int32_t n, float* out) {
+    if (!m) return GE_ERR_INVALID;
+    if (n < 0 || (n > 0 && (!tokens || !lengths || !out))) return ge::model_fail(m, GE_ERR_INVALID, "null argument");
+    if (n == 0) return GE_OK;
+    std::vector<std::vector<int32_t>> seqs{size_t(n)};
+    size_t off = 0;
+    for (int i = 0; i < n; i++) {
+        if (lengths[i] <= 0) return ge::model_fail(m, GE_ERR_INVALID, "text " + std::to_string(i) + " has no tokens");
+        seqs[size_t(i)].assign(tokens + off, tokens + off + lengths[i]);
+        off += size_t(lengths[i]);
+    }
+    std::vector<float> pooled;
+    int rc = ge::run_batch(m, seqs, &pooled);
+    if (rc != GE_OK) return rc;
+    std::memcpy(out, pooled.data(), pooled.size() * sizeof(float));
+    return GE_OK;
+}
+
+}  // extern "C"

@@ -1,0 +1,495 @@
+"""ctypes binding of libgemmaembed.so, the MI355X GemmaEmbed text-encoder library.
+
+Mirrors the reference's Swift API names (Sources/GemmaEmbed/EmbeddingModel.swift):
+``EmbeddingModel.load`` / ``embed`` / ``embed_tokens`` / ``similarity``, ``EmbedOptions``,
+``plan_batches`` (EmbeddingModel.batches) and ``finish``. Errors raise ``GemmaEmbedError``
+carrying the C status code (Errors.swift:6-24). Compute always runs in the native library: when
+``libgemmaembed.so`` is missing, importing this module raises instead of falling back.
+"""
+from __future__ import annotations
+
+import ctypes as C
+import os
+from dataclasses import dataclass
+from typing import Callable, Iterable, List, Optional, Sequence
+
+import numpy as np
+
+_HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(os.path.dirname(_HERE), "libgemmaembed.so")
+
+GE_OK = 0
+ERRORS = {
+    1: "invalid",
+    2: "invalidGGUF",
+    3: "model",
+    4: "gpuFailure",
+    5: "invalidOptions",
+    6: "state",
+    7: "cancelled",
+    8: "noDevice",
+}
+GE_TYPE_F32, GE_TYPE_F16, GE_TYPE_Q8_0, GE_TYPE_BF16 = 0, 1, 8, 30
+
+
+class GemmaEmbedError(RuntimeError):
+    def __init__(self, code: int, message: str):
+        super().__init__(f"[{ERRORS.get(code, code)}] {message}")
+        self.code = code
+        self.kind = ERRORS.get(code, str(code))
+        self.message = message
+
+
+class ge_seq(C.Structure):
+    _fields_ = [("start", C.c_uint32), ("length", C.c_uint32)]
+
+
+class ge_attention_work(C.Structure):
+    _fields_ = [("seq_start", C.c_uint32), ("seq_len", C.c_uint32), ("q0", C.c_uint32)]
+
+
+class ge_load_options(C.Structure):
+    _fields_ = [("device", C.c_int32), ("batch_token_budget", C.c_int32), ("warm_up", C.c_int32)]
+
+
+class ge_embed_options(C.Structure):
+    _fields_ = [("max_tokens", C.c_int32), ("dimensions", C.c_int32), ("normalise", C.c_int32),
+                ("batch_size", C.c_int32)]
+
+
+class ge_model_info(C.Structure):
+    _fields_ = [("architecture", C.c_char * 64), ("name", C.c_char * 128),
+                ("layers", C.c_int32), ("hidden", C.c_int32), ("out_dims", C.c_int32),
+                ("feed_forward", C.c_int32), ("per_layer_input", C.c_int32), ("heads", C.c_int32),
+                ("vocab", C.c_int32), ("sliding_window", C.c_int32), ("max_tokens", C.c_int32),
+                ("eps", C.c_float), ("quantization", C.c_char * 16), ("device_name", C.c_char * 128),
+                ("file_size", C.c_int64), ("bos_id", C.c_int32), ("eos_id", C.c_int32)]
+
+
+class ge_synth_spec(C.Structure):
+    _fields_ = [("layers", C.c_int32), ("hidden", C.c_int32), ("heads", C.c_int32),
+                ("feed_forward", C.c_int32), ("out_dims", C.c_int32), ("per_layer_input", C.c_int32),
+                ("vocab", C.c_int32), ("sliding_window", C.c_int32), ("head_dim_swa", C.c_int32),
+                ("head_dim_global", C.c_int32), ("kv_heads_swa", C.c_int32), ("kv_heads_global", C.c_int32),
+                ("eps", C.c_float), ("rope_base", C.c_float), ("rope_base_swa", C.c_float),
+                ("pattern", C.POINTER(C.c_uint8)), ("seed", C.c_uint64)]
+
+
+PROGRESS_FN = C.CFUNCTYPE(C.c_int, C.c_void_p, C.c_int32, C.c_int32, C.c_int64)
+
+# Every symbol include/gemmaembed.h declares, with its ctypes signature.
+_P = C.c_void_p
+_I = C.c_int
+_PI32 = C.POINTER(C.c_int32)
+_PF = C.POINTER(C.c_float)
+SIGNATURES = {
+    "ge_create": (_I, [C.c_int, C.POINTER(_P)]),
+    "ge_destroy": (None, [_P]),
+    "ge_last_error": (C.c_char_p, [_P]),
+    "ge_create_error": (C.c_char_p, []),
+    "ge_device_name": (C.c_char_p, [_P]),
+    "ge_upload_model": (_I, [_P, _P, _P, C.c_size_t]),
+    "ge_forward": (_I, [_P, _PI32, _PI32, C.c_int32, C.POINTER(ge_seq), C.c_int32, _PF, C.POINTER(C.c_double)]),
+    "ge_forward_trace": (_I, [_P, _PI32, _PI32, C.c_int32, C.POINTER(ge_seq), C.c_int32, C.c_char_p, C.c_int32,
+                              _PF, C.c_size_t, C.POINTER(C.c_size_t)]),
+    "ge_batch_stage": (_I, [_P, _PI32, _PI32, C.c_int32, C.POINTER(ge_seq), C.c_int32]),
+    "ge_batch_run": (_I, [_P]),
+    "ge_batch_read": (_I, [_P, _PF]),
+    "ge_sync": (_I, [_P]),
+    "ge_profile_enable": (_I, [_P, C.c_char_p]),
+    "ge_profile_disable": (_I, [_P]),
+    "ge_profile_reset": (_I, [_P]),
+    "ge_profile_get": (_I, [_P, C.c_int32, C.POINTER(C.c_char_p), C.POINTER(C.c_int64), C.POINTER(C.c_double)]),
+    "ge_dev_alloc": (_P, [_P, C.c_size_t]),
+    "ge_dev_free": (_I, [_P, _P]),
+    "ge_dev_upload": (_I, [_P, _P, _P, C.c_size_t]),
+    "ge_dev_download": (_I, [_P, _P, _P, C.c_size_t]),
+    "ge_op_f32_to_f16": (_I, [_P, _P, _P, C.c_size_t]),
+    "ge_op_f16_to_f32": (_I, [_P, _P, _P, C.c_size_t]),
+    "ge_op_q8_create": (_I, [_P, _P, C.c_int32, C.c_int32, C.POINTER(_P)]),
+    "ge_op_q8_destroy": (_I, [_P, _P]),
+    "ge_op_gemm_q8": (_I, [_P, _P, _P, C.c_int32, _P, C.c_int32]),
+    "ge_op_gemm_q8_geglu": (_I, [_P, _P, _P, _P, C.c_int32, _P]),
+    "ge_attention_queries": (C.c_int32, []),
+    "ge_op_attention": (_I, [_P, _P, _P, _P, _P, _P, C.c_int32, C.c_int32, C.c_int32, C.c_int32, C.c_int32,
+                             C.c_float]),
+    "ge_model_load": (_I, [C.c_char_p, C.POINTER(ge_load_options), C.POINTER(_P), C.c_char_p, C.c_size_t]),
+    "ge_model_free": (None, [_P]),
+    "ge_model_last_error": (C.c_char_p, [_P]),
+    "ge_model_get_info": (_I, [_P, C.POINTER(ge_model_info)]),
+    "ge_model_context": (_P, [_P]),
+    "ge_model_embed": (_I, [_P, _PI32, _PI32, C.c_int32, C.POINTER(ge_embed_options), _PF, _PI32,
+                            C.POINTER(C.c_uint8), PROGRESS_FN, _P]),
+    "ge_model_embed_tokens": (_I, [_P, _PI32, _PI32, C.c_int32, _PF]),
+    "ge_plan_batches": (_I, [_PI32, C.c_int32, _PI32, C.c_int32, C.c_int32, _PI32, _PI32]),
+    "ge_finish": (_I, [_PF, C.c_int32, C.c_int32, C.c_int32, _PF]),
+    "ge_synth_write_gguf": (_I, [C.c_char_p, C.POINTER(ge_synth_spec), C.c_char_p, C.c_size_t]),
+    "ge_synth_tokens": (_I, [C.c_uint64, C.c_int32, C.c_int32, C.c_int32, _PI32]),
+}
+
+
+def _load() -> C.CDLL:
+    if not os.path.exists(LIB_PATH):
+        raise ImportError(f"{LIB_PATH} is not built; run __graft_entry__.build() (make -C gemma-embed-swift_amd)")
+    lib = C.CDLL(LIB_PATH)
+    for name, (res, args) in SIGNATURES.items():
+        fn = getattr(lib, name)
+        fn.restype = res
+        fn.argtypes = args
+    return lib
+
+
+lib = _load()
+
+
+def _i32(a) -> np.ndarray:
+    return np.ascontiguousarray(a, dtype=np.int32)
+
+
+def _ptr(a: np.ndarray, ctype):
+    return a.ctypes.data_as(C.POINTER(ctype))
+
+
+# ---------------------------------------------------------------------------- pure host helpers
+
+def plan_batches(costs: Sequence[Sequence[int]] | Sequence[int], budgets: Sequence[int],
+                 batch_size: Optional[int] = None) -> List[range]:
+    """EmbeddingModel.batches (EmbeddingModel.swift:200-215) through the native implementation."""
+    c = np.asarray(costs, dtype=np.int32)
+    if c.ndim == 1:
+        c = c.reshape(-1, 1)
+    n = c.shape[0] if c.size else 0
+    b = _i32(budgets)
+    if c.size == 0:
+        c = np.zeros((0, len(b)), dtype=np.int32)
+    c = np.ascontiguousarray(c)
+    starts = np.zeros(n + 1, dtype=np.int32)
+    nr = C.c_int32(0)
+    rc = lib.ge_plan_batches(_ptr(c, C.c_int32), n, _ptr(b, C.c_int32), len(b), int(batch_size or 0),
+                             _ptr(starts, C.c_int32), C.byref(nr))
+    if rc != GE_OK:
+        raise GemmaEmbedError(rc, "ge_plan_batches")
+    return [range(int(starts[i]), int(starts[i + 1])) for i in range(nr.value)]
+
+
+def finish(vector: np.ndarray, dimensions: int, normalise: bool = True) -> np.ndarray:
+    """EmbeddingModel.finish (EmbeddingModel.swift:260-267)."""
+    v = np.ascontiguousarray(vector, dtype=np.float32)
+    out = np.zeros(dimensions, dtype=np.float32)
+    rc = lib.ge_finish(_ptr(v, C.c_float), v.size, dimensions, int(normalise), _ptr(out, C.c_float))
+    if rc != GE_OK:
+        raise GemmaEmbedError(rc, "ge_finish: dimensions out of range")
+    return out
+
+
+def synth_tokens(seed: int, lo: int, hi: int, count: int) -> np.ndarray:
+    out = np.zeros(count, dtype=np.int32)
+    rc = lib.ge_synth_tokens(seed, lo, hi, count, _ptr(out, C.c_int32))
+    if rc != GE_OK:
+        raise GemmaEmbedError(rc, "ge_synth_tokens")
+    return out
+
+
+# Synthetic model shapes. CONFIG2 is BASELINE.json's "Gemma-3-style" encoder (configs 2-4):
+# 24 layers, d 768, 3 query heads / 1 KV head of 256, GeGLU 1152, window 512, global layers at
+# 5, 11, 17, 23 with RoPE base 1e6 (sliding 1e4), vocab 262144, output 768, no per-layer input.
+CONFIG2 = dict(layers=24, hidden=768, heads=3, feed_forward=1152, out_dims=768, per_layer_input=0,
+               vocab=262144, sliding_window=512, head_dim_swa=256, head_dim_global=256, kv_heads_swa=1,
+               kv_heads_global=1, eps=1e-6, rope_base=1e6, rope_base_swa=1e4,
+               pattern=[1, 1, 1, 1, 1, 0] * 4, seed=4)
+# A two-layer model small enough for brute-force float64 checks.
+TINY = dict(layers=2, hidden=128, heads=2, feed_forward=256, out_dims=128, per_layer_input=0, vocab=512,
+            sliding_window=16, head_dim_swa=128, head_dim_global=128, kv_heads_swa=1, kv_heads_global=1,
+            eps=1e-6, rope_base=1e6, rope_base_swa=1e4, pattern=[1, 0], seed=7)
+
+
+def synth_write_gguf(path: str, **spec) -> str:
+    """Writes a seeded synthetic gemma-embedding2 GGUF (see ge_synth_write_gguf)."""
+    pattern = np.ascontiguousarray(spec["pattern"], dtype=np.uint8)
+    s = ge_synth_spec()
+    for k in ("layers", "hidden", "heads", "feed_forward", "out_dims", "per_layer_input", "vocab",
+              "sliding_window", "head_dim_swa", "head_dim_global", "kv_heads_swa", "kv_heads_global"):
+        setattr(s, k, int(spec[k]))
+    s.eps, s.rope_base, s.rope_base_swa = spec["eps"], spec["rope_base"], spec["rope_base_swa"]
+    s.pattern = _ptr(pattern, C.c_uint8)
+    s.seed = int(spec["seed"])
+    err = C.create_string_buffer(512)
+    rc = lib.ge_synth_write_gguf(path.encode(), C.byref(s), err, 512)
+    if rc != GE_OK:
+        raise GemmaEmbedError(rc, err.value.decode())
+    return path
+
+
+# ---------------------------------------------------------------------------- device context
+
+def pack(sequences: Sequence[Sequence[int]]):
+    """PackedBatch.append (Metal/MetalForward.swift:17-21): ids back to back, positions from 0."""
+    toks, pos, seqs = [], [], []
+    for s in sequences:
+        seqs.append((len(toks), len(s)))
+        toks.extend(int(t) for t in s)
+        pos.extend(range(len(s)))
+    return _i32(toks), _i32(pos), seqs
+
+
+def _seq_array(seqs) -> C.Array:
+    arr = (ge_seq * max(len(seqs), 1))()
+    for i, (st, ln) in enumerate(seqs):
+        arr[i].start, arr[i].length = st, ln
+    return arr
+
+
+class Context:
+    """A device context (ge_ctx). Owned contexts are destroyed on close(); borrowed ones
+    (a loaded model's) are not."""
+
+    def __init__(self, handle: int, owned: bool, out_dims: int = 0):
+        self.handle = C.c_void_p(handle)
+        self.owned = owned
+        self.out_dims = out_dims
+
+    @classmethod
+    def create(cls, device: int = 0) -> "Context":
+        h = C.c_void_p()
+        rc = lib.ge_create(device, C.byref(h))
+        if rc != GE_OK:
+            raise GemmaEmbedError(rc, lib.ge_create_error().decode())
+        return cls(h.value, True)
+
+    def close(self):
+        if self.owned and self.handle:
+            lib.ge_destroy(self.handle)
+        self.handle = C.c_void_p()
+
+    def _check(self, rc: int, what: str):
+        if rc != GE_OK:
+            raise GemmaEmbedError(rc, f"{what}: {lib.ge_last_error(self.handle).decode()}")
+
+    @property
+    def device_name(self) -> str:
+        return lib.ge_device_name(self.handle).decode()
+
+    def forward(self, sequences: Sequence[Sequence[int]]):
+        """One packed batch -> (pooled [n_seqs, out_dims], gpu_seconds)."""
+        toks, pos, seqs = pack(sequences)
+        out = np.zeros((len(seqs), self.out_dims), dtype=np.float32)
+        secs = C.c_double(0)
+        self._check(lib.ge_forward(self.handle, _ptr(toks, C.c_int32), _ptr(pos, C.c_int32), len(toks),
+                                   _seq_array(seqs), len(seqs), _ptr(out, C.c_float), C.byref(secs)), "ge_forward")
+        return out, secs.value
+
+    def trace(self, sequences: Sequence[Sequence[int]], name: str, layer: int = -1) -> np.ndarray:
+        """The named intermediate (llama.cpp names) over the packed tokens, fp32 [T, width]."""
+        toks, pos, seqs = pack(sequences)
+        need = C.c_size_t(0)
+        sa = _seq_array(seqs)
+        self._check(lib.ge_forward_trace(self.handle, _ptr(toks, C.c_int32), _ptr(pos, C.c_int32), len(toks), sa,
+                                         len(seqs), name.encode(), layer, None, 0, C.byref(need)), "ge_forward_trace")
+        out = np.zeros(need.value, dtype=np.float32)
+        self._check(lib.ge_forward_trace(self.handle, _ptr(toks, C.c_int32), _ptr(pos, C.c_int32), len(toks), sa,
+                                         len(seqs), name.encode(), layer, _ptr(out, C.c_float), out.size,
+                                         C.byref(need)), "ge_forward_trace")
+        return out.reshape(len(toks), -1)
+
+    def batch_stage(self, sequences: Sequence[Sequence[int]]):
+        toks, pos, seqs = pack(sequences)
+        self._check(lib.ge_batch_stage(self.handle, _ptr(toks, C.c_int32), _ptr(pos, C.c_int32), len(toks),
+                                       _seq_array(seqs), len(seqs)), "ge_batch_stage")
+        self._staged = len(seqs)
+
+    def batch_run(self):
+        self._check(lib.ge_batch_run(self.handle), "ge_batch_run")
+
+    def batch_read(self) -> np.ndarray:
+        out = np.zeros((self._staged, self.out_dims), dtype=np.float32)
+        self._check(lib.ge_batch_read(self.handle, _ptr(out, C.c_float)), "ge_batch_read")
+        return out
+
+    def sync(self):
+        self._check(lib.ge_sync(self.handle), "ge_sync")
+
+    def profile_enable(self, prefix: str = ""):
+        self._check(lib.ge_profile_enable(self.handle, prefix.encode()), "ge_profile_enable")
+
+    def profile_disable(self):
+        self._check(lib.ge_profile_disable(self.handle), "ge_profile_disable")
+
+    def profile_reset(self):
+        self._check(lib.ge_profile_reset(self.handle), "ge_profile_reset")
+
+    def profile_stats(self) -> dict:
+        stats, i = {}, 0
+        while True:
+            name, n, ms = C.c_char_p(), C.c_int64(), C.c_double()
+            if lib.ge_profile_get(self.handle, i, C.byref(name), C.byref(n), C.byref(ms)) != GE_OK:
+                break
+            stats[name.value.decode()] = (n.value, ms.value)
+            i += 1
+        return stats
+
+    # -- device memory and per-op entry points
+    def alloc(self, nbytes: int) -> int:
+        p = lib.ge_dev_alloc(self.handle, nbytes)
+        if not p:
+            raise GemmaEmbedError(4, f"ge_dev_alloc: {lib.ge_last_error(self.handle).decode()}")
+        return p
+
+    def free(self, p: int):
+        self._check(lib.ge_dev_free(self.handle, C.c_void_p(p)), "ge_dev_free")
+
+    def upload(self, p: int, a: np.ndarray):
+        a = np.ascontiguousarray(a)
+        self._check(lib.ge_dev_upload(self.handle, C.c_void_p(p), a.ctypes.data_as(C.c_void_p), a.nbytes),
+                    "ge_dev_upload")
+
+    def download(self, p: int, shape, dtype) -> np.ndarray:
+        out = np.zeros(shape, dtype=dtype)
+        self._check(lib.ge_dev_download(self.handle, out.ctypes.data_as(C.c_void_p), C.c_void_p(p), out.nbytes),
+                    "ge_dev_download")
+        return out
+
+    def f32_to_f16(self, src: int, dst: int, n: int):
+        self._check(lib.ge_op_f32_to_f16(self.handle, C.c_void_p(src), C.c_void_p(dst), n), "ge_op_f32_to_f16")
+
+    def f16_to_f32(self, src: int, dst: int, n: int):
+        self._check(lib.ge_op_f16_to_f32(self.handle, C.c_void_p(src), C.c_void_p(dst), n), "ge_op_f16_to_f32")
+
+    def q8_create(self, rows_q8: np.ndarray, rows: int, cols: int) -> int:
+        h = C.c_void_p()
+        b = np.ascontiguousarray(rows_q8, dtype=np.uint8)
+        self._check(lib.ge_op_q8_create(self.handle, b.ctypes.data_as(C.c_void_p), rows, cols, C.byref(h)),
+                    "ge_op_q8_create")
+        return h.value
+
+    def q8_destroy(self, h: int):
+        self._check(lib.ge_op_q8_destroy(self.handle, C.c_void_p(h)), "ge_op_q8_destroy")
+
+    def gemm_q8(self, w: int, x: int, m: int, y: int, y_f16: bool = False):
+        self._check(lib.ge_op_gemm_q8(self.handle, C.c_void_p(w), C.c_void_p(x), m, C.c_void_p(y), int(y_f16)),
+                    "ge_op_gemm_q8")
+
+    def gemm_q8_geglu(self, gate: int, up: int, x: int, m: int, act: int):
+        self._check(lib.ge_op_gemm_q8_geglu(self.handle, C.c_void_p(gate), C.c_void_p(up), C.c_void_p(x), m,
+                                            C.c_void_p(act)), "ge_op_gemm_q8_geglu")
+
+    def attention(self, q: int, k: int, v: int, out: int, work: int, n_work: int, heads: int, kv_heads: int,
+                  head_dim: int, half_window: int, scale: float = 1.0):
+        self._check(lib.ge_op_attention(self.handle, C.c_void_p(q), C.c_void_p(k), C.c_void_p(v), C.c_void_p(out),
+                                        C.c_void_p(work), n_work, heads, kv_heads, head_dim, half_window, scale),
+                    "ge_op_attention")
+
+
+def attention_work(sequences_ranges, queries: Optional[int] = None) -> np.ndarray:
+    """AttentionWork.items (Metal/MetalForward.swift:47-57) as a (n, 3) uint32 array."""
+    q = queries or lib.ge_attention_queries()
+    items = []
+    for start, length in sequences_ranges:
+        for q0 in range(0, length, q):
+            items.append((start, length, q0))
+    return np.asarray(items, dtype=np.uint32).reshape(-1, 3)
+
+
+# ---------------------------------------------------------------------------- host API mirror
+
+@dataclass
+class EmbedOptions:
+    """EmbedOptions (EmbedOptions.swift:35-56) minus the task prefix (applied before tokenizing)."""
+    max_tokens: int = 2048
+    dimensions: int = 768
+    normalise: bool = True
+    batch_size: Optional[int] = None
+
+    allowed_dimensions = (768, 512, 256, 128)
+
+
+@dataclass
+class Embedding:
+    """Embedding (EmbedOptions.swift:148-161)."""
+    vector: np.ndarray
+    token_count: int
+    truncated: bool
+
+
+@dataclass
+class EmbeddingProgress:
+    completed_texts: int
+    total_texts: int
+    completed_tokens: int
+
+
+class EmbeddingModel:
+    """EmbeddingModel (EmbeddingModel.swift:24-290) over pre-tokenized texts."""
+
+    def __init__(self, handle: int):
+        self._h = C.c_void_p(handle)
+        info = ge_model_info()
+        if lib.ge_model_get_info(self._h, C.byref(info)) != GE_OK:
+            raise GemmaEmbedError(1, "ge_model_get_info")
+        self.info = info
+        self.context = Context(lib.ge_model_context(self._h), owned=False, out_dims=info.out_dims)
+
+    @classmethod
+    def load(cls, path: str, device: int = 0, batch_token_budget: int = 8192, warm_up: bool = True):
+        opt = ge_load_options(device, batch_token_budget, int(warm_up))
+        h = C.c_void_p()
+        err = C.create_string_buffer(1024)
+        rc = lib.ge_model_load(path.encode(), C.byref(opt), C.byref(h), err, 1024)
+        if rc != GE_OK:
+            raise GemmaEmbedError(rc, err.value.decode())
+        return cls(h.value)
+
+    def close(self):
+        if self._h:
+            lib.ge_model_free(self._h)
+            self._h = C.c_void_p()
+
+    def __enter__(self):
+        return self
+
+    def __exit__(self, *a):
+        self.close()
+
+    def _err(self, rc: int):
+        raise GemmaEmbedError(rc, lib.ge_model_last_error(self._h).decode())
+
+    def embed(self, texts: Sequence[Sequence[int]], options: EmbedOptions = EmbedOptions(),
+              progress: Optional[Callable[[EmbeddingProgress], Optional[bool]]] = None) -> List[Embedding]:
+        """embed(_:options:progress:) (EmbeddingModel.swift:145-175) over token id lists. A
+        progress callback returning True cancels before the next batch."""
+        lengths = _i32([len(t) for t in texts])
+        flat = _i32([int(x) for t in texts for x in t])
+        n = len(texts)
+        out = np.zeros((max(n, 1), options.dimensions), dtype=np.float32)
+        counts = np.zeros(max(n, 1), dtype=np.int32)
+        cut = np.zeros(max(n, 1), dtype=np.uint8)
+        opt = ge_embed_options(options.max_tokens, options.dimensions, int(options.normalise),
+                               int(options.batch_size or 0))
+
+        def cb(_user, done, total, tokens):
+            if progress is None:
+                return 0
+            return 1 if progress(EmbeddingProgress(done, total, tokens)) else 0
+
+        fn = PROGRESS_FN(cb)
+        rc = lib.ge_model_embed(self._h, _ptr(flat, C.c_int32), _ptr(lengths, C.c_int32), n, C.byref(opt),
+                                _ptr(out, C.c_float), _ptr(counts, C.c_int32), _ptr(cut, C.c_uint8), fn, None)
+        if rc != GE_OK:
+            self._err(rc)
+        return [Embedding(out[i].copy(), int(counts[i]), bool(cut[i])) for i in range(n)]
+
+    def embed_tokens(self, sequences: Sequence[Sequence[int]]) -> np.ndarray:
+        """embedTokens (EmbeddingModel.swift:285-289): unnormalised pooled vectors, one batch."""
+        lengths = _i32([len(t) for t in sequences])
+        flat = _i32([int(x) for t in sequences for x in t])
+        out = np.zeros((len(sequences), self.info.out_dims), dtype=np.float32)
+        rc = lib.ge_model_embed_tokens(self._h, _ptr(flat, C.c_int32), _ptr(lengths, C.c_int32), len(sequences),
+                                       _ptr(out, C.c_float))
+        if rc != GE_OK:
+            self._err(rc)
+        return out
+
+    @staticmethod
+    def similarity(a: Embedding, b: Embedding) -> float:
+        """Dot product over the shorter length (EmbeddingModel.swift:178-182)."""
+        n = min(a.vector.size, b.vector.size)
+        return float(np.dot(a.vector[:n].astype(np.float32), b.vector[:n].astype(np.float32)))

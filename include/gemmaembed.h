@@ -1,0 +1,264 @@
+/*
+ * gemmaembed.h - C-ABI of the MI355X-native GemmaEmbed text-encoder forward pass.
+ *
+ * Two layers, both plain C (no HIP or torch types in any signature):
+ *
+ *  1. The device library (ge_ctx): the replacement for the reference's Metal runtime
+ *     (Sources/GemmaEmbed/Metal/MetalContext.swift, MetalForward.swift). The Swift host's
+ *     EmbeddingModel would bind these through a SwiftPM C target.
+ *  2. The host mirror (ge_model): EmbeddingModel.load / embed / batches / finish
+ *     (Sources/GemmaEmbed/EmbeddingModel.swift) and the GGUF loader (GGUF/GGUFFile.swift),
+ *     written in C++ because no Swift toolchain is available.
+ *
+ * Conventions (replacing Swift `throws GemmaEmbedError`, Errors.swift:6-24):
+ *  - every call returns an int status, GE_OK (0) on success;
+ *  - ge_last_error(ctx) / ge_model_last_error(model) give the message of the last failure;
+ *  - invalid shapes and arguments return GE_ERR_INVALID instead of trapping.
+ * Threading (EmbeddingModel.swift:37,274-281 serialises every call on one queue): one context
+ * is externally synchronised; use one context per GPU.
+ */
+#ifndef GEMMAEMBED_H
+#define GEMMAEMBED_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* Status codes. Each maps onto one GemmaEmbedError case (Errors.swift:6-24). */
+enum {
+    GE_OK = 0,
+    GE_ERR_INVALID = 1,    /* bad argument or shape (reference: precondition trap) */
+    GE_ERR_GGUF = 2,       /* GemmaEmbedError.invalidGGUF / fileNotReadable */
+    GE_ERR_MODEL = 3,      /* missingTensor / missingMetadata / tensorShapeMismatch / unsupportedTensorType / unsupportedArchitecture */
+    GE_ERR_GPU = 4,        /* GemmaEmbedError.gpuFailure (a HIP call failed) */
+    GE_ERR_OPTIONS = 5,    /* GemmaEmbedError.invalidOptions */
+    GE_ERR_STATE = 6,      /* no model uploaded / no batch staged */
+    GE_ERR_CANCELLED = 7,  /* GemmaEmbedError.cancelled */
+    GE_ERR_NO_DEVICE = 8   /* GemmaEmbedError.noMetalDevice */
+};
+
+/* ggml tensor types the loader accepts (GGUF/GGUFValue.swift:84-89). */
+enum { GE_TYPE_F32 = 0, GE_TYPE_F16 = 1, GE_TYPE_Q8_0 = 8, GE_TYPE_BF16 = 30 };
+
+/* ===================================================================== device library */
+
+typedef struct ge_ctx ge_ctx;
+
+/* MetalContext(device:) (Metal/MetalContext.swift:23-44): selects HIP device `device`, creates the
+ * stream and events. On failure *out is NULL and ge_create_error() holds the message. */
+int ge_create(int device, ge_ctx** out);
+void ge_destroy(ge_ctx* ctx);
+const char* ge_last_error(const ge_ctx* ctx);
+const char* ge_create_error(void);
+/* Device name (ModelInfo.deviceName, Model/ModelConfig.swift:26). */
+const char* ge_device_name(const ge_ctx* ctx);
+
+/* One tensor of the weight file: name, byte offset from `file_base`, ggml type and GGUF `ne`
+ * shape (fastest dimension first), as GGUFTensorInfo (GGUF/GGUFValue.swift:117-131). */
+typedef struct ge_tensor_desc {
+    const char* name;
+    uint64_t offset;
+    int32_t type;
+    int32_t ndim;
+    int64_t shape[4];
+} ge_tensor_desc;
+
+/* Shapes and constants of the text encoder (ModelConfig.swift:54-112, LayerConfig :34-40).
+ * per_layer_input = 0 means the model has no per-layer-input branch. */
+typedef struct ge_model_desc {
+    int32_t layers, hidden, heads, feed_forward, out_dims, per_layer_input, vocab, sliding_window, max_tokens;
+    float eps, embedding_scale, per_layer_scale;
+    const int32_t* kv_heads;  /* [layers] */
+    const int32_t* head_dim;  /* [layers] */
+    const uint8_t* sliding;   /* [layers], 1 = sliding-window layer */
+    const float* rope_base;   /* [layers] */
+    const float* out_scale;   /* [layers], layer_output_scale (1 when absent) */
+    const ge_tensor_desc* tensors;
+    int32_t n_tensors;
+} ge_model_desc;
+
+/* Replaces MetalForward.init's no-copy MTLBuffer over the mmap (Metal/MetalForward.swift:85-112):
+ * the weights are copied into HBM and Q8_0 matrices are repacked into separate int8 quant and
+ * fp16 scale planes. The caller may unmap the file afterwards. */
+int ge_upload_model(ge_ctx* ctx, const ge_model_desc* desc, const void* file_base, size_t len);
+
+/* SequenceRange (Shaders/Common.metal:86-89): one packed sequence. */
+typedef struct ge_seq {
+    uint32_t start;
+    uint32_t length;
+} ge_seq;
+
+/* MetalForward.run / timeForward (Metal/MetalForward.swift:199-209): one packed batch, tokens
+ * back to back, positions restarting at 0 per sequence (PackedBatch.append :17-21). Writes the
+ * unnormalised mean-pooled vectors, n_seqs x out_dims fp32, into caller-owned `pooled_out`.
+ * `gpu_seconds` (nullable) receives the GPU time of the forward. Synchronous. Token ids must be
+ * in [0, vocab); the reference's negative ids (vector rows, :6-7) are multimodal and rejected. */
+int ge_forward(ge_ctx* ctx, const int32_t* tokens, const int32_t* positions, int32_t n_tokens, const ge_seq* seqs,
+               int32_t n_seqs, float* pooled_out, double* gpu_seconds);
+
+/* Per-layer parity (CPUReference.forward's trace, Model/CPUReference.swift:204-276, and
+ * MetalForward.attentionInputs :278-284): runs the forward up to the op that produces the named
+ * tensor at `layer` (-1 for inp_scaled, result_norm, result_embd) and copies it out as fp32
+ * [n_tokens][width]. Names: inp_scaled, attn_norm, Qcur, Kcur, Vcur, Qcur_pos, Kcur_pos,
+ * Vcur_normed, kqv_out, attn_out, ffn_norm, ffn_geglu, ffn_out, pe_in, l_out, result_norm,
+ * result_embd, and with the per-layer-input branch inp_per_layer and per_layer_embd_out.
+ * `out_count` is the capacity of `out` in floats; the needed count is written to *needed. */
+int ge_forward_trace(ge_ctx* ctx, const int32_t* tokens, const int32_t* positions, int32_t n_tokens,
+                     const ge_seq* seqs, int32_t n_seqs, const char* tensor_name, int32_t layer, float* out,
+                     size_t out_count, size_t* needed);
+
+/* Device-resident batches, for callers that keep inputs in HBM across calls (and the bench):
+ * stage uploads tokens/positions/sequences and the attention work list once; run enqueues a
+ * forward over the staged batch on the context's stream and returns without waiting; read
+ * waits and copies the pooled vectors out. */
+int ge_batch_stage(ge_ctx* ctx, const int32_t* tokens, const int32_t* positions, int32_t n_tokens, const ge_seq* seqs,
+                   int32_t n_seqs);
+int ge_batch_run(ge_ctx* ctx);
+int ge_batch_read(ge_ctx* ctx, float* pooled_out);
+int ge_sync(ge_ctx* ctx);
+
+/* Kernel timing with HIP events on the context's stream (the reference's Profiler,
+ * Metal/Profiler.swift:16-88). While enabled, every launch whose kernel name starts with
+ * `prefix` ("" = all) is bracketed by events; stats accumulate per kernel name. */
+int ge_profile_enable(ge_ctx* ctx, const char* prefix);
+int ge_profile_disable(ge_ctx* ctx);
+int ge_profile_reset(ge_ctx* ctx);
+/* i-th kernel class: name, launch count and summed milliseconds. Returns GE_ERR_INVALID past the end. */
+int ge_profile_get(ge_ctx* ctx, int32_t i, const char** name, int64_t* launches, double* total_ms);
+
+/* ---- per-op entry points on device memory, for unit tests (the reference's `Kernels`,
+ * Metal/MetalForward.swift:427-759). Device buffers come from ge_dev_alloc. */
+void* ge_dev_alloc(ge_ctx* ctx, size_t bytes);
+int ge_dev_free(ge_ctx* ctx, void* ptr);
+int ge_dev_upload(ge_ctx* ctx, void* dst, const void* src, size_t bytes);
+int ge_dev_download(ge_ctx* ctx, void* dst, const void* src, size_t bytes);
+
+/* fp32 -> fp16 (round to nearest even) and back, elementwise on device. */
+int ge_op_f32_to_f16(ge_ctx* ctx, const void* src, void* dst, size_t count);
+int ge_op_f16_to_f32(ge_ctx* ctx, const void* src, void* dst, size_t count);
+
+/* A Q8_0 weight matrix (`rows` GGUF rows of `cols` elements, 34-byte blocks, host memory)
+ * repacked into device memory. Replaces WeightTensor as GEMM operand (Model/Weights.swift:6-17). */
+typedef struct ge_q8_matrix ge_q8_matrix;
+int ge_op_q8_create(ge_ctx* ctx, const void* q8_rows, int32_t rows, int32_t cols, ge_q8_matrix** out);
+int ge_op_q8_destroy(ge_ctx* ctx, ge_q8_matrix* m);
+
+/* Kernels.gemm (Metal/MetalForward.swift:524-557): y[M][N] = x[M][K] * W^T with x fp16 [M][K]
+ * and W [N][K] Q8_0; y fp32 (y_f16 = 0) or fp16 (y_f16 = 1), row stride N. */
+int ge_op_gemm_q8(ge_ctx* ctx, const ge_q8_matrix* w, const void* x, int32_t m, void* y, int32_t y_f16);
+/* Kernels.gemm with the geglu epilogue (:566-569, Shaders/GEMM.metal:41-67):
+ * act[M][F] = gelu_tanh(x * Wg^T) * (x * Wu^T), fp16 out. */
+int ge_op_gemm_q8_geglu(ge_ctx* ctx, const ge_q8_matrix* gate, const ge_q8_matrix* up, const void* x, int32_t m,
+                        void* act);
+
+/* AttentionWork (Shaders/Common.metal:75-79): a block of query rows of one sequence. */
+typedef struct ge_attention_work {
+    uint32_t seq_start;
+    uint32_t seq_len;
+    uint32_t q0;
+} ge_attention_work;
+
+/* Rows of queries one attention work item covers (the reference's queriesPerGroup). */
+int32_t ge_attention_queries(void);
+
+/* Kernels.attention (Metal/MetalForward.swift:669-694; Shaders/Attention.metal:25-170): q fp16
+ * [T][heads][hd], k and v fp16 [T][kv_heads][hd], out fp16 [T][heads][hd]; `work` is a device
+ * array of n_work items; half_window 0 = no window; scale multiplies the scores. Buffers must
+ * hold ge_attention_queries() rows of slack past the last token. */
+int ge_op_attention(ge_ctx* ctx, const void* q, const void* k, const void* v, void* out, const void* work,
+                    int32_t n_work, int32_t heads, int32_t kv_heads, int32_t head_dim, int32_t half_window,
+                    float scale);
+
+/* ===================================================================== host mirror */
+
+typedef struct ge_model ge_model;
+
+/* LoadOptions (EmbedOptions.swift:172-203) for the text path. */
+typedef struct ge_load_options {
+    int32_t device;              /* HIP device ordinal */
+    int32_t batch_token_budget;  /* default 8192; at least 64 (EmbeddingModel.swift:110) */
+    int32_t warm_up;             /* run one small forward at load (EmbeddingModel.swift:111-114) */
+} ge_load_options;
+
+/* EmbedOptions (EmbedOptions.swift:35-56), minus the task prefix: prefixes and tokenization
+ * happen before the token ids reach this API. */
+typedef struct ge_embed_options {
+    int32_t max_tokens;  /* 2 ... max_tokens of the model; default 2048 */
+    int32_t dimensions;  /* 768, 512, 256 or 128 */
+    int32_t normalise;   /* L2-normalise the output */
+    int32_t batch_size;  /* texts per batch; 0 = pack by token count */
+} ge_embed_options;
+
+/* ModelInfo (Model/ModelConfig.swift:6-32). */
+typedef struct ge_model_info {
+    char architecture[64];
+    char name[128];
+    int32_t layers, hidden, out_dims, feed_forward, per_layer_input, heads, vocab, sliding_window, max_tokens;
+    float eps;
+    char quantization[16];
+    char device_name[128];
+    int64_t file_size;
+    int32_t bos_id, eos_id;
+} ge_model_info;
+
+/* EmbeddingProgress (EmbedOptions.swift:165-169); returning non-zero cancels between batches. */
+typedef int (*ge_progress_fn)(void* user, int32_t completed_texts, int32_t total_texts, int64_t completed_tokens);
+
+/* EmbeddingModel.load(from:options:) (EmbeddingModel.swift:40-122): GGUF parse and validation,
+ * context creation, weight upload, warm forward. err receives the message on failure. */
+int ge_model_load(const char* path, const ge_load_options* options, ge_model** out, char* err, size_t errlen);
+void ge_model_free(ge_model* model);
+const char* ge_model_last_error(const ge_model* model);
+int ge_model_get_info(const ge_model* model, ge_model_info* info);
+/* The model's device context, for ge_forward_trace / ge_profile_* on a loaded model. */
+ge_ctx* ge_model_context(ge_model* model);
+
+/* EmbeddingModel.embed(_:options:progress:) (EmbeddingModel.swift:145-175) over pre-tokenized
+ * texts: `tokens` holds n_texts sequences back to back, `lengths[i]` ids each (BOS/EOS included,
+ * as the tokenizer returns them). Truncates to max_tokens keeping EOS (:189-196), batches
+ * (:200-215), runs, then Matryoshka-truncates and normalises (:260-267). `out` receives
+ * n_texts x dimensions floats; token_counts and truncated (both nullable) one entry per text. */
+int ge_model_embed(ge_model* model, const int32_t* tokens, const int32_t* lengths, int32_t n_texts,
+                   const ge_embed_options* options, float* out, int32_t* token_counts, uint8_t* truncated,
+                   ge_progress_fn progress, void* user);
+
+/* EmbeddingModel.embedTokens (EmbeddingModel.swift:285-289): one packed batch of all the
+ * sequences, unnormalised pooled out_dims vectors. */
+int ge_model_embed_tokens(ge_model* model, const int32_t* tokens, const int32_t* lengths, int32_t n_texts,
+                          float* out);
+
+/* EmbeddingModel.batches (EmbeddingModel.swift:200-215): consecutive ranges of at least one
+ * item, cut by count when batch_size > 0, else before the item that would take any summed cost
+ * past its budget. costs is n_items x n_budgets. Writes range starts (n_ranges + 1 entries, the
+ * last = n_items) into `starts` (capacity n_items + 1) and the range count into *n_ranges. */
+int ge_plan_batches(const int32_t* costs, int32_t n_items, const int32_t* budgets, int32_t n_budgets,
+                    int32_t batch_size, int32_t* starts, int32_t* n_ranges);
+
+/* EmbeddingModel.finish (EmbeddingModel.swift:260-267): prefix to `dimensions`, then L2
+ * normalise unless the norm is 0. */
+int ge_finish(const float* vector, int32_t width, int32_t dimensions, int32_t normalise, float* out);
+
+/* Synthetic GGUF writer for seeded test and bench models (no reference counterpart: the
+ * reference's models are downloaded). Rules: q ~ U{-127..127} per Q8_0 block with fp16 scale
+ * |N(0, 0.02)| * max|q| / 127; fp32 norm weights 1 + 0.1 N(0,1); SplitMix64 streams seeded per
+ * tensor from (seed, tensor name). per_layer_input = 0 writes no per-layer-input tensors. */
+typedef struct ge_synth_spec {
+    int32_t layers, hidden, heads, feed_forward, out_dims, per_layer_input, vocab, sliding_window;
+    int32_t head_dim_swa, head_dim_global, kv_heads_swa, kv_heads_global;
+    float eps, rope_base, rope_base_swa;
+    const uint8_t* pattern; /* [layers], 1 = sliding */
+    uint64_t seed;
+} ge_synth_spec;
+int ge_synth_write_gguf(const char* path, const ge_synth_spec* spec, char* err, size_t errlen);
+
+/* SplitMix64 helpers shared by tests and the bench (the reference tests' SeededRandom,
+ * Tests/GemmaEmbedTests/KernelTests.swift:9-26): `count` ids uniform in [lo, hi). */
+int ge_synth_tokens(uint64_t seed, int32_t lo, int32_t hi, int32_t count, int32_t* out);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

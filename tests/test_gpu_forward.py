@@ -1,0 +1,189 @@
+"""Whole-forward parity on the GPU against the CPU oracle, through the C-ABI.
+
+Bars: per-layer max relative error max|d| / max|ref| <= 1e-2 on
+every layer's output, final pooled-embedding cosine >= 0.99999. Also the reference's bitwise
+invariants (packing independence, determinism; MetalForwardTests.swift:54-120) and the
+embed API's options, truncation, batching and progress (EmbeddingModelTests.swift)."""
+import numpy as np
+import pytest
+
+import ge_oracle as ora
+import gemma_embed as ge
+
+pytestmark = pytest.mark.gpu
+
+PER_LAYER_TOL = 1e-2
+COSINE_BAR = 0.99999
+
+
+def cosine(a, b):
+    a, b = np.asarray(a, np.float64), np.asarray(b, np.float64)
+    return float(a @ b / (np.linalg.norm(a) * np.linalg.norm(b)))
+
+
+def max_rel(got, want):
+    got, want = np.asarray(got, np.float64), np.asarray(want, np.float64)
+    assert np.all(np.isfinite(got)), "non-finite output"
+    return float(np.abs(got - want).max() / max(np.abs(want).max(), 1e-30))
+
+
+@pytest.fixture(scope="module")
+def tiny_model(tiny_gguf):
+    m = ge.EmbeddingModel.load(tiny_gguf)
+    print("device:", m.info.device_name.decode(), flush=True)
+    yield m
+    m.close()
+
+
+@pytest.fixture(scope="module")
+def c2_model(config2_gguf):
+    m = ge.EmbeddingModel.load(config2_gguf, batch_token_budget=8192)
+    yield m
+    m.close()
+
+
+@pytest.fixture(scope="module")
+def c2_oracle(config2_gguf):
+    m = ora.OracleModel(config2_gguf)
+    yield m
+    m.close()
+
+
+def test_tiny_forward_vs_oracle(tiny_model, tiny_gguf):
+    seqs = [ge.synth_tokens(s, 2, 512, n).tolist() for s, n in ((1, 40), (2, 7), (3, 1), (4, 64), (5, 33))]
+    pooled = tiny_model.embed_tokens(seqs)
+    with ora.OracleModel(tiny_gguf) as o:
+        for i, s in enumerate(seqs):
+            want, tr = o.forward(s, keep=[("l_out", 0), ("l_out", 1)])
+            assert cosine(pooled[i], want) >= COSINE_BAR, i
+    for layer in range(2):
+        got = tiny_model.context.trace(seqs, "l_out", layer)
+        off = 0
+        with ora.OracleModel(tiny_gguf) as o:
+            for s in seqs:
+                _, tr = o.forward(s, keep=[("l_out", layer)])
+                assert max_rel(got[off:off + len(s)], tr[("l_out", layer)].reshape(len(s), -1)) <= PER_LAYER_TOL
+                off += len(s)
+
+
+@pytest.fixture(scope="module")
+def config2_batch():
+    # 32 texts x 512 tokens, ids uniform in [2, 262144)
+    toks = ge.synth_tokens(3, 2, 262144, 32 * 512).reshape(32, 512)
+    return [t.tolist() for t in toks]
+
+
+def test_config2_pooled_vs_oracle(c2_model, c2_oracle, config2_batch):
+    print("config2 forward 32 x 512 (one pack of 16384)", flush=True)
+    pooled, secs = c2_model.context.forward(config2_batch)
+    print(f"gpu forward {secs * 1e3:.2f} ms", flush=True)
+    assert pooled.shape == (32, 768)
+    for i in (0, 13, 31):
+        want, _ = c2_oracle.forward(config2_batch[i])
+        c = cosine(pooled[i], want)
+        print(f"seq {i} cosine {c:.9f} max_rel {max_rel(pooled[i], want):.3e}", flush=True)
+        assert c >= COSINE_BAR
+
+
+def test_config2_per_layer_vs_oracle(c2_model, c2_oracle, config2_batch):
+    names = [("l_out", l) for l in range(24)] + [("Qcur_pos", 0), ("Kcur_pos", 5), ("Vcur_normed", 5),
+                                                  ("kqv_out", 0), ("kqv_out", 5), ("ffn_geglu", 3),
+                                                  ("attn_out", 11), ("result_embd", -1)]
+    batch = config2_batch[:4]
+    idx = 2  # check the third sequence of the pack: its rows start at 1024
+    _, tr = c2_oracle.forward(batch[idx], keep=names)
+    worst = 0.0
+    for name, layer in names:
+        got = c2_model.context.trace(batch, name, layer)
+        rows = got[idx * 512:(idx + 1) * 512]
+        want = tr[(name, layer)].reshape(512, -1)
+        if name == "ffn_geglu":  # stored scaled by a power of two; compare the shape-invariant ratio
+            rows = rows * (np.abs(want).max() / max(np.abs(rows).max(), 1e-30))
+        r = max_rel(rows, want)
+        worst = max(worst, r) if name == "l_out" else worst
+        print(f"{name}-{layer}: max_rel {r:.3e}", flush=True)
+        assert r <= PER_LAYER_TOL, (name, layer)
+    print(f"worst l_out max_rel {worst:.3e}", flush=True)
+
+
+def test_packing_invariance_and_determinism(c2_model, config2_batch):
+    batch = config2_batch[:8]
+    a = c2_model.embed_tokens(batch)
+    b = c2_model.embed_tokens(batch)
+    assert np.array_equal(a, b)  # run to run
+    alone = c2_model.embed_tokens([batch[5]])
+    assert np.array_equal(alone[0], a[5])  # a text alone vs inside a batch (MetalForwardTests.swift:54-73)
+    mixed = c2_model.embed_tokens([batch[5][:100], batch[1], batch[5]])
+    assert np.array_equal(mixed[2], a[5])
+    assert np.array_equal(mixed[1], a[1])
+
+
+def test_embed_api_options(c2_model, config2_batch):
+    texts = [t[: 20 + 37 * i] for i, t in enumerate(config2_batch[:10])]
+    full = c2_model.embed(texts, ge.EmbedOptions(normalise=False))
+    raw = c2_model.embed_tokens(texts)
+    for i in range(10):
+        assert np.allclose(full[i].vector, raw[i], atol=1e-5 * np.abs(raw[i]).max())
+        assert full[i].token_count == len(texts[i]) and not full[i].truncated
+    for dims in (768, 512, 256, 128):
+        e = c2_model.embed(texts[:3], ge.EmbedOptions(dimensions=dims))
+        for i in range(3):
+            v = raw[i][:dims] / np.linalg.norm(raw[i][:dims])
+            assert e[i].vector.shape == (dims,)
+            assert abs(np.linalg.norm(e[i].vector) - 1) < 1e-5
+            assert np.allclose(e[i].vector, v, atol=1e-5)
+    with pytest.raises(ge.GemmaEmbedError) as err:
+        c2_model.embed(texts[:1], ge.EmbedOptions(dimensions=100))
+    assert err.value.kind == "invalidOptions"
+
+
+def test_embed_truncation_keeps_eos(c2_model, config2_batch):
+    text = config2_batch[0]
+    e = c2_model.embed([text], ge.EmbedOptions(max_tokens=16))[0]
+    assert e.truncated and e.token_count == 16
+    direct = c2_model.embed_tokens([text[:15] + [c2_model.info.eos_id]])[0]
+    assert np.allclose(e.vector, direct / np.linalg.norm(direct), atol=1e-5)
+    assert not c2_model.embed([text[:10]], ge.EmbedOptions(max_tokens=16))[0].truncated
+
+
+def test_embed_batching_progress_and_cancel(c2_model, config2_batch):
+    texts = [t[: 50 + 300 * (i % 3)] for i, t in enumerate(config2_batch[:20])]
+    events = []
+    auto = c2_model.embed(texts, progress=lambda p: events.append(p))
+    one = c2_model.embed(texts, ge.EmbedOptions(batch_size=1))
+    three = c2_model.embed(texts, ge.EmbedOptions(batch_size=3))
+    for i in range(20):
+        assert np.abs(auto[i].vector - one[i].vector).max() < 1e-5
+        assert np.abs(auto[i].vector - three[i].vector).max() < 1e-5
+    assert events and events[-1].completed_texts == 20 and events[-1].total_texts == 20
+    assert events[-1].completed_tokens == sum(len(t) for t in texts)
+    with pytest.raises(ge.GemmaEmbedError) as err:
+        c2_model.embed(texts, ge.EmbedOptions(batch_size=1), progress=lambda p: True)
+    assert err.value.kind == "cancelled"
+
+
+def test_config3_ragged_vs_oracle(c2_model, c2_oracle):
+    """256 texts, lengths U[8, 256], packed by token count, Matryoshka 256."""
+    lengths = ge.synth_tokens(5, 8, 257, 256)
+    ids = ge.synth_tokens(6, 2, 262144, int(lengths.sum()))
+    texts, off = [], 0
+    for n in lengths:
+        texts.append(ids[off:off + n].tolist())
+        off += n
+    out = c2_model.embed(texts, ge.EmbedOptions(dimensions=256))
+    assert len(out) == 256 and all(o.vector.shape == (256,) for o in out)
+    for i in (0, 77, 255):
+        want, _ = c2_oracle.forward(texts[i])
+        w = want[:256] / np.linalg.norm(want[:256])
+        assert cosine(out[i].vector, w) >= COSINE_BAR, i
+
+
+def test_rejects_bad_batches(c2_model):
+    ctx = c2_model.context
+    with pytest.raises(ge.GemmaEmbedError) as e:
+        ctx.forward([[5, 262144]])
+    assert e.value.kind == "invalid"
+    with pytest.raises(ge.GemmaEmbedError):
+        ctx.forward([[]])
+    with pytest.raises(ge.GemmaEmbedError):
+        ctx.forward([list(range(2, 8200))])  # longer than the 8192-token context

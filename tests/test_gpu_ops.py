@@ -1,0 +1,163 @@
+"""Per-kernel parity on the GPU through the C-ABI, against the CPU oracle on the same inputs
+(the reference's KernelTests.swift style: max |got - want| / max |want|, TestSupport.swift:100-110).
+
+Inputs the GPU takes in fp16 are rounded to fp16 first and the oracle gets the same rounded
+values, so the remaining difference is the kernel's own arithmetic: fp16 rounding of each
+dequantised weight (relative 2^-12) and fp32 accumulation order."""
+import numpy as np
+import pytest
+
+import ge_oracle as ora
+import gemma_embed as ge
+import npref
+
+pytestmark = pytest.mark.gpu
+
+RNG = np.random.default_rng(77)
+
+
+def max_rel(got, want):
+    got, want = np.asarray(got, np.float64), np.asarray(want, np.float64)
+    assert np.all(np.isfinite(got)), "non-finite output"
+    return float(np.abs(got - want).max() / max(np.abs(want).max(), 1e-30))
+
+
+@pytest.fixture(scope="module")
+def ctx():
+    c = ge.Context.create(0)
+    print("device:", c.device_name, flush=True)
+    yield c
+    c.close()
+
+
+@pytest.fixture(scope="module")
+def c2(config2_gguf):
+    return npref.Gguf(config2_gguf)
+
+
+def f16_round(a):
+    return np.asarray(a, np.float32).astype(np.float16)
+
+
+def run_gemm(ctx, raw_q8, rows, cols, x16, y_f16=False):
+    M = x16.shape[0]
+    w = ctx.q8_create(raw_q8, rows, cols)
+    dx = ctx.alloc(x16.nbytes)
+    dy = ctx.alloc(M * rows * (2 if y_f16 else 4))
+    try:
+        ctx.upload(dx, x16)
+        ctx.gemm_q8(w, dx, M, dy, y_f16)
+        y = ctx.download(dy, (M, rows), np.float16 if y_f16 else np.float32)
+    finally:
+        ctx.free(dx)
+        ctx.free(dy)
+        ctx.q8_destroy(w)
+    return y.astype(np.float32)
+
+
+GEMM_SHAPES = [  # (tensor, M): every config-2 projection plus ragged row counts
+    ("blk.0.attn_q.weight", 200), ("blk.0.attn_k.weight", 129), ("blk.0.attn_v.weight", 1),
+    ("blk.0.attn_output.weight", 300), ("blk.0.ffn_gate.weight", 128), ("blk.0.ffn_up.weight", 513),
+    ("blk.0.ffn_down.weight", 257), ("output.weight", 64),
+]
+
+
+@pytest.mark.parametrize("name,M", GEMM_SHAPES)
+def test_gemm_q8_vs_oracle(ctx, c2, name, M):
+    shape, _, _ = c2.tensors[name]
+    cols, rows = shape
+    print(f"gemm {name} M={M} N={rows} K={cols}", flush=True)
+    x16 = f16_round(RNG.standard_normal((M, cols)))
+    y = run_gemm(ctx, np.asarray(c2.raw(name)), rows, cols, x16)
+    want = ora.matmul(x16.astype(np.float32), c2.tensor(name).astype(np.float32))
+    assert max_rel(y, want) < 2e-3
+
+
+def test_gemm_config1(ctx, c2):
+    """X fp32 [128 x 768] ~ N(0, 1), W Q8_0 [1152 x 768] (blk.0.ffn_gate of the
+    config-2 model, drawn by the same Q8_0 rule), Y fp32 [128 x 1152]."""
+    x = np.random.default_rng(1).standard_normal((128, 768)).astype(np.float32)
+    name = "blk.0.ffn_gate.weight"
+    y = run_gemm(ctx, np.asarray(c2.raw(name)), 1152, 768, f16_round(x))
+    want = ora.matmul(x, c2.tensor(name).astype(np.float32))
+    # the input's own fp16 rounding (2^-12 relative) is inside this bound
+    assert max_rel(y, want) < 3e-3
+
+
+def test_gemm_f16_output_and_row_independence(ctx, c2):
+    name = "blk.3.attn_output.weight"
+    x16 = f16_round(RNG.standard_normal((300, 768)))
+    raw = np.asarray(c2.raw(name))
+    y = run_gemm(ctx, raw, 768, 768, x16, y_f16=True)
+    want = ora.matmul(x16.astype(np.float32), c2.tensor(name).astype(np.float32))
+    assert max_rel(y, want) < 3e-3
+    # a row's result does not depend on the other rows or on M (no split-K, fixed K order)
+    y32 = run_gemm(ctx, raw, 768, 768, x16)
+    y_part = run_gemm(ctx, raw, 768, 768, x16[131:140].copy())
+    assert np.array_equal(y32[131:140], y_part)
+
+
+def test_gemm_geglu_vs_oracle(ctx, c2):
+    M = 333
+    x16 = f16_round(RNG.standard_normal((M, 768)) * 0.05)
+    g = ctx.q8_create(np.asarray(c2.raw("blk.2.ffn_gate.weight")), 1152, 768)
+    u = ctx.q8_create(np.asarray(c2.raw("blk.2.ffn_up.weight")), 1152, 768)
+    dx, da = ctx.alloc(x16.nbytes), ctx.alloc(M * 1152 * 2)
+    try:
+        ctx.upload(dx, x16)
+        ctx.gemm_q8_geglu(g, u, dx, M, da)
+        act = ctx.download(da, (M, 1152), np.float16).astype(np.float32)
+    finally:
+        ctx.free(dx)
+        ctx.free(da)
+        ctx.q8_destroy(g)
+        ctx.q8_destroy(u)
+    xf = x16.astype(np.float32)
+    gate = ora.matmul(xf, c2.tensor("blk.2.ffn_gate.weight").astype(np.float32))
+    up = ora.matmul(xf, c2.tensor("blk.2.ffn_up.weight").astype(np.float32))
+    want = np.vectorize(ora.gelu_tanh)(gate) * up
+    assert max_rel(act, want) < 3e-3
+
+
+ATTN_CASES = [  # (lengths, H, KV, hd, half_window): the reference's packed-length mixes (KernelTests.swift:552-559)
+    ([1, 7, 64], 3, 1, 256, 0),
+    ([100, 33, 5], 3, 1, 256, 16),
+    ([1024, 5], 3, 1, 256, 256),
+    ([600], 3, 1, 256, 0),
+    ([70, 1, 129], 4, 2, 256, 64),
+    ([300, 31], 4, 1, 512, 0),
+    ([96, 40], 2, 1, 128, 8),
+    ([257], 4, 4, 128, 0),
+]
+
+
+@pytest.mark.parametrize("lengths,H,KV,hd,hw", ATTN_CASES)
+def test_attention_vs_oracle(ctx, lengths, H, KV, hd, hw):
+    print(f"attention lengths={lengths} H={H} KV={KV} hd={hd} hw={hw}", flush=True)
+    T = sum(lengths)
+    slack = 64
+    q = f16_round(RNG.standard_normal((T, H, hd)) * 1.5)
+    k = f16_round(RNG.standard_normal((T, KV, hd)))
+    v = f16_round(RNG.standard_normal((T, KV, hd)))
+    ranges, s = [], 0
+    for n in lengths:
+        ranges.append((s, n))
+        s += n
+    work = ge.attention_work(ranges)
+    pad = lambda a: np.concatenate([a, np.zeros((slack,) + a.shape[1:], a.dtype)])
+    dq, dk, dv = ctx.alloc(pad(q).nbytes), ctx.alloc(pad(k).nbytes), ctx.alloc(pad(v).nbytes)
+    do, dw = ctx.alloc(pad(q).nbytes), ctx.alloc(work.nbytes)
+    try:
+        ctx.upload(dq, pad(q))
+        ctx.upload(dk, pad(k))
+        ctx.upload(dv, pad(v))
+        ctx.upload(dw, work)
+        ctx.attention(dq, dk, dv, do, dw, len(work), H, KV, hd, hw, 1.0)
+        out = ctx.download(do, (T, H, hd), np.float16).astype(np.float32)
+    finally:
+        for p in (dq, dk, dv, do, dw):
+            ctx.free(p)
+    for st, n in ranges:
+        want = ora.attention(q[st:st + n].astype(np.float32), k[st:st + n].astype(np.float32),
+                             v[st:st + n].astype(np.float32), n, H, KV, hd, 1.0, 2 * hw)
+        assert max_rel(out[st:st + n], want) < 5e-3, (st, n)
