@@ -1,0 +1,321 @@
+// Bidirectional flash attention over packed sequences on gfx950 MFMA.
+//
+// One workgroup of 4 waves per (work item of 32 query rows, KV head). Waves 0..G-1 (G = query
+// heads per KV head) each own one query head; every K/V block staged in LDS serves the whole
+// group. Keys stream in blocks of 64 with an online softmax in fp32 (reference
+// Shaders/Attention.metal:25-170).
+//
+// Pipelining: when G < 4 the remaining waves are producers. While the compute waves work on key
+// block i from one LDS buffer, the producers load block i + 1 from HBM/L2 into the other buffer,
+// issuing eight 16-byte loads before their first LDS store so the load latency is paid once per
+// eight loads instead of once per load. One workgroup barrier per block separates the roles.
+// With G = 4 (or a head dim whose double buffer does not fit LDS) every wave stages the next
+// block after computing the current one.
+//
+// Both products run transposed so a query is an accumulator column, owned by lane l % 32:
+//   S^T[key][query] = K[key][:] . Q[query][:]    (A = K from LDS, B = Q fragments in registers)
+//   O^T[d][query]  += V^T[d][key] . P^T[key][query] (A = V^T from LDS, B = P from the S registers)
+// so the softmax max / sum over keys is a reduction over a lane's own registers plus its
+// partner lane l ^ 32, and the rescale by alpha is per lane. For the second product the 16
+// keys of a k-step are split between the two lane halves in the order the S accumulator
+// already holds them (keys 4h..4h+3 and 8+4h..8+4h+3 for half h); V^T is read in that order.
+// Scores are kept in the log2 domain (s * scale * log2 e) so the exponentials are v_exp_f32.
+#include "common.hpp"
+#include "kernels.hpp"
+
+namespace ge {
+
+namespace attn {
+constexpr int BKV = 64;
+constexpr int LDV = BKV + 8;
+constexpr int WAVES = 4;
+constexpr int BATCH = 8;  // 16-byte loads a producer thread keeps in flight
+constexpr int BATCH_INLINE = 2;  // the same when compute waves stage between blocks
+}  // namespace attn
+
+// Stages key block [kb, kb + 64) of one KV head: K as [64][HD + 8] and V^T as [DS][64 + 8].
+// `t` is this thread's index among the `nt` staging threads. Chunks go in full batches of BATCH
+// loads with no per-load condition, so the batch's loads are all in flight before the first
+// LDS store; a guarded tail takes what the batches leave.
+__device__ __forceinline__ void attn_store_vt(uint32_t* dst, const uint4& a, const uint4& b) {
+    constexpr int ROW = attn::LDV / 2;  // one V^T row in 32-bit words
+    dst[0 * ROW] = (a.x & 0xffffu) | (b.x << 16);
+    dst[1 * ROW] = (a.x >> 16) | (b.x & 0xffff0000u);
+    dst[2 * ROW] = (a.y & 0xffffu) | (b.y << 16);
+    dst[3 * ROW] = (a.y >> 16) | (b.y & 0xffff0000u);
+    dst[4 * ROW] = (a.z & 0xffffu) | (b.z << 16);
+    dst[5 * ROW] = (a.z >> 16) | (b.z & 0xffff0000u);
+    dst[6 * ROW] = (a.w & 0xffffu) | (b.w << 16);
+    dst[7 * ROW] = (a.w >> 16) | (b.w & 0xffff0000u);
+}
+
+template <int HD, int DS, int BATCH, int nt>
+__device__ __forceinline__ void attn_stage(_Float16* __restrict__ Ks, _Float16* __restrict__ Vt,
+                                           const _Float16* __restrict__ kbase, const _Float16* __restrict__ vbase,
+                                           int kb, int kvStride, int t) {
+    using namespace attn;
+    constexpr int LDK = HD + 8;
+    constexpr int KCH = BKV * HD / 8;          // 16-byte K chunks: (key, 8 columns)
+    constexpr int VCH = (BKV / 2) * (DS / 8);  // V chunks: (key pair, 8 columns)
+    constexpr int KFULL = KCH / (nt * BATCH), VB = BATCH / 2, VFULL = VCH / (nt * VB);
+    auto kaddr = [&](int c) { return kbase + (size_t)(kb + c / (HD / 8)) * kvStride + (c % (HD / 8)) * 8; };
+    auto klds = [&](int c) { return reinterpret_cast<uint4*>(&Ks[(c / (HD / 8)) * LDK + (c % (HD / 8)) * 8]); };
+    auto vaddr = [&](int c) { return vbase + (size_t)(kb + 2 * (c % (BKV / 2))) * kvStride + (c / (BKV / 2)) * 8; };
+    auto vlds = [&](int c) { return reinterpret_cast<uint32_t*>(&Vt[(c / (BKV / 2)) * 8 * LDV + 2 * (c % (BKV / 2))]); };
+#pragma unroll 1
+    for (int bi = 0; bi < KFULL; bi++) {
+        uint4 r[BATCH];
+#pragma unroll
+        for (int j = 0; j < BATCH; j++) r[j] = *reinterpret_cast<const uint4*>(kaddr(t + (bi * BATCH + j) * nt));
+#pragma unroll
+        for (int j = 0; j < BATCH; j++) *klds(t + (bi * BATCH + j) * nt) = r[j];
+    }
+    for (int c = t + KFULL * BATCH * nt; c < KCH; c += nt) *klds(c) = *reinterpret_cast<const uint4*>(kaddr(c));
+#pragma unroll 1
+    for (int bi = 0; bi < VFULL; bi++) {
+        uint4 a[VB], b[VB];
+#pragma unroll
+        for (int j = 0; j < VB; j++) {
+            const _Float16* p = vaddr(t + (bi * VB + j) * nt);
+            a[j] = *reinterpret_cast<const uint4*>(p);
+            b[j] = *reinterpret_cast<const uint4*>(p + kvStride);
+        }
+#pragma unroll
+        for (int j = 0; j < VB; j++) attn_store_vt(vlds(t + (bi * VB + j) * nt), a[j], b[j]);
+    }
+    for (int c = t + VFULL * VB * nt; c < VCH; c += nt) {
+        const _Float16* p = vaddr(c);
+        attn_store_vt(vlds(c), *reinterpret_cast<const uint4*>(p), *reinterpret_cast<const uint4*>(p + kvStride));
+    }
+}
+
+template <int HD, int DS, int G>
+__global__ __launch_bounds__(256) void attention_kernel(const uint16_t* __restrict__ Qg, const uint16_t* __restrict__ Kg,
+                                                        const uint16_t* __restrict__ Vg, uint16_t* __restrict__ Og,
+                                                        const AttnWork* __restrict__ work, int H, int KV, int hw,
+                                                        float scale_log2) {
+    using namespace attn;
+    constexpr int LDK = HD + 8;
+    constexpr int BUF = BKV * LDK + DS * LDV;  // halves per K + V^T buffer
+    constexpr bool PIPE = G < WAVES && HD <= 256;
+    constexpr int NP = PIPE ? (WAVES - G) * 64 : WAVES * 64;  // staging threads
+    extern __shared__ __attribute__((aligned(16))) _Float16 lds[];
+    const AttnWork wi = work[blockIdx.x];
+    const int kvh = blockIdx.y, slice = blockIdx.z;
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const bool computes = wave < G;
+    const int h = kvh * G + wave;
+    const int len = int(wi.seq_len), q0 = int(wi.q0);
+    const int qStride = H * HD, kvStride = KV * HD;
+    const int d0 = slice * DS;
+    const int qi = q0 + (lane & 31);
+    const bool qvalid = computes && qi < len;
+
+    int kstart = 0, kend = len;
+    if (hw > 0) {
+        kstart = q0 - hw > 0 ? q0 - hw : 0;
+        const int hi = q0 + kAttnQueries + hw;
+        kend = hi < len ? hi : len;
+    }
+    kstart = kstart / BKV * BKV;
+    const int nblocks = (kend - kstart + BKV - 1) / BKV;
+
+    const _Float16* kbase = reinterpret_cast<const _Float16*>(Kg) + (size_t)wi.seq_start * kvStride + kvh * HD;
+    const _Float16* vbase = reinterpret_cast<const _Float16*>(Vg) + (size_t)wi.seq_start * kvStride + kvh * HD + d0;
+    // Producers: the waves past G when pipelined; everyone otherwise.
+    const int pt = PIPE ? tid - G * 64 : tid;
+
+    half8_t qf[HD / 16];
+    if (computes) {
+        const _Float16* qp = reinterpret_cast<const _Float16*>(Qg) + (size_t)(wi.seq_start + qi) * qStride + h * HD + (lane >> 5) * 8;
+#pragma unroll
+        for (int ks = 0; ks < HD / 16; ks++) {
+            if (qvalid)
+                qf[ks] = *reinterpret_cast<const half8_t*>(qp + ks * 16);
+            else
+#pragma unroll
+                for (int j = 0; j < 8; j++) qf[ks][j] = _Float16(0.0f);
+        }
+    }
+
+    float16_t o[DS / 32];
+#pragma unroll
+    for (int i = 0; i < DS / 32; i++)
+#pragma unroll
+        for (int r = 0; r < 16; r++) o[i][r] = 0.0f;
+    float m_run = -INFINITY, l_run = 0.0f;
+
+    if (PIPE && !computes) {
+        // Producer waves: block 0, then block it + 1 while the compute waves work on block it.
+        // They pass the same number of barriers as the compute waves.
+        if (nblocks > 0) attn_stage<HD, DS, BATCH, NP>(lds, lds + BKV * LDK, kbase, vbase, kstart, kvStride, pt);
+        __syncthreads();
+        for (int it = 0; it < nblocks; it++) {
+            if (it + 1 < nblocks) {
+                _Float16* nK = lds + ((it + 1) & 1) * BUF;
+                attn_stage<HD, DS, BATCH, NP>(nK, nK + BKV * LDK, kbase, vbase, kstart + (it + 1) * BKV, kvStride, pt);
+            }
+            __syncthreads();
+        }
+        return;
+    }
+    if (!PIPE && nblocks > 0) attn_stage<HD, DS, BATCH_INLINE, NP>(lds, lds + BKV * LDK, kbase, vbase, kstart, kvStride, pt);
+    __syncthreads();
+    for (int it = 0; it < nblocks; it++) {
+        const int kb = kstart + it * BKV;
+        _Float16* Ks = lds + (PIPE ? (it & 1) * BUF : 0);
+        _Float16* Vt = Ks + BKV * LDK;
+        if (computes) {
+            float16_t s[2];
+#pragma unroll
+            for (int kt = 0; kt < 2; kt++) {
+#pragma unroll
+                for (int r = 0; r < 16; r++) s[kt][r] = 0.0f;
+                const _Float16* kp = &Ks[(kt * 32 + (lane & 31)) * LDK + (lane >> 5) * 8];
+#pragma unroll
+                for (int ks = 0; ks < HD / 16; ks++) {
+                    const half8_t a = *reinterpret_cast<const half8_t*>(kp + ks * 16);
+                    s[kt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, qf[ks], s[kt], 0, 0, 0);
+                }
+            }
+            float bmax = -INFINITY;
+#pragma unroll
+            for (int kt = 0; kt < 2; kt++)
+#pragma unroll
+                for (int r = 0; r < 16; r++) {
+                    const int key = kb + kt * 32 + (r >> 2) * 8 + (lane >> 5) * 4 + (r & 3);
+                    bool valid = key < len;
+                    if (hw > 0) valid = valid && abs(qi - key) <= hw;
+                    const float val = valid ? s[kt][r] * scale_log2 : -INFINITY;
+                    s[kt][r] = val;
+                    bmax = fmaxf(bmax, val);
+                }
+            bmax = fmaxf(bmax, __shfl_xor(bmax, 32, 64));
+            const float m_new = fmaxf(m_run, bmax);
+            float alpha = 1.0f, sum = 0.0f;
+            if (m_new == -INFINITY) {
+#pragma unroll
+                for (int kt = 0; kt < 2; kt++)
+#pragma unroll
+                    for (int r = 0; r < 16; r++) s[kt][r] = 0.0f;
+            } else {
+                alpha = __builtin_amdgcn_exp2f(m_run - m_new);
+#pragma unroll
+                for (int kt = 0; kt < 2; kt++)
+#pragma unroll
+                    for (int r = 0; r < 16; r++) {
+                        const float p = __builtin_amdgcn_exp2f(s[kt][r] - m_new);
+                        s[kt][r] = p;
+                        sum += p;
+                    }
+            }
+            sum += __shfl_xor(sum, 32, 64);
+            l_run = l_run * alpha + sum;
+            m_run = m_new;
+            if (alpha != 1.0f) {
+#pragma unroll
+                for (int i = 0; i < DS / 32; i++)
+#pragma unroll
+                    for (int r = 0; r < 16; r++) o[i][r] *= alpha;
+            }
+#pragma unroll
+            for (int ks = 0; ks < BKV / 16; ks++) {
+                half8_t pb;
+#pragma unroll
+                for (int j = 0; j < 8; j++) pb[j] = _Float16(s[ks >> 1][(ks & 1) * 8 + j]);
+                const _Float16* vp = &Vt[(lane & 31) * LDV + ks * 16 + (lane >> 5) * 4];
+#pragma unroll
+                for (int dt = 0; dt < DS / 32; dt++) {
+                    const half4_t lo4 = *reinterpret_cast<const half4_t*>(vp + dt * 32 * LDV);
+                    const half4_t hi4 = *reinterpret_cast<const half4_t*>(vp + dt * 32 * LDV + 8);
+                    const half8_t a = {lo4[0], lo4[1], lo4[2], lo4[3], hi4[0], hi4[1], hi4[2], hi4[3]};
+                    o[dt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, pb, o[dt], 0, 0, 0);
+                }
+            }
+        }
+        __syncthreads();
+        if (!PIPE && it + 1 < nblocks) {
+            attn_stage<HD, DS, BATCH_INLINE, NP>(lds, lds + BKV * LDK, kbase, vbase, kb + BKV, kvStride, pt);
+            __syncthreads();
+        }
+    }
+    if (!qvalid) return;
+    const float inv = l_run > 0.0f ? 1.0f / l_run : 0.0f;
+    _Float16* op = reinterpret_cast<_Float16*>(Og) + (size_t)(wi.seq_start + qi) * qStride + h * HD + d0 + (lane >> 5) * 4;
+#pragma unroll
+    for (int dt = 0; dt < DS / 32; dt++)
+#pragma unroll
+        for (int g = 0; g < 4; g++) {
+            half4_t v4;
+#pragma unroll
+            for (int j = 0; j < 4; j++) v4[j] = _Float16(o[dt][g * 4 + j] * inv);
+            *reinterpret_cast<half4_t*>(op + dt * 32 + g * 8) = v4;
+        }
+}
+
+static size_t attention_lds_bytes(int hd, int ds, bool pipe) {
+    return (size_t)(pipe ? 2 : 1) * (attn::BKV * (hd + 8) + ds * attn::LDV) * sizeof(_Float16);
+}
+
+template <int HD, int DS, int G>
+static hipError_t attention_configure() {
+    constexpr bool pipe = G < attn::WAVES && HD <= 256;
+    return hipFuncSetAttribute(reinterpret_cast<const void*>(&attention_kernel<HD, DS, G>),
+                               hipFuncAttributeMaxDynamicSharedMemorySize, int(attention_lds_bytes(HD, DS, pipe)));
+}
+
+template <int HD, int DS>
+static hipError_t attention_configure_all() {
+    hipError_t e = attention_configure<HD, DS, 1>();
+    if (e == hipSuccess) e = attention_configure<HD, DS, 2>();
+    if (e == hipSuccess) e = attention_configure<HD, DS, 3>();
+    if (e == hipSuccess) e = attention_configure<HD, DS, 4>();
+    return e;
+}
+
+hipError_t configure_kernels() {
+    hipError_t e = attention_configure_all<128, 128>();
+    if (e == hipSuccess) e = attention_configure_all<256, 256>();
+    if (e == hipSuccess) e = attention_configure_all<512, 256>();
+    return e;
+}
+
+template <int HD, int DS, int G>
+static hipError_t attention_dispatch(hipStream_t s, const uint16_t* q, const uint16_t* k, const uint16_t* v,
+                                     uint16_t* o, const AttnWork* work, int n_work, int H, int KV, int hw,
+                                     float scale) {
+    constexpr bool pipe = G < attn::WAVES && HD <= 256;
+    const size_t lds = attention_lds_bytes(HD, DS, pipe);
+    dim3 grid(n_work, KV, HD / DS);
+    const float scale_log2 = scale * 1.4426950408889634f;
+    launch_kernel(attention_kernel<HD, DS, G>, grid, 64 * attn::WAVES, lds, s, q, k, v, o, work, H, KV, hw, scale_log2);
+    return hipGetLastError();
+}
+
+template <int HD, int DS>
+static hipError_t attention_dispatch_g(hipStream_t s, const uint16_t* q, const uint16_t* k, const uint16_t* v,
+                                       uint16_t* o, const AttnWork* work, int n_work, int H, int KV, int hw,
+                                       float scale) {
+    switch (H / KV) {
+    case 1: return attention_dispatch<HD, DS, 1>(s, q, k, v, o, work, n_work, H, KV, hw, scale);
+    case 2: return attention_dispatch<HD, DS, 2>(s, q, k, v, o, work, n_work, H, KV, hw, scale);
+    case 3: return attention_dispatch<HD, DS, 3>(s, q, k, v, o, work, n_work, H, KV, hw, scale);
+    case 4: return attention_dispatch<HD, DS, 4>(s, q, k, v, o, work, n_work, H, KV, hw, scale);
+    default: return hipErrorInvalidValue;
+    }
+}
+
+hipError_t launch_attention(hipStream_t s, const uint16_t* q, const uint16_t* k, const uint16_t* v, uint16_t* o,
+                            const AttnWork* work, int n_work, int H, int KV, int hd, int half_window, float scale) {
+    if (n_work < 0 || H <= 0 || KV <= 0 || H % KV != 0 || H / KV > attn::WAVES || half_window < 0)
+        return hipErrorInvalidValue;
+    if (n_work == 0) return hipSuccess;
+    switch (hd) {
+    case 128: return attention_dispatch_g<128, 128>(s, q, k, v, o, work, n_work, H, KV, half_window, scale);
+    case 256: return attention_dispatch_g<256, 256>(s, q, k, v, o, work, n_work, H, KV, half_window, scale);
+    case 512: return attention_dispatch_g<512, 256>(s, q, k, v, o, work, n_work, H, KV, half_window, scale);
+    default: return hipErrorInvalidValue;
+    }
+}
+
+}  // namespace ge

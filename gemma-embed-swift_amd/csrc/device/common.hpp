@@ -1,0 +1,51 @@
+// Device helpers shared by the gfx950 kernels.
+#pragma once
+
+#include <hip/hip_ext.h>
+#include <hip/hip_runtime.h>
+
+#include <cmath>
+#include <cstdint>
+
+namespace ge {
+
+// Events the next launch records from its own dispatch timestamps (set by the runtime while
+// profiling; null otherwise). hipExtLaunchKernelGGL stamps the kernel's start and end the way
+// the profiler does, without separate marker packets between kernels.
+struct LaunchEvents {
+    hipEvent_t start = nullptr, stop = nullptr;
+};
+LaunchEvents& launch_events();
+
+template <typename... KArgs, typename... Args>
+inline void launch_kernel(void (*kernel)(KArgs...), dim3 grid, dim3 block, uint32_t lds, hipStream_t s, Args... args) {
+    const LaunchEvents& ev = launch_events();
+    if (ev.start)
+        hipExtLaunchKernelGGL(kernel, grid, block, lds, s, ev.start, ev.stop, 0u, static_cast<KArgs>(args)...);
+    else
+        hipLaunchKernelGGL(kernel, grid, block, lds, s, static_cast<KArgs>(args)...);
+}
+
+
+typedef _Float16 half4_t __attribute__((ext_vector_type(4)));
+typedef _Float16 half8_t __attribute__((ext_vector_type(8)));
+typedef float float4_t __attribute__((ext_vector_type(4)));
+typedef float float16_t __attribute__((ext_vector_type(16)));
+
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+    for (int m = 32; m >= 1; m >>= 1) v += __shfl_xor(v, m, 64);
+    return v;
+}
+
+__device__ __forceinline__ float gelu_tanh(float x) {
+    // ggml's gelu_tanh constants (reference Shaders/Common.metal:18-21, Model/Architecture.md:45).
+    const float c = 0.79788456080286535587989211986876f;
+    return 0.5f * x * (1.0f + tanhf(c * x * (1.0f + 0.044715f * x * x)));
+}
+
+__device__ __forceinline__ float h2f(uint16_t b) { return float(__builtin_bit_cast(_Float16, b)); }
+__device__ __forceinline__ uint16_t f2h(float f) { return __builtin_bit_cast(uint16_t, _Float16(f)); }
+
+
+}  // namespace ge

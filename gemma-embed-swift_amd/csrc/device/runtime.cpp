@@ -15,6 +15,7 @@
 #include <vector>
 
 #include "gemmaembed.h"
+#include "common.hpp"
 #include "kernels.hpp"
 
 namespace ge {
@@ -145,6 +146,12 @@ struct ge_ctx {
 };
 
 namespace ge {
+
+LaunchEvents& launch_events() {
+    static thread_local LaunchEvents ev;
+    return ev;
+}
+
 namespace {
 
 thread_local std::string g_create_error;
@@ -212,7 +219,8 @@ void resolve_profile(ge_ctx* c) {
     c->prof_pending.clear();
 }
 
-// Runs one launch, bracketed by events when profiling covers `name`.
+// Runs one launch. When profiling covers `name`, the kernel's dispatch records a start and a
+// stop event itself (hipExtLaunchKernelGGL), so the measured time is the kernel's own.
 template <typename F>
 void launch(ge_ctx* c, const char* name, F&& f) {
     const bool prof = c->prof && std::strncmp(name, c->prof_prefix.c_str(), c->prof_prefix.size()) == 0;
@@ -220,14 +228,12 @@ void launch(ge_ctx* c, const char* name, F&& f) {
     if (prof) {
         a = take_event(c);
         b = take_event(c);
-        hip_check(hipEventRecord(a, c->stream), "hipEventRecord");
+        launch_events() = LaunchEvents{a, b};
     }
     hipError_t e = f();
+    launch_events() = LaunchEvents{};
     if (e != hipSuccess) fail(e == hipErrorInvalidValue ? GE_ERR_INVALID : GE_ERR_GPU, "GPU execution failed: %s: %s", name, hipGetErrorString(e));
-    if (prof) {
-        hip_check(hipEventRecord(b, c->stream), "hipEventRecord");
-        c->prof_pending.push_back({name, a, b});
-    }
+    if (prof) c->prof_pending.push_back({name, a, b});
 }
 
 // ---------------------------------------------------------------- upload
