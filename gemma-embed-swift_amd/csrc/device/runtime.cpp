@@ -304,7 +304,17 @@ HostQ8 host_q8(int rows, int cols) {
     return h;
 }
 
-Q8Dev upload_q8(ge_ctx* c, const HostQ8& h, const char* what) {
+// The dequantised fragment-order copy serves GEMMs whose K is a multiple of 128 (the fragment
+// kernel's stage pair); rows must fill 32-row fragment blocks.
+bool wants_fragments(const Q8Dev& d) { return d.rows % 32 == 0 && d.cols % 128 == 0; }
+
+void build_fragments(hipStream_t s, Q8Dev* d, const char* what) {
+    d->fh = static_cast<uint16_t*>(dev_alloc((size_t)d->rows * d->cols * 2, what));
+    hip_check(launch_q8_fragments(s, *d, d->fh), "q8 fragment order");
+}
+
+// Quant and scale planes, plus (for GEMM weights) the dequantised fragment-order copy.
+Q8Dev upload_q8(ge_ctx* c, const HostQ8& h, const char* what, bool gemm_weight = true) {
     Q8Dev d;
     d.rows = h.rows;
     d.cols = h.cols;
@@ -314,6 +324,11 @@ Q8Dev upload_q8(ge_ctx* c, const HostQ8& h, const char* what) {
     c->weight_allocs.push_back(d.s);
     hip_check(hipMemcpy(d.q, h.q.data(), h.q.size(), hipMemcpyHostToDevice), "hipMemcpy weights");
     hip_check(hipMemcpy(d.s, h.s.data(), h.s.size() * 2, hipMemcpyHostToDevice), "hipMemcpy weights");
+    if (gemm_weight && wants_fragments(d)) {
+        build_fragments(c->stream, &d, what);
+        c->weight_allocs.push_back(d.fh);
+        hip_check(hipStreamSynchronize(c->stream), "hipStreamSynchronize");
+    }
     return d;
 }
 
@@ -442,7 +457,7 @@ void upload(ge_ctx* c, const ge_model_desc* d, const void* base, size_t len) {
     {
         HostQ8 h = host_q8(m.vocab, D);
         repack_rows(q8_tensor(d, "token_embd.weight", D, m.vocab, base, len), m.vocab, D, &h, 0);
-        m.tok_embd = upload_q8(c, h, "token_embd");
+        m.tok_embd = upload_q8(c, h, "token_embd", false);
     }
     {
         HostQ8 h = host_q8(m.out_dims, D);
@@ -956,10 +971,15 @@ int ge_op_q8_create(ge_ctx* c, const void* rows_q8, int32_t rows, int32_t cols, 
         m->m.s = static_cast<uint16_t*>(ge::dev_alloc(h.s.size() * 2, "q8 matrix"));
         ge::hip_check(hipMemcpy(m->m.q, h.q.data(), h.q.size(), hipMemcpyHostToDevice), "hipMemcpy");
         ge::hip_check(hipMemcpy(m->m.s, h.s.data(), h.s.size() * 2, hipMemcpyHostToDevice), "hipMemcpy");
+        if (ge::wants_fragments(m->m)) {
+            ge::build_fragments(c->stream, &m->m, "q8 matrix");
+            ge::hip_check(hipStreamSynchronize(c->stream), "hipStreamSynchronize");
+        }
     });
     if (rc != GE_OK) {
         if (m->m.q) (void)hipFree(m->m.q);
         if (m->m.s) (void)hipFree(m->m.s);
+        if (m->m.fh) (void)hipFree(m->m.fh);
         return rc;
     }
     *out = m.release();
@@ -971,6 +991,7 @@ int ge_op_q8_destroy(ge_ctx* c, ge_q8_matrix* m) {
     int rc = guarded(c, [&] {
         ge::hip_check(hipFree(m->m.q), "hipFree");
         ge::hip_check(hipFree(m->m.s), "hipFree");
+        if (m->m.fh) ge::hip_check(hipFree(m->m.fh), "hipFree");
     });
     delete m;
     return rc;
@@ -1003,6 +1024,7 @@ int ge_op_gemm_q8_geglu(ge_ctx* c, const ge_q8_matrix* gate, const ge_q8_matrix*
             ~Free() {
                 (void)hipFree(p->q);
                 (void)hipFree(p->s);
+                if (p->fh) (void)hipFree(p->fh);
             }
         } guard{&gu};
         for (int jb = 0; jb < F / 32; jb++) {
@@ -1014,6 +1036,7 @@ int ge_op_gemm_q8_geglu(ge_ctx* c, const ge_q8_matrix* gate, const ge_q8_matrix*
                                              (size_t)32 * (K / 32) * 2, hipMemcpyDeviceToDevice, c->stream), "hipMemcpy");
             }
         }
+        if (ge::wants_fragments(gu)) ge::build_fragments(c->stream, &gu, "geglu");
         ge::launch(c, "gemm_geglu", [&] {
             return ge::launch_gemm_q8(c->stream, gu, static_cast<const uint16_t*>(x), m, act, ge::kEpiGeglu);
         });
