@@ -32,6 +32,7 @@ sys.path.insert(0, os.path.join(ROOT, "gemma-embed-swift_amd"))
 METRIC = "embedded tokens/sec, 24L Q8_0 encoder 32×512 @1 GPU; Q8 GEMM % MFMA peak"
 PEAK_FP16_TFLOPS = 2500.0  # MI355X dense fp16/bf16 MFMA
 HBM_PEAK_GBS = 8000.0
+COPY_ELEMS = 1 << 28  # calibration kernel of the --probe run: reads 512 MiB, writes 1 GiB
 TEXTS, TOKENS = 32, 512
 D, FF, OUT, HD, H, KV, LAYERS = 768, 1152, 768, 256, 3, 1, 24
 
@@ -51,6 +52,17 @@ def gemm_flops(m: int):
     return {"gemm_qkv": qkv, "gemm_o": o, "gemm_gate_up": gu, "gemm_down": down, "gemm_output": out}
 
 
+def gemm_bytes(m: int):
+    """Algorithmic HBM bytes of one launch: fp16 activations in, fp16 dequantised weights, output
+    (fp32, or fp16 for the GeGLU product)."""
+    b = {}
+    for name, n, k, out_bytes in (("gemm_qkv", (H + 2 * KV) * HD, D, 4), ("gemm_o", D, H * HD, 4),
+                                  ("gemm_gate_up", 2 * FF, D, 2), ("gemm_down", D, FF, 4), ("gemm_output", OUT, D, 4)):
+        n_out = n // 2 if name == "gemm_gate_up" else n
+        b[name] = 2 * m * k + 2 * n * k + out_bytes * m * n_out
+    return b
+
+
 def attention_flops(lengths, window=512, pattern=(1, 1, 1, 1, 1, 0) * 4):
     """4 * hd * H * visible (query, key) pairs, summed over layers."""
     total = 0
@@ -64,6 +76,21 @@ def attention_flops(lengths, window=512, pattern=(1, 1, 1, 1, 1, 0) * 4):
                 pairs = n * n
             total += 4 * HD * H * pairs
     return total
+
+
+def measured_traffic(label: str):
+    """HBM bytes per launch of `label` at this workload, from the committed rocprofv3 summary of two
+    counter runs of `bench.py --probe` (FETCH_SIZE, then WRITE_SIZE, each scaled by what the same
+    counter reads for a conversion kernel of known size). Returns (bytes, kernel) or (None, None)."""
+    import re
+    path = os.path.join(ROOT, "profiles", f"{label}_config2_traffic.md")
+    try:
+        with open(path) as f:
+            text = f.read()
+    except OSError:
+        return None, None
+    m = re.search(rf"traffic_bytes_per_launch {label} (.+) grid (\d+): (\d+)", text)
+    return (int(m.group(3)), m.group(1)) if m else (None, None)
 
 
 def cpu_baseline(model_path: str, batch, budget_s: float = 12.0):
@@ -99,6 +126,9 @@ def main():
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU oracle baseline")
     ap.add_argument("--model", default=None, help="existing config-2 GGUF (default: generate one)")
+    ap.add_argument("--probe", action="store_true",
+                    help="counter-collection run: a known-size conversion kernel (the calibration for HBM "
+                         "byte counters), then the warmup and timed steps only")
     args = ap.parse_args()
     if args.gpus != 1:
         print(json.dumps({"error": "this build runs on one GPU; --gpus above 1 is not supported "
@@ -121,6 +151,14 @@ def main():
     model = ge.EmbeddingModel.load(path, batch_token_budget=16384)
     ctx = model.context
     log(f"loaded on {model.info.device_name.decode()}")
+
+    if args.probe:
+        # fp16 -> fp32 conversion of COPY_ELEMS values: reads 2 and writes 4 bytes per value.
+        src, dst = ctx.alloc(2 * COPY_ELEMS), ctx.alloc(4 * COPY_ELEMS)
+        ctx.f16_to_f32(src, dst, COPY_ELEMS)
+        ctx.free(src)
+        ctx.free(dst)
+        log(f"calibration conversion of {COPY_ELEMS} values done")
 
     # ---- main measurement: one resident 16384-token pack per step
     ctx.batch_stage(batch)
@@ -149,6 +187,10 @@ def main():
     ms_per_step = elapsed * 1e3 / args.steps
     value = n_tokens / (elapsed / args.steps)
     log(f"resident pack: {ms_per_step:.3f} ms/step, {value:,.0f} tokens/s")
+    if args.probe:
+        model.close()
+        print(json.dumps({"probe": True, "ms_per_step": round(ms_per_step, 4), "value": round(value, 1)}))
+        return
 
     flops = gemm_flops(n_tokens)
     step_gemm_flops = LAYERS * (flops["gemm_qkv"] + flops["gemm_o"] + flops["gemm_gate_up"] + flops["gemm_down"]) \
@@ -192,6 +234,7 @@ def main():
     log(f"default budget {default_budget:,.0f} tok/s; embed API {api_rate:,.0f} tok/s")
 
     total_flops = step_gemm_flops + attention_flops([TOKENS] * TEXTS)
+    traffic, traffic_kernel = measured_traffic(dom)
     result = {
         "metric": METRIC,
         "value": round(value, 1),
@@ -209,7 +252,9 @@ def main():
                    "texts": TEXTS, "tokens_per_text": TOKENS, "batch_token_budget": 16384,
                    "model": "synthetic gemma-embedding2 d768 3q/1kv hd256 ff1152 vocab262144, window 512, 5:1 pattern"},
         "roofline": {"bound": "mfma", "kernel": dom, "achieved": round(achieved, 2), "peak": PEAK_FP16_TFLOPS,
-                     "unit": "TFLOP/s", "frac": round(achieved / PEAK_FP16_TFLOPS, 4), "traffic": None,
+                     "unit": "TFLOP/s", "frac": round(achieved / PEAK_FP16_TFLOPS, 4), "traffic": traffic,
+                     "traffic_source": f"profiles/{dom}_config2_traffic.md ({traffic_kernel})" if traffic else None,
+                     "algorithmic_bytes": gemm_bytes(n_tokens)[dom],
                      "avg_launch_us": round(avg_ms * 1e3, 2), "flops_per_launch": flops[dom],
                      "profiled_ms_per_step": round(profiled_ms, 4)},
         "gemm_all": {"achieved": round(gemm_all, 2), "unit": "TFLOP/s", "frac": round(gemm_all / PEAK_FP16_TFLOPS, 4),
