@@ -1,26 +1,12 @@
-// Q8_0 GEMM on gfx950 MFMA: activations fp16, weights Q8_0 repacked into int8 quant and fp16
-// scale planes, dequantised to fp16 while staged into LDS, v_mfma_f32_32x32x16_f16 with fp32
-// accumulation. Replaces the reference's gemm_q8_* Metal kernels (Shaders/GEMM.metal:72-165,
-// 218-355), which widen Q8_0 to fp32 in threadgroup memory for fp32 8x8 simdgroup MMA.
-#include <cstring>
-
+// Q8_0 GEMM on gfx950 MFMA: y = x * W^T with x fp16 activations and W a Q8_0 matrix that was
+// dequantised once, at upload, into fp16 in MFMA fragment order (Q8Dev::fh); v_mfma_f32_32x32x16_f16
+// with fp32 accumulation. Replaces the reference's gemm_q8_* Metal kernels
+// (Shaders/GEMM.metal:72-165, 218-355), which widen Q8_0 to fp32 in threadgroup memory for fp32
+// 8x8 simdgroup MMA on every call.
 #include "common.hpp"
 #include "kernels.hpp"
 
 namespace ge {
-
-// ============================================================================ Q8_0 GEMM
-//
-// Y[M][N] = X[M][K] * W[N][K]^T. A workgroup computes a BM x BN tile with WM x WN waves, each
-// wave a (BM / WM) x (BN / WN) sub-tile of 32 x 32 MFMA accumulators. K advances in stages of
-// BK (a multiple of the 32-wide Q8_0 block): the stage after the current one is loaded from
-// global memory into registers while the current one is multiplied from LDS, then dequantised
-// and stored into the other LDS buffer, one barrier per stage. LDS rows are padded by 8 halves
-// so the 16-byte fragment reads of 16 consecutive lanes fall in distinct banks.
-//
-// Tile order is XCD-aware: workgroups are dealt to the 8 XCDs round robin, so workgroup b runs
-// on XCD b % 8; tile (b % 8) * (T / 8) + b / 8 gives each XCD a contiguous, M-major run of tiles,
-// whose A row blocks and whole weight matrix stay in that XCD's L2.
 
 __device__ __forceinline__ half8_t dequant8(uint32_t a, uint32_t b, _Float16 d) {
     half8_t r;
@@ -32,144 +18,28 @@ __device__ __forceinline__ half8_t dequant8(uint32_t a, uint32_t b, _Float16 d) 
     return r;
 }
 
-template <int BM, int BN, int BK, int WM, int WN, int EPI>
-__global__ __launch_bounds__(WM* WN * 64) void gemm_q8_kernel(const uint16_t* __restrict__ X,
-                                                               const int8_t* __restrict__ Wq,
-                                                               const uint16_t* __restrict__ Ws, void* __restrict__ Y,
-                                                               int M, int N, int K, float out_scale, int tiles_n,
-                                                               int tiles) {
-    constexpr int NT = WM * WN * 64;
-    constexpr int LDK = BK + 8;
-    constexpr int TM = BM / WM, TN = BN / WN, FM = TM / 32, FN = TN / 32;
-    constexpr int ACH = BM * BK / 8;   // 16-byte A chunks per stage (8 halves)
-    constexpr int BCH = BN * BK / 16;  // 16-byte B chunks per stage (16 int8)
-    constexpr int AL = ACH / NT, BL = BCH / NT;
-    static_assert(ACH % NT == 0 && BCH % NT == 0, "staging must divide evenly");
-    static_assert(BK % 32 == 0 && TM % 32 == 0 && TN % 32 == 0, "tile shape");
-    __shared__ __attribute__((aligned(16))) _Float16 As[2][BM * LDK];
-    __shared__ __attribute__((aligned(16))) _Float16 Bs[2][BN * LDK];
-
-    const int b = blockIdx.x;
-    const int full = tiles / 8 * 8;
-    const int tile = b < full ? (b % 8) * (full / 8) + b / 8 : b;
-    const int m0 = (tile / tiles_n) * BM, n0 = (tile % tiles_n) * BN;
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const int KB = K / BK, KQ = K / 32;
-
-    // Global sources of this thread's staging chunks. Rows past M or N are clamped to the last
-    // row: their products land only in outputs that are never stored.
-    const uint16_t* ap[AL];
-#pragma unroll
-    for (int i = 0; i < AL; i++) {
-        const int c = tid + i * NT, r = c / (BK / 8), col = (c % (BK / 8)) * 8;
-        ap[i] = X + (size_t)min(m0 + r, M - 1) * K + col;
-    }
-    const int8_t* bp[BL];
-    const uint16_t* sp[BL];
-#pragma unroll
-    for (int i = 0; i < BL; i++) {
-        const int c = tid + i * NT, r = c / (BK / 16), col = (c % (BK / 16)) * 16;
-        const int rr = min(n0 + r, N - 1);
-        bp[i] = Wq + (size_t)rr * K + col;
-        sp[i] = Ws + (size_t)rr * KQ + col / 32;
-    }
-
-    // Two register slots: stage kb + 2 loads into one while stage kb + 1, loaded a full stage
-    // earlier, drains from the other into LDS, so each load has two stages of MFMA work to land.
-    u32x4 ra0[AL], rb0[BL], ra1[AL], rb1[BL];
-    uint16_t rs0[BL], rs1[BL];
-#define GEMM_LOAD(RA, RB, RS, kb)                                                           \
-    do {                                                                                    \
-        _Pragma("unroll") for (int i = 0; i < AL; i++) RA[i] =                              \
-            *reinterpret_cast<const u32x4*>(ap[i] + (kb) * BK);                             \
-        _Pragma("unroll") for (int i = 0; i < BL; i++) {                                    \
-            RB[i] = *reinterpret_cast<const u32x4*>(bp[i] + (kb) * BK);                     \
-            RS[i] = sp[i][(kb) * (BK / 32)];                                                \
-        }                                                                                   \
-    } while (0)
-    // int8 and the fp16 scale are exact in fp16, so q * d rounds once.
-#define GEMM_STORE(RA, RB, RS, buf)                                                         \
-    do {                                                                                    \
-        _Pragma("unroll") for (int i = 0; i < AL; i++) {                                    \
-            const int c = tid + i * NT, r = c / (BK / 8), col = (c % (BK / 8)) * 8;         \
-            *reinterpret_cast<u32x4*>(&As[buf][r * LDK + col]) = RA[i];                     \
-        }                                                                                   \
-        _Pragma("unroll") for (int i = 0; i < BL; i++) {                                    \
-            const int c = tid + i * NT, r = c / (BK / 16), col = (c % (BK / 16)) * 16;      \
-            const _Float16 d = __builtin_bit_cast(_Float16, RS[i]);                         \
-            *reinterpret_cast<half8_t*>(&Bs[buf][r * LDK + col]) = dequant8(RB[i][0], RB[i][1], d);     \
-            *reinterpret_cast<half8_t*>(&Bs[buf][r * LDK + col + 8]) = dequant8(RB[i][2], RB[i][3], d); \
-        }                                                                                   \
-    } while (0)
-
-    float16_t acc[FM][FN];
-#pragma unroll
-    for (int i = 0; i < FM; i++)
-#pragma unroll
-        for (int j = 0; j < FN; j++)
-#pragma unroll
-            for (int r = 0; r < 16; r++) acc[i][j][r] = 0.0f;
-
-    const int wm = wave / WN, wn = wave % WN;
-    const int fr = lane & 31, fk = (lane >> 5) * 8;
-#define GEMM_MMA_STAGE(buf)                                                                          \
-    do {                                                                                             \
-        const _Float16* as = &As[buf][(wm * TM + fr) * LDK + fk];                                    \
-        const _Float16* bs = &Bs[buf][(wn * TN + fr) * LDK + fk];                                    \
-        _Pragma("unroll") for (int ks = 0; ks < BK / 16; ks++) {                                     \
-            half8_t af[FM], bf[FN];                                                                  \
-            _Pragma("unroll") for (int i = 0; i < FM; i++) af[i] =                                   \
-                *reinterpret_cast<const half8_t*>(as + i * 32 * LDK + ks * 16);                      \
-            _Pragma("unroll") for (int j = 0; j < FN; j++) bf[j] =                                   \
-                *reinterpret_cast<const half8_t*>(bs + j * 32 * LDK + ks * 16);                      \
-            _Pragma("unroll") for (int i = 0; i < FM; i++)                                           \
-                _Pragma("unroll") for (int j = 0; j < FN; j++) acc[i][j] =                           \
-                    __builtin_amdgcn_mfma_f32_32x32x16_f16(af[i], bf[j], acc[i][j], 0, 0, 0);        \
-        }                                                                                            \
-    } while (0)
-
-    // KB is even (checked by the launcher). Stage s lives in register slot s % 2 and LDS buffer s % 2.
-    GEMM_LOAD(ra0, rb0, rs0, 0);
-    GEMM_LOAD(ra1, rb1, rs1, 1);
-    GEMM_STORE(ra0, rb0, rs0, 0);
-    __syncthreads();
-    // Loads past the last stage re-read the last stage (in bounds, never stored), which keeps
-    // every load unconditional so the register slots stay in registers.
-    for (int kb = 0; kb < KB; kb += 2) {
-        GEMM_LOAD(ra0, rb0, rs0, min(kb + 2, KB - 1));
-        GEMM_MMA_STAGE(0);
-        GEMM_STORE(ra1, rb1, rs1, 1);
-        __syncthreads();
-        GEMM_LOAD(ra1, rb1, rs1, min(kb + 3, KB - 1));
-        GEMM_MMA_STAGE(1);
-        if (kb + 2 < KB) GEMM_STORE(ra0, rb0, rs0, 0);
-        __syncthreads();
-    }
-#undef GEMM_LOAD
-#undef GEMM_STORE
-#undef GEMM_MMA_STAGE
-
-    // Accumulator layout of a 32x32 MFMA tile: register r of lane l holds
-    // row (r / 4) * 8 + (l / 32) * 4 + r % 4, column l % 32.
-    const int rbase = m0 + wm * TM + (lane >> 5) * 4;
+// Stores a wave's FM x FN accumulator tiles; row0, cbase: the wave's first row and column.
+// GUARD false: the caller has checked that every row and column is inside Y.
+template <int FM, int FN, int EPI, bool GUARD>
+__device__ __forceinline__ void gemm_store_tile_impl(const float16_t (&acc)[FM][FN], void* __restrict__ Y, int M, int N,
+                                                     int row0, int cbase, int lane, float out_scale) {
+    const int rbase = row0 + (lane >> 5) * 4;
     if constexpr (EPI == kEpiGeglu) {
-        // Weight rows come in 32-row gate/up pairs: tile column pair (2p, 2p + 1) of the wave is
-        // (gate, up) for output column (n0 + wn * TN) / 2 + p * 32 + lane % 32.
         static_assert(FN % 2 == 0, "geglu pairs tiles");
         const int F = N / 2;
         _Float16* act = static_cast<_Float16*>(Y);
 #pragma unroll
         for (int p = 0; p < FN / 2; p++) {
-            const int gcol = n0 + wn * TN + p * 64;
-            if (gcol >= N) continue;
-            const int col = gcol / 2 + (lane & 31);
+            const int gcol = cbase + p * 64;
+            if (GUARD && gcol >= N) continue;
+            _Float16* dst = act + gcol / 2 + (lane & 31);
 #pragma unroll
             for (int i = 0; i < FM; i++)
 #pragma unroll
                 for (int r = 0; r < 16; r++) {
                     const int row = rbase + i * 32 + (r >> 2) * 8 + (r & 3);
-                    if (row < M)
-                        act[(size_t)row * F + col] = _Float16(gelu_tanh(acc[i][2 * p][r]) * acc[i][2 * p + 1][r] * out_scale);
+                    if (!GUARD || row < M)
+                        dst[(size_t)row * F] = _Float16(gelu_tanh(acc[i][2 * p][r]) * acc[i][2 * p + 1][r] * out_scale);
                 }
         }
     } else {
@@ -177,13 +47,13 @@ __global__ __launch_bounds__(WM* WN * 64) void gemm_q8_kernel(const uint16_t* __
         for (int i = 0; i < FM; i++)
 #pragma unroll
             for (int j = 0; j < FN; j++) {
-                const int col = n0 + wn * TN + j * 32 + (lane & 31);
-                if (col >= N) continue;
+                const int col = cbase + j * 32 + (lane & 31);
+                if (GUARD && col >= N) continue;
 #pragma unroll
                 for (int r = 0; r < 16; r++) {
                     const int row = rbase + i * 32 + (r >> 2) * 8 + (r & 3);
-                    if (row >= M) continue;
-                    if (EPI == kEpiF32)
+                    if (GUARD && row >= M) continue;
+                    if constexpr (EPI == kEpiF32)
                         static_cast<float*>(Y)[(size_t)row * N + col] = acc[i][j][r] * out_scale;
                     else
                         static_cast<_Float16*>(Y)[(size_t)row * N + col] = _Float16(acc[i][j][r] * out_scale);
@@ -192,285 +62,117 @@ __global__ __launch_bounds__(WM* WN * 64) void gemm_q8_kernel(const uint16_t* __
     }
 }
 
-void q8_fragment_order(const int8_t* q, const uint16_t* s, int rows, int cols, int8_t* fq, uint16_t* fs) {
-    const int KQ = cols / 32;
-    for (int j = 0; j < rows / 32; j++)
-        for (int b = 0; b < KQ; b++) {
-            int8_t* chunk = fq + ((size_t)j * KQ + b) * 1024;
-            for (int l = 0; l < 64; l++) {
-                const int8_t* row = q + (size_t)(32 * j + l % 32) * cols + 32 * b + 8 * (l / 32);
-                std::memcpy(chunk + l * 16, row, 8);
-                std::memcpy(chunk + l * 16 + 8, row + 16, 8);
-            }
-            for (int r = 0; r < 32; r++) fs[((size_t)j * KQ + b) * 32 + r] = s[(size_t)(32 * j + r) * KQ + b];
-        }
+template <int FM, int FN, int EPI>
+__device__ __forceinline__ void gemm_store_tile(const float16_t (&acc)[FM][FN], void* __restrict__ Y, int M, int N,
+                                                int row0, int cbase, int lane, float out_scale) {
+    if (row0 + FM * 32 <= M && cbase + FN * 32 <= N)
+        gemm_store_tile_impl<FM, FN, EPI, false>(acc, Y, M, N, row0, cbase, lane, out_scale);
+    else
+        gemm_store_tile_impl<FM, FN, EPI, true>(acc, Y, M, N, row0, cbase, lane, out_scale);
 }
 
-// ============================================================================ Q8_0 GEMM, weights in fragment order
+// ============================================================================ GEMM
 //
-// The same product with the weights read straight from global memory (L2-resident: a layer's
-// matrices are at most a few MB) into registers in fragment order: one coalesced 16-byte load
-// per lane brings a lane its B fragments for the two k-steps of one Q8_0 block, dequantised in
-// registers. Only the activations go through LDS. Waves split N, so no weight element is
-// dequantised twice inside a workgroup. K advances 64 (two Q8_0 blocks) per stage; both operands
-// are loaded two stages ahead into a pair of register slots (the loop runs stages in pairs so
-// every slot index is a compile-time constant).
-template <int BM, int BN, int WM, int WN, int EPI>
-__global__ __launch_bounds__(WM* WN * 64) void gemm_q8f_kernel(const uint16_t* __restrict__ X,
-                                                                const int8_t* __restrict__ Fq,
-                                                                const uint16_t* __restrict__ Fs, void* __restrict__ Y,
-                                                                int M, int N, int K, float out_scale, int tiles_n,
-                                                                int tiles) {
-    constexpr int BK = 64, NT = WM * WN * 64, LDK = BK + 8;
-    constexpr int TM = BM / WM, TN = BN / WN, FM = TM / 32, FN = TN / 32;
-    constexpr int ACH = BM * BK / 8, AL = ACH / NT;
-    static_assert(ACH % NT == 0 && TM % 32 == 0 && TN % 32 == 0, "tile shape");
-    __shared__ __attribute__((aligned(16))) _Float16 As[2][BM * LDK];
-
-    const int b = blockIdx.x;
-    const int full = tiles / 8 * 8;
-    const int tile = b < full ? (b % 8) * (full / 8) + b / 8 : b;
-    const int m0 = (tile / tiles_n) * BM, n0 = (tile % tiles_n) * BN;
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const int KB = K / BK, KQ = K / 32;
-    const int wm = wave / WN, wn = wave % WN;
-
-    const uint16_t* ap[AL];
-#pragma unroll
-    for (int i = 0; i < AL; i++) {
-        const int c = tid + i * NT, r = c / (BK / 8), col = (c % (BK / 8)) * 8;
-        ap[i] = X + (size_t)min(m0 + r, M - 1) * K + col;
-    }
-    // This wave's 32-row weight blocks (clamped past N: their outputs are never stored).
-    const u32x4* fp[FN];
-    const uint16_t* fsp[FN];
-#pragma unroll
-    for (int j = 0; j < FN; j++) {
-        const int jg = min((n0 + wn * TN) / 32 + j, N / 32 - 1);
-        fp[j] = reinterpret_cast<const u32x4*>(Fq + (size_t)jg * KQ * 1024) + lane;
-        fsp[j] = Fs + (size_t)jg * KQ * 32 + (lane & 31);
-    }
-
-    u32x4 ra0[AL], ra1[AL], rb0[FN][2], rb1[FN][2];
-    uint16_t rs0[FN][2], rs1[FN][2];
-#define GQ_LOAD_A(RA, kb)                                                                                \
-    do {                                                                                                 \
-        _Pragma("unroll") for (int i = 0; i < AL; i++) RA[i] = *reinterpret_cast<const u32x4*>(ap[i] + (kb) * BK); \
-    } while (0)
-#define GQ_LOAD_B(RB, RS, kb)                                                                            \
-    do {                                                                                                 \
-        _Pragma("unroll") for (int j = 0; j < FN; j++) _Pragma("unroll") for (int h = 0; h < 2; h++) {   \
-            RB[j][h] = fp[j][(size_t)(2 * (kb) + h) * 64];                                               \
-            RS[j][h] = fsp[j][(size_t)(2 * (kb) + h) * 32];                                              \
-        }                                                                                                \
-    } while (0)
-#define GQ_STORE_A(RA, buf)                                                                              \
-    do {                                                                                                 \
-        _Pragma("unroll") for (int i = 0; i < AL; i++) {                                                 \
-            const int c = tid + i * NT, r = c / (BK / 8), col = (c % (BK / 8)) * 8;                      \
-            *reinterpret_cast<u32x4*>(&As[buf][r * LDK + col]) = RA[i];                                  \
-        }                                                                                                \
-    } while (0)
-    // k-step ks of the stage: Q8_0 block ks / 2, first or second 8-byte half of the lane's chunk.
-#define GQ_MMA(buf, RB, RS)                                                                              \
-    do {                                                                                                 \
-        const _Float16* as = &As[buf][(wm * TM + (lane & 31)) * LDK + (lane >> 5) * 8];                  \
-        _Pragma("unroll") for (int ks = 0; ks < BK / 16; ks++) {                                         \
-            half8_t af[FM], bf[FN];                                                                      \
-            _Pragma("unroll") for (int i = 0; i < FM; i++) af[i] =                                       \
-                *reinterpret_cast<const half8_t*>(as + i * 32 * LDK + ks * 16);                          \
-            _Pragma("unroll") for (int j = 0; j < FN; j++) {                                             \
-                const u32x4 w = RB[j][ks >> 1];                                                          \
-                const _Float16 d = __builtin_bit_cast(_Float16, RS[j][ks >> 1]);                         \
-                bf[j] = (ks & 1) ? dequant8(w[2], w[3], d) : dequant8(w[0], w[1], d);                    \
-            }                                                                                            \
-            _Pragma("unroll") for (int i = 0; i < FM; i++)                                               \
-                _Pragma("unroll") for (int j = 0; j < FN; j++) acc[i][j] =                               \
-                    __builtin_amdgcn_mfma_f32_32x32x16_f16(af[i], bf[j], acc[i][j], 0, 0, 0);            \
-        }                                                                                                \
-    } while (0)
-
-    float16_t acc[FM][FN];
-#pragma unroll
-    for (int i = 0; i < FM; i++)
-#pragma unroll
-        for (int j = 0; j < FN; j++)
-#pragma unroll
-            for (int r = 0; r < 16; r++) acc[i][j][r] = 0.0f;
-
-    // KB is even (checked by the launcher). Stage s uses slot s % 2 and LDS buffer s % 2; loads
-    // past the last stage re-read the last stage (in bounds, never used).
-    GQ_LOAD_A(ra0, 0);
-    GQ_LOAD_B(rb0, rs0, 0);
-    GQ_LOAD_A(ra1, 1);
-    GQ_LOAD_B(rb1, rs1, 1);
-    GQ_STORE_A(ra0, 0);
-    __syncthreads();
-    for (int kb = 0; kb < KB; kb += 2) {
-        GQ_LOAD_A(ra0, min(kb + 2, KB - 1));
-        GQ_MMA(0, rb0, rs0);
-        GQ_LOAD_B(rb0, rs0, min(kb + 2, KB - 1));
-        GQ_STORE_A(ra1, 1);
-        __syncthreads();
-        GQ_LOAD_A(ra1, min(kb + 3, KB - 1));
-        GQ_MMA(1, rb1, rs1);
-        GQ_LOAD_B(rb1, rs1, min(kb + 3, KB - 1));
-        if (kb + 2 < KB) GQ_STORE_A(ra0, 0);
-        __syncthreads();
-    }
-#undef GQ_LOAD_A
-#undef GQ_LOAD_B
-#undef GQ_STORE_A
-#undef GQ_MMA
-
-    const int rbase = m0 + wm * TM + (lane >> 5) * 4;
-    if constexpr (EPI == kEpiGeglu) {
-        static_assert(FN % 2 == 0, "geglu pairs tiles");
-        const int F = N / 2;
-        _Float16* act = static_cast<_Float16*>(Y);
-#pragma unroll
-        for (int p = 0; p < FN / 2; p++) {
-            const int gcol = n0 + wn * TN + p * 64;
-            if (gcol >= N) continue;
-            const int col = gcol / 2 + (lane & 31);
-#pragma unroll
-            for (int i = 0; i < FM; i++)
-#pragma unroll
-                for (int r = 0; r < 16; r++) {
-                    const int row = rbase + i * 32 + (r >> 2) * 8 + (r & 3);
-                    if (row < M)
-                        act[(size_t)row * F + col] = _Float16(gelu_tanh(acc[i][2 * p][r]) * acc[i][2 * p + 1][r] * out_scale);
-                }
-        }
-    } else {
-#pragma unroll
-        for (int i = 0; i < FM; i++)
-#pragma unroll
-            for (int j = 0; j < FN; j++) {
-                const int col = n0 + wn * TN + j * 32 + (lane & 31);
-                if (col >= N) continue;
-#pragma unroll
-                for (int r = 0; r < 16; r++) {
-                    const int row = rbase + i * 32 + (r >> 2) * 8 + (r & 3);
-                    if (row >= M) continue;
-                    if (EPI == kEpiF32)
-                        static_cast<float*>(Y)[(size_t)row * N + col] = acc[i][j][r] * out_scale;
-                    else
-                        static_cast<_Float16*>(Y)[(size_t)row * N + col] = _Float16(acc[i][j][r] * out_scale);
-                }
-            }
-    }
-}
-
-template <int BM, int BN, int WM, int WN>
-hipError_t gemm_q8f_launch(hipStream_t s, const Q8Dev& w, const uint16_t* x, int M, void* y, GemmEpilogue epi,
-                           float out_scale) {
-    const int N = w.rows, K = w.cols;
-    if (K % 128 != 0 || N % 32 != 0 || !w.fq || !w.fs) return hipErrorInvalidValue;
-    const int tiles_m = (M + BM - 1) / BM, tiles_n = (N + BN - 1) / BN, tiles = tiles_m * tiles_n;
-    const dim3 grid(tiles), block(WM * WN * 64);
-    switch (epi) {
-    case kEpiF32: launch_kernel(gemm_q8f_kernel<BM, BN, WM, WN, kEpiF32>, grid, block, 0, s, x, w.fq, w.fs, y, M, N, K, out_scale, tiles_n, tiles); break;
-    case kEpiF16: launch_kernel(gemm_q8f_kernel<BM, BN, WM, WN, kEpiF16>, grid, block, 0, s, x, w.fq, w.fs, y, M, N, K, out_scale, tiles_n, tiles); break;
-    case kEpiGeglu:
-        if constexpr ((BN / WN / 32) % 2 == 0)
-            launch_kernel(gemm_q8f_kernel<BM, BN, WM, WN, kEpiGeglu>, grid, block, 0, s, x, w.fq, w.fs, y, M, N, K, out_scale, tiles_n, tiles);
-        else
-            return hipErrorInvalidValue;
-        break;
-    default: return hipErrorInvalidValue;
-    }
-    return hipGetLastError();
-}
-
-void q8_dequant_fragment_order(const int8_t* q, const uint16_t* s, int rows, int cols, uint16_t* fh) {
-    const int KQ = cols / 32, KT = cols / 16;
-    for (int j = 0; j < rows / 32; j++)
-        for (int t = 0; t < KT; t++) {
-            uint16_t* chunk = fh + ((size_t)j * KT + t) * 512;
-            for (int l = 0; l < 64; l++) {
-                const int row = 32 * j + l % 32, k0 = 16 * t + 8 * (l / 32);
-                for (int e = 0; e < 8; e++) {
-                    const int k = k0 + e;
-                    const _Float16 d = __builtin_bit_cast(_Float16, s[(size_t)row * KQ + k / 32]);
-                    // fp32 holds q * d exactly; one rounding to fp16, as dequant8 does on the device.
-                    const float v = float(q[(size_t)row * cols + k]) * float(d);
-                    chunk[l * 8 + e] = __builtin_bit_cast(uint16_t, _Float16(v));
-                }
-            }
-        }
-}
-
-// ============================================================================ GEMM, dequantised weights in fragment order
+// Y[M][N] = X[M][K] * W[N][K]^T. A workgroup computes a BM x BN tile with WM x WN waves, each wave
+// a (BM / WM) x (BN / WN) block of 32 x 32 MFMA accumulators. Both operands move from global memory into LDS with global_load_lds_dwordx4: each lane's 16
+// bytes land at (wave's LDS base) + 16 * lane, and no register holds them on the way. A stage is
+// BK columns of K: the activation tile (BM rows, row-major in global memory) and the weight tile
+// (BN rows, Q8Dev::fh fragment order, so each of its 1 KB chunks is one contiguous copy). ST stages
+// rotate through LDS: while stage s is multiplied, stages s + 1 .. s + ST - 1 are in flight.
 //
-// The Q8_0 weights are dequantised once at upload (fp16 of q * d, the value the in-kernel
-// dequantisation produces) and laid out so that one coalesced 16-byte load per lane is that
-// lane's B fragment for one 16-wide k-step. Waves split N and stream their fragments straight
-// from L2 into registers; only the activations go through LDS. The MFMA loop then carries no
-// conversion work: per k-step a wave issues FM LDS reads, FN global loads and FM x FN MFMAs.
-// K advances 64 per stage; both operands are loaded two stages ahead into a pair of register
-// slots (stages run in pairs so slot indices are compile-time constants).
-template <int BM, int BN, int WM, int WN, int EPI>
-__global__ __launch_bounds__(WM* WN * 64) void gemm_h_kernel(const uint16_t* __restrict__ X,
+// Activation chunks hold 1024 / (2 BK) rows of BK halves. The 16-byte slot of logical column
+// group g of row r sits at slot g ^ swz(r), which spreads the 32-row fragment reads of one
+// k-step over all 64 banks (16 lanes, 16 consecutive rows, are served per cycle); the swizzle is
+// applied by choosing each lane's source address.
+//
+// Tile order is XCD-aware: workgroups are dealt to the 8 XCDs round robin, so workgroup b runs
+// on XCD b % 8; tile (b % 8) * (T / 8) + b / 8 gives each XCD a contiguous, M-major run of tiles,
+// whose activation row blocks and the weight matrix stay in that XCD's L2.
+// s_waitcnt with only the vector-memory counter constrained (gfx9 encoding: vmcnt in bits 3:0
+// and 15:14; expcnt and lgkmcnt at their maxima).
+// s_waitcnt lgkmcnt(0) alone (vmcnt and expcnt at their maxima).
+__device__ __forceinline__ void wait_lgkmcnt0() { __builtin_amdgcn_s_waitcnt(0xc07f); }
+
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+    static_assert(N >= 0 && N < 64, "vmcnt range");
+    __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
+}
+
+// global_load_lds_dwordx4: lane l's 16 bytes from src land at lds_base + 16 l (lds_base is
+// wave-uniform). The copy counts against vmcnt like a load.
+__device__ __forceinline__ void lds_copy16(const void* src, void* lds_base) {
+    __builtin_amdgcn_global_load_lds(src, (__attribute__((address_space(3))) void*)lds_base, 16, 0, 0);
+}
+
+// A workgroup barrier without the release fence of __syncthreads(): that fence would wait for
+// every outstanding global->LDS copy, including the stages still meant to be in flight. The asm
+// memory clobbers keep the compiler from moving LDS accesses across it; the copies a barrier must
+// cover are waited for explicitly (wait_vmcnt) before it.
+__device__ __forceinline__ void workgroup_barrier() {
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
+}
+
+template <int BK>
+struct DTile {
+    static constexpr int RB = 2 * BK;          // bytes per activation row in LDS
+    static constexpr int RPC = 1024 / RB;      // rows per 1 KB chunk
+    static constexpr int SPR = BK / 8;         // 16-byte slots per row
+    static constexpr int RSH = 256 / RB;       // rows covering the 256 bytes of the 64 banks
+    __device__ static constexpr int swz(int r) { return (r / RSH) % SPR; }
+    // byte offset of (row r, column group g) inside the activation tile
+    __device__ static constexpr int a_off(int r, int g) { return (r / RPC) * 1024 + (r % RPC) * RB + ((g ^ swz(r)) * 16); }
+};
+
+template <int BM, int BN, int WM, int WN, int BK, int ST>
+constexpr int gemm_d_lds_bytes() { return ST * (BM + BN) * BK * 2; }
+
+template <int BM, int BN, int WM, int WN, int BK, int ST, int EPI>
+__global__ __launch_bounds__(WM* WN * 64) void gemm_d_kernel(const uint16_t* __restrict__ X,
                                                               const uint16_t* __restrict__ Fh, void* __restrict__ Y,
                                                               int M, int N, int K, float out_scale, int tiles_n,
                                                               int tiles) {
-    constexpr int BK = 64, KS = BK / 16, NT = WM * WN * 64, LDK = BK + 8;
+    using T = DTile<BK>;
+    constexpr int NW = WM * WN, KS = BK / 16;
     constexpr int TM = BM / WM, TN = BN / WN, FM = TM / 32, FN = TN / 32;
-    constexpr int ACH = BM * BK / 8, AL = ACH / NT;
-    static_assert(ACH % NT == 0 && TM % 32 == 0 && TN % 32 == 0, "tile shape");
-    __shared__ __attribute__((aligned(16))) _Float16 As[2][BM * LDK];
+    constexpr int ACH = BM * BK / 512, BCH = BN * BK / 512;  // 1 KB chunks per stage
+    constexpr int AW = ACH / NW, BW = BCH / NW;               // chunks per wave per stage
+    constexpr int A_BYTES = BM * BK * 2, STAGE = (BM + BN) * BK * 2;
+    static_assert(ACH % NW == 0 && BCH % NW == 0 && TM % 32 == 0 && TN % 32 == 0, "tile shape");
+    extern __shared__ __attribute__((aligned(1024))) unsigned char lds[];
 
     const int b = blockIdx.x;
     const int full = tiles / 8 * 8;
     const int tile = b < full ? (b % 8) * (full / 8) + b / 8 : b;
     const int m0 = (tile / tiles_n) * BM, n0 = (tile % tiles_n) * BN;
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int KB = K / BK, KT = K / 16;
     const int wm = wave / WN, wn = wave % WN;
 
-    const uint16_t* ap[AL];
+    // Source of this lane's 16 bytes for each of the wave's chunks, at stage 0.
+    const uint16_t* asrc[AW];
 #pragma unroll
-    for (int i = 0; i < AL; i++) {
-        const int c = tid + i * NT, r = c / (BK / 8), col = (c % (BK / 8)) * 8;
-        ap[i] = X + (size_t)min(m0 + r, M - 1) * K + col;
+    for (int i = 0; i < AW; i++) {
+        const int c = wave * AW + i, r = c * T::RPC + lane / T::SPR, slot = lane % T::SPR;
+        asrc[i] = X + (size_t)min(m0 + r, M - 1) * K + (slot ^ T::swz(r)) * 8;
     }
-    const u32x4* fp[FN];
+    const uint16_t* bsrc[BW];
 #pragma unroll
-    for (int j = 0; j < FN; j++) {
-        const int jg = min((n0 + wn * TN) / 32 + j, N / 32 - 1);
-        fp[j] = reinterpret_cast<const u32x4*>(Fh + (size_t)jg * KT * 512) + lane;
+    for (int i = 0; i < BW; i++) {
+        const int c = wave * BW + i, jb = c / KS, t = c % KS;
+        const int jg = min(n0 / 32 + jb, N / 32 - 1);
+        bsrc[i] = Fh + ((size_t)jg * KT + t) * 512 + lane * 8;
     }
 
-    u32x4 ra0[AL], ra1[AL], rb0[FN][KS], rb1[FN][KS];
-#define GH_LOAD_A(RA, kb)                                                                                \
-    do {                                                                                                 \
-        _Pragma("unroll") for (int i = 0; i < AL; i++) RA[i] = *reinterpret_cast<const u32x4*>(ap[i] + (kb) * BK); \
-    } while (0)
-#define GH_LOAD_B(RB, kb)                                                                                \
-    do {                                                                                                 \
-        _Pragma("unroll") for (int j = 0; j < FN; j++) _Pragma("unroll") for (int t = 0; t < KS; t++)  \
-            RB[j][t] = fp[j][(size_t)((kb) * KS + t) * 64];                                              \
-    } while (0)
-#define GH_STORE_A(RA, buf)                                                                              \
-    do {                                                                                                 \
-        _Pragma("unroll") for (int i = 0; i < AL; i++) {                                                 \
-            const int c = tid + i * NT, r = c / (BK / 8), col = (c % (BK / 8)) * 8;                      \
-            *reinterpret_cast<u32x4*>(&As[buf][r * LDK + col]) = RA[i];                                  \
-        }                                                                                                \
-    } while (0)
-#define GH_MMA(buf, RB)                                                                                  \
-    do {                                                                                                 \
-        const _Float16* as = &As[buf][(wm * TM + (lane & 31)) * LDK + (lane >> 5) * 8];                  \
-        _Pragma("unroll") for (int ks = 0; ks < KS; ks++) {                                              \
-            half8_t af[FM];                                                                              \
-            _Pragma("unroll") for (int i = 0; i < FM; i++) af[i] =                                       \
-                *reinterpret_cast<const half8_t*>(as + i * 32 * LDK + ks * 16);                          \
-            _Pragma("unroll") for (int i = 0; i < FM; i++)                                               \
-                _Pragma("unroll") for (int j = 0; j < FN; j++) acc[i][j] =                               \
-                    __builtin_amdgcn_mfma_f32_32x32x16_f16(af[i], __builtin_bit_cast(half8_t, RB[j][ks]), \
-                                                           acc[i][j], 0, 0, 0);                          \
-        }                                                                                                \
+#define GD_ISSUE(stage, buf)                                                                               \
+    do {                                                                                                   \
+        unsigned char* base_ = lds + (buf) * STAGE;                                                        \
+        _Pragma("unroll") for (int i = 0; i < AW; i++)                                                     \
+            lds_copy16(asrc[i] + (size_t)(stage) * BK, base_ + (wave * AW + i) * 1024);                    \
+        _Pragma("unroll") for (int i = 0; i < BW; i++)                                                     \
+            lds_copy16(bsrc[i] + (size_t)(stage) * KS * 512, base_ + A_BYTES + (wave * BW + i) * 1024);    \
     } while (0)
 
     float16_t acc[FM][FN];
@@ -481,83 +183,96 @@ __global__ __launch_bounds__(WM* WN * 64) void gemm_h_kernel(const uint16_t* __r
 #pragma unroll
             for (int r = 0; r < 16; r++) acc[i][j][r] = 0.0f;
 
-    // Two register slots: stage kb + 2 loads into one while stage kb + 1, loaded a stage earlier,
-    // is in the other; loads past the last stage re-read it (in bounds, never used).
-    GH_LOAD_A(ra0, 0);
-    GH_LOAD_B(rb0, 0);
-    GH_LOAD_A(ra1, 1);
-    GH_LOAD_B(rb1, 1);
-    GH_STORE_A(ra0, 0);
-    __syncthreads();
-    for (int kb = 0; kb < KB; kb += 2) {
-        GH_LOAD_A(ra0, min(kb + 2, KB - 1));
-        GH_MMA(0, rb0);
-        GH_LOAD_B(rb0, min(kb + 2, KB - 1));
-        GH_STORE_A(ra1, 1);
-        __syncthreads();
-        GH_LOAD_A(ra1, min(kb + 3, KB - 1));
-        GH_MMA(1, rb1);
-        GH_LOAD_B(rb1, min(kb + 3, KB - 1));
-        if (kb + 2 < KB) GH_STORE_A(ra0, 0);
-        __syncthreads();
-    }
-#undef GH_LOAD_A
-#undef GH_LOAD_B
-#undef GH_STORE_A
-#undef GH_MMA
-
-    const int rbase = m0 + wm * TM + (lane >> 5) * 4;
-    if constexpr (EPI == kEpiGeglu) {
-        static_assert(FN % 2 == 0, "geglu pairs tiles");
-        const int F = N / 2;
-        _Float16* act = static_cast<_Float16*>(Y);
 #pragma unroll
-        for (int p = 0; p < FN / 2; p++) {
-            const int gcol = n0 + wn * TN + p * 64;
-            if (gcol >= N) continue;
-            const int col = gcol / 2 + (lane & 31);
+    for (int s = 0; s < ST - 1; s++)
+        if (s < KB) GD_ISSUE(s, s);
+
+    const int arow = wm * TM + (lane & 31), half = lane >> 5;
+    // Fragment registers are double-buffered: the reads of k-step ks + 1 are issued before the
+    // MFMAs of k-step ks. The stage boundary (wait for the next stage's copies, barrier) sits
+    // before the last k-step's MFMAs, so reading the next stage's first fragments overlaps them.
+    half8_t af[2][FM], bf[2][FN];
+#define GD_FRAGS(p, buf, ks)                                                                                  \
+    do {                                                                                                      \
+        const unsigned char* ab_ = lds + (buf) * STAGE;                                                       \
+        _Pragma("unroll") for (int i = 0; i < FM; i++) af[p][i] =                                             \
+            *reinterpret_cast<const half8_t*>(ab_ + T::a_off(arow + i * 32, 2 * (ks) + half));                \
+        _Pragma("unroll") for (int j = 0; j < FN; j++) bf[p][j] =                                             \
+            *reinterpret_cast<const half8_t*>(ab_ + A_BYTES + ((wn * FN + j) * KS + (ks)) * 1024 + lane * 16); \
+    } while (0)
+#define GD_STAGE_WAIT(kb)                                                                                     \
+    do {                                                                                                      \
+        if ((kb) + ST - 2 < KB)                                                                               \
+            wait_vmcnt<(ST - 2) * (AW + BW)>();                                                               \
+        else                                                                                                  \
+            wait_vmcnt<0>();                                                                                  \
+        wait_lgkmcnt0();                                                                                      \
+        workgroup_barrier();                                                                                  \
+    } while (0)
+
+    // Stage kb's copies have landed once at most (ST - 2) later stages' copies are outstanding;
+    // the barrier then covers every wave's copies. Waiting for this wave's LDS reads first makes
+    // the barrier also mean that every read of the buffer the next copies overwrite is done.
+    GD_STAGE_WAIT(0);
+    GD_FRAGS(0, 0, 0);
+    int buf = 0;
+    for (int kb = 0; kb < KB; kb++) {
+        if (kb + ST - 1 < KB) GD_ISSUE(kb + ST - 1, (buf + ST - 1) % ST);
+        const int next = buf + 1 == ST ? 0 : buf + 1;
+#pragma unroll
+        for (int ks = 0; ks < KS; ks++) {
+            const int p = ks & 1;
+            if (ks + 1 < KS) {
+                GD_FRAGS(p ^ 1, buf, ks + 1);
+            } else if (kb + 1 < KB) {
+                GD_STAGE_WAIT(kb + 1);
+                GD_FRAGS(p ^ 1, next, 0);
+            }
 #pragma unroll
             for (int i = 0; i < FM; i++)
 #pragma unroll
-                for (int r = 0; r < 16; r++) {
-                    const int row = rbase + i * 32 + (r >> 2) * 8 + (r & 3);
-                    if (row < M)
-                        act[(size_t)row * F + col] = _Float16(gelu_tanh(acc[i][2 * p][r]) * acc[i][2 * p + 1][r] * out_scale);
-                }
+                for (int j = 0; j < FN; j++)
+                    acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(af[p][i], bf[p][j], acc[i][j], 0, 0, 0);
         }
-    } else {
-#pragma unroll
-        for (int i = 0; i < FM; i++)
-#pragma unroll
-            for (int j = 0; j < FN; j++) {
-                const int col = n0 + wn * TN + j * 32 + (lane & 31);
-                if (col >= N) continue;
-#pragma unroll
-                for (int r = 0; r < 16; r++) {
-                    const int row = rbase + i * 32 + (r >> 2) * 8 + (r & 3);
-                    if (row >= M) continue;
-                    if (EPI == kEpiF32)
-                        static_cast<float*>(Y)[(size_t)row * N + col] = acc[i][j][r] * out_scale;
-                    else
-                        static_cast<_Float16*>(Y)[(size_t)row * N + col] = _Float16(acc[i][j][r] * out_scale);
-                }
-            }
+        buf = next;
     }
+#undef GD_FRAGS
+#undef GD_STAGE_WAIT
+#undef GD_ISSUE
+    gemm_store_tile<FM, FN, EPI>(acc, Y, M, N, m0 + wm * TM, n0 + wn * TN, lane, out_scale);
 }
 
-template <int BM, int BN, int WM, int WN>
-hipError_t gemm_h_launch(hipStream_t s, const Q8Dev& w, const uint16_t* x, int M, void* y, GemmEpilogue epi,
+template <typename... KArgs>
+hipError_t set_lds_limit(void (*kernel)(KArgs...), int bytes) {
+    return hipFuncSetAttribute(reinterpret_cast<const void*>(kernel), hipFuncAttributeMaxDynamicSharedMemorySize, bytes);
+}
+
+template <int BM, int BN, int WM, int WN, int BK, int ST>
+hipError_t gemm_d_launch(hipStream_t s, const Q8Dev& w, const uint16_t* x, int M, void* y, GemmEpilogue epi,
                          float out_scale) {
     const int N = w.rows, K = w.cols;
-    if (K % 128 != 0 || N % 32 != 0 || !w.fh) return hipErrorInvalidValue;
+    if (K % BK != 0 || N % 32 != 0 || !w.fh) return hipErrorInvalidValue;
     const int tiles_m = (M + BM - 1) / BM, tiles_n = (N + BN - 1) / BN, tiles = tiles_m * tiles_n;
     const dim3 grid(tiles), block(WM * WN * 64);
+    constexpr uint32_t lds = gemm_d_lds_bytes<BM, BN, WM, WN, BK, ST>();
+    if (lds > 65536) {
+        hipError_t e = hipSuccess;
+        switch (epi) {
+        case kEpiF32: e = set_lds_limit(gemm_d_kernel<BM, BN, WM, WN, BK, ST, kEpiF32>, lds); break;
+        case kEpiF16: e = set_lds_limit(gemm_d_kernel<BM, BN, WM, WN, BK, ST, kEpiF16>, lds); break;
+        case kEpiGeglu:
+            if constexpr ((BN / WN / 32) % 2 == 0) e = set_lds_limit(gemm_d_kernel<BM, BN, WM, WN, BK, ST, kEpiGeglu>, lds);
+            break;
+        default: break;
+        }
+        if (e != hipSuccess) return e;
+    }
     switch (epi) {
-    case kEpiF32: launch_kernel(gemm_h_kernel<BM, BN, WM, WN, kEpiF32>, grid, block, 0, s, x, w.fh, y, M, N, K, out_scale, tiles_n, tiles); break;
-    case kEpiF16: launch_kernel(gemm_h_kernel<BM, BN, WM, WN, kEpiF16>, grid, block, 0, s, x, w.fh, y, M, N, K, out_scale, tiles_n, tiles); break;
+    case kEpiF32: launch_kernel(gemm_d_kernel<BM, BN, WM, WN, BK, ST, kEpiF32>, grid, block, lds, s, x, w.fh, y, M, N, K, out_scale, tiles_n, tiles); break;
+    case kEpiF16: launch_kernel(gemm_d_kernel<BM, BN, WM, WN, BK, ST, kEpiF16>, grid, block, lds, s, x, w.fh, y, M, N, K, out_scale, tiles_n, tiles); break;
     case kEpiGeglu:
         if constexpr ((BN / WN / 32) % 2 == 0)
-            launch_kernel(gemm_h_kernel<BM, BN, WM, WN, kEpiGeglu>, grid, block, 0, s, x, w.fh, y, M, N, K, out_scale, tiles_n, tiles);
+            launch_kernel(gemm_d_kernel<BM, BN, WM, WN, BK, ST, kEpiGeglu>, grid, block, lds, s, x, w.fh, y, M, N, K, out_scale, tiles_n, tiles);
         else
             return hipErrorInvalidValue;
         break;
@@ -588,34 +303,14 @@ hipError_t launch_q8_fragments(hipStream_t s, const Q8Dev& w, uint16_t* fh) {
     return hipGetLastError();
 }
 
-template <int BM, int BN, int BK, int WM, int WN>
-hipError_t gemm_q8_launch(hipStream_t s, const Q8Dev& w, const uint16_t* x, int M, void* y, GemmEpilogue epi,
-                          float out_scale) {
-    const int N = w.rows, K = w.cols;
-    if (K % (2 * BK) != 0) return hipErrorInvalidValue;  // the K loop runs stages in pairs
-    const int tiles_m = (M + BM - 1) / BM, tiles_n = (N + BN - 1) / BN, tiles = tiles_m * tiles_n;
-    const dim3 grid(tiles), block(WM * WN * 64);
-    switch (epi) {
-    case kEpiF32: launch_kernel(gemm_q8_kernel<BM, BN, BK, WM, WN, kEpiF32>, grid, block, 0, s, x, w.q, w.s, y, M, N, K, out_scale, tiles_n, tiles); break;
-    case kEpiF16: launch_kernel(gemm_q8_kernel<BM, BN, BK, WM, WN, kEpiF16>, grid, block, 0, s, x, w.q, w.s, y, M, N, K, out_scale, tiles_n, tiles); break;
-    case kEpiGeglu: launch_kernel(gemm_q8_kernel<BM, BN, BK, WM, WN, kEpiGeglu>, grid, block, 0, s, x, w.q, w.s, y, M, N, K, out_scale, tiles_n, tiles); break;
-    default: return hipErrorInvalidValue;
-    }
-    return hipGetLastError();
-}
-
 hipError_t launch_gemm_q8(hipStream_t s, const Q8Dev& w, const uint16_t* x, int M, void* y, GemmEpilogue epi,
                           float out_scale) {
     const int N = w.rows, K = w.cols;
-    if (M < 0 || N <= 0 || K <= 0 || K % 32 != 0 || N % 64 != 0 || !w.q || !w.s || !x || !y) return hipErrorInvalidValue;
+    if (M < 0 || N <= 0 || K <= 0 || K % 32 != 0 || N % 64 != 0 || !w.fh || !x || !y) return hipErrorInvalidValue;
     if (M == 0) return hipSuccess;
-    if (w.fh && K % 128 == 0) {
-        if (epi == kEpiGeglu) return gemm_h_launch<64, 256, 1, 4>(s, w, x, M, y, epi, out_scale);
-        return gemm_h_launch<128, 128, 1, 4>(s, w, x, M, y, epi, out_scale);
-    }
-    if (K % 128 == 0) return gemm_q8_launch<128, 128, 64, 2, 2>(s, w, x, M, y, epi, out_scale);
-    if (K % 64 == 0) return gemm_q8_launch<128, 128, 32, 2, 2>(s, w, x, M, y, epi, out_scale);
-    return hipErrorInvalidValue;
+    // 128 x 128 tiles, 2 x 2 waves of 64 x 64, K in stages of 32, three stages in LDS (48 KB):
+    // the fastest of the tile sweep on every projection shape of the encoder (M = 16384).
+    return gemm_d_launch<128, 128, 2, 2, 32, 3>(s, w, x, M, y, epi, out_scale);
 }
 
 }  // namespace ge

@@ -26,22 +26,15 @@ constexpr int kAttnQueries = 32;
 // GEMM row block and of the last attention query/key block stay inside the allocation.
 constexpr int kRowSlack = 256;
 
-// A repacked Q8_0 matrix in device memory: quants [rows][cols] int8 and scales
-// [rows][cols / 32] fp16 (raw bits).
+// A Q8_0 matrix in device memory. q / s: the row-major planes, quants [rows][cols] int8 and scales
+// [rows][cols / 32] fp16 (raw bits). fh: for GEMM weights, the dequantised matrix (fp16 of q * d,
+// rounded once) in MFMA fragment order: for 32-row block j and 16-wide k-step t, 512 halves at
+// ((j * cols / 16) + t) * 512 where lane l's 8 halves are row 32 j + l % 32, columns
+// 16 t + 8 (l / 32) + [0, 8) -- the B operand of one v_mfma_f32_32x32x16_f16.
 struct Q8Dev {
     int rows = 0, cols = 0;
     int8_t* q = nullptr;
     uint16_t* s = nullptr;
-    // The same matrix in MFMA fragment order (rows a multiple of 32): for 32-row block j and
-    // 32-wide Q8_0 block b, a 1 KB chunk at ((j * cols / 32) + b) * 1024 where lane l's 16 bytes
-    // are row 32 j + l % 32, columns 32 b + 8 (l / 32) + [0, 8) then 32 b + 16 + 8 (l / 32) + [0, 8)
-    // (its B fragments of the two 16-wide k-steps of the block); the 32 rows' scales of the chunk
-    // at fs[((j * cols / 32) + b) * 32].
-    int8_t* fq = nullptr;
-    uint16_t* fs = nullptr;
-    // The dequantised matrix (fp16 of q * d, rounded once) in MFMA fragment order: for 32-row
-    // block j and 16-wide k-step t, 512 halves at ((j * cols / 16) + t) * 512 where lane l's 8
-    // halves are row 32 j + l % 32, columns 16 t + 8 (l / 32) + [0, 8).
     uint16_t* fh = nullptr;
 };
 
@@ -49,16 +42,10 @@ struct Q8Dev {
 // halves; rows a multiple of 32).
 hipError_t launch_q8_fragments(hipStream_t s, const Q8Dev& w, uint16_t* fh);
 
-// Host-side dequantisation of row-major planes into Q8Dev::fh order.
-void q8_dequant_fragment_order(const int8_t* q, const uint16_t* s, int rows, int cols, uint16_t* fh);
-
-// Host-side repack of row-major planes into fragment order (sizes as Q8Dev::fq / fs).
-void q8_fragment_order(const int8_t* q, const uint16_t* s, int rows, int cols, int8_t* fq, uint16_t* fs);
-
 enum GemmEpilogue { kEpiF32 = 0, kEpiF16 = 1, kEpiGeglu = 2 };
 
-// y[M][N] = (x[M][K] (fp16) * W[N][K]^T (Q8_0)) * out_scale. Uses W.fh when it is set and K is a
-// multiple of 128, the row-major planes otherwise; both give bitwise the same result. kEpiGeglu expects W's rows
+// y[M][N] = (x[M][K] (fp16) * W[N][K]^T (Q8_0, through W.fh)) * out_scale; N a multiple of 64,
+// K of 32. kEpiGeglu expects W's rows
 // interleaved in 32-row gate/up groups and writes fp16 act[M][N / 2] = gelu_tanh(gate) * up *
 // out_scale. out_scale is a power of two wherever the forward uses it, so it is exact.
 hipError_t launch_gemm_q8(hipStream_t s, const Q8Dev& w, const uint16_t* x, int M, void* y, GemmEpilogue epi,

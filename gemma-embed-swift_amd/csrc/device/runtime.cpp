@@ -304,9 +304,8 @@ HostQ8 host_q8(int rows, int cols) {
     return h;
 }
 
-// The dequantised fragment-order copy serves GEMMs whose K is a multiple of 128 (the fragment
-// kernel's stage pair); rows must fill 32-row fragment blocks.
-bool wants_fragments(const Q8Dev& d) { return d.rows % 32 == 0 && d.cols % 128 == 0; }
+// The GEMMs read the dequantised fragment-order copy; it needs whole 32-row fragment blocks.
+bool wants_fragments(const Q8Dev& d) { return d.rows % 32 == 0 && d.cols % 32 == 0; }
 
 void build_fragments(hipStream_t s, Q8Dev* d, const char* what) {
     d->fh = static_cast<uint16_t*>(dev_alloc((size_t)d->rows * d->cols * 2, what));
