@@ -253,6 +253,282 @@ __global__ __launch_bounds__(256) void attention_kernel(const uint16_t* __restri
         }
 }
 
+// ============================================================================ attention, Q/K/V copied straight into LDS
+//
+// One workgroup of 2 G waves per (work item of 64 query rows, KV head): wave w owns query head
+// kvh * G + w % G for the query half w / G (32 rows). Q, K and V move from global memory into
+// LDS with global_load_lds_dwordx4 -- no register or producer wave carries them. Each wave's
+// 32 query rows sit in LDS for the whole kernel (so the fp32 output accumulators, 32 x hd per
+// wave, are the only large register array); keys stream in blocks of 32 through two LDS
+// buffers, the next block's copy in flight while the current one is multiplied. V arrives
+// transposed (V^T [kv head][d][key], written by launch_v_transpose), so every MFMA operand is a
+// 16-byte fragment read.
+//
+// The rows of the S^T tile are taken from the key block in the order 0-3, 8-11, 4-7, 12-15
+// within each 16 keys. The accumulator then holds, for lane half h, keys 8h .. 8h + 7 of each
+// 16-key step in consecutive registers: the B operand of the P.V product needs no shuffling
+// and V^T is read as one 16-byte slot per lane.
+//
+// LDS layouts (16-byte slots, swizzled through each lane's copy source so that every 16 lanes
+// of a fragment read hit all 64 banks once):
+//   Q: per wave [32 queries][hd], slot s of query row r holds column slot s ^ (r % 16);
+//   K: [32 keys][hd], slot s of key row r holds column slot s ^ (r % 16);
+//   V^T: [hd][32 keys], slot s of row d holds key slot s ^ ((d / 4) % 4).
+namespace attn2 {
+constexpr int QB = 64;   // query rows per work item
+constexpr int BKV = 32;  // keys per block
+}  // namespace attn2
+
+template <int HD, int G>
+constexpr int attention_v2_lds_bytes() { return 2 * G * 32 * HD * 2 + 2 * (2 * attn2::BKV * HD * 2); }
+
+template <int HD, int G>
+__global__ __launch_bounds__(2 * G * 64) void attention_v2_kernel(const uint16_t* __restrict__ Qg,
+                                                                  const uint16_t* __restrict__ Kg,
+                                                                  const uint16_t* __restrict__ VTg,
+                                                                  uint16_t* __restrict__ Og,
+                                                                  const AttnWork* __restrict__ work, int H, int KV,
+                                                                  int vt_cols, int hw, float scale_log2) {
+    using namespace attn2;
+    constexpr int NW = 2 * G, KSQ = HD / 16, DT = HD / 32;
+    constexpr int Q_BYTES = 32 * HD * 2;            // one wave's query rows
+    constexpr int K_BYTES = BKV * HD * 2, STAGE = 2 * K_BYTES;
+    constexpr int KCH = K_BYTES / 1024, CH = 2 * KCH;  // 1 KB copies per key block (K, then V^T)
+    constexpr int LPR = HD / 8;                       // 16-byte slots per Q / K row
+    constexpr int VRB = BKV * 2, VSL = VRB / 16;      // V^T row bytes and slots
+    extern __shared__ __attribute__((aligned(1024))) unsigned char ldsb[];
+    unsigned char* const kv = ldsb + NW * Q_BYTES;
+
+    const AttnWork wi = work[blockIdx.x];
+    const int kvh = blockIdx.y;
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int h = kvh * G + wave % G;
+    const int len = int(wi.seq_len), q0 = int(wi.q0) + (wave / G) * 32;
+    const int qi = q0 + (lane & 31), half = lane >> 5;
+    const bool active = q0 < len;  // wave-uniform: the wave has at least one query row
+    const int qStride = H * HD, kvStride = KV * HD;
+
+    int kstart = 0, kend = len;
+    if (hw > 0) {
+        kstart = max(int(wi.q0) - hw, 0);
+        kend = min(int(wi.q0) + QB + hw, len);
+    }
+    kstart = kstart / BKV * BKV;
+    const int nblocks = (kend - kstart + BKV - 1) / BKV;
+
+    const uint16_t* kbase = Kg + (size_t)wi.seq_start * kvStride + kvh * HD;
+    const uint16_t* vtbase = VTg + (size_t)kvh * HD * vt_cols + wi.vt_start;
+
+    // This wave's query rows (rows past the sequence re-read its last row; their outputs are
+    // never stored).
+    unsigned char* const qs = ldsb + wave * Q_BYTES;
+    for (int c = 0; c < Q_BYTES / 1024; c++) {
+        const int r = c * (64 / LPR) + lane / LPR, sl = lane % LPR;
+        const uint16_t* src = Qg + (size_t)(wi.seq_start + min(q0 + r, len - 1)) * qStride + h * HD + ((sl ^ (r & 15)) * 8);
+        lds_copy16(src, qs + c * 1024);
+    }
+
+#define A2_ISSUE(kb, b)                                                                                    \
+    do {                                                                                                   \
+        for (int c = wave; c < CH; c += NW) {                                                              \
+            const uint16_t* src;                                                                           \
+            if (c < KCH) {                                                                                 \
+                const int key = c * (64 / LPR) + lane / LPR, sl = lane % LPR;                              \
+                src = kbase + (size_t)((kb) + key) * kvStride + ((sl ^ (key & 15)) * 8);                   \
+            } else {                                                                                       \
+                const int d = (c - KCH) * (64 / VSL) + lane / VSL, sl = lane % VSL;                        \
+                src = vtbase + (size_t)d * vt_cols + (kb) + ((sl ^ ((d >> 2) & 3)) * 8);                   \
+            }                                                                                              \
+            lds_copy16(src, kv + (b) * STAGE + c * 1024);                                                  \
+        }                                                                                                  \
+    } while (0)
+
+    float16_t o[DT];
+#pragma unroll
+    for (int i = 0; i < DT; i++)
+#pragma unroll
+        for (int r = 0; r < 16; r++) o[i][r] = 0.0f;
+    float m_run = -INFINITY, l_run = 0.0f;
+
+    // S^T row i reads key (i / 16) * 16 + perm(i % 16): 0-3, 8-11, 4-7, 12-15.
+    const int i16 = lane & 15;
+    const int krow = (lane & 16) + (i16 < 4 || i16 >= 12 ? i16 : (i16 < 8 ? i16 + 4 : i16 - 4));
+    const int qrow = lane & 31;
+
+    if (nblocks > 0) A2_ISSUE(kstart, 0);
+    wait_vmcnt<0>();
+    workgroup_barrier();
+    for (int it = 0; it < nblocks; it++) {
+        const int kb = kstart + it * BKV, b = it & 1;
+        if (it + 1 < nblocks) A2_ISSUE(kb + BKV, b ^ 1);
+        if (active) {
+            const unsigned char* Ks = kv + b * STAGE;
+            const unsigned char* Vs = Ks + K_BYTES;
+            float16_t sc;
+#pragma unroll
+            for (int r = 0; r < 16; r++) sc[r] = 0.0f;
+            const unsigned char* kp = Ks + krow * (HD * 2);
+            const unsigned char* qp = qs + qrow * (HD * 2);
+#pragma unroll
+            for (int ks = 0; ks < KSQ; ks++) {
+                const int slot = 2 * ks + half;
+                const half8_t a = *reinterpret_cast<const half8_t*>(kp + ((slot ^ (krow & 15)) * 16));
+                const half8_t bq = *reinterpret_cast<const half8_t*>(qp + ((slot ^ (qrow & 15)) * 16));
+                sc = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, bq, sc, 0, 0, 0);
+            }
+            // key of accumulator element r for this lane: kb + 16 (r / 8) + 8 half + r % 8
+            const bool inside = kb + BKV <= len && (hw == 0 || (kb >= q0 + 31 - hw && kb + BKV - 1 <= q0 + hw));
+            float bmax = -INFINITY;
+            if (inside) {
+#pragma unroll
+                for (int r = 0; r < 16; r++) {
+                    sc[r] *= scale_log2;
+                    bmax = fmaxf(bmax, sc[r]);
+                }
+            } else {
+#pragma unroll
+                for (int r = 0; r < 16; r++) {
+                    const int key = kb + (r >> 3) * 16 + half * 8 + (r & 7);
+                    bool valid = key < len;
+                    if (hw > 0) valid = valid && abs(qi - key) <= hw;
+                    const float val = valid ? sc[r] * scale_log2 : -INFINITY;
+                    sc[r] = val;
+                    bmax = fmaxf(bmax, val);
+                }
+            }
+            bmax = fmaxf(bmax, __shfl_xor(bmax, 32, 64));
+            const float m_new = fmaxf(m_run, bmax);
+            float alpha = 1.0f, sum = 0.0f;
+            if (m_new == -INFINITY) {
+#pragma unroll
+                for (int r = 0; r < 16; r++) sc[r] = 0.0f;
+            } else {
+                alpha = __builtin_amdgcn_exp2f(m_run - m_new);
+#pragma unroll
+                for (int r = 0; r < 16; r++) {
+                    const float p = __builtin_amdgcn_exp2f(sc[r] - m_new);
+                    sc[r] = p;
+                    sum += p;
+                }
+            }
+            sum += __shfl_xor(sum, 32, 64);
+            l_run = l_run * alpha + sum;
+            m_run = m_new;
+            if (alpha != 1.0f) {
+#pragma unroll
+                for (int i = 0; i < DT; i++)
+#pragma unroll
+                    for (int r = 0; r < 16; r++) o[i][r] *= alpha;
+            }
+#pragma unroll
+            for (int ks = 0; ks < BKV / 16; ks++) {
+                half8_t pb;
+#pragma unroll
+                for (int j = 0; j < 8; j++) pb[j] = _Float16(sc[ks * 8 + j]);
+                const int slot = 2 * ks + half;
+#pragma unroll
+                for (int dt = 0; dt < DT; dt++) {
+                    const int d = dt * 32 + (lane & 31);
+                    const half8_t a = *reinterpret_cast<const half8_t*>(Vs + d * VRB + ((slot ^ ((d >> 2) & 3)) * 16));
+                    o[dt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, pb, o[dt], 0, 0, 0);
+                }
+            }
+        }
+        wait_vmcnt<0>();
+        wait_lgkmcnt0();
+        workgroup_barrier();
+    }
+#undef A2_ISSUE
+    if (!active || qi >= len) return;
+    const float inv = l_run > 0.0f ? 1.0f / l_run : 0.0f;
+    _Float16* op = reinterpret_cast<_Float16*>(Og) + (size_t)(wi.seq_start + qi) * qStride + h * HD + half * 4;
+#pragma unroll
+    for (int dt = 0; dt < DT; dt++)
+#pragma unroll
+        for (int g = 0; g < 4; g++) {
+            half4_t v4;
+#pragma unroll
+            for (int j = 0; j < 4; j++) v4[j] = _Float16(o[dt][g * 4 + j] * inv);
+            *reinterpret_cast<half4_t*>(op + dt * 32 + g * 8) = v4;
+        }
+}
+
+template <int HD, int G>
+static hipError_t attention_v2_dispatch(hipStream_t s, const uint16_t* q, const uint16_t* k, const uint16_t* vt,
+                                        int vt_cols, uint16_t* o, const AttnWork* work, int n_work, int H, int KV, int hw,
+                                        float scale) {
+    const float scale_log2 = scale * 1.4426950408889634f;
+    launch_kernel(attention_v2_kernel<HD, G>, dim3(n_work, KV), dim3(2 * G * 64), uint32_t(attention_v2_lds_bytes<HD, G>()), s,
+                  q, k, vt, o, work, H, KV, vt_cols, hw, scale_log2);
+    return hipGetLastError();
+}
+
+template <int HD>
+static hipError_t attention_v2_dispatch_g(hipStream_t s, const uint16_t* q, const uint16_t* k, const uint16_t* vt,
+                                          int vt_cols, uint16_t* o, const AttnWork* work, int n_work, int H, int KV,
+                                          int hw, float scale) {
+    switch (H / KV) {
+    case 1: return attention_v2_dispatch<HD, 1>(s, q, k, vt, vt_cols, o, work, n_work, H, KV, hw, scale);
+    case 2: return attention_v2_dispatch<HD, 2>(s, q, k, vt, vt_cols, o, work, n_work, H, KV, hw, scale);
+    case 3: return attention_v2_dispatch<HD, 3>(s, q, k, vt, vt_cols, o, work, n_work, H, KV, hw, scale);
+    case 4:
+        if constexpr (attention_v2_lds_bytes<HD, 4>() <= 160 * 1024)
+            return attention_v2_dispatch<HD, 4>(s, q, k, vt, vt_cols, o, work, n_work, H, KV, hw, scale);
+        return hipErrorInvalidValue;
+    default: return hipErrorInvalidValue;
+    }
+}
+
+bool attention_v2_supported(int hd, int H, int KV) {
+    if (!((hd == 128 || hd == 256) && KV > 0 && H % KV == 0 && H / KV >= 1 && H / KV <= 4)) return false;
+    const int G = H / KV;
+    return 2 * G * 32 * hd * 2 + 2 * (2 * attn2::BKV * hd * 2) <= 160 * 1024;  // LDS of one workgroup
+}
+
+hipError_t launch_attention_v2(hipStream_t s, const uint16_t* q, const uint16_t* k, const uint16_t* vt, int vt_cols,
+                               uint16_t* o, const AttnWork* work, int n_work, int H, int KV, int hd, int half_window,
+                               float scale) {
+    if (n_work < 0 || !attention_v2_supported(hd, H, KV) || half_window < 0 || vt_cols <= 0 || vt_cols % 8)
+        return hipErrorInvalidValue;
+    if (n_work == 0) return hipSuccess;
+    if (hd == 128) return attention_v2_dispatch_g<128>(s, q, k, vt, vt_cols, o, work, n_work, H, KV, half_window, scale);
+    return attention_v2_dispatch_g<256>(s, q, k, vt, vt_cols, o, work, n_work, H, KV, half_window, scale);
+}
+
+// V [T][KV][hd] fp16 -> V^T [KV * hd][vt_cols] at column vcol[t]. A workgroup transposes 64
+// tokens through LDS: reads are 16-byte row pieces, writes are one d row of 64 tokens per wave
+// instruction (consecutive columns within a sequence).
+__global__ __launch_bounds__(256) void v_transpose_kernel(const uint16_t* __restrict__ v, int T, int width,
+                                                          const int32_t* __restrict__ vcol, int vt_cols,
+                                                          uint16_t* __restrict__ vt) {
+    __shared__ uint16_t tile[64][64 + 2];
+    const int t0 = blockIdx.x * 64, c0 = blockIdx.y * 64, tid = threadIdx.x;
+    for (int i = tid; i < 64 * 8; i += 256) {
+        const int r = i / 8, cc = (i % 8) * 8;
+        if (t0 + r < T) {
+            const u32x4 w = *reinterpret_cast<const u32x4*>(v + (size_t)(t0 + r) * width + c0 + cc);
+#pragma unroll
+            for (int j = 0; j < 4; j++) {
+                tile[r][cc + 2 * j] = uint16_t(w[j] & 0xffffu);
+                tile[r][cc + 2 * j + 1] = uint16_t(w[j] >> 16);
+            }
+        }
+    }
+    __syncthreads();
+    const int lane = tid & 63, wave = tid >> 6;
+    if (t0 + lane >= T) return;
+    const int col = vcol[t0 + lane];
+    for (int d = wave; d < 64; d += 4) vt[(size_t)(c0 + d) * vt_cols + col] = tile[lane][d];
+}
+
+hipError_t launch_v_transpose(hipStream_t s, const uint16_t* v, int T, int width, const int32_t* vcol, int vt_cols,
+                              uint16_t* vt) {
+    if (T < 0 || width <= 0 || width % 64 || !v || !vcol || !vt) return hipErrorInvalidValue;
+    if (T == 0) return hipSuccess;
+    launch_kernel(v_transpose_kernel, dim3((T + 63) / 64, width / 64), dim3(256), 0, s, v, T, width, vcol, vt_cols, vt);
+    return hipGetLastError();
+}
+
 static size_t attention_lds_bytes(int hd, int ds, bool pipe) {
     return (size_t)(pipe ? 2 : 1) * (attn::BKV * (hd + 8) + ds * attn::LDV) * sizeof(_Float16);
 }
@@ -273,8 +549,21 @@ static hipError_t attention_configure_all() {
     return e;
 }
 
+template <int HD, int G>
+static hipError_t attention_v2_configure() {
+    return hipFuncSetAttribute(reinterpret_cast<const void*>(&attention_v2_kernel<HD, G>),
+                               hipFuncAttributeMaxDynamicSharedMemorySize, attention_v2_lds_bytes<HD, G>());
+}
+
 hipError_t configure_kernels() {
     hipError_t e = attention_configure_all<128, 128>();
+    if (e == hipSuccess) e = attention_v2_configure<128, 1>();
+    if (e == hipSuccess) e = attention_v2_configure<128, 2>();
+    if (e == hipSuccess) e = attention_v2_configure<128, 3>();
+    if (e == hipSuccess) e = attention_v2_configure<128, 4>();
+    if (e == hipSuccess) e = attention_v2_configure<256, 1>();
+    if (e == hipSuccess) e = attention_v2_configure<256, 2>();
+    if (e == hipSuccess) e = attention_v2_configure<256, 3>();
     if (e == hipSuccess) e = attention_configure_all<256, 256>();
     if (e == hipSuccess) e = attention_configure_all<512, 256>();
     return e;

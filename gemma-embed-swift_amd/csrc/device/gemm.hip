@@ -90,31 +90,6 @@ __device__ __forceinline__ void gemm_store_tile(const float16_t (&acc)[FM][FN], 
 // whose activation row blocks and the weight matrix stay in that XCD's L2.
 // s_waitcnt with only the vector-memory counter constrained (gfx9 encoding: vmcnt in bits 3:0
 // and 15:14; expcnt and lgkmcnt at their maxima).
-// s_waitcnt lgkmcnt(0) alone (vmcnt and expcnt at their maxima).
-__device__ __forceinline__ void wait_lgkmcnt0() { __builtin_amdgcn_s_waitcnt(0xc07f); }
-
-template <int N>
-__device__ __forceinline__ void wait_vmcnt() {
-    static_assert(N >= 0 && N < 64, "vmcnt range");
-    __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
-}
-
-// global_load_lds_dwordx4: lane l's 16 bytes from src land at lds_base + 16 l (lds_base is
-// wave-uniform). The copy counts against vmcnt like a load.
-__device__ __forceinline__ void lds_copy16(const void* src, void* lds_base) {
-    __builtin_amdgcn_global_load_lds(src, (__attribute__((address_space(3))) void*)lds_base, 16, 0, 0);
-}
-
-// A workgroup barrier without the release fence of __syncthreads(): that fence would wait for
-// every outstanding global->LDS copy, including the stages still meant to be in flight. The asm
-// memory clobbers keep the compiler from moving LDS accesses across it; the copies a barrier must
-// cover are waited for explicitly (wait_vmcnt) before it.
-__device__ __forceinline__ void workgroup_barrier() {
-    asm volatile("" ::: "memory");
-    __builtin_amdgcn_s_barrier();
-    asm volatile("" ::: "memory");
-}
-
 template <int BK>
 struct DTile {
     static constexpr int RB = 2 * BK;          // bytes per activation row in LDS

@@ -8,11 +8,13 @@
 
 namespace ge {
 
-// One block of query rows of one packed sequence (AttentionWork, Shaders/Common.metal:75-79).
+// One block of query rows of one packed sequence (AttentionWork, Shaders/Common.metal:75-79),
+// plus the column of the sequence's first key in the transposed V buffer (a multiple of 8).
 struct AttnWork {
     uint32_t seq_start;
     uint32_t seq_len;
     uint32_t q0;
+    uint32_t vt_start;
 };
 
 struct SeqRange {
@@ -68,6 +70,19 @@ hipError_t launch_qk_norm_rope(hipStream_t s, const float* qkv, int T, int H, in
 // Flash-style bidirectional attention over packed sequences.
 hipError_t launch_attention(hipStream_t s, const uint16_t* q, const uint16_t* k, const uint16_t* v, uint16_t* o,
                             const AttnWork* work, int n_work, int H, int KV, int hd, int half_window, float scale);
+
+// Attention with K/V copied straight into LDS (head dims 128 and 256, at most 4 query heads per
+// KV head): work items of kAttnQueriesV2 query rows; V given transposed, vt [KV * hd][vt_cols],
+// each sequence's keys starting at its work items' vt_start.
+constexpr int kAttnQueriesV2 = 64;
+bool attention_v2_supported(int hd, int H, int KV);
+hipError_t launch_attention_v2(hipStream_t s, const uint16_t* q, const uint16_t* k, const uint16_t* vt, int vt_cols,
+                               uint16_t* o, const AttnWork* work, int n_work, int H, int KV, int hd, int half_window,
+                               float scale);
+
+// v [T][width] fp16 -> vt [width][vt_cols] with token t at column vcol[t]; width a multiple of 64.
+hipError_t launch_v_transpose(hipStream_t s, const uint16_t* v, int T, int width, const int32_t* vcol, int vt_cols,
+                              uint16_t* vt);
 
 // pooled[s] = mean of the sequence's rows of x [*][width].
 hipError_t launch_mean_pool(hipStream_t s, const float* x, const SeqRange* seqs, int n_seqs, int width, float* pooled);

@@ -71,6 +71,7 @@ float host_h2f(uint16_t h) {
 
 struct DevLayer {
     bool sliding = false;
+    bool attn_v2 = false;  // attention with Q/K/V copied into LDS and V transposed
     int kv_heads = 0, head_dim = 0, qd = 0, kvd = 0;
     float rope_base = 0, out_scale = 1;
     // act is stored in fp16 as gelu(gate) * up * act_scale; the down projection multiplies by
@@ -89,6 +90,7 @@ struct DevModel {
     float* out_norm = nullptr;
     std::vector<DevLayer> layer;
     int max_qd = 0, max_kvd = 0, max_qkv = 0;
+    bool any_v2 = false;
 };
 
 struct Workspace {
@@ -100,6 +102,12 @@ struct Workspace {
     SeqRange* seqs = nullptr;
     AttnWork* work = nullptr;
     float* pooled = nullptr;
+    // transposed V for the LDS-copy attention: vt [max_kvd][vt_cap], token t at column vcol[t];
+    // its 64-query work list
+    int vt_cap = 0, work2_cap = 0;
+    uint16_t* vt = nullptr;
+    int32_t* vcol = nullptr;
+    AttnWork* work2 = nullptr;
 };
 
 struct ProfStat {
@@ -136,7 +144,7 @@ struct ge_ctx {
     std::map<std::pair<int, float>, float*> rope_tables;
     ge::Workspace ws;
     // staged batch
-    int staged_tokens = -1, staged_seqs = 0, staged_work = 0;
+    int staged_tokens = -1, staged_seqs = 0, staged_work = 0, staged_work2 = 0, staged_vt_cols = 0;
     // profiling
     bool prof = false;
     std::string prof_prefix;
@@ -420,7 +428,8 @@ void free_model(ge_ctx* c) {
 
 void free_workspace(ge_ctx* c) {
     Workspace& w = c->ws;
-    void* ps[] = {w.x, w.qkv, w.t, w.out, w.h, w.q, w.k, w.v, w.attn, w.act, w.tokens, w.positions, w.seqs, w.work, w.pooled};
+    void* ps[] = {w.x, w.qkv, w.t, w.out, w.h, w.q, w.k, w.v, w.attn, w.act, w.tokens, w.positions, w.seqs, w.work, w.pooled,
+                  w.vt, w.vcol, w.work2};
     for (void* p : ps)
         if (p) (void)hipFree(p);
     c->ws = Workspace{};
@@ -517,6 +526,8 @@ void upload(ge_ctx* c, const ge_model_desc* d, const void* base, size_t len) {
         L.rope = rope_table(c, hd, L.rope_base, m.max_tokens);
         m.max_qd = std::max(m.max_qd, L.qd);
         m.max_kvd = std::max(m.max_kvd, L.kvd);
+        L.attn_v2 = attention_v2_supported(L.head_dim, m.heads, L.kv_heads);
+        m.any_v2 = m.any_v2 || L.attn_v2;
         m.max_qkv = std::max(m.max_qkv, L.qd + 2 * L.kvd);
         m.layer.push_back(L);
     }
@@ -533,7 +544,7 @@ T* ws_alloc(size_t rows, size_t width, const char* what) {
     return static_cast<T*>(p);
 }
 
-void ensure_workspace(ge_ctx* c, int tokens, int seqs, int work) {
+void ensure_workspace(ge_ctx* c, int tokens, int seqs, int work, int work2, int vt_cols) {
     Workspace& w = c->ws;
     const DevModel& m = c->model;
     const int rows = (tokens + 63) / 64 * 64 + kRowSlack;
@@ -555,11 +566,16 @@ void ensure_workspace(ge_ctx* c, int tokens, int seqs, int work) {
         w.out = ws_alloc<float>(rows, m.out_dims, "out");
         w.tokens = ws_alloc<int32_t>(rows, 1, "tokens");
         w.positions = ws_alloc<int32_t>(rows, 1, "positions");
+        w.vcol = ws_alloc<int32_t>(rows, 1, "vt columns");
         w.seqs = nullptr;
         w.work = nullptr;
         w.pooled = nullptr;
         w.seq_cap = 0;
         w.work_cap = 0;
+        w.vt = nullptr;
+        w.work2 = nullptr;
+        w.vt_cap = 0;
+        w.work2_cap = 0;
     }
     if (seqs > w.seq_cap || !w.seqs) {
         if (w.seqs) (void)hipFree(w.seqs);
@@ -573,6 +589,43 @@ void ensure_workspace(ge_ctx* c, int tokens, int seqs, int work) {
         w.work_cap = std::max(work, 1);
         w.work = ws_alloc<AttnWork>(w.work_cap, 1, "attention work");
     }
+    if (m.any_v2 && (work2 > w.work2_cap || !w.work2)) {
+        if (w.work2) (void)hipFree(w.work2);
+        w.work2_cap = std::max(work2, 1);
+        w.work2 = ws_alloc<AttnWork>(w.work2_cap, 1, "attention work");
+    }
+    // Zero-filled once: columns no token writes (alignment gaps, slack) stay finite, and keys
+    // read from them are masked, so they contribute exact zeros.
+    if (m.any_v2 && (vt_cols > w.vt_cap || !w.vt)) {
+        if (w.vt) (void)hipFree(w.vt);
+        w.vt_cap = std::max(vt_cols, w.vt_cap + w.vt_cap / 2);
+        w.vt = ws_alloc<uint16_t>(size_t(m.max_kvd), size_t(w.vt_cap), "transposed v");
+    }
+}
+
+// Transposed-V layout of a packed batch: each sequence's keys start at a column that is a
+// multiple of 8 (16-byte aligned copies); vt_cols leaves a key block of slack past the end.
+struct VtLayout {
+    std::vector<uint32_t> start;  // per sequence
+    std::vector<int32_t> vcol;    // per token
+    int cols = 0;
+};
+
+VtLayout vt_layout(int n_tokens, const ge_seq* seqs, int n_seqs) {
+    VtLayout v;
+    v.start.resize(size_t(n_seqs));
+    v.vcol.assign(size_t(n_tokens), -1);
+    uint32_t col = 0;
+    for (int s = 0; s < n_seqs; s++) {
+        v.start[size_t(s)] = col;
+        for (uint32_t i = 0; i < seqs[s].length; i++) v.vcol[seqs[s].start + i] = int32_t(col + i);
+        col += (seqs[s].length + 7) / 8 * 8;
+    }
+    v.cols = int(col) + 64;
+    // tokens outside every sequence write to the last slack column, which no key block reaches
+    for (auto& x : v.vcol)
+        if (x < 0) x = v.cols - 1;
+    return v;
 }
 
 // ---------------------------------------------------------------- batch staging
@@ -597,19 +650,43 @@ void stage(ge_ctx* c, const int32_t* tokens, const int32_t* positions, int n, co
         if (end > uint64_t(n)) fail(GE_ERR_INVALID, "sequence %d [%u, +%u) runs past the %d tokens", s, seqs[s].start, seqs[s].length, n);
         if (seqs[s].length > uint32_t(m.max_tokens)) fail(GE_ERR_INVALID, "sequence %d has %u tokens, more than %d", s, seqs[s].length, m.max_tokens);
         sr[s] = SeqRange{seqs[s].start, seqs[s].length};
-        for (uint32_t q0 = 0; q0 < seqs[s].length; q0 += kAttnQueries) work.push_back(AttnWork{seqs[s].start, seqs[s].length, q0});
+        for (uint32_t q0 = 0; q0 < seqs[s].length; q0 += kAttnQueries)
+            work.push_back(AttnWork{seqs[s].start, seqs[s].length, q0, 0});
     }
-    ensure_workspace(c, n, n_seqs, int(work.size()));
+    // Sequences may not share tokens: each token's key and value belong to one sequence.
+    {
+        std::vector<std::pair<uint32_t, uint32_t>> iv;
+        for (int s = 0; s < n_seqs; s++)
+            if (seqs[s].length) iv.push_back({seqs[s].start, seqs[s].start + seqs[s].length});
+        std::sort(iv.begin(), iv.end());
+        for (size_t i = 1; i < iv.size(); i++)
+            if (iv[i].first < iv[i - 1].second) fail(GE_ERR_INVALID, "sequences overlap at token %u", iv[i].first);
+    }
+    std::vector<AttnWork> work2;
+    VtLayout vl;
+    if (m.any_v2) {
+        vl = vt_layout(n, seqs, n_seqs);
+        for (int s = 0; s < n_seqs; s++)
+            for (uint32_t q0 = 0; q0 < seqs[s].length; q0 += kAttnQueriesV2)
+                work2.push_back(AttnWork{seqs[s].start, seqs[s].length, q0, vl.start[size_t(s)]});
+    }
+    ensure_workspace(c, n, n_seqs, int(work.size()), int(work2.size()), vl.cols);
     Workspace& w = c->ws;
     hip_check(hipMemcpyAsync(w.tokens, tokens, size_t(n) * 4, hipMemcpyHostToDevice, c->stream), "upload tokens");
     hip_check(hipMemcpyAsync(w.positions, positions, size_t(n) * 4, hipMemcpyHostToDevice, c->stream), "upload positions");
     hip_check(hipMemcpyAsync(w.seqs, sr.data(), sr.size() * sizeof(SeqRange), hipMemcpyHostToDevice, c->stream), "upload sequences");
     if (!work.empty())
         hip_check(hipMemcpyAsync(w.work, work.data(), work.size() * sizeof(AttnWork), hipMemcpyHostToDevice, c->stream), "upload work");
+    if (!work2.empty()) {
+        hip_check(hipMemcpyAsync(w.work2, work2.data(), work2.size() * sizeof(AttnWork), hipMemcpyHostToDevice, c->stream), "upload work");
+        hip_check(hipMemcpyAsync(w.vcol, vl.vcol.data(), size_t(n) * 4, hipMemcpyHostToDevice, c->stream), "upload columns");
+    }
     hip_check(hipStreamSynchronize(c->stream), "hipStreamSynchronize");
     c->staged_tokens = n;
     c->staged_seqs = n_seqs;
     c->staged_work = int(work.size());
+    c->staged_work2 = int(work2.size());
+    c->staged_vt_cols = vl.cols;
 }
 
 // ---------------------------------------------------------------- forward
@@ -645,9 +722,17 @@ void encode(ge_ctx* c, StopPoint* sp) {
         });
         if (at(sp, "Qcur_pos", l) || at(sp, "Kcur_pos", l) || at(sp, "Vcur_normed", l)) return;
         const int hw = L.sliding ? m.window / 2 : 0;  // halfWindow = slidingWindow / 2 (MetalForward.swift:399)
-        launch(c, "attention", [&] {
-            return launch_attention(s, w.q, w.k, w.v, w.attn, w.work, c->staged_work, m.heads, L.kv_heads, L.head_dim, hw, 1.0f);
-        });
+        if (L.attn_v2) {
+            launch(c, "v_transpose", [&] { return launch_v_transpose(s, w.v, T, L.kvd, w.vcol, w.vt_cap, w.vt); });
+            launch(c, "attention", [&] {
+                return launch_attention_v2(s, w.q, w.k, w.vt, w.vt_cap, w.attn, w.work2, c->staged_work2, m.heads, L.kv_heads,
+                                           L.head_dim, hw, 1.0f);
+            });
+        } else {
+            launch(c, "attention", [&] {
+                return launch_attention(s, w.q, w.k, w.v, w.attn, w.work, c->staged_work, m.heads, L.kv_heads, L.head_dim, hw, 1.0f);
+            });
+        }
         if (at(sp, "kqv_out", l)) return;
         launch(c, "gemm_o", [&] { return launch_gemm_q8(s, L.wo, w.attn, T, w.t, kEpiF32); });
         launch(c, "residual_norm", [&] {
@@ -1048,12 +1133,63 @@ int32_t ge_attention_queries(void) { return ge::kAttnQueries; }
 int ge_op_attention(ge_ctx* c, const void* q, const void* k, const void* v, void* out, const void* work, int32_t n_work,
                     int32_t heads, int32_t kv_heads, int32_t head_dim, int32_t half_window, float scale) {
     return guarded(c, [&] {
-        ge::launch(c, "attention", [&] {
-            return ge::launch_attention(c->stream, static_cast<const uint16_t*>(q), static_cast<const uint16_t*>(k),
-                                        static_cast<const uint16_t*>(v), static_cast<uint16_t*>(out),
-                                        static_cast<const ge::AttnWork*>(work), n_work, heads, kv_heads, head_dim,
-                                        half_window, scale);
-        });
+        if (n_work < 0 || (n_work > 0 && !work)) fail(GE_ERR_INVALID, "bad attention work list");
+        if (n_work == 0) return;
+        // The ABI's work items (ge_attention_work) come in; the kernels take ge::AttnWork.
+        std::vector<ge_attention_work> items(static_cast<size_t>(n_work), ge_attention_work{});
+        ge::hip_check(hipMemcpy(items.data(), work, items.size() * sizeof(ge_attention_work), hipMemcpyDeviceToHost), "read work");
+        std::vector<void*> temps;
+        struct Free {
+            std::vector<void*>* p;
+            ~Free() {
+                for (void* x : *p) (void)hipFree(x);
+            }
+        } guard{&temps};
+        auto temp = [&](size_t bytes) {
+            void* p = ge::dev_alloc(bytes, "attention op");
+            temps.push_back(p);
+            return p;
+        };
+        if (ge::attention_v2_supported(head_dim, heads, kv_heads)) {
+            // The sequences behind the work items, in order; V transposed into their layout.
+            std::vector<ge_seq> seqs;
+            int T = 0;
+            for (const auto& it : items) {
+                if (seqs.empty() || seqs.back().start != it.seq_start || seqs.back().length != it.seq_len)
+                    if (it.q0 == 0) seqs.push_back(ge_seq{it.seq_start, it.seq_len});
+                T = std::max(T, int(it.seq_start + it.seq_len));
+            }
+            const ge::VtLayout vl = ge::vt_layout(T, seqs.data(), int(seqs.size()));
+            std::vector<ge::AttnWork> w2;
+            for (size_t s = 0; s < seqs.size(); s++)
+                for (uint32_t q0 = 0; q0 < seqs[s].length; q0 += ge::kAttnQueriesV2)
+                    w2.push_back(ge::AttnWork{seqs[s].start, seqs[s].length, q0, vl.start[s]});
+            const int kvd = kv_heads * head_dim;
+            auto* vt = static_cast<uint16_t*>(temp(size_t(kvd) * vl.cols * 2));
+            auto* vcol = static_cast<int32_t*>(temp(size_t(T) * 4));
+            auto* dw = static_cast<ge::AttnWork*>(temp(w2.size() * sizeof(ge::AttnWork)));
+            ge::hip_check(hipMemsetAsync(vt, 0, size_t(kvd) * vl.cols * 2, c->stream), "hipMemset");
+            ge::hip_check(hipMemcpyAsync(vcol, vl.vcol.data(), size_t(T) * 4, hipMemcpyHostToDevice, c->stream), "upload");
+            ge::hip_check(hipMemcpyAsync(dw, w2.data(), w2.size() * sizeof(ge::AttnWork), hipMemcpyHostToDevice, c->stream), "upload");
+            ge::launch(c, "v_transpose", [&] {
+                return ge::launch_v_transpose(c->stream, static_cast<const uint16_t*>(v), T, kvd, vcol, vl.cols, vt);
+            });
+            ge::launch(c, "attention", [&] {
+                return ge::launch_attention_v2(c->stream, static_cast<const uint16_t*>(q), static_cast<const uint16_t*>(k), vt,
+                                               vl.cols, static_cast<uint16_t*>(out), dw, int(w2.size()), heads, kv_heads,
+                                               head_dim, half_window, scale);
+            });
+        } else {
+            std::vector<ge::AttnWork> w1;
+            for (const auto& it : items) w1.push_back(ge::AttnWork{it.seq_start, it.seq_len, it.q0, 0});
+            auto* dw = static_cast<ge::AttnWork*>(temp(w1.size() * sizeof(ge::AttnWork)));
+            ge::hip_check(hipMemcpyAsync(dw, w1.data(), w1.size() * sizeof(ge::AttnWork), hipMemcpyHostToDevice, c->stream), "upload");
+            ge::launch(c, "attention", [&] {
+                return ge::launch_attention(c->stream, static_cast<const uint16_t*>(q), static_cast<const uint16_t*>(k),
+                                            static_cast<const uint16_t*>(v), static_cast<uint16_t*>(out), dw, n_work, heads,
+                                            kv_heads, head_dim, half_window, scale);
+            });
+        }
         ge::hip_check(hipStreamSynchronize(c->stream), "hipStreamSynchronize");
     });
 }

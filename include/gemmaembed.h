@@ -166,8 +166,9 @@ int32_t ge_attention_queries(void);
 
 /* Kernels.attention (Metal/MetalForward.swift:669-694; Shaders/Attention.metal:25-170): q fp16
  * [T][heads][hd], k and v fp16 [T][kv_heads][hd], out fp16 [T][heads][hd]; `work` is a device
- * array of n_work items; half_window 0 = no window; scale multiplies the scores. Buffers must
- * hold ge_attention_queries() rows of slack past the last token. */
+ * array of n_work items covering each sequence's queries from q0 = 0 in steps of
+ * ge_attention_queries(); half_window 0 = no window; scale multiplies the scores. q, k and v
+ * must hold 64 rows of slack past the last token (key blocks are read whole). */
 int ge_op_attention(ge_ctx* ctx, const void* q, const void* k, const void* v, void* out, const void* work,
                     int32_t n_work, int32_t heads, int32_t kv_heads, int32_t head_dim, int32_t half_window,
                     float scale);
