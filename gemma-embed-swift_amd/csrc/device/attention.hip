@@ -299,13 +299,15 @@ __global__ __launch_bounds__(2 * G * 64) void attention_v2_kernel(const uint16_t
     extern __shared__ __attribute__((aligned(1024))) unsigned char ldsb[];
     unsigned char* const kv = ldsb + NW * Q_BYTES;
 
-    const AttnWork wi = work[blockIdx.x];
+    // XCD-aware order: workgroup b runs on XCD b % 8, so giving each XCD a contiguous run of work
+    // items keeps a sequence's K and V^T in one XCD's L2.
+    const int nb = int(gridDim.x), full = nb / 8 * 8, bx = int(blockIdx.x);
+    const AttnWork wi = work[bx < full ? (bx % 8) * (full / 8) + bx / 8 : bx];
     const int kvh = blockIdx.y;
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int h = kvh * G + wave % G;
     const int len = int(wi.seq_len), q0 = int(wi.q0) + (wave / G) * 32;
     const int qi = q0 + (lane & 31), half = lane >> 5;
-    const bool active = q0 < len;  // wave-uniform: the wave has at least one query row
     const int qStride = H * HD, kvStride = KV * HD;
 
     int kstart = 0, kend = len;
@@ -328,18 +330,28 @@ __global__ __launch_bounds__(2 * G * 64) void attention_v2_kernel(const uint16_t
         lds_copy16(src, qs + c * 1024);
     }
 
+    // This wave's copies of a key block: chunks wave, wave + NW, ... (at most CPW). The lane part
+    // of each source address is fixed; a block only moves the wave-uniform base.
+    constexpr int CPW = (CH + NW - 1) / NW;
+    uint32_t coff[CPW];
+#pragma unroll
+    for (int i = 0; i < CPW; i++) {
+        const int c = wave + i * NW;
+        if (c < KCH) {
+            const int key = c * (64 / LPR) + lane / LPR, sl = lane % LPR;
+            coff[i] = uint32_t((key * kvStride + ((sl ^ (key & 15)) * 8)) * 2);
+        } else {
+            const int d = (c - KCH) * (64 / VSL) + lane / VSL, sl = lane % VSL;
+            coff[i] = uint32_t((d * vt_cols + ((sl ^ ((d >> 2) & 3)) * 8)) * 2);
+        }
+    }
 #define A2_ISSUE(kb, b)                                                                                    \
     do {                                                                                                   \
-        for (int c = wave; c < CH; c += NW) {                                                              \
-            const uint16_t* src;                                                                           \
-            if (c < KCH) {                                                                                 \
-                const int key = c * (64 / LPR) + lane / LPR, sl = lane % LPR;                              \
-                src = kbase + (size_t)((kb) + key) * kvStride + ((sl ^ (key & 15)) * 8);                   \
-            } else {                                                                                       \
-                const int d = (c - KCH) * (64 / VSL) + lane / VSL, sl = lane % VSL;                        \
-                src = vtbase + (size_t)d * vt_cols + (kb) + ((sl ^ ((d >> 2) & 3)) * 8);                   \
-            }                                                                                              \
-            lds_copy16(src, kv + (b) * STAGE + c * 1024);                                                  \
+        const unsigned char* kb_ = reinterpret_cast<const unsigned char*>(kbase + (size_t)(kb) * kvStride); \
+        const unsigned char* vb_ = reinterpret_cast<const unsigned char*>(vtbase + (kb));                   \
+        _Pragma("unroll") for (int i = 0; i < CPW; i++) {                                                  \
+            const int c = wave + i * NW;                                                                   \
+            if (c < CH) lds_copy16((c < KCH ? kb_ : vb_) + coff[i], kv + (b) * STAGE + c * 1024);          \
         }                                                                                                  \
     } while (0)
 
@@ -361,21 +373,28 @@ __global__ __launch_bounds__(2 * G * 64) void attention_v2_kernel(const uint16_t
     for (int it = 0; it < nblocks; it++) {
         const int kb = kstart + it * BKV, b = it & 1;
         if (it + 1 < nblocks) A2_ISSUE(kb + BKV, b ^ 1);
-        if (active) {
+        // Every wave computes, also one whose query rows all lie past the sequence (they read
+        // the clamped last row; nothing of theirs is stored): no branch around the block.
+        {
             const unsigned char* Ks = kv + b * STAGE;
             const unsigned char* Vs = Ks + K_BYTES;
-            float16_t sc;
+            // two accumulation chains over the k-steps halve the MFMA dependency latency
+            float16_t sc, sc1;
 #pragma unroll
-            for (int r = 0; r < 16; r++) sc[r] = 0.0f;
+            for (int r = 0; r < 16; r++) sc[r] = sc1[r] = 0.0f;
             const unsigned char* kp = Ks + krow * (HD * 2);
             const unsigned char* qp = qs + qrow * (HD * 2);
 #pragma unroll
-            for (int ks = 0; ks < KSQ; ks++) {
+            for (int ks = 0; ks < KSQ; ks += 2) {
                 const int slot = 2 * ks + half;
-                const half8_t a = *reinterpret_cast<const half8_t*>(kp + ((slot ^ (krow & 15)) * 16));
-                const half8_t bq = *reinterpret_cast<const half8_t*>(qp + ((slot ^ (qrow & 15)) * 16));
-                sc = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, bq, sc, 0, 0, 0);
+                const half8_t a0 = *reinterpret_cast<const half8_t*>(kp + ((slot ^ (krow & 15)) * 16));
+                const half8_t b0 = *reinterpret_cast<const half8_t*>(qp + ((slot ^ (qrow & 15)) * 16));
+                const half8_t a1 = *reinterpret_cast<const half8_t*>(kp + (((slot + 2) ^ (krow & 15)) * 16));
+                const half8_t b1 = *reinterpret_cast<const half8_t*>(qp + (((slot + 2) ^ (qrow & 15)) * 16));
+                sc = __builtin_amdgcn_mfma_f32_32x32x16_f16(a0, b0, sc, 0, 0, 0);
+                sc1 = __builtin_amdgcn_mfma_f32_32x32x16_f16(a1, b1, sc1, 0, 0, 0);
             }
+            sc += sc1;
             // key of accumulator element r for this lane: kb + 16 (r / 8) + 8 half + r % 8
             const bool inside = kb + BKV <= len && (hw == 0 || (kb >= q0 + 31 - hw && kb + BKV - 1 <= q0 + hw));
             float bmax = -INFINITY;
@@ -397,29 +416,32 @@ __global__ __launch_bounds__(2 * G * 64) void attention_v2_kernel(const uint16_t
                 }
             }
             bmax = fmaxf(bmax, __shfl_xor(bmax, 32, 64));
-            const float m_new = fmaxf(m_run, bmax);
-            float alpha = 1.0f, sum = 0.0f;
-            if (m_new == -INFINITY) {
-#pragma unroll
-                for (int r = 0; r < 16; r++) sc[r] = 0.0f;
-            } else {
-                alpha = __builtin_amdgcn_exp2f(m_run - m_new);
-#pragma unroll
-                for (int r = 0; r < 16; r++) {
-                    const float p = __builtin_amdgcn_exp2f(sc[r] - m_new);
-                    sc[r] = p;
-                    sum += p;
-                }
-            }
-            sum += __shfl_xor(sum, 32, 64);
-            l_run = l_run * alpha + sum;
-            m_run = m_new;
-            if (alpha != 1.0f) {
+            // Lazy rescaling: the reference point m_run moves only when a score exceeds it by more
+            // than 2^8 (log2 domain), so P stays below 256 -- exact in fp16 to the same relative
+            // precision -- and the o *= alpha pass runs only on the rare blocks that move it.
+            // o / l is unchanged by the choice of reference point.
+            if (__builtin_amdgcn_ballot_w64(bmax > m_run + 8.0f)) {
+                const float m_new = fmaxf(m_run, bmax);
+                const float alpha = m_new == -INFINITY ? 1.0f : __builtin_amdgcn_exp2f(m_run - m_new);
+                l_run *= alpha;
 #pragma unroll
                 for (int i = 0; i < DT; i++)
 #pragma unroll
                     for (int r = 0; r < 16; r++) o[i][r] *= alpha;
+                m_run = m_new;
             }
+            // m_run is -inf only while every key seen so far is masked (all scores -inf): the
+            // reference point 0 then gives p = 0.
+            const float m_ref = m_run == -INFINITY ? 0.0f : m_run;
+            float sum = 0.0f;
+#pragma unroll
+            for (int r = 0; r < 16; r++) {
+                const float p = __builtin_amdgcn_exp2f(sc[r] - m_ref);
+                sc[r] = p;
+                sum += p;
+            }
+            sum += __shfl_xor(sum, 32, 64);
+            l_run += sum;
 #pragma unroll
             for (int ks = 0; ks < BKV / 16; ks++) {
                 half8_t pb;
@@ -439,7 +461,7 @@ __global__ __launch_bounds__(2 * G * 64) void attention_v2_kernel(const uint16_t
         workgroup_barrier();
     }
 #undef A2_ISSUE
-    if (!active || qi >= len) return;
+    if (qi >= len) return;
     const float inv = l_run > 0.0f ? 1.0f / l_run : 0.0f;
     _Float16* op = reinterpret_cast<_Float16*>(Og) + (size_t)(wi.seq_start + qi) * qStride + h * HD + half * 4;
 #pragma unroll
