@@ -214,6 +214,150 @@ hipError_t launch_qk_norm_rope(hipStream_t s, const float* qkv, int T, int H, in
     return hipGetLastError();
 }
 
+// ============================================================================ QK norm + RoPE, V transposed
+//
+// The same arithmetic as qk_norm_rope_kernel, reorganised for bandwidth and fused with the V
+// transpose the LDS-copy attention reads. A workgroup of 16 waves takes 64 consecutive tokens,
+// 4 per wave; per token a wave loads all S = H + 2 KV head slots before reducing any of them,
+// and the S sums of squares go through the butterfly together. Each lane owns
+// C = hd / 128 elements of the first half of every head and their NeoX partners. Normalised V
+// rows are written row-major and also staged in LDS as [KV * hd][64 tokens], then written to
+// V^T one d row (64 tokens, 128 contiguous bytes within a sequence) per wave instruction.
+template <int HD, int S>
+__global__ __launch_bounds__(1024) void qkv_norm_rope_vt_kernel(const float* __restrict__ qkv, int T, int H, int KV,
+                                                               const float* __restrict__ q_norm,
+                                                               const float* __restrict__ k_norm, float eps,
+                                                               const int32_t* __restrict__ positions,
+                                                               const float* __restrict__ table,
+                                                               uint16_t* __restrict__ q, uint16_t* __restrict__ k,
+                                                               uint16_t* __restrict__ v, const int32_t* __restrict__ vcol,
+                                                               int vt_cols, uint16_t* __restrict__ vt) {
+    constexpr int C = HD / 128, HALF = HD / 2, TS = 66;  // tile row stride in halves
+    extern __shared__ __attribute__((aligned(16))) uint16_t vtile[];
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int t0 = blockIdx.x * 64;
+    float wq[2 * C], wk[2 * C];
+#pragma unroll
+    for (int j = 0; j < C; j++) {
+        wq[j] = q_norm[lane * C + j];
+        wq[C + j] = q_norm[HALF + lane * C + j];
+        wk[j] = k_norm[lane * C + j];
+        wk[C + j] = k_norm[HALF + lane * C + j];
+    }
+    for (int i = 0; i < 4; i++) {
+        const int tok = wave * 4 + i, t = t0 + tok;
+        if (t >= T) break;
+        const float* row = qkv + (size_t)t * S * HD + lane * C;
+        float lo[S][C], hi[S][C], ss[S];
+#pragma unroll
+        for (int sl = 0; sl < S; sl++)
+#pragma unroll
+            for (int j = 0; j < C; j++) {
+                lo[sl][j] = row[sl * HD + j];
+                hi[sl][j] = row[sl * HD + HALF + j];
+            }
+        const float* cs = table + (size_t)positions[t] * HALF * 2 + lane * C * 2;
+        float cr[2 * C];
+#pragma unroll
+        for (int j = 0; j < 2 * C; j++) cr[j] = cs[j];
+#pragma unroll
+        for (int sl = 0; sl < S; sl++) {
+            ss[sl] = 0.0f;
+#pragma unroll
+            for (int j = 0; j < C; j++) ss[sl] += lo[sl][j] * lo[sl][j] + hi[sl][j] * hi[sl][j];
+        }
+#pragma unroll
+        for (int m = 32; m >= 1; m >>= 1)
+#pragma unroll
+            for (int sl = 0; sl < S; sl++) ss[sl] += __shfl_xor(ss[sl], m, 64);
+#pragma unroll
+        for (int sl = 0; sl < S; sl++) {
+            const float inv = 1.0f / sqrtf(ss[sl] / float(HD) + eps);
+            const bool isq = sl < H, isk = !isq && sl < H + KV;
+            uint16_t* dst = isq ? q + ((size_t)t * H + sl) * HD
+                                : (isk ? k + ((size_t)t * KV + (sl - H)) * HD : v + ((size_t)t * KV + (sl - H - KV)) * HD);
+            uint16_t olo[C], ohi[C];
+#pragma unroll
+            for (int j = 0; j < C; j++) {
+                float a = lo[sl][j] * inv, b = hi[sl][j] * inv;
+                if (isq || isk) {
+                    // a blend rather than a select between the two register arrays, which the
+                    // compiler would turn into a select of their addresses (scratch memory)
+                    const float fq = isq ? 1.0f : 0.0f, fk = 1.0f - fq;
+                    a *= wq[j] * fq + wk[j] * fk;
+                    b *= wq[C + j] * fq + wk[C + j] * fk;
+                    const float c = cr[2 * j], sn = cr[2 * j + 1];
+                    const float ra = a * c - b * sn, rb = a * sn + b * c;
+                    a = ra;
+                    b = rb;
+                }
+                olo[j] = f2h(a);
+                ohi[j] = f2h(b);
+            }
+#pragma unroll
+            for (int j = 0; j < C; j++) {
+                dst[lane * C + j] = olo[j];
+                dst[HALF + lane * C + j] = ohi[j];
+            }
+            if (!isq && !isk && vt) {
+                const int r0 = (sl - H - KV) * HD;
+#pragma unroll
+                for (int j = 0; j < C; j++) {
+                    vtile[(r0 + lane * C + j) * TS + tok] = olo[j];
+                    vtile[(r0 + HALF + lane * C + j) * TS + tok] = ohi[j];
+                }
+            }
+        }
+    }
+    if (!vt) return;
+    __syncthreads();
+    if (t0 + lane >= T) return;
+    const int col = vcol[t0 + lane];
+    for (int r = wave; r < KV * HD; r += 16) vt[(size_t)r * vt_cols + col] = vtile[r * TS + lane];
+}
+
+template <int HD, int S>
+static hipError_t qkv_norm_rope_vt_launch(hipStream_t s, const float* qkv, int T, int H, int KV, const float* q_norm,
+                                          const float* k_norm, float eps, const int32_t* positions, const float* rope_table,
+                                          uint16_t* q, uint16_t* k, uint16_t* v, const int32_t* vcol, int vt_cols,
+                                          uint16_t* vt) {
+    const uint32_t lds = vt ? uint32_t(KV * HD * 66 * 2) : 0u;
+    launch_kernel(qkv_norm_rope_vt_kernel<HD, S>, dim3((T + 63) / 64), dim3(1024), lds, s, qkv, T, H, KV, q_norm, k_norm, eps,
+                  positions, rope_table, q, k, v, vcol, vt_cols, vt);
+    return hipGetLastError();
+}
+
+template <int HD>
+static hipError_t qkv_norm_rope_vt_dispatch(hipStream_t s, const float* qkv, int T, int H, int KV, const float* q_norm,
+                                            const float* k_norm, float eps, const int32_t* positions,
+                                            const float* rope_table, uint16_t* q, uint16_t* k, uint16_t* v,
+                                            const int32_t* vcol, int vt_cols, uint16_t* vt) {
+#define QNR_CASE(SL) \
+    case SL: return qkv_norm_rope_vt_launch<HD, SL>(s, qkv, T, H, KV, q_norm, k_norm, eps, positions, rope_table, q, k, v, vcol, vt_cols, vt);
+    switch (H + 2 * KV) {
+        QNR_CASE(3) QNR_CASE(4) QNR_CASE(5) QNR_CASE(6) QNR_CASE(8) QNR_CASE(10)
+    default: return hipErrorInvalidValue;
+    }
+#undef QNR_CASE
+}
+
+bool qkv_norm_rope_vt_supported(int hd, int H, int KV) {
+    const int sl = H + 2 * KV;
+    return (hd == 128 || hd == 256) && (sl == 3 || sl == 4 || sl == 5 || sl == 6 || sl == 8 || sl == 10) &&
+           KV * hd * 66 * 2 <= 64 * 1024;
+}
+
+hipError_t launch_qkv_norm_rope_vt(hipStream_t s, const float* qkv, int T, int H, int KV, int hd, const float* q_norm,
+                                   const float* k_norm, float eps, const int32_t* positions, const float* rope_table,
+                                   uint16_t* q, uint16_t* k, uint16_t* v, const int32_t* vcol, int vt_cols, uint16_t* vt) {
+    if (T < 0 || H <= 0 || KV <= 0 || !qkv_norm_rope_vt_supported(hd, H, KV) || (vt && (!vcol || vt_cols <= 0)))
+        return hipErrorInvalidValue;
+    if (T == 0) return hipSuccess;
+    if (hd == 128)
+        return qkv_norm_rope_vt_dispatch<128>(s, qkv, T, H, KV, q_norm, k_norm, eps, positions, rope_table, q, k, v, vcol, vt_cols, vt);
+    return qkv_norm_rope_vt_dispatch<256>(s, qkv, T, H, KV, q_norm, k_norm, eps, positions, rope_table, q, k, v, vcol, vt_cols, vt);
+}
+
 // ============================================================================ mean pool
 //
 // pooled[s] = mean over the sequence's rows (reference Shaders/Elementwise.metal:243-256;

@@ -67,6 +67,14 @@ hipError_t launch_qk_norm_rope(hipStream_t s, const float* qkv, int T, int H, in
                                const float* k_norm, float eps, const int32_t* positions, const float* rope_table,
                                uint16_t* q, uint16_t* k, uint16_t* v);
 
+// The same as launch_qk_norm_rope (head dims 128 and 256, H + 2 KV in {3, 4, 5, 6, 8, 10}), and
+// when vt is set also writes normalised V transposed: vt [KV * hd][vt_cols], token t at column
+// vcol[t].
+bool qkv_norm_rope_vt_supported(int hd, int H, int KV);
+hipError_t launch_qkv_norm_rope_vt(hipStream_t s, const float* qkv, int T, int H, int KV, int hd, const float* q_norm,
+                                   const float* k_norm, float eps, const int32_t* positions, const float* rope_table,
+                                   uint16_t* q, uint16_t* k, uint16_t* v, const int32_t* vcol, int vt_cols, uint16_t* vt);
+
 // Flash-style bidirectional attention over packed sequences.
 hipError_t launch_attention(hipStream_t s, const uint16_t* q, const uint16_t* k, const uint16_t* v, uint16_t* o,
                             const AttnWork* work, int n_work, int H, int KV, int hd, int half_window, float scale);

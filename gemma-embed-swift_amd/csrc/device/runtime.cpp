@@ -716,14 +716,20 @@ void encode(ge_ctx* c, StopPoint* sp) {
         const DevLayer& L = m.layer[size_t(l)];
         launch(c, "gemm_qkv", [&] { return launch_gemm_q8(s, L.wqkv, w.h, T, w.qkv, kEpiF32); });
         if (at(sp, "Qcur", l) || at(sp, "Kcur", l) || at(sp, "Vcur", l)) return;
+        // The fused kernel also writes V^T for the LDS-copy attention.
+        const bool fused_vt = qkv_norm_rope_vt_supported(L.head_dim, m.heads, L.kv_heads);
         launch(c, "qk_norm_rope", [&] {
+            if (fused_vt)
+                return launch_qkv_norm_rope_vt(s, w.qkv, T, m.heads, L.kv_heads, L.head_dim, L.q_norm, L.k_norm, m.eps,
+                                               w.positions, L.rope, w.q, w.k, w.v, w.vcol, w.vt_cap,
+                                               L.attn_v2 ? w.vt : nullptr);
             return launch_qk_norm_rope(s, w.qkv, T, m.heads, L.kv_heads, L.head_dim, L.q_norm, L.k_norm, m.eps, w.positions,
                                        L.rope, w.q, w.k, w.v);
         });
         if (at(sp, "Qcur_pos", l) || at(sp, "Kcur_pos", l) || at(sp, "Vcur_normed", l)) return;
         const int hw = L.sliding ? m.window / 2 : 0;  // halfWindow = slidingWindow / 2 (MetalForward.swift:399)
         if (L.attn_v2) {
-            launch(c, "v_transpose", [&] { return launch_v_transpose(s, w.v, T, L.kvd, w.vcol, w.vt_cap, w.vt); });
+            if (!fused_vt) launch(c, "v_transpose", [&] { return launch_v_transpose(s, w.v, T, L.kvd, w.vcol, w.vt_cap, w.vt); });
             launch(c, "attention", [&] {
                 return launch_attention_v2(s, w.q, w.k, w.vt, w.vt_cap, w.attn, w.work2, c->staged_work2, m.heads, L.kv_heads,
                                            L.head_dim, hw, 1.0f);
