@@ -42,9 +42,14 @@ __device__ __forceinline__ float wave_sum(float v) {
 }
 
 __device__ __forceinline__ float gelu_tanh(float x) {
-    // ggml's gelu_tanh constants (reference Shaders/Common.metal:18-21, Model/Architecture.md:45).
+    // 0.5 x (1 + tanh(u)), u = sqrt(2 / pi) (x + 0.044715 x^3) (ggml's gelu_tanh, reference
+    // Shaders/Common.metal:18-21, Model/Architecture.md:45), evaluated through the identity
+    // 0.5 (1 + tanh(u)) = 1 / (1 + e^(-2u)): one v_exp_f32 and one v_rcp_f32 instead of tanhf.
+    // e^(-2u) = 2^(-2u log2 e); it overflows to +inf for very negative x, giving x * 0.
     const float c = 0.79788456080286535587989211986876f;
-    return 0.5f * x * (1.0f + tanhf(c * x * (1.0f + 0.044715f * x * x)));
+    const float u = c * x * (1.0f + 0.044715f * x * x);
+    const float e = __builtin_amdgcn_exp2f(-2.0f * 1.4426950408889634f * u);
+    return x * __builtin_amdgcn_rcpf(1.0f + e);
 }
 
 __device__ __forceinline__ float h2f(uint16_t b) { return float(__builtin_bit_cast(_Float16, b)); }
