@@ -71,26 +71,30 @@ hipError_t launch_embed_norm(hipStream_t s, const Q8Dev& table, const int32_t* t
 // post-attention / post-FFN norm, the residual add and the next block's pre-norm in one pass
 // (reference Shaders/Elementwise.metal:260-354; Model/CPUReference.swift:240-245, :254-257, :269).
 template <int CH>
-__global__ __launch_bounds__(256) void residual_norm_kernel(float* __restrict__ x, const float* __restrict__ t,
-                                                            const float* __restrict__ w, float out_scale,
+__global__ __launch_bounds__(256) void residual_norm_kernel(float* __restrict__ x, const uint16_t* __restrict__ t16,
+                                                            float t_eps, const float* __restrict__ w, float out_scale,
                                                             const float* __restrict__ next_w, float eps, int T, int d,
                                                             uint16_t* __restrict__ h) {
     const int row = blockIdx.x * 4 + (threadIdx.x >> 6), lane = threadIdx.x & 63;
     if (row >= T) return;
+    // t arrives as fp16 t * c (c a power of two) with t_eps = eps * c^2: the RMSNorm of the
+    // stored values with t_eps is the RMSNorm of t.
     float tv[CH][4], xv[CH][4];
     float ss = 0.0f;
 #pragma unroll
     for (int c = 0; c < CH; c++) {
         const int e = c * 256 + lane * 4;
         if (e < d) {
-            const float4 a = *reinterpret_cast<const float4*>(t + (size_t)row * d + e);
-            tv[c][0] = a.x; tv[c][1] = a.y; tv[c][2] = a.z; tv[c][3] = a.w;
+            const half4_t a = *reinterpret_cast<const half4_t*>(t16 + (size_t)row * d + e);
 #pragma unroll
-            for (int j = 0; j < 4; j++) ss += tv[c][j] * tv[c][j];
+            for (int j = 0; j < 4; j++) {
+                tv[c][j] = float(a[j]);
+                ss += tv[c][j] * tv[c][j];
+            }
         }
     }
     ss = wave_sum(ss);
-    const float inv = 1.0f / sqrtf(ss / float(d) + eps);
+    const float inv = 1.0f / sqrtf(ss / float(d) + t_eps);
     float ss2 = 0.0f;
 #pragma unroll
     for (int c = 0; c < CH; c++) {
@@ -122,16 +126,16 @@ __global__ __launch_bounds__(256) void residual_norm_kernel(float* __restrict__ 
     }
 }
 
-hipError_t launch_residual_norm(hipStream_t s, float* x, const float* t, const float* w, float out_scale,
-                                const float* next_w, float eps, int T, int d, uint16_t* h) {
-    if (T < 0 || d <= 0 || d % 4 != 0 || d > 1024 || (next_w && !h)) return hipErrorInvalidValue;
+hipError_t launch_residual_norm(hipStream_t s, float* x, const uint16_t* t16, float t_eps, const float* w,
+                                float out_scale, const float* next_w, float eps, int T, int d, uint16_t* h) {
+    if (T < 0 || d <= 0 || d % 4 != 0 || d > 1024 || (next_w && !h) || !t16) return hipErrorInvalidValue;
     if (T == 0) return hipSuccess;
     const int blocks = (T + 3) / 4, CH = (d + 255) / 256;
     switch (CH) {
-    case 1: launch_kernel(residual_norm_kernel<1>, blocks, 256, 0, s, x, t, w, out_scale, next_w, eps, T, d, h); break;
-    case 2: launch_kernel(residual_norm_kernel<2>, blocks, 256, 0, s, x, t, w, out_scale, next_w, eps, T, d, h); break;
-    case 3: launch_kernel(residual_norm_kernel<3>, blocks, 256, 0, s, x, t, w, out_scale, next_w, eps, T, d, h); break;
-    default: launch_kernel(residual_norm_kernel<4>, blocks, 256, 0, s, x, t, w, out_scale, next_w, eps, T, d, h); break;
+    case 1: launch_kernel(residual_norm_kernel<1>, blocks, 256, 0, s, x, t16, t_eps, w, out_scale, next_w, eps, T, d, h); break;
+    case 2: launch_kernel(residual_norm_kernel<2>, blocks, 256, 0, s, x, t16, t_eps, w, out_scale, next_w, eps, T, d, h); break;
+    case 3: launch_kernel(residual_norm_kernel<3>, blocks, 256, 0, s, x, t16, t_eps, w, out_scale, next_w, eps, T, d, h); break;
+    default: launch_kernel(residual_norm_kernel<4>, blocks, 256, 0, s, x, t16, t_eps, w, out_scale, next_w, eps, T, d, h); break;
     }
     return hipGetLastError();
 }
@@ -216,15 +220,16 @@ hipError_t launch_qk_norm_rope(hipStream_t s, const float* qkv, int T, int H, in
 
 // ============================================================================ QK norm + RoPE, V transposed
 //
-// The same arithmetic as qk_norm_rope_kernel, reorganised for bandwidth and fused with the V
-// transpose the LDS-copy attention reads. A workgroup of 16 waves takes 64 consecutive tokens,
-// 4 per wave; per token a wave loads all S = H + 2 KV head slots before reducing any of them,
-// and the S sums of squares go through the butterfly together. Each lane owns
-// C = hd / 128 elements of the first half of every head and their NeoX partners. Normalised V
+// The arithmetic of qk_norm_rope_kernel on the QKV projection stored as scaled fp16 (see
+// launch_qkv_norm_rope_vt), fused with the V transpose the LDS-copy attention reads. A workgroup
+// of 16 waves takes 64 consecutive tokens, 4 per wave; per token a wave loads all S = H + 2 KV
+// head slots before reducing any of them, and the S sums of squares go through the butterfly
+// together. Each lane owns C = hd / 128 elements of the first half of every head and their NeoX
+// partners. Normalised V
 // rows are written row-major and also staged in LDS as [KV * hd][64 tokens], then written to
 // V^T one d row (64 tokens, 128 contiguous bytes within a sequence) per wave instruction.
 template <int HD, int S>
-__global__ __launch_bounds__(1024) void qkv_norm_rope_vt_kernel(const float* __restrict__ qkv, int T, int H, int KV,
+__global__ __launch_bounds__(1024) void qkv_norm_rope_vt_kernel(const uint16_t* __restrict__ qkv16, int T, int H, int KV,
                                                                const float* __restrict__ q_norm,
                                                                const float* __restrict__ k_norm, float eps,
                                                                const int32_t* __restrict__ positions,
@@ -247,14 +252,15 @@ __global__ __launch_bounds__(1024) void qkv_norm_rope_vt_kernel(const float* __r
     for (int i = 0; i < 4; i++) {
         const int tok = wave * 4 + i, t = t0 + tok;
         if (t >= T) break;
-        const float* row = qkv + (size_t)t * S * HD + lane * C;
+        // The projection arrives as fp16 qkv * c (c a power of two, eps already scaled by c^2).
+        const uint16_t* row = qkv16 + (size_t)t * S * HD + lane * C;
         float lo[S][C], hi[S][C], ss[S];
 #pragma unroll
         for (int sl = 0; sl < S; sl++)
 #pragma unroll
             for (int j = 0; j < C; j++) {
-                lo[sl][j] = row[sl * HD + j];
-                hi[sl][j] = row[sl * HD + HALF + j];
+                lo[sl][j] = h2f(row[sl * HD + j]);
+                hi[sl][j] = h2f(row[sl * HD + HALF + j]);
             }
         const float* cs = table + (size_t)positions[t] * HALF * 2 + lane * C * 2;
         float cr[2 * C];
@@ -317,7 +323,7 @@ __global__ __launch_bounds__(1024) void qkv_norm_rope_vt_kernel(const float* __r
 }
 
 template <int HD, int S>
-static hipError_t qkv_norm_rope_vt_launch(hipStream_t s, const float* qkv, int T, int H, int KV, const float* q_norm,
+static hipError_t qkv_norm_rope_vt_launch(hipStream_t s, const uint16_t* qkv, int T, int H, int KV, const float* q_norm,
                                           const float* k_norm, float eps, const int32_t* positions, const float* rope_table,
                                           uint16_t* q, uint16_t* k, uint16_t* v, const int32_t* vcol, int vt_cols,
                                           uint16_t* vt) {
@@ -328,7 +334,7 @@ static hipError_t qkv_norm_rope_vt_launch(hipStream_t s, const float* qkv, int T
 }
 
 template <int HD>
-static hipError_t qkv_norm_rope_vt_dispatch(hipStream_t s, const float* qkv, int T, int H, int KV, const float* q_norm,
+static hipError_t qkv_norm_rope_vt_dispatch(hipStream_t s, const uint16_t* qkv, int T, int H, int KV, const float* q_norm,
                                             const float* k_norm, float eps, const int32_t* positions,
                                             const float* rope_table, uint16_t* q, uint16_t* k, uint16_t* v,
                                             const int32_t* vcol, int vt_cols, uint16_t* vt) {
@@ -347,9 +353,10 @@ bool qkv_norm_rope_vt_supported(int hd, int H, int KV) {
            KV * hd * 66 * 2 <= 64 * 1024;
 }
 
-hipError_t launch_qkv_norm_rope_vt(hipStream_t s, const float* qkv, int T, int H, int KV, int hd, const float* q_norm,
-                                   const float* k_norm, float eps, const int32_t* positions, const float* rope_table,
-                                   uint16_t* q, uint16_t* k, uint16_t* v, const int32_t* vcol, int vt_cols, uint16_t* vt) {
+hipError_t launch_qkv_norm_rope_vt(hipStream_t s, const uint16_t* qkv, int T, int H, int KV, int hd,
+                                   const float* q_norm, const float* k_norm, float eps, const int32_t* positions,
+                                   const float* rope_table, uint16_t* q, uint16_t* k, uint16_t* v, const int32_t* vcol,
+                                   int vt_cols, uint16_t* vt) {
     if (T < 0 || H <= 0 || KV <= 0 || !qkv_norm_rope_vt_supported(hd, H, KV) || (vt && (!vcol || vt_cols <= 0)))
         return hipErrorInvalidValue;
     if (T == 0) return hipSuccess;

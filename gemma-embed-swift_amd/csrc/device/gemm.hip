@@ -226,33 +226,36 @@ template <int BM, int BN, int WM, int WN, int BK, int ST>
 hipError_t gemm_d_launch(hipStream_t s, const Q8Dev& w, const uint16_t* x, int M, void* y, GemmEpilogue epi,
                          float out_scale) {
     const int N = w.rows, K = w.cols;
+    constexpr int FN = BN / WN / 32;
     if (K % BK != 0 || N % 32 != 0 || !w.fh) return hipErrorInvalidValue;
     const int tiles_m = (M + BM - 1) / BM, tiles_n = (N + BN - 1) / BN, tiles = tiles_m * tiles_n;
     const dim3 grid(tiles), block(WM * WN * 64);
     constexpr uint32_t lds = gemm_d_lds_bytes<BM, BN, WM, WN, BK, ST>();
+#define GD_LAUNCH(E) launch_kernel(gemm_d_kernel<BM, BN, WM, WN, BK, ST, E>, grid, block, lds, s, x, w.fh, y, M, N, K, out_scale, tiles_n, tiles)
     if (lds > 65536) {
         hipError_t e = hipSuccess;
         switch (epi) {
         case kEpiF32: e = set_lds_limit(gemm_d_kernel<BM, BN, WM, WN, BK, ST, kEpiF32>, lds); break;
         case kEpiF16: e = set_lds_limit(gemm_d_kernel<BM, BN, WM, WN, BK, ST, kEpiF16>, lds); break;
         case kEpiGeglu:
-            if constexpr ((BN / WN / 32) % 2 == 0) e = set_lds_limit(gemm_d_kernel<BM, BN, WM, WN, BK, ST, kEpiGeglu>, lds);
+            if constexpr (FN % 2 == 0) e = set_lds_limit(gemm_d_kernel<BM, BN, WM, WN, BK, ST, kEpiGeglu>, lds);
             break;
         default: break;
         }
         if (e != hipSuccess) return e;
     }
     switch (epi) {
-    case kEpiF32: launch_kernel(gemm_d_kernel<BM, BN, WM, WN, BK, ST, kEpiF32>, grid, block, lds, s, x, w.fh, y, M, N, K, out_scale, tiles_n, tiles); break;
-    case kEpiF16: launch_kernel(gemm_d_kernel<BM, BN, WM, WN, BK, ST, kEpiF16>, grid, block, lds, s, x, w.fh, y, M, N, K, out_scale, tiles_n, tiles); break;
+    case kEpiF32: GD_LAUNCH(kEpiF32); break;
+    case kEpiF16: GD_LAUNCH(kEpiF16); break;
     case kEpiGeglu:
-        if constexpr ((BN / WN / 32) % 2 == 0)
-            launch_kernel(gemm_d_kernel<BM, BN, WM, WN, BK, ST, kEpiGeglu>, grid, block, lds, s, x, w.fh, y, M, N, K, out_scale, tiles_n, tiles);
+        if constexpr (FN % 2 == 0)
+            GD_LAUNCH(kEpiGeglu);
         else
             return hipErrorInvalidValue;
         break;
     default: return hipErrorInvalidValue;
     }
+#undef GD_LAUNCH
     return hipGetLastError();
 }
 

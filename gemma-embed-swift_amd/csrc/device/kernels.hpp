@@ -58,8 +58,10 @@ hipError_t launch_embed_norm(hipStream_t s, const Q8Dev& table, const int32_t* t
                              const float* norm_w, float eps, float* x, uint16_t* h);
 
 // x = (x + rmsnorm(t) * w) * out_scale; if next_w: h = rmsnorm(x) * next_w (fp16).
-hipError_t launch_residual_norm(hipStream_t s, float* x, const float* t, const float* w, float out_scale,
-                                const float* next_w, float eps, int T, int d, uint16_t* h);
+// t arrives as fp16 t16 = t * c for a power of two c, and t_eps = eps * c^2, so rmsnorm(t16)
+// with t_eps is rmsnorm(t) exactly. d a multiple of 4, at most 1024.
+hipError_t launch_residual_norm(hipStream_t s, float* x, const uint16_t* t16, float t_eps, const float* w,
+                                float out_scale, const float* next_w, float eps, int T, int d, uint16_t* h);
 
 // qkv fp32 [T][(H + 2 KV) hd] -> q fp16 [T][H][hd], k, v fp16 [T][KV][hd]: weighted RMSNorm and
 // NeoX RoPE on q and k, unweighted RMSNorm on v.
@@ -67,13 +69,15 @@ hipError_t launch_qk_norm_rope(hipStream_t s, const float* qkv, int T, int H, in
                                const float* k_norm, float eps, const int32_t* positions, const float* rope_table,
                                uint16_t* q, uint16_t* k, uint16_t* v);
 
-// The same as launch_qk_norm_rope (head dims 128 and 256, H + 2 KV in {3, 4, 5, 6, 8, 10}), and
-// when vt is set also writes normalised V transposed: vt [KV * hd][vt_cols], token t at column
-// vcol[t].
+// The same as launch_qk_norm_rope (head dims 128 and 256, H + 2 KV in {3, 4, 5, 6, 8, 10}) on the
+// QKV projection stored as fp16 qkv16 = qkv * c for a power of two c, with eps = eps_model * c^2;
+// when vt is set it also writes normalised V transposed: vt [KV * hd][vt_cols], token t at
+// column vcol[t].
 bool qkv_norm_rope_vt_supported(int hd, int H, int KV);
-hipError_t launch_qkv_norm_rope_vt(hipStream_t s, const float* qkv, int T, int H, int KV, int hd, const float* q_norm,
-                                   const float* k_norm, float eps, const int32_t* positions, const float* rope_table,
-                                   uint16_t* q, uint16_t* k, uint16_t* v, const int32_t* vcol, int vt_cols, uint16_t* vt);
+hipError_t launch_qkv_norm_rope_vt(hipStream_t s, const uint16_t* qkv16, int T, int H, int KV, int hd,
+                                   const float* q_norm, const float* k_norm, float eps, const int32_t* positions,
+                                   const float* rope_table, uint16_t* q, uint16_t* k, uint16_t* v, const int32_t* vcol,
+                                   int vt_cols, uint16_t* vt);
 
 // Flash-style bidirectional attention over packed sequences.
 hipError_t launch_attention(hipStream_t s, const uint16_t* q, const uint16_t* k, const uint16_t* v, uint16_t* o,

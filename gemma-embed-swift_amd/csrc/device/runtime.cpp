@@ -72,6 +72,12 @@ float host_h2f(uint16_t h) {
 struct DevLayer {
     bool sliding = false;
     bool attn_v2 = false;  // attention with Q/K/V copied into LDS and V transposed
+    bool qkv_gn = false;   // QKV projection stored as scaled fp16 and read by the fused norm kernel
+    // Projections stored in fp16 before an RMSNorm are multiplied by these powers of two, chosen
+    // from load-time bounds so the values stay inside fp16's range; the norm then uses
+    // eps * c^2, which makes it exact for the scaled values.
+    float qkv_c = 1, o_c = 1, down_c = 1;
+    double act_norm_bound = 0;  // bound on ||gelu(gate) * up||_2 of one row
     int kv_heads = 0, head_dim = 0, qd = 0, kvd = 0;
     float rope_base = 0, out_scale = 1;
     // act is stored in fp16 as gelu(gate) * up * act_scale; the down projection multiplies by
@@ -95,6 +101,7 @@ struct DevModel {
 
 struct Workspace {
     int rows = 0;  // capacity in rows, slack included
+    // qkv and t hold fp16 (scaled, see DevLayer::qkv_c) where the layer's kernels take it
     float *x = nullptr, *qkv = nullptr, *t = nullptr, *out = nullptr;
     uint16_t *h = nullptr, *q = nullptr, *k = nullptr, *v = nullptr, *attn = nullptr, *act = nullptr;
     int32_t *tokens = nullptr, *positions = nullptr;
@@ -394,7 +401,7 @@ void choose_act_scale(ge_ctx*, const ge_model_desc* d, const std::string& b, con
     double wmax = 0;
     for (int i = 0; i < D; i++) wmax = std::max(wmax, double(std::fabs(w[i])));
     const size_t rb = size_t(D / 32) * 34;
-    double worst = 0;
+    double worst = 0, sumsq = 0;
     for (int j = 0; j < ff; j++) {
         double gg = 0, uu = 0;
         for (int blk = 0; blk < D / 32; blk++) {
@@ -410,12 +417,50 @@ void choose_act_scale(ge_ctx*, const ge_model_desc* d, const std::string& b, con
             uu += ud * ud * us;
         }
         worst = std::max(worst, std::sqrt(gg * uu));
+        sumsq += gg * uu;
     }
     const double bound = double(D) * wmax * wmax * worst;
+    L->act_norm_bound = double(D) * wmax * wmax * std::sqrt(sumsq);
     int shift = 0;
     while (bound * std::ldexp(1.0, -shift) > 32768.0 && shift < 60) shift++;
     L->act_scale = float(std::ldexp(1.0, -shift));
     L->down_scale = float(std::ldexp(1.0, shift));
+}
+
+// max_j ||W_j||_2 of repacked Q8_0 rows.
+double max_row_norm(const HostQ8& h) {
+    const int kb = h.cols / 32;
+    double worst = 0;
+    for (int r = 0; r < h.rows; r++) {
+        double ss = 0;
+        for (int b = 0; b < kb; b++) {
+            const double d = host_h2f(h.s[(size_t)r * kb + b]);
+            double qq = 0;
+            for (int e = 0; e < 32; e++) {
+                const double q = h.q[(size_t)r * h.cols + b * 32 + e];
+                qq += q * q;
+            }
+            ss += d * d * qq;
+        }
+        worst = std::max(worst, ss);
+    }
+    return std::sqrt(worst);
+}
+
+// The power of two c <= 1 that brings `bound` under 2^15 (half of fp16's largest finite value).
+float fp16_range_scale(double bound) {
+    int shift = 0;
+    while (bound * std::ldexp(1.0, -shift) > 32768.0 && shift < 60) shift++;
+    return float(std::ldexp(1.0, -shift));
+}
+
+double max_abs(const ge_model_desc* d, const std::string& name, int n, const void* base, size_t len) {
+    const ge_tensor_desc* t = find(d, name);
+    check_shape(t, n, 1);
+    const float* w = reinterpret_cast<const float*>(tensor_ptr(t, base, len));
+    double m = 0;
+    for (int i = 0; i < n; i++) m = std::max(m, double(std::fabs(w[i])));
+    return m;
 }
 
 void free_model(ge_ctx* c) {
@@ -494,11 +539,16 @@ void upload(ge_ctx* c, const ge_model_desc* d, const void* base, size_t len) {
             repack_rows(q8_tensor(d, b + "attn_k.weight", D, L.kvd, base, len), L.kvd, D, &h, L.qd);
             repack_rows(q8_tensor(d, b + "attn_v.weight", D, L.kvd, base, len), L.kvd, D, &h, L.qd + L.kvd);
             L.wqkv = upload_q8(c, h, "attn_qkv");
+            // |qkv_j| <= ||h|| ||W_j||, ||h|| <= sqrt(D) max|attn_norm|
+            const double hn = std::sqrt(double(D)) * max_abs(d, b + "attn_norm.weight", D, base, len);
+            L.qkv_c = fp16_range_scale(hn * max_row_norm(h));
         }
         {
             HostQ8 h = host_q8(D, L.qd);
             repack_rows(q8_tensor(d, b + "attn_output.weight", L.qd, D, base, len), D, L.qd, &h, 0);
             L.wo = upload_q8(c, h, "attn_output");
+            // each head's output is a convex combination of RMS-normalised V rows: norm <= sqrt(hd)
+            L.o_c = fp16_range_scale(std::sqrt(double(L.qd)) * max_row_norm(h));
         }
         {
             HostQ8 h = host_q8(2 * m.ff, D);
@@ -516,6 +566,7 @@ void upload(ge_ctx* c, const ge_model_desc* d, const void* base, size_t len) {
             HostQ8 h = host_q8(D, m.ff);
             repack_rows(q8_tensor(d, b + "ffn_down.weight", m.ff, D, base, len), D, m.ff, &h, 0);
             L.wd = upload_q8(c, h, "ffn_down");
+            L.down_c = fp16_range_scale(L.act_norm_bound * max_row_norm(h));
         }
         L.attn_norm = upload_f32(c, d, b + "attn_norm.weight", D, base, len);
         L.q_norm = upload_f32(c, d, b + "attn_q_norm.weight", hd, base, len);
@@ -527,6 +578,7 @@ void upload(ge_ctx* c, const ge_model_desc* d, const void* base, size_t len) {
         m.max_qd = std::max(m.max_qd, L.qd);
         m.max_kvd = std::max(m.max_kvd, L.kvd);
         L.attn_v2 = attention_v2_supported(L.head_dim, m.heads, L.kv_heads);
+        L.qkv_gn = qkv_norm_rope_vt_supported(L.head_dim, m.heads, L.kv_heads);
         m.any_v2 = m.any_v2 || L.attn_v2;
         m.max_qkv = std::max(m.max_qkv, L.qd + 2 * L.kvd);
         m.layer.push_back(L);
@@ -714,15 +766,18 @@ void encode(ge_ctx* c, StopPoint* sp) {
     if (at(sp, "inp_scaled", -1) || at(sp, "attn_norm", 0)) return;
     for (int l = 0; l < m.layers; l++) {
         const DevLayer& L = m.layer[size_t(l)];
-        launch(c, "gemm_qkv", [&] { return launch_gemm_q8(s, L.wqkv, w.h, T, w.qkv, kEpiF32); });
+        launch(c, "gemm_qkv", [&] {
+            return L.qkv_gn ? launch_gemm_q8(s, L.wqkv, w.h, T, w.qkv, kEpiF16, L.qkv_c)
+                            : launch_gemm_q8(s, L.wqkv, w.h, T, w.qkv, kEpiF32);
+        });
         if (at(sp, "Qcur", l) || at(sp, "Kcur", l) || at(sp, "Vcur", l)) return;
         // The fused kernel also writes V^T for the LDS-copy attention.
-        const bool fused_vt = qkv_norm_rope_vt_supported(L.head_dim, m.heads, L.kv_heads);
+        const bool fused_vt = L.qkv_gn;
         launch(c, "qk_norm_rope", [&] {
             if (fused_vt)
-                return launch_qkv_norm_rope_vt(s, w.qkv, T, m.heads, L.kv_heads, L.head_dim, L.q_norm, L.k_norm, m.eps,
-                                               w.positions, L.rope, w.q, w.k, w.v, w.vcol, w.vt_cap,
-                                               L.attn_v2 ? w.vt : nullptr);
+                return launch_qkv_norm_rope_vt(s, reinterpret_cast<const uint16_t*>(w.qkv), T, m.heads, L.kv_heads,
+                                               L.head_dim, L.q_norm, L.k_norm, m.eps * L.qkv_c * L.qkv_c, w.positions,
+                                               L.rope, w.q, w.k, w.v, w.vcol, w.vt_cap, L.attn_v2 ? w.vt : nullptr);
             return launch_qk_norm_rope(s, w.qkv, T, m.heads, L.kv_heads, L.head_dim, L.q_norm, L.k_norm, m.eps, w.positions,
                                        L.rope, w.q, w.k, w.v);
         });
@@ -740,18 +795,20 @@ void encode(ge_ctx* c, StopPoint* sp) {
             });
         }
         if (at(sp, "kqv_out", l)) return;
-        launch(c, "gemm_o", [&] { return launch_gemm_q8(s, L.wo, w.attn, T, w.t, kEpiF32); });
+        uint16_t* t16 = reinterpret_cast<uint16_t*>(w.t);
+        launch(c, "gemm_o", [&] { return launch_gemm_q8(s, L.wo, w.attn, T, t16, kEpiF16, L.o_c); });
         launch(c, "residual_norm", [&] {
-            return launch_residual_norm(s, w.x, w.t, L.post_attn, 1.0f, L.ffn_norm, m.eps, T, D, w.h);
+            return launch_residual_norm(s, w.x, t16, m.eps * L.o_c * L.o_c, L.post_attn, 1.0f, L.ffn_norm, m.eps, T, D, w.h);
         });
         if (at(sp, "attn_out", l) || at(sp, "ffn_norm", l)) return;
         launch(c, "gemm_gate_up", [&] { return launch_gemm_q8(s, L.wgu, w.h, T, w.act, kEpiGeglu, L.act_scale); });
         if (at(sp, "ffn_geglu", l)) return;
-        launch(c, "gemm_down", [&] { return launch_gemm_q8(s, L.wd, w.act, T, w.t, kEpiF32, L.down_scale); });
+        launch(c, "gemm_down", [&] { return launch_gemm_q8(s, L.wd, w.act, T, t16, kEpiF16, L.down_scale * L.down_c); });
         if (at(sp, "ffn_out", l)) return;
         const float* next = l + 1 < m.layers ? m.layer[size_t(l) + 1].attn_norm : m.out_norm;
         launch(c, "residual_norm", [&] {
-            return launch_residual_norm(s, w.x, w.t, L.post_ffw, L.out_scale, next, m.eps, T, D, w.h);
+            return launch_residual_norm(s, w.x, t16, m.eps * L.down_c * L.down_c, L.post_ffw, L.out_scale, next, m.eps, T, D,
+                                        w.h);
         });
         if (at(sp, "pe_in", l) || at(sp, "l_out", l) || at(sp, "attn_norm", l + 1)) return;
     }
@@ -812,6 +869,7 @@ void trace(ge_ctx* c, const char* name, int layer, float* out, size_t cap, size_
     const std::string n = name;
     // Which buffer holds the tensor, its element type, row stride, column range.
     const void* buf = nullptr;
+    float unscale = 1;  // a tensor stored scaled (DevLayer::qkv_c, down_c) is multiplied back
     bool f16 = false;
     int stride = 0, col0 = 0, width = 0;
     auto need_layer = [&] {
@@ -826,6 +884,7 @@ void trace(ge_ctx* c, const char* name, int layer, float* out, size_t cap, size_
     } else if (n == "Qcur" || n == "Kcur" || n == "Vcur") {
         need_layer();
         buf = w.qkv; stride = L->qd + 2 * L->kvd;
+        if (L->qkv_gn) { f16 = true; unscale = 1.0f / L->qkv_c; }
         if (n == "Qcur") { col0 = 0; width = L->qd; }
         else if (n == "Kcur") { col0 = L->qd; width = L->kvd; }
         else { col0 = L->qd + L->kvd; width = L->kvd; }
@@ -844,6 +903,8 @@ void trace(ge_ctx* c, const char* name, int layer, float* out, size_t cap, size_
     } else if (n == "ffn_out") {
         need_layer();
         buf = w.t; stride = width = m.hidden;
+        f16 = true;
+        unscale = 1.0f / L->down_c;
     } else if (n == "result_embd") {
         buf = w.out; stride = width = m.out_dims;
     } else {
@@ -857,6 +918,8 @@ void trace(ge_ctx* c, const char* name, int layer, float* out, size_t cap, size_
     encode(c, &sp);
     if (!sp.hit) fail(GE_ERR_INVALID, "tensor %s at layer %d is not produced by this forward", name, layer);
     copy_out(c, buf, f16, T, stride, col0, width, out);
+    if (unscale != 1.0f)
+        for (size_t i = 0; i < count; i++) out[i] *= unscale;
 }
 
 }  // namespace
