@@ -578,7 +578,8 @@ static hipError_t attention_v2_configure() {
 }
 
 hipError_t configure_kernels() {
-    hipError_t e = attention_configure_all<128, 128>();
+    hipError_t e = gemm_configure();
+    if (e == hipSuccess) e = attention_configure_all<128, 128>();
     if (e == hipSuccess) e = attention_v2_configure<128, 1>();
     if (e == hipSuccess) e = attention_v2_configure<128, 2>();
     if (e == hipSuccess) e = attention_v2_configure<128, 3>();

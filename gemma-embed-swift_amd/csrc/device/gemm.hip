@@ -74,10 +74,13 @@ __device__ __forceinline__ void gemm_store_tile(const float16_t (&acc)[FM][FN], 
 // ============================================================================ GEMM
 //
 // Y[M][N] = X[M][K] * W[N][K]^T. A workgroup computes a BM x BN tile with WM x WN waves, each wave
-// a (BM / WM) x (BN / WN) block of 32 x 32 MFMA accumulators. Both operands move from global memory into LDS with global_load_lds_dwordx4: each lane's 16
-// bytes land at (wave's LDS base) + 16 * lane, and no register holds them on the way. A stage is
-// BK columns of K: the activation tile (BM rows, row-major in global memory) and the weight tile
-// (BN rows, Q8Dev::fh fragment order, so each of its 1 KB chunks is one contiguous copy). ST stages
+// a (BM / WM) x (BN / WN) block of 32 x 32 MFMA accumulators. Both operands move from global
+// memory into LDS with buffer_load_dwordx4 ... lds: each lane's 16 bytes land at (wave's LDS
+// base) + 16 * lane and no register holds them on the way. (The global_load_lds form of the same
+// copy is a FLAT instruction, which makes the compiler treat every LDS wait after it as a full
+// lgkmcnt(0); the buffer form leaves the fragment reads their partial waits.) A stage is BK
+// columns of K: the activation tile (BM rows, row-major in global memory) and the weight tile (BN
+// rows, Q8Dev::fh fragment order, so each of its 1 KB chunks is one contiguous copy). ST stages
 // rotate through LDS: while stage s is multiplied, stages s + 1 .. s + ST - 1 are in flight.
 //
 // Activation chunks hold 1024 / (2 BK) rows of BK halves. The 16-byte slot of logical column
@@ -88,8 +91,6 @@ __device__ __forceinline__ void gemm_store_tile(const float16_t (&acc)[FM][FN], 
 // Tile order is XCD-aware: workgroups are dealt to the 8 XCDs round robin, so workgroup b runs
 // on XCD b % 8; tile (b % 8) * (T / 8) + b / 8 gives each XCD a contiguous, M-major run of tiles,
 // whose activation row blocks and the weight matrix stay in that XCD's L2.
-// s_waitcnt with only the vector-memory counter constrained (gfx9 encoding: vmcnt in bits 3:0
-// and 15:14; expcnt and lgkmcnt at their maxima).
 template <int BK>
 struct DTile {
     static constexpr int RB = 2 * BK;          // bytes per activation row in LDS
@@ -101,14 +102,26 @@ struct DTile {
     __device__ static constexpr int a_off(int r, int g) { return (r / RPC) * 1024 + (r % RPC) * RB + ((g ^ swz(r)) * 16); }
 };
 
-template <int BM, int BN, int WM, int WN, int BK, int ST>
-constexpr int gemm_d_lds_bytes() { return ST * (BM + BN) * BK * 2; }
+template <int BM, int BN, int BK, int ST>
+constexpr int gemm_lds_bytes() { return ST * (BM + BN) * BK * 2; }
+
+// Buffer resource over [p, p + bytes): raw (untyped) dword access, no swizzle; reads past the
+// end return zero.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t buffer_rsrc(const void* p, uint32_t bytes) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(p), 0, bytes, 0x00020000);
+}
+
+// buffer_load_dwordx4 ... lds: lane l's 16 bytes at byte offset voff + soff of r land at
+// lds_base + 16 l (lds_base is wave-uniform). The copy counts against vmcnt like a load.
+__device__ __forceinline__ void lds_copy16(__amdgpu_buffer_rsrc_t r, void* lds_base, uint32_t voff, uint32_t soff) {
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (__attribute__((address_space(3))) void*)lds_base, 16, voff, soff, 0, 0);
+}
 
 template <int BM, int BN, int WM, int WN, int BK, int ST, int EPI>
-__global__ __launch_bounds__(WM* WN * 64) void gemm_d_kernel(const uint16_t* __restrict__ X,
-                                                              const uint16_t* __restrict__ Fh, void* __restrict__ Y,
-                                                              int M, int N, int K, float out_scale, int tiles_n,
-                                                              int tiles) {
+__global__ __launch_bounds__(WM* WN * 64) void gemm_kernel(const uint16_t* __restrict__ X,
+                                                            const uint16_t* __restrict__ Fh, void* __restrict__ Y,
+                                                            int M, int N, int K, float out_scale, int tiles_n,
+                                                            int tiles) {
     using T = DTile<BK>;
     constexpr int NW = WM * WN, KS = BK / 16;
     constexpr int TM = BM / WM, TN = BN / WN, FM = TM / 32, FN = TN / 32;
@@ -116,6 +129,7 @@ __global__ __launch_bounds__(WM* WN * 64) void gemm_d_kernel(const uint16_t* __r
     constexpr int AW = ACH / NW, BW = BCH / NW;               // chunks per wave per stage
     constexpr int A_BYTES = BM * BK * 2, STAGE = (BM + BN) * BK * 2;
     static_assert(ACH % NW == 0 && BCH % NW == 0 && TM % 32 == 0 && TN % 32 == 0, "tile shape");
+    static_assert(KS % 2 == 0, "fragment buffers alternate per k-step and restart at each stage");
     extern __shared__ __attribute__((aligned(1024))) unsigned char lds[];
 
     const int b = blockIdx.x;
@@ -125,29 +139,33 @@ __global__ __launch_bounds__(WM* WN * 64) void gemm_d_kernel(const uint16_t* __r
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int KB = K / BK, KT = K / 16;
     const int wm = wave / WN, wn = wave % WN;
+    // The epilogue's kernel arguments into SGPRs before the main loop: a scalar load still in
+    // flight there would turn every LDS wait of the loop into a full lgkmcnt(0).
+    asm volatile("" ::"s"(Y), "s"(out_scale), "s"(M), "s"(N));
 
-    // Source of this lane's 16 bytes for each of the wave's chunks, at stage 0.
-    const uint16_t* asrc[AW];
+    // Byte offset of this lane's 16 bytes for each of the wave's chunks, at stage 0; a stage
+    // adds BK * 2 bytes (activations) or KS KB (weights) through the scalar offset.
+    const __amdgpu_buffer_rsrc_t xr = buffer_rsrc(X, uint32_t(M) * uint32_t(K) * 2u);
+    const __amdgpu_buffer_rsrc_t fr = buffer_rsrc(Fh, uint32_t(N) * uint32_t(K) * 2u);
+    uint32_t aoff[AW], boff[BW];
 #pragma unroll
     for (int i = 0; i < AW; i++) {
         const int c = wave * AW + i, r = c * T::RPC + lane / T::SPR, slot = lane % T::SPR;
-        asrc[i] = X + (size_t)min(m0 + r, M - 1) * K + (slot ^ T::swz(r)) * 8;
+        aoff[i] = uint32_t(((size_t)min(m0 + r, M - 1) * K + (slot ^ T::swz(r)) * 8) * 2);
     }
-    const uint16_t* bsrc[BW];
 #pragma unroll
     for (int i = 0; i < BW; i++) {
         const int c = wave * BW + i, jb = c / KS, t = c % KS;
         const int jg = min(n0 / 32 + jb, N / 32 - 1);
-        bsrc[i] = Fh + ((size_t)jg * KT + t) * 512 + lane * 8;
+        boff[i] = uint32_t((((size_t)jg * KT + t) * 512 + lane * 8) * 2);
     }
-
-#define GD_ISSUE(stage, buf)                                                                               \
-    do {                                                                                                   \
-        unsigned char* base_ = lds + (buf) * STAGE;                                                        \
-        _Pragma("unroll") for (int i = 0; i < AW; i++)                                                     \
-            lds_copy16(asrc[i] + (size_t)(stage) * BK, base_ + (wave * AW + i) * 1024);                    \
-        _Pragma("unroll") for (int i = 0; i < BW; i++)                                                     \
-            lds_copy16(bsrc[i] + (size_t)(stage) * KS * 512, base_ + A_BYTES + (wave * BW + i) * 1024);    \
+#define G_ISSUE(stage, buf)                                                                               \
+    do {                                                                                                  \
+        unsigned char* base_ = lds + (buf) * STAGE;                                                       \
+        _Pragma("unroll") for (int i = 0; i < AW; i++)                                                    \
+            lds_copy16(xr, base_ + (wave * AW + i) * 1024, aoff[i], (stage) * BK * 2);                    \
+        _Pragma("unroll") for (int i = 0; i < BW; i++)                                                    \
+            lds_copy16(fr, base_ + A_BYTES + (wave * BW + i) * 1024, boff[i], (stage) * KS * 1024);       \
     } while (0)
 
     float16_t acc[FM][FN];
@@ -160,14 +178,15 @@ __global__ __launch_bounds__(WM* WN * 64) void gemm_d_kernel(const uint16_t* __r
 
 #pragma unroll
     for (int s = 0; s < ST - 1; s++)
-        if (s < KB) GD_ISSUE(s, s);
+        if (s < KB) G_ISSUE(s, s);
 
     const int arow = wm * TM + (lane & 31), half = lane >> 5;
     // Fragment registers are double-buffered: the reads of k-step ks + 1 are issued before the
     // MFMAs of k-step ks. The stage boundary (wait for the next stage's copies, barrier) sits
     // before the last k-step's MFMAs, so reading the next stage's first fragments overlaps them.
+    // The scheduling barriers keep the compiler from sinking those reads below the MFMAs.
     half8_t af[2][FM], bf[2][FN];
-#define GD_FRAGS(p, buf, ks)                                                                                  \
+#define G_FRAGS(p, buf, ks)                                                                                   \
     do {                                                                                                      \
         const unsigned char* ab_ = lds + (buf) * STAGE;                                                       \
         _Pragma("unroll") for (int i = 0; i < FM; i++) af[p][i] =                                             \
@@ -175,45 +194,48 @@ __global__ __launch_bounds__(WM* WN * 64) void gemm_d_kernel(const uint16_t* __r
         _Pragma("unroll") for (int j = 0; j < FN; j++) bf[p][j] =                                             \
             *reinterpret_cast<const half8_t*>(ab_ + A_BYTES + ((wn * FN + j) * KS + (ks)) * 1024 + lane * 16); \
     } while (0)
-#define GD_STAGE_WAIT(kb)                                                                                     \
+    // One stage. ISSUE: copy stage kb + ST - 1; VMW: copies this wave may leave in flight when
+    // stage kb + 1 must have landed (at most ST - 2 later stages); LAST: no next stage. The
+    // barrier after waiting for this wave's copies and LDS reads covers every wave's, so it also
+    // means every read of the buffer the next copies overwrite is done. ISSUE and LAST are
+    // literals, so the loop below has no branch that merges a path without the stage wait into
+    // the MFMAs (which would make the compiler wait for the next stage's fragment reads there).
+#define G_STAGE(ISSUE, VMW, LAST)                                                                             \
     do {                                                                                                      \
-        if ((kb) + ST - 2 < KB)                                                                               \
-            wait_vmcnt<(ST - 2) * (AW + BW)>();                                                               \
-        else                                                                                                  \
-            wait_vmcnt<0>();                                                                                  \
-        wait_lgkmcnt0();                                                                                      \
-        workgroup_barrier();                                                                                  \
+        if (ISSUE) G_ISSUE(kb + ST - 1, (buf + ST - 1) % ST);                                                 \
+        const int next = buf + 1 == ST ? 0 : buf + 1;                                                         \
+        _Pragma("unroll") for (int ks = 0; ks < KS; ks++) {                                                   \
+            const int p = ks & 1;                                                                             \
+            if (ks + 1 < KS) {                                                                                \
+                G_FRAGS(p ^ 1, buf, ks + 1);                                                                  \
+            } else if (!(LAST)) {                                                                             \
+                wait_vmcnt<VMW>();                                                                            \
+                wait_lgkmcnt0();                                                                              \
+                workgroup_barrier();                                                                          \
+                G_FRAGS(p ^ 1, next, 0);                                                                      \
+            }                                                                                                 \
+            __builtin_amdgcn_sched_barrier(0);                                                                \
+            _Pragma("unroll") for (int i = 0; i < FM; i++) _Pragma("unroll") for (int j = 0; j < FN; j++)      \
+                acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(af[p][i], bf[p][j], acc[i][j], 0, 0, 0);    \
+            __builtin_amdgcn_sched_barrier(0);                                                                \
+        }                                                                                                     \
+        buf = next;                                                                                           \
     } while (0)
 
-    // Stage kb's copies have landed once at most (ST - 2) later stages' copies are outstanding;
-    // the barrier then covers every wave's copies. Waiting for this wave's LDS reads first makes
-    // the barrier also mean that every read of the buffer the next copies overwrite is done.
-    GD_STAGE_WAIT(0);
-    GD_FRAGS(0, 0, 0);
-    int buf = 0;
-    for (int kb = 0; kb < KB; kb++) {
-        if (kb + ST - 1 < KB) GD_ISSUE(kb + ST - 1, (buf + ST - 1) % ST);
-        const int next = buf + 1 == ST ? 0 : buf + 1;
-#pragma unroll
-        for (int ks = 0; ks < KS; ks++) {
-            const int p = ks & 1;
-            if (ks + 1 < KS) {
-                GD_FRAGS(p ^ 1, buf, ks + 1);
-            } else if (kb + 1 < KB) {
-                GD_STAGE_WAIT(kb + 1);
-                GD_FRAGS(p ^ 1, next, 0);
-            }
-#pragma unroll
-            for (int i = 0; i < FM; i++)
-#pragma unroll
-                for (int j = 0; j < FN; j++)
-                    acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(af[p][i], bf[p][j], acc[i][j], 0, 0, 0);
-        }
-        buf = next;
-    }
-#undef GD_FRAGS
-#undef GD_STAGE_WAIT
-#undef GD_ISSUE
+    if (ST - 2 < KB)
+        wait_vmcnt<(ST - 2) * (AW + BW)>();
+    else
+        wait_vmcnt<0>();
+    wait_lgkmcnt0();
+    workgroup_barrier();
+    G_FRAGS(0, 0, 0);
+    int buf = 0, kb = 0;
+    for (; kb + ST - 1 < KB; kb++) G_STAGE(1, (ST - 2) * (AW + BW), 0);
+    for (; kb < KB - 1; kb++) G_STAGE(0, 0, 0);
+    G_STAGE(0, 0, 1);
+#undef G_STAGE
+#undef G_FRAGS
+#undef G_ISSUE
     gemm_store_tile<FM, FN, EPI>(acc, Y, M, N, m0 + wm * TM, n0 + wn * TN, lane, out_scale);
 }
 
@@ -222,40 +244,57 @@ hipError_t set_lds_limit(void (*kernel)(KArgs...), int bytes) {
     return hipFuncSetAttribute(reinterpret_cast<const void*>(kernel), hipFuncAttributeMaxDynamicSharedMemorySize, bytes);
 }
 
-template <int BM, int BN, int WM, int WN, int BK, int ST>
-hipError_t gemm_d_launch(hipStream_t s, const Q8Dev& w, const uint16_t* x, int M, void* y, GemmEpilogue epi,
-                         float out_scale) {
+// The tile shapes the forward uses (M = 16384 tokens, from the tile sweep over the encoder's
+// projections): 128 x 256 tiles of 2 x 4 waves, K in stages of 32, three stages in LDS (72 KB,
+// two workgroups per CU) for the wide projections (QKV, gate/up); 256 x 256 tiles of 4 x 4 waves,
+// K in stages of 64, two stages (128 KB) for the 768-wide ones (attention output, down).
+struct GemmWide {
+    static constexpr int BM = 128, BN = 256, WM = 2, WN = 4, BK = 32, ST = 3;
+};
+struct GemmSquare {
+    static constexpr int BM = 256, BN = 256, WM = 4, WN = 4, BK = 64, ST = 2;
+};
+
+template <class C, int EPI>
+constexpr auto gemm_kernel_of() { return gemm_kernel<C::BM, C::BN, C::WM, C::WN, C::BK, C::ST, EPI>; }
+
+template <class C>
+hipError_t gemm_configure_shape() {
+    constexpr int lds = gemm_lds_bytes<C::BM, C::BN, C::BK, C::ST>();
+    static_assert(lds <= 160 * 1024, "LDS");
+    if constexpr (lds <= 65536) return hipSuccess;
+    hipError_t e = set_lds_limit(gemm_kernel_of<C, kEpiF32>(), lds);
+    if (e == hipSuccess) e = set_lds_limit(gemm_kernel_of<C, kEpiF16>(), lds);
+    if (e == hipSuccess) e = set_lds_limit(gemm_kernel_of<C, kEpiGeglu>(), lds);
+    return e;
+}
+
+hipError_t gemm_configure() {
+    hipError_t e = gemm_configure_shape<GemmWide>();
+    if (e == hipSuccess) e = gemm_configure_shape<GemmSquare>();
+    return e;
+}
+
+template <class C>
+hipError_t gemm_launch(hipStream_t s, const Q8Dev& w, const uint16_t* x, int M, void* y, GemmEpilogue epi,
+                       float out_scale) {
     const int N = w.rows, K = w.cols;
-    constexpr int FN = BN / WN / 32;
-    if (K % BK != 0 || N % 32 != 0 || !w.fh) return hipErrorInvalidValue;
-    const int tiles_m = (M + BM - 1) / BM, tiles_n = (N + BN - 1) / BN, tiles = tiles_m * tiles_n;
-    const dim3 grid(tiles), block(WM * WN * 64);
-    constexpr uint32_t lds = gemm_d_lds_bytes<BM, BN, WM, WN, BK, ST>();
-#define GD_LAUNCH(E) launch_kernel(gemm_d_kernel<BM, BN, WM, WN, BK, ST, E>, grid, block, lds, s, x, w.fh, y, M, N, K, out_scale, tiles_n, tiles)
-    if (lds > 65536) {
-        hipError_t e = hipSuccess;
-        switch (epi) {
-        case kEpiF32: e = set_lds_limit(gemm_d_kernel<BM, BN, WM, WN, BK, ST, kEpiF32>, lds); break;
-        case kEpiF16: e = set_lds_limit(gemm_d_kernel<BM, BN, WM, WN, BK, ST, kEpiF16>, lds); break;
-        case kEpiGeglu:
-            if constexpr (FN % 2 == 0) e = set_lds_limit(gemm_d_kernel<BM, BN, WM, WN, BK, ST, kEpiGeglu>, lds);
-            break;
-        default: break;
-        }
-        if (e != hipSuccess) return e;
-    }
+    const int tiles_m = (M + C::BM - 1) / C::BM, tiles_n = (N + C::BN - 1) / C::BN, tiles = tiles_m * tiles_n;
+    const dim3 grid(tiles), block(C::WM * C::WN * 64);
+    constexpr uint32_t lds = gemm_lds_bytes<C::BM, C::BN, C::BK, C::ST>();
     switch (epi) {
-    case kEpiF32: GD_LAUNCH(kEpiF32); break;
-    case kEpiF16: GD_LAUNCH(kEpiF16); break;
+    case kEpiF32:
+        launch_kernel(gemm_kernel_of<C, kEpiF32>(), grid, block, lds, s, x, w.fh, y, M, N, K, out_scale, tiles_n, tiles);
+        break;
+    case kEpiF16:
+        launch_kernel(gemm_kernel_of<C, kEpiF16>(), grid, block, lds, s, x, w.fh, y, M, N, K, out_scale, tiles_n, tiles);
+        break;
     case kEpiGeglu:
-        if constexpr (FN % 2 == 0)
-            GD_LAUNCH(kEpiGeglu);
-        else
-            return hipErrorInvalidValue;
+        launch_kernel(gemm_kernel_of<C, kEpiGeglu>(), grid, block, lds, s, x, w.fh, y, M, N, K, out_scale, tiles_n,
+                      tiles);
         break;
     default: return hipErrorInvalidValue;
     }
-#undef GD_LAUNCH
     return hipGetLastError();
 }
 
@@ -285,10 +324,11 @@ hipError_t launch_gemm_q8(hipStream_t s, const Q8Dev& w, const uint16_t* x, int 
                           float out_scale) {
     const int N = w.rows, K = w.cols;
     if (M < 0 || N <= 0 || K <= 0 || K % 32 != 0 || N % 64 != 0 || !w.fh || !x || !y) return hipErrorInvalidValue;
+    // The buffer resources address the operands with 32-bit byte offsets.
+    if ((uint64_t)M * K * 2 >= (1ull << 32) || (uint64_t)N * K * 2 >= (1ull << 32)) return hipErrorInvalidValue;
     if (M == 0) return hipSuccess;
-    // 128 x 128 tiles, 2 x 2 waves of 64 x 64, K in stages of 32, three stages in LDS (48 KB):
-    // the fastest of the tile sweep on every projection shape of the encoder (M = 16384).
-    return gemm_d_launch<128, 128, 2, 2, 32, 3>(s, w, x, M, y, epi, out_scale);
+    if (N <= 1024 && K % GemmSquare::BK == 0) return gemm_launch<GemmSquare>(s, w, x, M, y, epi, out_scale);
+    return gemm_launch<GemmWide>(s, w, x, M, y, epi, out_scale);
 }
 
 }  // namespace ge

@@ -101,6 +101,7 @@ hipError_t launch_mean_pool(hipStream_t s, const float* x, const SeqRange* seqs,
 
 // Per-device kernel attributes (dynamic LDS limits); call once per device before launching.
 hipError_t configure_kernels();
+hipError_t gemm_configure();
 
 hipError_t launch_f32_to_f16(hipStream_t s, const float* src, uint16_t* dst, size_t n);
 hipError_t launch_f16_to_f32(hipStream_t s, const uint16_t* src, float* dst, size_t n);
