@@ -102,8 +102,26 @@ struct DTile {
     __device__ static constexpr int a_off(int r, int g) { return (r / RPC) * 1024 + (r % RPC) * RB + ((g ^ swz(r)) * 16); }
 };
 
-template <int BM, int BN, int BK, int ST>
-constexpr int gemm_lds_bytes() { return ST * (BM + BN) * BK * 2; }
+// A tile shape: BM x BN tile, WM x WN waves, K in stages of BK, ST stages in LDS.
+template <int BM_, int BN_, int WM_, int WN_, int BK_, int ST_>
+struct GemmCfg {
+    static constexpr int BM = BM_, BN = BN_, WM = WM_, WN = WN_, BK = BK_, ST = ST_;
+    static constexpr int NW = WM * WN, NT = NW * 64, KS = BK / 16;
+    static constexpr int TM = BM / WM, TN = BN / WN, FM = TM / 32, FN = TN / 32;
+    static constexpr int ACH = BM * BK / 512, BCH = BN * BK / 512;  // 1 KB chunks per stage
+    static constexpr int AW = ACH / NW, BW = BCH / NW;               // chunks per wave per stage
+    static constexpr int A_BYTES = BM * BK * 2, STAGE = (BM + BN) * BK * 2, LDS = ST * STAGE;
+    static_assert(ACH % NW == 0 && BCH % NW == 0 && TM % 32 == 0 && TN % 32 == 0, "tile shape");
+    static_assert(KS % 2 == 0, "fragment buffers alternate per k-step and restart at each stage");
+    static_assert(LDS <= 160 * 1024, "LDS");
+};
+
+// The tile shapes the forward uses (M = 16384 tokens, from the tile sweep over the encoder's
+// projections): 128 x 256 tiles of 2 x 4 waves, K in stages of 32, three stages in LDS (72 KB,
+// two workgroups per CU) for the wide projections (QKV, gate/up); 256 x 256 tiles of 4 x 4 waves,
+// K in stages of 64, two stages (128 KB) for the 768-wide ones (attention output, down).
+using GemmWide = GemmCfg<128, 256, 2, 4, 32, 3>;
+using GemmSquare = GemmCfg<256, 256, 4, 4, 64, 2>;
 
 // Buffer resource over [p, p + bytes): raw (untyped) dword access, no swizzle; reads past the
 // end return zero.
@@ -117,31 +135,28 @@ __device__ __forceinline__ void lds_copy16(__amdgpu_buffer_rsrc_t r, void* lds_b
     __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (__attribute__((address_space(3))) void*)lds_base, 16, voff, soff, 0, 0);
 }
 
-template <int BM, int BN, int WM, int WN, int BK, int ST, int EPI>
-__global__ __launch_bounds__(WM* WN * 64) void gemm_kernel(const uint16_t* __restrict__ X,
-                                                            const uint16_t* __restrict__ Fh, void* __restrict__ Y,
-                                                            int M, int N, int K, float out_scale, int tiles_n,
-                                                            int tiles) {
-    using T = DTile<BK>;
-    constexpr int NW = WM * WN, KS = BK / 16;
-    constexpr int TM = BM / WM, TN = BN / WN, FM = TM / 32, FN = TN / 32;
-    constexpr int ACH = BM * BK / 512, BCH = BN * BK / 512;  // 1 KB chunks per stage
-    constexpr int AW = ACH / NW, BW = BCH / NW;               // chunks per wave per stage
-    constexpr int A_BYTES = BM * BK * 2, STAGE = (BM + BN) * BK * 2;
-    static_assert(ACH % NW == 0 && BCH % NW == 0 && TM % 32 == 0 && TN % 32 == 0, "tile shape");
-    static_assert(KS % 2 == 0, "fragment buffers alternate per k-step and restart at each stage");
-    extern __shared__ __attribute__((aligned(1024))) unsigned char lds[];
-
-    const int b = blockIdx.x;
+// Workgroup b's tile: workgroups are dealt to the 8 XCDs round robin (b runs on XCD b % 8), and
+// tile (b % 8) * (T / 8) + b / 8 gives each XCD a contiguous, M-major run of tiles.
+__device__ __forceinline__ int xcd_tile(int b, int tiles) {
     const int full = tiles / 8 * 8;
-    const int tile = b < full ? (b % 8) * (full / 8) + b / 8 : b;
-    const int m0 = (tile / tiles_n) * BM, n0 = (tile % tiles_n) * BN;
+    return b < full ? (b % 8) * (full / 8) + b / 8 : b;
+}
+
+// The main loop: acc = X[m0 .. m0 + BM) * W[n0 .. n0 + BN)^T over all of K for this wave's
+// (TM x TN) block. TR: accumulate the transposed block (operands swapped in the MFMA): register
+// 4 g + e of acc[i][j] then holds row i * 32 + lane % 32, column j * 32 + g * 8 + (lane / 32) * 4 + e
+// of the wave's block, instead of row i * 32 + g * 8 + (lane / 32) * 4 + e, column j * 32 + lane % 32.
+// Leaves the stage buffers' reads outstanding (the caller waits before reusing LDS).
+template <class C, bool TR>
+__device__ __forceinline__ void gemm_mainloop(const uint16_t* __restrict__ X, const uint16_t* __restrict__ Fh, int M,
+                                              int N, int K, int m0, int n0, unsigned char* lds,
+                                              float16_t (&acc)[C::FM][C::FN]) {
+    using T = DTile<C::BK>;
+    constexpr int BK = C::BK, ST = C::ST, KS = C::KS, FM = C::FM, FN = C::FN, AW = C::AW, BW = C::BW;
+    constexpr int A_BYTES = C::A_BYTES, STAGE = C::STAGE;
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int KB = K / BK, KT = K / 16;
-    const int wm = wave / WN, wn = wave % WN;
-    // The epilogue's kernel arguments into SGPRs before the main loop: a scalar load still in
-    // flight there would turn every LDS wait of the loop into a full lgkmcnt(0).
-    asm volatile("" ::"s"(Y), "s"(out_scale), "s"(M), "s"(N));
+    const int wm = wave / C::WN, wn = wave % C::WN;
 
     // Byte offset of this lane's 16 bytes for each of the wave's chunks, at stage 0; a stage
     // adds BK * 2 bytes (activations) or KS KB (weights) through the scalar offset.
@@ -168,7 +183,6 @@ __global__ __launch_bounds__(WM* WN * 64) void gemm_kernel(const uint16_t* __res
             lds_copy16(fr, base_ + A_BYTES + (wave * BW + i) * 1024, boff[i], (stage) * KS * 1024);       \
     } while (0)
 
-    float16_t acc[FM][FN];
 #pragma unroll
     for (int i = 0; i < FM; i++)
 #pragma unroll
@@ -180,7 +194,7 @@ __global__ __launch_bounds__(WM* WN * 64) void gemm_kernel(const uint16_t* __res
     for (int s = 0; s < ST - 1; s++)
         if (s < KB) G_ISSUE(s, s);
 
-    const int arow = wm * TM + (lane & 31), half = lane >> 5;
+    const int arow = wm * C::TM + (lane & 31), half = lane >> 5;
     // Fragment registers are double-buffered: the reads of k-step ks + 1 are issued before the
     // MFMAs of k-step ks. The stage boundary (wait for the next stage's copies, barrier) sits
     // before the last k-step's MFMAs, so reading the next stage's first fragments overlaps them.
@@ -216,7 +230,8 @@ __global__ __launch_bounds__(WM* WN * 64) void gemm_kernel(const uint16_t* __res
             }                                                                                                 \
             __builtin_amdgcn_sched_barrier(0);                                                                \
             _Pragma("unroll") for (int i = 0; i < FM; i++) _Pragma("unroll") for (int j = 0; j < FN; j++)      \
-                acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(af[p][i], bf[p][j], acc[i][j], 0, 0, 0);    \
+                acc[i][j] = TR ? __builtin_amdgcn_mfma_f32_32x32x16_f16(bf[p][j], af[p][i], acc[i][j], 0, 0, 0) \
+                               : __builtin_amdgcn_mfma_f32_32x32x16_f16(af[p][i], bf[p][j], acc[i][j], 0, 0, 0); \
             __builtin_amdgcn_sched_barrier(0);                                                                \
         }                                                                                                     \
         buf = next;                                                                                           \
@@ -236,7 +251,176 @@ __global__ __launch_bounds__(WM* WN * 64) void gemm_kernel(const uint16_t* __res
 #undef G_STAGE
 #undef G_FRAGS
 #undef G_ISSUE
-    gemm_store_tile<FM, FN, EPI>(acc, Y, M, N, m0 + wm * TM, n0 + wn * TN, lane, out_scale);
+}
+
+template <class C, int EPI>
+__global__ __launch_bounds__(C::NT) void gemm_kernel(const uint16_t* __restrict__ X, const uint16_t* __restrict__ Fh,
+                                                      void* __restrict__ Y, int M, int N, int K, float out_scale,
+                                                      int tiles_n, int tiles) {
+    extern __shared__ __attribute__((aligned(1024))) unsigned char lds[];
+    const int tile = xcd_tile(blockIdx.x, tiles);
+    const int m0 = (tile / tiles_n) * C::BM, n0 = (tile % tiles_n) * C::BN;
+    // The epilogue's kernel arguments into SGPRs before the main loop: a scalar load still in
+    // flight there would turn every LDS wait of the loop into a full lgkmcnt(0).
+    asm volatile("" ::"s"(Y), "s"(out_scale));
+    float16_t acc[C::FM][C::FN];
+    gemm_mainloop<C, false>(X, Fh, M, N, K, m0, n0, lds, acc);
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    gemm_store_tile<C::FM, C::FN, EPI>(acc, Y, M, N, m0 + (wave / C::WN) * C::TM, n0 + (wave % C::WN) * C::TN, lane,
+                                       out_scale);
+}
+
+// ============================================================================ QKV + norms + RoPE
+//
+// The QKV projection with the per-head RMSNorms, NeoX RoPE and the V transpose of the attention
+// input in its epilogue (the reference's separate rms_norm_rows / rope_neox kernels,
+// Metal/MetalForward.swift:375-395, Shaders/Elementwise.metal). A 128 x 256 tile holds 256 / HD
+// whole heads of 128 tokens. The accumulators (transposed, so a lane holds 4 consecutive columns of
+// one token) are staged in LDS as fp16 qkv * scale, the rounding the unfused path stores; then
+// each wave takes whole token rows: a lane holds 4 columns of one head, the head's sum of
+// squares is a butterfly over its HD / 4 lanes, and the NeoX partner of column j (j + HD / 2) sits
+// HD / 8 lanes away. Normalised V rows go back into LDS for the transposed write, one V^T row
+// (128 tokens) per wave instruction pair.
+struct QkvStage {
+    static constexpr int RB = 512;  // bytes per staged row (256 halves)
+    // 16-byte chunk c of row r at chunk c ^ (r % 16): the transposed fragment writes of one
+    // instruction (32 rows, one chunk) and the V^T column reads spread over the banks.
+    __device__ static constexpr int off(int r, int c) { return r * RB + ((c ^ (r & 15)) << 4); }
+    static constexpr int BYTES = 128 * RB;
+};
+
+template <int HD>
+__global__ __launch_bounds__(GemmWide::NT) void gemm_qkv_kernel(const uint16_t* __restrict__ X,
+                                                                 const uint16_t* __restrict__ Fh, int M, int N, int K,
+                                                                 int tiles_n, int tiles, QkvEpilogue a) {
+    using C = GemmWide;
+    static_assert(C::BM == 128 && C::BN == 256 && 256 % HD == 0, "heads per tile");
+    static_assert(QkvStage::BYTES <= C::LDS, "staging fits the stage buffers");
+    constexpr int LPH = HD / 4;  // lanes per head in the row pass
+    extern __shared__ __attribute__((aligned(1024))) unsigned char lds[];
+    const int tile = xcd_tile(blockIdx.x, tiles);
+    const int m0 = (tile / tiles_n) * C::BM, n0 = (tile % tiles_n) * C::BN;
+    asm volatile("" ::"s"(a.q_norm), "s"(a.k_norm), "s"(a.positions), "s"(a.rope), "s"(a.q), "s"(a.k), "s"(a.v),
+                 "s"(a.vcol), "s"(a.vt), "s"(a.scale), "s"(a.eps), "s"(a.vt_cols), "s"(a.heads), "s"(a.kv_heads));
+    float16_t acc[C::FM][C::FN];
+    gemm_mainloop<C, true>(X, Fh, M, N, K, m0, n0, lds, acc);
+
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int wm = wave / C::WN, wn = wave % C::WN;
+    wait_lgkmcnt0();
+    workgroup_barrier();  // every wave's last fragment reads are done: the stages become the tile
+#pragma unroll
+    for (int i = 0; i < C::FM; i++)
+#pragma unroll
+        for (int j = 0; j < C::FN; j++)
+#pragma unroll
+            for (int g = 0; g < 4; g++) {
+                half4_t h;
+#pragma unroll
+                for (int e = 0; e < 4; e++) h[e] = _Float16(acc[i][j][4 * g + e] * a.scale);
+                const int r = wm * C::TM + i * 32 + (lane & 31), c = wn * (C::TN / 8) + j * 4 + g;
+                *reinterpret_cast<half4_t*>(lds + QkvStage::off(r, c) + (lane >> 5) * 8) = h;
+            }
+    wait_lgkmcnt0();
+    workgroup_barrier();
+
+    const int H = a.heads, KV = a.kv_heads, S = N / HD;
+    const int hl = lane / LPH, cl = (lane % LPH) * 4;  // head within the tile, first column within it
+    const int slot = n0 / HD + hl;
+    const bool valid = slot < S, isq = slot < H, isk = !isq && slot < H + KV, isv = valid && !isq && !isk;
+    const bool lo = cl < HD / 2;  // holds the first half of the NeoX pairs
+    float w[4] = {1.0f, 1.0f, 1.0f, 1.0f};
+    if (valid && (isq || isk)) {
+        const float4_t wv = *reinterpret_cast<const float4_t*>((isq ? a.q_norm : a.k_norm) + cl);
+#pragma unroll
+        for (int e = 0; e < 4; e++) w[e] = wv[e];
+    }
+    uint16_t* dst = isq ? a.q : (isk ? a.k : a.v);
+    const int dst_heads = isq ? H : KV, dst_slot = isq ? slot : (isk ? slot - H : slot - H - KV);
+    // Rows r = wave + NW k; lane k holds row k's position. Four rows at a time; the RoPE table
+    // entries of the next four rows are loaded while the current ones are processed, so the
+    // table's latency is paid once per wave rather than once per batch.
+    constexpr int RPW = C::BM / C::NW, RBATCH = 4, NB = RPW / RBATCH;
+    const int my_row = wave + C::NW * lane;
+    const int my_pos = lane < RPW && m0 + my_row < M ? a.positions[m0 + my_row] : 0;
+    const bool rope = isq || isk;
+    const int tcol = (lo ? cl : cl - HD / 2) * 2;  // this lane's first (cos, sin) pair in a table row
+    float4_t cs[2][RBATCH][2];
+#define QKV_TABLE(buf, b)                                                                                   \
+    do {                                                                                                    \
+        _Pragma("unroll") for (int k = 0; k < RBATCH; k++) {                                                \
+            const float* row_ = a.rope + (size_t)__shfl(my_pos, (b) * RBATCH + k, 64) * HD + tcol;          \
+            cs[buf][k][0] = *reinterpret_cast<const float4_t*>(row_);                                       \
+            cs[buf][k][1] = *reinterpret_cast<const float4_t*>(row_ + 4);                                   \
+        }                                                                                                   \
+    } while (0)
+    if (rope) QKV_TABLE(0, 0);
+#pragma unroll
+    for (int b = 0; b < NB; b++) {
+        if (rope && b + 1 < NB) QKV_TABLE((b + 1) & 1, b + 1);
+        float f[RBATCH][4], ss[RBATCH];
+#pragma unroll
+        for (int k = 0; k < RBATCH; k++) {
+            const int r = wave + C::NW * (b * RBATCH + k);
+            const half4_t x = *reinterpret_cast<const half4_t*>(lds + QkvStage::off(r, lane >> 1) + (lane & 1) * 8);
+            ss[k] = 0.0f;
+#pragma unroll
+            for (int e = 0; e < 4; e++) {
+                f[k][e] = float(x[e]);
+                ss[k] += f[k][e] * f[k][e];
+            }
+        }
+#pragma unroll
+        for (int m = LPH / 2; m >= 1; m >>= 1)
+#pragma unroll
+            for (int k = 0; k < RBATCH; k++) ss[k] += __shfl_xor(ss[k], m, 64);
+#pragma unroll
+        for (int k = 0; k < RBATCH; k++) {
+            const int r = wave + C::NW * (b * RBATCH + k), t = m0 + r;
+            const float inv = 1.0f / sqrtf(ss[k] / float(HD) + a.eps);
+            half4_t o;
+            if (rope) {
+                const float4_t c01 = cs[b & 1][k][0], c23 = cs[b & 1][k][1];
+                const float cr[8] = {c01[0], c01[1], c01[2], c01[3], c23[0], c23[1], c23[2], c23[3]};
+#pragma unroll
+                for (int e = 0; e < 4; e++) {
+                    const float mine = f[k][e] * inv * w[e];
+                    const float other = __shfl_xor(mine, LPH / 2, 64);
+                    const float c = cr[2 * e], sn = cr[2 * e + 1];
+                    // (a, b) = (first, second) half of the pair: a' = a c - b s, b' = a s + b c
+                    o[e] = _Float16(lo ? mine * c - other * sn : other * sn + mine * c);
+                }
+            } else {
+#pragma unroll
+                for (int e = 0; e < 4; e++) o[e] = _Float16(f[k][e] * inv);
+            }
+            if (valid && t < M) {
+                if (dst) *reinterpret_cast<half4_t*>(dst + ((size_t)t * dst_heads + dst_slot) * HD + cl) = o;
+                if (isv && a.vt) *reinterpret_cast<half4_t*>(lds + QkvStage::off(r, lane >> 1) + (lane & 1) * 8) = o;
+            }
+        }
+    }
+#undef QKV_TABLE
+    if (!a.vt) return;
+    // V^T rows: vt[(slot - H - KV) * HD + d][vcol[t]] for this tile's V heads.
+    const int first_v = H + KV, tile_slot0 = n0 / HD;
+    if (tile_slot0 + 256 / HD <= first_v || tile_slot0 >= S) return;  // no V head in this tile
+    wait_lgkmcnt0();
+    workgroup_barrier();
+    const int t0 = m0 + lane, t1 = m0 + 64 + lane;
+    const int vc0 = t0 < M ? a.vcol[t0] : -1, vc1 = t1 < M ? a.vcol[t1] : -1;
+    for (int hh = 0; hh < 256 / HD; hh++) {
+        const int sl = tile_slot0 + hh;
+        if (sl < first_v || sl >= S) continue;
+        for (int d = wave; d < HD; d += C::NW) {
+            const int col = hh * HD + d;
+            uint16_t* row = a.vt + (size_t)((sl - first_v) * HD + d) * a.vt_cols;
+            const uint16_t v0 = *reinterpret_cast<const uint16_t*>(lds + QkvStage::off(lane, col >> 3) + (col & 7) * 2);
+            const uint16_t v1 = *reinterpret_cast<const uint16_t*>(lds + QkvStage::off(64 + lane, col >> 3) + (col & 7) * 2);
+            if (vc0 >= 0) row[vc0] = v0;
+            if (vc1 >= 0) row[vc1] = v1;
+        }
+    }
 }
 
 template <typename... KArgs>
@@ -244,34 +428,20 @@ hipError_t set_lds_limit(void (*kernel)(KArgs...), int bytes) {
     return hipFuncSetAttribute(reinterpret_cast<const void*>(kernel), hipFuncAttributeMaxDynamicSharedMemorySize, bytes);
 }
 
-// The tile shapes the forward uses (M = 16384 tokens, from the tile sweep over the encoder's
-// projections): 128 x 256 tiles of 2 x 4 waves, K in stages of 32, three stages in LDS (72 KB,
-// two workgroups per CU) for the wide projections (QKV, gate/up); 256 x 256 tiles of 4 x 4 waves,
-// K in stages of 64, two stages (128 KB) for the 768-wide ones (attention output, down).
-struct GemmWide {
-    static constexpr int BM = 128, BN = 256, WM = 2, WN = 4, BK = 32, ST = 3;
-};
-struct GemmSquare {
-    static constexpr int BM = 256, BN = 256, WM = 4, WN = 4, BK = 64, ST = 2;
-};
-
-template <class C, int EPI>
-constexpr auto gemm_kernel_of() { return gemm_kernel<C::BM, C::BN, C::WM, C::WN, C::BK, C::ST, EPI>; }
-
 template <class C>
 hipError_t gemm_configure_shape() {
-    constexpr int lds = gemm_lds_bytes<C::BM, C::BN, C::BK, C::ST>();
-    static_assert(lds <= 160 * 1024, "LDS");
-    if constexpr (lds <= 65536) return hipSuccess;
-    hipError_t e = set_lds_limit(gemm_kernel_of<C, kEpiF32>(), lds);
-    if (e == hipSuccess) e = set_lds_limit(gemm_kernel_of<C, kEpiF16>(), lds);
-    if (e == hipSuccess) e = set_lds_limit(gemm_kernel_of<C, kEpiGeglu>(), lds);
+    if constexpr (C::LDS <= 65536) return hipSuccess;
+    hipError_t e = set_lds_limit(gemm_kernel<C, kEpiF32>, C::LDS);
+    if (e == hipSuccess) e = set_lds_limit(gemm_kernel<C, kEpiF16>, C::LDS);
+    if (e == hipSuccess) e = set_lds_limit(gemm_kernel<C, kEpiGeglu>, C::LDS);
     return e;
 }
 
 hipError_t gemm_configure() {
     hipError_t e = gemm_configure_shape<GemmWide>();
     if (e == hipSuccess) e = gemm_configure_shape<GemmSquare>();
+    if (e == hipSuccess) e = set_lds_limit(gemm_qkv_kernel<128>, GemmWide::LDS);
+    if (e == hipSuccess) e = set_lds_limit(gemm_qkv_kernel<256>, GemmWide::LDS);
     return e;
 }
 
@@ -280,22 +450,28 @@ hipError_t gemm_launch(hipStream_t s, const Q8Dev& w, const uint16_t* x, int M, 
                        float out_scale) {
     const int N = w.rows, K = w.cols;
     const int tiles_m = (M + C::BM - 1) / C::BM, tiles_n = (N + C::BN - 1) / C::BN, tiles = tiles_m * tiles_n;
-    const dim3 grid(tiles), block(C::WM * C::WN * 64);
-    constexpr uint32_t lds = gemm_lds_bytes<C::BM, C::BN, C::BK, C::ST>();
+    const dim3 grid(tiles), block(C::NT);
     switch (epi) {
     case kEpiF32:
-        launch_kernel(gemm_kernel_of<C, kEpiF32>(), grid, block, lds, s, x, w.fh, y, M, N, K, out_scale, tiles_n, tiles);
+        launch_kernel(gemm_kernel<C, kEpiF32>, grid, block, C::LDS, s, x, w.fh, y, M, N, K, out_scale, tiles_n, tiles);
         break;
     case kEpiF16:
-        launch_kernel(gemm_kernel_of<C, kEpiF16>(), grid, block, lds, s, x, w.fh, y, M, N, K, out_scale, tiles_n, tiles);
+        launch_kernel(gemm_kernel<C, kEpiF16>, grid, block, C::LDS, s, x, w.fh, y, M, N, K, out_scale, tiles_n, tiles);
         break;
     case kEpiGeglu:
-        launch_kernel(gemm_kernel_of<C, kEpiGeglu>(), grid, block, lds, s, x, w.fh, y, M, N, K, out_scale, tiles_n,
-                      tiles);
+        launch_kernel(gemm_kernel<C, kEpiGeglu>, grid, block, C::LDS, s, x, w.fh, y, M, N, K, out_scale, tiles_n, tiles);
         break;
     default: return hipErrorInvalidValue;
     }
     return hipGetLastError();
+}
+
+// Operand checks shared by the GEMM launchers; the buffer resources address the operands with
+// 32-bit byte offsets.
+static bool gemm_operands_ok(const Q8Dev& w, const void* x, int M, const void* y) {
+    const int N = w.rows, K = w.cols;
+    if (M < 0 || N <= 0 || K <= 0 || K % 32 != 0 || N % 64 != 0 || !w.fh || !x || !y) return false;
+    return (uint64_t)M * K * 2 < (1ull << 32) && (uint64_t)N * K * 2 < (1ull << 32);
 }
 
 // One thread per lane fragment: 8 halves of Q8Dev::fh from the row-major planes.
@@ -322,13 +498,28 @@ hipError_t launch_q8_fragments(hipStream_t s, const Q8Dev& w, uint16_t* fh) {
 
 hipError_t launch_gemm_q8(hipStream_t s, const Q8Dev& w, const uint16_t* x, int M, void* y, GemmEpilogue epi,
                           float out_scale) {
-    const int N = w.rows, K = w.cols;
-    if (M < 0 || N <= 0 || K <= 0 || K % 32 != 0 || N % 64 != 0 || !w.fh || !x || !y) return hipErrorInvalidValue;
-    // The buffer resources address the operands with 32-bit byte offsets.
-    if ((uint64_t)M * K * 2 >= (1ull << 32) || (uint64_t)N * K * 2 >= (1ull << 32)) return hipErrorInvalidValue;
+    if (!gemm_operands_ok(w, x, M, y)) return hipErrorInvalidValue;
     if (M == 0) return hipSuccess;
-    if (N <= 1024 && K % GemmSquare::BK == 0) return gemm_launch<GemmSquare>(s, w, x, M, y, epi, out_scale);
+    if (w.rows <= 1024 && w.cols % GemmSquare::BK == 0) return gemm_launch<GemmSquare>(s, w, x, M, y, epi, out_scale);
     return gemm_launch<GemmWide>(s, w, x, M, y, epi, out_scale);
+}
+
+bool gemm_qkv_supported(int hd, int H, int KV) { return (hd == 128 || hd == 256) && H > 0 && KV > 0; }
+
+hipError_t launch_gemm_qkv(hipStream_t s, const Q8Dev& w, const uint16_t* x, int M, int hd, const QkvEpilogue& e) {
+    if (!gemm_operands_ok(w, x, M, e.q) || !gemm_qkv_supported(hd, e.heads, e.kv_heads) || !e.k || (!e.v && !e.vt) ||
+        !e.q_norm || !e.k_norm || !e.positions || !e.rope || w.rows != (e.heads + 2 * e.kv_heads) * hd ||
+        (e.vt && (!e.vcol || e.vt_cols <= 0)))
+        return hipErrorInvalidValue;
+    if (M == 0) return hipSuccess;
+    using C = GemmWide;
+    const int N = w.rows, K = w.cols;
+    const int tiles_m = (M + C::BM - 1) / C::BM, tiles_n = (N + C::BN - 1) / C::BN, tiles = tiles_m * tiles_n;
+    if (hd == 128)
+        launch_kernel(gemm_qkv_kernel<128>, dim3(tiles), dim3(C::NT), C::LDS, s, x, w.fh, M, N, K, tiles_n, tiles, e);
+    else
+        launch_kernel(gemm_qkv_kernel<256>, dim3(tiles), dim3(C::NT), C::LDS, s, x, w.fh, M, N, K, tiles_n, tiles, e);
+    return hipGetLastError();
 }
 
 }  // namespace ge

@@ -53,6 +53,31 @@ enum GemmEpilogue { kEpiF32 = 0, kEpiF16 = 1, kEpiGeglu = 2 };
 hipError_t launch_gemm_q8(hipStream_t s, const Q8Dev& w, const uint16_t* x, int M, void* y, GemmEpilogue epi,
                           float out_scale = 1.0f);
 
+// The QKV projection with the per-head norms and RoPE in its epilogue: the GEMM's fp32 result,
+// rounded to fp16 as qkv * scale (scale a power of two; eps is eps_model * scale^2), then the
+// same as launch_qk_norm_rope / launch_qkv_norm_rope_vt: q [T][H][hd], k, v [T][KV][hd] fp16,
+// and when vt is set, normalised V transposed: vt [KV * hd][vt_cols], token t at column vcol[t]
+// (v may then be null: row-major V is not written). W's rows are the H query heads, then KV key
+// heads, then KV value heads.
+struct QkvEpilogue {
+    const float* q_norm = nullptr;
+    const float* k_norm = nullptr;
+    const int32_t* positions = nullptr;
+    const float* rope = nullptr;  // [position][hd / 2] (cos, sin) pairs
+    uint16_t* q = nullptr;
+    uint16_t* k = nullptr;
+    uint16_t* v = nullptr;
+    const int32_t* vcol = nullptr;
+    uint16_t* vt = nullptr;
+    float scale = 1.0f;
+    float eps = 0.0f;
+    int vt_cols = 0;
+    int heads = 0;
+    int kv_heads = 0;
+};
+bool gemm_qkv_supported(int hd, int H, int KV);
+hipError_t launch_gemm_qkv(hipStream_t s, const Q8Dev& w, const uint16_t* x, int M, int hd, const QkvEpilogue& e);
+
 // x = table[id] * scale (fp32 [T][d]), h = rmsnorm(x) * w (fp16 [T][d]).
 hipError_t launch_embed_norm(hipStream_t s, const Q8Dev& table, const int32_t* tokens, int T, float scale,
                              const float* norm_w, float eps, float* x, uint16_t* h);

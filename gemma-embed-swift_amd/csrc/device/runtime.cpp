@@ -73,6 +73,7 @@ struct DevLayer {
     bool sliding = false;
     bool attn_v2 = false;  // attention with Q/K/V copied into LDS and V transposed
     bool qkv_gn = false;   // QKV projection stored as scaled fp16 and read by the fused norm kernel
+    bool qkv_fused = false;  // QKV projection with the norms, RoPE and V^T in its epilogue
     // Projections stored in fp16 before an RMSNorm are multiplied by these powers of two, chosen
     // from load-time bounds so the values stay inside fp16's range; the norm then uses
     // eps * c^2, which makes it exact for the scaled values.
@@ -579,6 +580,7 @@ void upload(ge_ctx* c, const ge_model_desc* d, const void* base, size_t len) {
         m.max_kvd = std::max(m.max_kvd, L.kvd);
         L.attn_v2 = attention_v2_supported(L.head_dim, m.heads, L.kv_heads);
         L.qkv_gn = qkv_norm_rope_vt_supported(L.head_dim, m.heads, L.kv_heads);
+        L.qkv_fused = L.qkv_gn && gemm_qkv_supported(L.head_dim, m.heads, L.kv_heads);
         m.any_v2 = m.any_v2 || L.attn_v2;
         m.max_qkv = std::max(m.max_qkv, L.qd + 2 * L.kvd);
         m.layer.push_back(L);
@@ -766,21 +768,45 @@ void encode(ge_ctx* c, StopPoint* sp) {
     if (at(sp, "inp_scaled", -1) || at(sp, "attn_norm", 0)) return;
     for (int l = 0; l < m.layers; l++) {
         const DevLayer& L = m.layer[size_t(l)];
-        launch(c, "gemm_qkv", [&] {
-            return L.qkv_gn ? launch_gemm_q8(s, L.wqkv, w.h, T, w.qkv, kEpiF16, L.qkv_c)
-                            : launch_gemm_q8(s, L.wqkv, w.h, T, w.qkv, kEpiF32);
-        });
-        if (at(sp, "Qcur", l) || at(sp, "Kcur", l) || at(sp, "Vcur", l)) return;
-        // The fused kernel also writes V^T for the LDS-copy attention.
+        // The raw projection (trace points Qcur / Kcur / Vcur) only exists on the unfused path.
+        const bool raw_qkv = sp && sp->layer == l && (sp->name == "Qcur" || sp->name == "Kcur" || sp->name == "Vcur");
+        if (L.qkv_fused && !raw_qkv) {
+            launch(c, "gemm_qkv", [&] {
+                QkvEpilogue e;
+                e.q_norm = L.q_norm;
+                e.k_norm = L.k_norm;
+                e.positions = w.positions;
+                e.rope = L.rope;
+                e.q = w.q;
+                e.k = w.k;
+                // Row-major V is read only by the attention without V^T and by traces.
+                e.v = L.attn_v2 && !sp ? nullptr : w.v;
+                e.vcol = w.vcol;
+                e.vt = L.attn_v2 ? w.vt : nullptr;
+                e.vt_cols = w.vt_cap;
+                e.scale = L.qkv_c;
+                e.eps = m.eps * L.qkv_c * L.qkv_c;
+                e.heads = m.heads;
+                e.kv_heads = L.kv_heads;
+                return launch_gemm_qkv(s, L.wqkv, w.h, T, L.head_dim, e);
+            });
+        } else {
+            launch(c, "gemm_qkv", [&] {
+                return L.qkv_gn ? launch_gemm_q8(s, L.wqkv, w.h, T, w.qkv, kEpiF16, L.qkv_c)
+                                : launch_gemm_q8(s, L.wqkv, w.h, T, w.qkv, kEpiF32);
+            });
+            if (at(sp, "Qcur", l) || at(sp, "Kcur", l) || at(sp, "Vcur", l)) return;
+            launch(c, "qk_norm_rope", [&] {
+                if (L.qkv_gn)
+                    return launch_qkv_norm_rope_vt(s, reinterpret_cast<const uint16_t*>(w.qkv), T, m.heads, L.kv_heads,
+                                                   L.head_dim, L.q_norm, L.k_norm, m.eps * L.qkv_c * L.qkv_c, w.positions,
+                                                   L.rope, w.q, w.k, w.v, w.vcol, w.vt_cap, L.attn_v2 ? w.vt : nullptr);
+                return launch_qk_norm_rope(s, w.qkv, T, m.heads, L.kv_heads, L.head_dim, L.q_norm, L.k_norm, m.eps,
+                                           w.positions, L.rope, w.q, w.k, w.v);
+            });
+        }
+        // The fused kernels also write V^T for the LDS-copy attention.
         const bool fused_vt = L.qkv_gn;
-        launch(c, "qk_norm_rope", [&] {
-            if (fused_vt)
-                return launch_qkv_norm_rope_vt(s, reinterpret_cast<const uint16_t*>(w.qkv), T, m.heads, L.kv_heads,
-                                               L.head_dim, L.q_norm, L.k_norm, m.eps * L.qkv_c * L.qkv_c, w.positions,
-                                               L.rope, w.q, w.k, w.v, w.vcol, w.vt_cap, L.attn_v2 ? w.vt : nullptr);
-            return launch_qk_norm_rope(s, w.qkv, T, m.heads, L.kv_heads, L.head_dim, L.q_norm, L.k_norm, m.eps, w.positions,
-                                       L.rope, w.q, w.k, w.v);
-        });
         if (at(sp, "Qcur_pos", l) || at(sp, "Kcur_pos", l) || at(sp, "Vcur_normed", l)) return;
         const int hw = L.sliding ? m.window / 2 : 0;  // halfWindow = slidingWindow / 2 (MetalForward.swift:399)
         if (L.attn_v2) {
