@@ -257,23 +257,25 @@ __global__ __launch_bounds__(256) void attention_kernel(const uint16_t* __restri
 //
 // One workgroup of 2 G waves per (work item of 64 query rows, KV head): wave w owns query head
 // kvh * G + w % G for the query half w / G (32 rows). Q, K and V move from global memory into
-// LDS with global_load_lds_dwordx4 -- no register or producer wave carries them. Each wave's
+// LDS with buffer_load ... lds copies -- no register or producer wave carries them. Each wave's
 // 32 query rows sit in LDS for the whole kernel (so the fp32 output accumulators, 32 x hd per
 // wave, are the only large register array); keys stream in blocks of 32 through two LDS
 // buffers, the next block's copy in flight while the current one is multiplied. V arrives
-// transposed (V^T [kv head][d][key], written by launch_v_transpose), so every MFMA operand is a
-// 16-byte fragment read.
+// transposed (V^T [kv head][d][key], written by the QKV epilogue or launch_v_transpose).
+//
+// Everything in LDS is stored in MFMA fragment order: a 1 KB chunk holds one operand fragment
+// of v_mfma_f32_32x32x16_f16, lane l's 16 bytes at 16 l. The copies gather the fragments
+// (lane l of a chunk reads 16 bytes of row l % 32, columns 8 (l / 32) .. + 8 of the k-step), so
+// every fragment read is base + 16 lane + a constant: no per-k-step address registers and no
+// bank conflicts.
+//   Q (per wave): chunk ks = query rows q0 .. q0 + 31, head dims 16 ks .. 16 ks + 15.
+//   K (per block): chunk ks = S^T rows (keys, permuted as below), head dims 16 ks ...
+//   V^T (per block): chunk ks2 * DT + dt = head dims 32 dt .. + 31, keys 16 ks2 .. + 15.
 //
 // The rows of the S^T tile are taken from the key block in the order 0-3, 8-11, 4-7, 12-15
 // within each 16 keys. The accumulator then holds, for lane half h, keys 8h .. 8h + 7 of each
-// 16-key step in consecutive registers: the B operand of the P.V product needs no shuffling
-// and V^T is read as one 16-byte slot per lane.
-//
-// LDS layouts (16-byte slots, swizzled through each lane's copy source so that every 16 lanes
-// of a fragment read hit all 64 banks once):
-//   Q: per wave [32 queries][hd], slot s of query row r holds column slot s ^ (r % 16);
-//   K: [32 keys][hd], slot s of key row r holds column slot s ^ (r % 16);
-//   V^T: [hd][32 keys], slot s of row d holds key slot s ^ ((d / 4) % 4).
+// 16-key step in consecutive registers: the B operand of the P.V product is the accumulator
+// itself, converted to fp16.
 namespace attn2 {
 constexpr int QB = 64;   // query rows per work item
 constexpr int BKV = 32;  // keys per block
@@ -291,11 +293,10 @@ __global__ __launch_bounds__(2 * G * 64) void attention_v2_kernel(const uint16_t
                                                                   int vt_cols, int hw, float scale_log2) {
     using namespace attn2;
     constexpr int NW = 2 * G, KSQ = HD / 16, DT = HD / 32;
-    constexpr int Q_BYTES = 32 * HD * 2;            // one wave's query rows
+    constexpr int Q_BYTES = 32 * HD * 2;              // one wave's query rows
     constexpr int K_BYTES = BKV * HD * 2, STAGE = 2 * K_BYTES;
-    constexpr int KCH = K_BYTES / 1024, CH = 2 * KCH;  // 1 KB copies per key block (K, then V^T)
-    constexpr int LPR = HD / 8;                       // 16-byte slots per Q / K row
-    constexpr int VRB = BKV * 2, VSL = VRB / 16;      // V^T row bytes and slots
+    constexpr int KCH = K_BYTES / 1024, CH = 2 * KCH;  // 1 KB chunks per key block (K, then V^T)
+    static_assert(KCH == KSQ && KCH == 2 * DT, "chunk counts");
     extern __shared__ __attribute__((aligned(1024))) unsigned char ldsb[];
     unsigned char* const kv = ldsb + NW * Q_BYTES;
 
@@ -318,40 +319,53 @@ __global__ __launch_bounds__(2 * G * 64) void attention_v2_kernel(const uint16_t
     kstart = kstart / BKV * BKV;
     const int nblocks = (kend - kstart + BKV - 1) / BKV;
 
-    const uint16_t* kbase = Kg + (size_t)wi.seq_start * kvStride + kvh * HD;
-    const uint16_t* vtbase = VTg + (size_t)kvh * HD * vt_cols + wi.vt_start;
+    // Buffer resources over this sequence's rows of the wave's query head and of the KV head, and
+    // over the KV head's V^T rows from the sequence's first column on: copies past them read
+    // zeros.
+    const __amdgpu_buffer_rsrc_t qr =
+        buffer_rsrc(Qg + (size_t)wi.seq_start * qStride + h * HD, uint32_t(((len - 1) * qStride + HD) * 2));
+    const __amdgpu_buffer_rsrc_t kr =
+        buffer_rsrc(Kg + (size_t)wi.seq_start * kvStride + kvh * HD, uint32_t(((len - 1) * kvStride + HD) * 2));
+    const __amdgpu_buffer_rsrc_t vr = buffer_rsrc(VTg + (size_t)kvh * HD * vt_cols + wi.vt_start,
+                                                  uint32_t(((HD - 1) * vt_cols + (vt_cols - int(wi.vt_start))) * 2));
 
-    // This wave's query rows (rows past the sequence re-read its last row; their outputs are
-    // never stored).
+    // This wave's query fragments (rows past the sequence re-read its last row; their outputs
+    // are never stored).
     unsigned char* const qs = ldsb + wave * Q_BYTES;
-    for (int c = 0; c < Q_BYTES / 1024; c++) {
-        const int r = c * (64 / LPR) + lane / LPR, sl = lane % LPR;
-        const uint16_t* src = Qg + (size_t)(wi.seq_start + min(q0 + r, len - 1)) * qStride + h * HD + ((sl ^ (r & 15)) * 8);
-        lds_copy16(src, qs + c * 1024);
+    {
+        const uint32_t qo = uint32_t((min(qi, len - 1) * qStride + 8 * half) * 2);
+#pragma unroll
+        for (int c = 0; c < KSQ; c++) lds_copy16(qr, qs + c * 1024, qo + c * 32, 0);
     }
 
+    // S^T row i (lane i % 32 of the A operand) reads key (i / 16) * 16 + perm(i % 16): 0-3,
+    // 8-11, 4-7, 12-15.
+    const int i16 = lane & 15;
+    const int krow = (lane & 16) + (i16 < 4 || i16 >= 12 ? i16 : (i16 < 8 ? i16 + 4 : i16 - 4));
+
     // This wave's copies of a key block: chunks wave, wave + NW, ... (at most CPW). The lane part
-    // of each source address is fixed; a block only moves the wave-uniform base.
+    // of each source offset is fixed; a block adds its key offset.
     constexpr int CPW = (CH + NW - 1) / NW;
     uint32_t coff[CPW];
 #pragma unroll
     for (int i = 0; i < CPW; i++) {
         const int c = wave + i * NW;
         if (c < KCH) {
-            const int key = c * (64 / LPR) + lane / LPR, sl = lane % LPR;
-            coff[i] = uint32_t((key * kvStride + ((sl ^ (key & 15)) * 8)) * 2);
+            coff[i] = uint32_t((krow * kvStride + 16 * c + 8 * half) * 2);
         } else {
-            const int d = (c - KCH) * (64 / VSL) + lane / VSL, sl = lane % VSL;
-            coff[i] = uint32_t((d * vt_cols + ((sl ^ ((d >> 2) & 3)) * 8)) * 2);
+            const int ks2 = (c - KCH) / DT, dt = (c - KCH) % DT;
+            coff[i] = uint32_t(((dt * 32 + (lane & 31)) * vt_cols + 16 * ks2 + 8 * half) * 2);
         }
     }
 #define A2_ISSUE(kb, b)                                                                                    \
     do {                                                                                                   \
-        const unsigned char* kb_ = reinterpret_cast<const unsigned char*>(kbase + (size_t)(kb) * kvStride); \
-        const unsigned char* vb_ = reinterpret_cast<const unsigned char*>(vtbase + (kb));                   \
+        const uint32_t ko_ = uint32_t((kb) * kvStride * 2), vo_ = uint32_t((kb) * 2);                      \
         _Pragma("unroll") for (int i = 0; i < CPW; i++) {                                                  \
             const int c = wave + i * NW;                                                                   \
-            if (c < CH) lds_copy16((c < KCH ? kb_ : vb_) + coff[i], kv + (b) * STAGE + c * 1024);          \
+            if (c < KCH)                                                                                   \
+                lds_copy16(kr, kv + (b) * STAGE + c * 1024, coff[i] + ko_, 0);                            \
+            else if (c < CH)                                                                               \
+                lds_copy16(vr, kv + (b) * STAGE + c * 1024, coff[i] + vo_, 0);                            \
         }                                                                                                  \
     } while (0)
 
@@ -362,98 +376,107 @@ __global__ __launch_bounds__(2 * G * 64) void attention_v2_kernel(const uint16_t
         for (int r = 0; r < 16; r++) o[i][r] = 0.0f;
     float m_run = -INFINITY, l_run = 0.0f;
 
-    // S^T row i reads key (i / 16) * 16 + perm(i % 16): 0-3, 8-11, 4-7, 12-15.
-    const int i16 = lane & 15;
-    const int krow = (lane & 16) + (i16 < 4 || i16 >= 12 ? i16 : (i16 < 8 ? i16 + 4 : i16 - 4));
-    const int qrow = lane & 31;
-
     if (nblocks > 0) A2_ISSUE(kstart, 0);
     wait_vmcnt<0>();
     workgroup_barrier();
+    const unsigned char* const qf = qs + lane * 16;
     for (int it = 0; it < nblocks; it++) {
         const int kb = kstart + it * BKV, b = it & 1;
         if (it + 1 < nblocks) A2_ISSUE(kb + BKV, b ^ 1);
         // Every wave computes, also one whose query rows all lie past the sequence (they read
         // the clamped last row; nothing of theirs is stored): no branch around the block.
-        {
-            const unsigned char* Ks = kv + b * STAGE;
-            const unsigned char* Vs = Ks + K_BYTES;
-            // two accumulation chains over the k-steps halve the MFMA dependency latency
-            float16_t sc, sc1;
+        const unsigned char* const kf = kv + b * STAGE + lane * 16;
+        const unsigned char* const vf = kf + K_BYTES;
+        // S^T = K Q^T over the head dims, two accumulation chains; fragments read PF k-steps
+        // ahead through a ring of PF + 1 registers, so LDS latency overlaps the MFMAs.
+        constexpr int PF = 3, RING = PF + 1;
+        float16_t sc, sc1;
 #pragma unroll
-            for (int r = 0; r < 16; r++) sc[r] = sc1[r] = 0.0f;
-            const unsigned char* kp = Ks + krow * (HD * 2);
-            const unsigned char* qp = qs + qrow * (HD * 2);
+        for (int r = 0; r < 16; r++) sc[r] = sc1[r] = 0.0f;
+        half8_t ka[RING], qa[RING];
 #pragma unroll
-            for (int ks = 0; ks < KSQ; ks += 2) {
-                const int slot = 2 * ks + half;
-                const half8_t a0 = *reinterpret_cast<const half8_t*>(kp + ((slot ^ (krow & 15)) * 16));
-                const half8_t b0 = *reinterpret_cast<const half8_t*>(qp + ((slot ^ (qrow & 15)) * 16));
-                const half8_t a1 = *reinterpret_cast<const half8_t*>(kp + (((slot + 2) ^ (krow & 15)) * 16));
-                const half8_t b1 = *reinterpret_cast<const half8_t*>(qp + (((slot + 2) ^ (qrow & 15)) * 16));
-                sc = __builtin_amdgcn_mfma_f32_32x32x16_f16(a0, b0, sc, 0, 0, 0);
-                sc1 = __builtin_amdgcn_mfma_f32_32x32x16_f16(a1, b1, sc1, 0, 0, 0);
+        for (int f = 0; f < PF; f++) {
+            ka[f] = *reinterpret_cast<const half8_t*>(kf + f * 1024);
+            qa[f] = *reinterpret_cast<const half8_t*>(qf + f * 1024);
+        }
+#pragma unroll
+        for (int ks = 0; ks < KSQ; ks++) {
+            if (ks + PF < KSQ) {
+                ka[(ks + PF) % RING] = *reinterpret_cast<const half8_t*>(kf + (ks + PF) * 1024);
+                qa[(ks + PF) % RING] = *reinterpret_cast<const half8_t*>(qf + (ks + PF) * 1024);
             }
-            sc += sc1;
-            // key of accumulator element r for this lane: kb + 16 (r / 8) + 8 half + r % 8
-            const bool inside = kb + BKV <= len && (hw == 0 || (kb >= q0 + 31 - hw && kb + BKV - 1 <= q0 + hw));
-            float bmax = -INFINITY;
-            if (inside) {
+            // keep the reads ahead of the MFMA (the scheduler would otherwise sink them)
+            __builtin_amdgcn_sched_barrier(0);
+            if (ks & 1)
+                sc1 = __builtin_amdgcn_mfma_f32_32x32x16_f16(ka[ks % RING], qa[ks % RING], sc1, 0, 0, 0);
+            else
+                sc = __builtin_amdgcn_mfma_f32_32x32x16_f16(ka[ks % RING], qa[ks % RING], sc, 0, 0, 0);
+        }
+        // the first V^T fragments are read while the softmax runs
+        half8_t va[RING];
 #pragma unroll
-                for (int r = 0; r < 16; r++) {
-                    sc[r] *= scale_log2;
-                    bmax = fmaxf(bmax, sc[r]);
-                }
-            } else {
-#pragma unroll
-                for (int r = 0; r < 16; r++) {
-                    const int key = kb + (r >> 3) * 16 + half * 8 + (r & 7);
-                    bool valid = key < len;
-                    if (hw > 0) valid = valid && abs(qi - key) <= hw;
-                    const float val = valid ? sc[r] * scale_log2 : -INFINITY;
-                    sc[r] = val;
-                    bmax = fmaxf(bmax, val);
-                }
-            }
-            bmax = fmaxf(bmax, __shfl_xor(bmax, 32, 64));
-            // Lazy rescaling: the reference point m_run moves only when a score exceeds it by more
-            // than 2^8 (log2 domain), so P stays below 256 -- exact in fp16 to the same relative
-            // precision -- and the o *= alpha pass runs only on the rare blocks that move it.
-            // o / l is unchanged by the choice of reference point.
-            if (__builtin_amdgcn_ballot_w64(bmax > m_run + 8.0f)) {
-                const float m_new = fmaxf(m_run, bmax);
-                const float alpha = m_new == -INFINITY ? 1.0f : __builtin_amdgcn_exp2f(m_run - m_new);
-                l_run *= alpha;
-#pragma unroll
-                for (int i = 0; i < DT; i++)
-#pragma unroll
-                    for (int r = 0; r < 16; r++) o[i][r] *= alpha;
-                m_run = m_new;
-            }
-            // m_run is -inf only while every key seen so far is masked (all scores -inf): the
-            // reference point 0 then gives p = 0.
-            const float m_ref = m_run == -INFINITY ? 0.0f : m_run;
-            float sum = 0.0f;
+        for (int f = 0; f < PF; f++) va[f] = *reinterpret_cast<const half8_t*>(vf + f * 1024);
+        sc += sc1;
+        // key of accumulator element r for this lane: kb + 16 (r / 8) + 8 half + r % 8
+        const bool inside = kb + BKV <= len && (hw == 0 || (kb >= q0 + 31 - hw && kb + BKV - 1 <= q0 + hw));
+        float bmax = -INFINITY;
+        if (inside) {
 #pragma unroll
             for (int r = 0; r < 16; r++) {
-                const float p = __builtin_amdgcn_exp2f(sc[r] - m_ref);
-                sc[r] = p;
-                sum += p;
+                sc[r] *= scale_log2;
+                bmax = fmaxf(bmax, sc[r]);
             }
-            sum += __shfl_xor(sum, 32, 64);
-            l_run += sum;
+        } else {
+            // keys past the sequence, and (sliding window) keys farther than hw from the query
+            const int lim = hw > 0 ? hw : 1 << 30;
 #pragma unroll
-            for (int ks = 0; ks < BKV / 16; ks++) {
-                half8_t pb;
+            for (int r = 0; r < 16; r++) {
+                const int key = kb + (r >> 3) * 16 + half * 8 + (r & 7);
+                const bool valid = key < len && abs(qi - key) <= lim;
+                const float val = valid ? sc[r] * scale_log2 : -INFINITY;
+                sc[r] = val;
+                bmax = fmaxf(bmax, val);
+            }
+        }
+        bmax = fmaxf(bmax, __shfl_xor(bmax, 32, 64));
+        // Lazy rescaling: the reference point m_run moves only when a score exceeds it by more
+        // than 2^8 (log2 domain), so P stays below 256 -- exact in fp16 to the same relative
+        // precision -- and the o *= alpha pass runs only on the rare blocks that move it.
+        // o / l is unchanged by the choice of reference point.
+        if (__builtin_amdgcn_ballot_w64(bmax > m_run + 8.0f)) {
+            const float m_new = fmaxf(m_run, bmax);
+            const float alpha = m_new == -INFINITY ? 1.0f : __builtin_amdgcn_exp2f(m_run - m_new);
+            l_run *= alpha;
 #pragma unroll
-                for (int j = 0; j < 8; j++) pb[j] = _Float16(sc[ks * 8 + j]);
-                const int slot = 2 * ks + half;
+            for (int i = 0; i < DT; i++)
 #pragma unroll
-                for (int dt = 0; dt < DT; dt++) {
-                    const int d = dt * 32 + (lane & 31);
-                    const half8_t a = *reinterpret_cast<const half8_t*>(Vs + d * VRB + ((slot ^ ((d >> 2) & 3)) * 16));
-                    o[dt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, pb, o[dt], 0, 0, 0);
-                }
+                for (int r = 0; r < 16; r++) o[i][r] *= alpha;
+            m_run = m_new;
+        }
+        // m_run is -inf only while every key seen so far is masked (all scores -inf): the
+        // reference point 0 then gives p = 0.
+        const float m_ref = m_run == -INFINITY ? 0.0f : m_run;
+        float sum = 0.0f;
+#pragma unroll
+        for (int r = 0; r < 16; r++) {
+            const float p = __builtin_amdgcn_exp2f(sc[r] - m_ref);
+            sc[r] = p;
+            sum += p;
+        }
+        sum += __shfl_xor(sum, 32, 64);
+        l_run += sum;
+        // O^T += V^T P^T: 16-key steps ks2, head-dim tiles dt; V^T fragments PF steps ahead.
+#pragma unroll
+        for (int ks2 = 0; ks2 < BKV / 16; ks2++) {
+            half8_t pb;
+#pragma unroll
+            for (int j = 0; j < 8; j++) pb[j] = _Float16(sc[ks2 * 8 + j]);
+#pragma unroll
+            for (int dt = 0; dt < DT; dt++) {
+                const int f = ks2 * DT + dt;
+                if (f + PF < 2 * DT) va[(f + PF) % RING] = *reinterpret_cast<const half8_t*>(vf + (f + PF) * 1024);
+                __builtin_amdgcn_sched_barrier(0);
+                o[dt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(va[f % RING], pb, o[dt], 0, 0, 0);
             }
         }
         wait_vmcnt<0>();

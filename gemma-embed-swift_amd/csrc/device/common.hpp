@@ -68,10 +68,18 @@ __device__ __forceinline__ void wait_vmcnt() {
     __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
 }
 
-// global_load_lds_dwordx4: lane l's 16 bytes from src land at lds_base + 16 l (lds_base is
-// wave-uniform). The copy counts against vmcnt like a load.
-__device__ __forceinline__ void lds_copy16(const void* src, void* lds_base) {
-    __builtin_amdgcn_global_load_lds(src, (__attribute__((address_space(3))) void*)lds_base, 16, 0, 0);
+// Buffer resource over [p, p + bytes): raw (untyped) dword access, no swizzle; reads past the
+// end return zero. p and bytes must be wave-uniform.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t buffer_rsrc(const void* p, uint32_t bytes) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(p), 0, bytes, 0x00020000);
+}
+
+// buffer_load_dwordx4 ... lds: lane l's 16 bytes at byte offset voff + soff of r land at
+// lds_base + 16 l (lds_base and soff wave-uniform). The copy counts against vmcnt like a load.
+// (The global_load_lds form of the same copy is a FLAT instruction, after which the compiler
+// treats every LDS wait as a full lgkmcnt(0), serialising fragment reads with the MFMAs.)
+__device__ __forceinline__ void lds_copy16(__amdgpu_buffer_rsrc_t r, void* lds_base, uint32_t voff, uint32_t soff) {
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (__attribute__((address_space(3))) void*)lds_base, 16, voff, soff, 0, 0);
 }
 
 // A workgroup barrier without the release fence of __syncthreads(): that fence would wait for

@@ -75,10 +75,8 @@ __device__ __forceinline__ void gemm_store_tile(const float16_t (&acc)[FM][FN], 
 //
 // Y[M][N] = X[M][K] * W[N][K]^T. A workgroup computes a BM x BN tile with WM x WN waves, each wave
 // a (BM / WM) x (BN / WN) block of 32 x 32 MFMA accumulators. Both operands move from global
-// memory into LDS with buffer_load_dwordx4 ... lds: each lane's 16 bytes land at (wave's LDS
-// base) + 16 * lane and no register holds them on the way. (The global_load_lds form of the same
-// copy is a FLAT instruction, which makes the compiler treat every LDS wait after it as a full
-// lgkmcnt(0); the buffer form leaves the fragment reads their partial waits.) A stage is BK
+// memory into LDS with buffer_load_dwordx4 ... lds (lds_copy16): each lane's 16 bytes land at
+// (wave's LDS base) + 16 * lane and no register holds them on the way. A stage is BK
 // columns of K: the activation tile (BM rows, row-major in global memory) and the weight tile (BN
 // rows, Q8Dev::fh fragment order, so each of its 1 KB chunks is one contiguous copy). ST stages
 // rotate through LDS: while stage s is multiplied, stages s + 1 .. s + ST - 1 are in flight.
@@ -122,18 +120,6 @@ struct GemmCfg {
 // K in stages of 64, two stages (128 KB) for the 768-wide ones (attention output, down).
 using GemmWide = GemmCfg<128, 256, 2, 4, 32, 3>;
 using GemmSquare = GemmCfg<256, 256, 4, 4, 64, 2>;
-
-// Buffer resource over [p, p + bytes): raw (untyped) dword access, no swizzle; reads past the
-// end return zero.
-__device__ __forceinline__ __amdgpu_buffer_rsrc_t buffer_rsrc(const void* p, uint32_t bytes) {
-    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(p), 0, bytes, 0x00020000);
-}
-
-// buffer_load_dwordx4 ... lds: lane l's 16 bytes at byte offset voff + soff of r land at
-// lds_base + 16 l (lds_base is wave-uniform). The copy counts against vmcnt like a load.
-__device__ __forceinline__ void lds_copy16(__amdgpu_buffer_rsrc_t r, void* lds_base, uint32_t voff, uint32_t soff) {
-    __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (__attribute__((address_space(3))) void*)lds_base, 16, voff, soff, 0, 0);
-}
 
 // Workgroup b's tile: workgroups are dealt to the 8 XCDs round robin (b runs on XCD b % 8), and
 // tile (b % 8) * (T / 8) + b / 8 gives each XCD a contiguous, M-major run of tiles.

@@ -7,6 +7,7 @@
 #include <algorithm>
 #include <cmath>
 #include <cstdarg>
+#include <cstdlib>
 #include <cstdio>
 #include <cstring>
 #include <map>
@@ -97,6 +98,7 @@ struct DevModel {
     float* out_norm = nullptr;
     std::vector<DevLayer> layer;
     int max_qd = 0, max_kvd = 0, max_qkv = 0;
+    bool all_fused = true;  // every layer: fused QKV epilogue and the LDS-copy attention
     bool any_v2 = false;
 };
 
@@ -144,7 +146,9 @@ struct ge_q8_matrix {
 struct ge_ctx {
     int device = 0;
     hipStream_t stream = nullptr;
-    hipEvent_t ev_start = nullptr, ev_stop = nullptr;
+    // The second half of a split batch runs its layers on stream2 (see stage()).
+    hipStream_t stream2 = nullptr;
+    hipEvent_t ev_start = nullptr, ev_stop = nullptr, ev_fork = nullptr, ev_join = nullptr;
     std::string err, name;
     bool has_model = false;
     ge::DevModel model;
@@ -153,6 +157,9 @@ struct ge_ctx {
     ge::Workspace ws;
     // staged batch
     int staged_tokens = -1, staged_seqs = 0, staged_work = 0, staged_work2 = 0, staged_vt_cols = 0;
+    // Split batch: rows [0, split_row) with work2 items [0, split_work2) on stream, the rest on
+    // stream2; 0 = not split.
+    int split_row = 0, split_work2 = 0;
     // profiling
     bool prof = false;
     std::string prof_prefix;
@@ -581,6 +588,7 @@ void upload(ge_ctx* c, const ge_model_desc* d, const void* base, size_t len) {
         L.attn_v2 = attention_v2_supported(L.head_dim, m.heads, L.kv_heads);
         L.qkv_gn = qkv_norm_rope_vt_supported(L.head_dim, m.heads, L.kv_heads);
         L.qkv_fused = L.qkv_gn && gemm_qkv_supported(L.head_dim, m.heads, L.kv_heads);
+        m.all_fused = m.all_fused && L.qkv_fused && L.attn_v2;
         m.any_v2 = m.any_v2 || L.attn_v2;
         m.max_qkv = std::max(m.max_qkv, L.qd + 2 * L.kvd);
         m.layer.push_back(L);
@@ -657,6 +665,9 @@ void ensure_workspace(ge_ctx* c, int tokens, int seqs, int work, int work2, int 
     }
 }
 
+// Batches of at least this many tokens are split into two halves on two streams.
+constexpr int kSplitMinTokens = 4096;
+
 // Transposed-V layout of a packed batch: each sequence's keys start at a column that is a
 // multiple of 8 (16-byte aligned copies); vt_cols leaves a key block of slack past the end.
 struct VtLayout {
@@ -724,6 +735,24 @@ void stage(ge_ctx* c, const int32_t* tokens, const int32_t* positions, int n, co
             for (uint32_t q0 = 0; q0 < seqs[s].length; q0 += kAttnQueriesV2)
                 work2.push_back(AttnWork{seqs[s].start, seqs[s].length, q0, vl.start[size_t(s)]});
     }
+    // Split a large batch of several sequences into two halves of whole sequences, near n / 2,
+    // whose layers run on two streams: one half's memory-bound kernels and its kernels' start
+    // and end phases overlap the other half's work.
+    int split_row = 0, split_work2 = 0;
+    if (m.all_fused && n >= kSplitMinTokens && n_seqs >= 2) {
+        std::vector<uint32_t> starts;
+        for (int s = 0; s < n_seqs; s++)
+            if (seqs[s].length && seqs[s].start > 0) starts.push_back(seqs[s].start);
+        int best = 0;
+        for (uint32_t r : starts)
+            if (!best || std::abs(int(r) - n / 2) < std::abs(best - n / 2)) best = int(r);
+        if (best > 0 && best < n) {
+            split_row = best;
+            std::stable_partition(work2.begin(), work2.end(), [&](const AttnWork& a) { return int(a.seq_start) < split_row; });
+            split_work2 = int(std::count_if(work2.begin(), work2.end(), [&](const AttnWork& a) { return int(a.seq_start) < split_row; }));
+            if (split_work2 == 0 || split_work2 == int(work2.size())) split_row = split_work2 = 0;
+        }
+    }
     ensure_workspace(c, n, n_seqs, int(work.size()), int(work2.size()), vl.cols);
     Workspace& w = c->ws;
     hip_check(hipMemcpyAsync(w.tokens, tokens, size_t(n) * 4, hipMemcpyHostToDevice, c->stream), "upload tokens");
@@ -741,6 +770,8 @@ void stage(ge_ctx* c, const int32_t* tokens, const int32_t* positions, int n, co
     c->staged_work = int(work.size());
     c->staged_work2 = int(work2.size());
     c->staged_vt_cols = vl.cols;
+    c->split_row = split_row;
+    c->split_work2 = split_work2;
 }
 
 // ---------------------------------------------------------------- forward
@@ -844,10 +875,99 @@ void encode(ge_ctx* c, StopPoint* sp) {
     launch(c, "mean_pool", [&] { return launch_mean_pool(s, w.out, w.seqs, c->staged_seqs, m.out_dims, w.pooled); });
 }
 
+// The forward of a split batch (see stage()): every layer's kernels run for rows
+// [0, split_row) on c->stream and for the rest on c->stream2, launched alternately, so the two
+// halves' kernels overlap. Only layers with the fused QKV epilogue and the LDS-copy attention.
+void encode_split(ge_ctx* c) {
+    const DevModel& m = c->model;
+    Workspace& w = c->ws;
+    const int T = c->staged_tokens, D = m.hidden;
+    struct Half {
+        hipStream_t s;
+        int r0, T;
+        const AttnWork* work;
+        int n_work;
+    };
+    const Half halves[2] = {{c->stream, 0, c->split_row, w.work2, c->split_work2},
+                            {c->stream2, c->split_row, T - c->split_row, w.work2 + c->split_work2,
+                             c->staged_work2 - c->split_work2}};
+    hip_check(hipEventRecord(c->ev_fork, c->stream), "hipEventRecord");
+    hip_check(hipStreamWaitEvent(c->stream2, c->ev_fork, 0), "hipStreamWaitEvent");
+    uint16_t* t16 = reinterpret_cast<uint16_t*>(w.t);
+    for (const Half& H : halves)
+        launch(c, "embed_norm", [&] {
+            return launch_embed_norm(H.s, m.tok_embd, w.tokens + H.r0, H.T, m.emb_scale, m.layer[0].attn_norm, m.eps,
+                                     w.x + (size_t)H.r0 * D, w.h + (size_t)H.r0 * D);
+        });
+    for (int l = 0; l < m.layers; l++) {
+        const DevLayer& L = m.layer[size_t(l)];
+        for (const Half& H : halves)
+            launch(c, "gemm_qkv", [&] {
+                QkvEpilogue e;
+                e.q_norm = L.q_norm;
+                e.k_norm = L.k_norm;
+                e.positions = w.positions + H.r0;
+                e.rope = L.rope;
+                e.q = w.q + (size_t)H.r0 * L.qd;
+                e.k = w.k + (size_t)H.r0 * L.kvd;
+                e.v = nullptr;
+                e.vcol = w.vcol + H.r0;
+                e.vt = w.vt;
+                e.vt_cols = w.vt_cap;
+                e.scale = L.qkv_c;
+                e.eps = m.eps * L.qkv_c * L.qkv_c;
+                e.heads = m.heads;
+                e.kv_heads = L.kv_heads;
+                return launch_gemm_qkv(H.s, L.wqkv, w.h + (size_t)H.r0 * D, H.T, L.head_dim, e);
+            });
+        const int hw = L.sliding ? m.window / 2 : 0;
+        for (const Half& H : halves)
+            launch(c, "attention", [&] {
+                return launch_attention_v2(H.s, w.q, w.k, w.vt, w.vt_cap, w.attn, H.work, H.n_work, m.heads, L.kv_heads,
+                                           L.head_dim, hw, 1.0f);
+            });
+        for (const Half& H : halves)
+            launch(c, "gemm_o", [&] {
+                return launch_gemm_q8(H.s, L.wo, w.attn + (size_t)H.r0 * L.qd, H.T, t16 + (size_t)H.r0 * D, kEpiF16, L.o_c);
+            });
+        for (const Half& H : halves)
+            launch(c, "residual_norm", [&] {
+                return launch_residual_norm(H.s, w.x + (size_t)H.r0 * D, t16 + (size_t)H.r0 * D, m.eps * L.o_c * L.o_c,
+                                            L.post_attn, 1.0f, L.ffn_norm, m.eps, H.T, D, w.h + (size_t)H.r0 * D);
+            });
+        for (const Half& H : halves)
+            launch(c, "gemm_gate_up", [&] {
+                return launch_gemm_q8(H.s, L.wgu, w.h + (size_t)H.r0 * D, H.T, w.act + (size_t)H.r0 * m.ff, kEpiGeglu,
+                                      L.act_scale);
+            });
+        for (const Half& H : halves)
+            launch(c, "gemm_down", [&] {
+                return launch_gemm_q8(H.s, L.wd, w.act + (size_t)H.r0 * m.ff, H.T, t16 + (size_t)H.r0 * D, kEpiF16,
+                                      L.down_scale * L.down_c);
+            });
+        const float* next = l + 1 < m.layers ? m.layer[size_t(l) + 1].attn_norm : m.out_norm;
+        for (const Half& H : halves)
+            launch(c, "residual_norm", [&] {
+                return launch_residual_norm(H.s, w.x + (size_t)H.r0 * D, t16 + (size_t)H.r0 * D, m.eps * L.down_c * L.down_c,
+                                            L.post_ffw, L.out_scale, next, m.eps, H.T, D, w.h + (size_t)H.r0 * D);
+            });
+    }
+    for (const Half& H : halves)
+        launch(c, "gemm_output", [&] {
+            return launch_gemm_q8(H.s, m.output, w.h + (size_t)H.r0 * D, H.T, w.out + (size_t)H.r0 * m.out_dims, kEpiF32);
+        });
+    hip_check(hipEventRecord(c->ev_join, c->stream2), "hipEventRecord");
+    hip_check(hipStreamWaitEvent(c->stream, c->ev_join, 0), "hipStreamWaitEvent");
+    launch(c, "mean_pool", [&] { return launch_mean_pool(c->stream, w.out, w.seqs, c->staged_seqs, m.out_dims, w.pooled); });
+}
+
 void run_forward(ge_ctx* c, double* gpu_seconds) {
     if (c->staged_tokens < 0) fail(GE_ERR_STATE, "no batch is staged");
     hip_check(hipEventRecord(c->ev_start, c->stream), "hipEventRecord");
-    encode(c, nullptr);
+    if (c->split_row > 0 && !c->prof)
+        encode_split(c);
+    else
+        encode(c, nullptr);
     hip_check(hipEventRecord(c->ev_stop, c->stream), "hipEventRecord");
     if (gpu_seconds) {
         hip_check(hipEventSynchronize(c->ev_stop), "hipEventSynchronize");
@@ -974,8 +1094,11 @@ int ge_create(int device, ge_ctx** out) {
     c->device = device;
     int rc = guarded(c.get(), [&] {
         ge::hip_check(hipStreamCreateWithFlags(&c->stream, hipStreamNonBlocking), "hipStreamCreate");
+        ge::hip_check(hipStreamCreateWithFlags(&c->stream2, hipStreamNonBlocking), "hipStreamCreate");
         ge::hip_check(hipEventCreate(&c->ev_start), "hipEventCreate");
         ge::hip_check(hipEventCreate(&c->ev_stop), "hipEventCreate");
+        ge::hip_check(hipEventCreateWithFlags(&c->ev_fork, hipEventDisableTiming), "hipEventCreate");
+        ge::hip_check(hipEventCreateWithFlags(&c->ev_join, hipEventDisableTiming), "hipEventCreate");
         hipDeviceProp_t prop;
         ge::hip_check(hipGetDeviceProperties(&prop, device), "hipGetDeviceProperties");
         c->name = std::string(prop.name) + " (" + prop.gcnArchName + ")";
@@ -986,6 +1109,7 @@ int ge_create(int device, ge_ctx** out) {
     if (rc != GE_OK) {
         ge::g_create_error = c->err;
         if (c->stream) (void)hipStreamDestroy(c->stream);
+        if (c->stream2) (void)hipStreamDestroy(c->stream2);
         return rc;
     }
     *out = c.release();
@@ -1005,7 +1129,11 @@ void ge_destroy(ge_ctx* c) {
     for (auto e : c->event_pool) (void)hipEventDestroy(e);
     if (c->ev_start) (void)hipEventDestroy(c->ev_start);
     if (c->ev_stop) (void)hipEventDestroy(c->ev_stop);
+    if (c->ev_fork) (void)hipEventDestroy(c->ev_fork);
+    if (c->ev_join) (void)hipEventDestroy(c->ev_join);
+    if (c->stream2) (void)hipStreamSynchronize(c->stream2);
     if (c->stream) (void)hipStreamDestroy(c->stream);
+    if (c->stream2) (void)hipStreamDestroy(c->stream2);
     delete c;
 }
 
