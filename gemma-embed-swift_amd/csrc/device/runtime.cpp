@@ -143,12 +143,17 @@ struct ge_q8_matrix {
     ge::Q8Dev m;
 };
 
+namespace ge {
+constexpr int kMaxParts = 2;  // streams a large batch is split over (2 measured fastest of 1-4)
+}
+
 struct ge_ctx {
     int device = 0;
     hipStream_t stream = nullptr;
-    // The second half of a split batch runs its layers on stream2 (see stage()).
-    hipStream_t stream2 = nullptr;
-    hipEvent_t ev_start = nullptr, ev_stop = nullptr, ev_fork = nullptr, ev_join = nullptr;
+    // Part p > 0 of a split batch runs its layers on part_stream[p] (see stage()).
+    hipStream_t part_stream[ge::kMaxParts] = {};
+    hipEvent_t part_join[ge::kMaxParts] = {};
+    hipEvent_t ev_start = nullptr, ev_stop = nullptr, ev_fork = nullptr;
     std::string err, name;
     bool has_model = false;
     ge::DevModel model;
@@ -157,9 +162,10 @@ struct ge_ctx {
     ge::Workspace ws;
     // staged batch
     int staged_tokens = -1, staged_seqs = 0, staged_work = 0, staged_work2 = 0, staged_vt_cols = 0;
-    // Split batch: rows [0, split_row) with work2 items [0, split_work2) on stream, the rest on
-    // stream2; 0 = not split.
-    int split_row = 0, split_work2 = 0;
+    // Split batch: part p is rows [part_row[p], part_row[p + 1]) with work2 items
+    // [part_work[p], part_work[p + 1]); n_parts 1 = not split.
+    int n_parts = 1;
+    int part_row[ge::kMaxParts + 1] = {}, part_work[ge::kMaxParts + 1] = {};
     // profiling
     bool prof = false;
     std::string prof_prefix;
@@ -735,22 +741,40 @@ void stage(ge_ctx* c, const int32_t* tokens, const int32_t* positions, int n, co
             for (uint32_t q0 = 0; q0 < seqs[s].length; q0 += kAttnQueriesV2)
                 work2.push_back(AttnWork{seqs[s].start, seqs[s].length, q0, vl.start[size_t(s)]});
     }
-    // Split a large batch of several sequences into two halves of whole sequences, near n / 2,
-    // whose layers run on two streams: one half's memory-bound kernels and its kernels' start
-    // and end phases overlap the other half's work.
-    int split_row = 0, split_work2 = 0;
+    // Split a large batch of several sequences into parts of whole sequences, cut at the
+    // sequence starts nearest to p n / P, whose layers run on their own streams: one part's
+    // memory-bound kernels and its kernels' start and end phases overlap the others' work.
+    int n_parts = 1;
+    int part_row[kMaxParts + 1] = {0}, part_work[kMaxParts + 1] = {0};
     if (m.all_fused && n >= kSplitMinTokens && n_seqs >= 2) {
-        std::vector<uint32_t> starts;
+        const int want = kMaxParts;
+        std::vector<int> starts;
         for (int s = 0; s < n_seqs; s++)
-            if (seqs[s].length && seqs[s].start > 0) starts.push_back(seqs[s].start);
-        int best = 0;
-        for (uint32_t r : starts)
-            if (!best || std::abs(int(r) - n / 2) < std::abs(best - n / 2)) best = int(r);
-        if (best > 0 && best < n) {
-            split_row = best;
-            std::stable_partition(work2.begin(), work2.end(), [&](const AttnWork& a) { return int(a.seq_start) < split_row; });
-            split_work2 = int(std::count_if(work2.begin(), work2.end(), [&](const AttnWork& a) { return int(a.seq_start) < split_row; }));
-            if (split_work2 == 0 || split_work2 == int(work2.size())) split_row = split_work2 = 0;
+            if (seqs[s].length && seqs[s].start > 0) starts.push_back(int(seqs[s].start));
+        std::sort(starts.begin(), starts.end());
+        std::vector<int> cuts;
+        for (int p = 1; p < want; p++) {
+            const int target = int((int64_t)n * p / want);
+            int best = -1;
+            for (int r : starts)
+                if (r > (cuts.empty() ? 0 : cuts.back()) && (best < 0 || std::abs(r - target) < std::abs(best - target)))
+                    best = r;
+            if (best > 0 && best < n) cuts.push_back(best);
+        }
+        if (!cuts.empty()) {
+            n_parts = int(cuts.size()) + 1;
+            for (int p = 1; p < n_parts; p++) part_row[p] = cuts[size_t(p) - 1];
+            part_row[n_parts] = n;
+            auto part_of = [&](const AttnWork& a) {
+                int p = 0;
+                while (p + 1 < n_parts && int(a.seq_start) >= part_row[p + 1]) p++;
+                return p;
+            };
+            std::stable_sort(work2.begin(), work2.end(), [&](const AttnWork& a, const AttnWork& b) { return part_of(a) < part_of(b); });
+            for (const AttnWork& a : work2) part_work[part_of(a) + 1]++;
+            for (int p = 0; p < n_parts; p++) part_work[p + 1] += part_work[p];
+            for (int p = 0; p < n_parts; p++)
+                if (part_work[p + 1] == part_work[p]) n_parts = 1;  // a part without work: do not split
         }
     }
     ensure_workspace(c, n, n_seqs, int(work.size()), int(work2.size()), vl.cols);
@@ -770,8 +794,9 @@ void stage(ge_ctx* c, const int32_t* tokens, const int32_t* positions, int n, co
     c->staged_work = int(work.size());
     c->staged_work2 = int(work2.size());
     c->staged_vt_cols = vl.cols;
-    c->split_row = split_row;
-    c->split_work2 = split_work2;
+    c->n_parts = n_parts;
+    std::copy(part_row, part_row + kMaxParts + 1, c->part_row);
+    std::copy(part_work, part_work + kMaxParts + 1, c->part_work);
 }
 
 // ---------------------------------------------------------------- forward
@@ -875,9 +900,9 @@ void encode(ge_ctx* c, StopPoint* sp) {
     launch(c, "mean_pool", [&] { return launch_mean_pool(s, w.out, w.seqs, c->staged_seqs, m.out_dims, w.pooled); });
 }
 
-// The forward of a split batch (see stage()): every layer's kernels run for rows
-// [0, split_row) on c->stream and for the rest on c->stream2, launched alternately, so the two
-// halves' kernels overlap. Only layers with the fused QKV epilogue and the LDS-copy attention.
+// The forward of a split batch (see stage()): every layer's kernels run for each part's rows
+// on the part's stream, launched part after part, so the parts' kernels overlap. Only layers
+// with the fused QKV epilogue and the LDS-copy attention.
 void encode_split(ge_ctx* c) {
     const DevModel& m = c->model;
     Workspace& w = c->ws;
@@ -888,11 +913,13 @@ void encode_split(ge_ctx* c) {
         const AttnWork* work;
         int n_work;
     };
-    const Half halves[2] = {{c->stream, 0, c->split_row, w.work2, c->split_work2},
-                            {c->stream2, c->split_row, T - c->split_row, w.work2 + c->split_work2,
-                             c->staged_work2 - c->split_work2}};
+    (void)T;
+    std::vector<Half> halves;
+    for (int p = 0; p < c->n_parts; p++)
+        halves.push_back(Half{c->part_stream[p], c->part_row[p], c->part_row[p + 1] - c->part_row[p],
+                              w.work2 + c->part_work[p], c->part_work[p + 1] - c->part_work[p]});
     hip_check(hipEventRecord(c->ev_fork, c->stream), "hipEventRecord");
-    hip_check(hipStreamWaitEvent(c->stream2, c->ev_fork, 0), "hipStreamWaitEvent");
+    for (int p = 1; p < c->n_parts; p++) hip_check(hipStreamWaitEvent(c->part_stream[p], c->ev_fork, 0), "hipStreamWaitEvent");
     uint16_t* t16 = reinterpret_cast<uint16_t*>(w.t);
     for (const Half& H : halves)
         launch(c, "embed_norm", [&] {
@@ -956,15 +983,17 @@ void encode_split(ge_ctx* c) {
         launch(c, "gemm_output", [&] {
             return launch_gemm_q8(H.s, m.output, w.h + (size_t)H.r0 * D, H.T, w.out + (size_t)H.r0 * m.out_dims, kEpiF32);
         });
-    hip_check(hipEventRecord(c->ev_join, c->stream2), "hipEventRecord");
-    hip_check(hipStreamWaitEvent(c->stream, c->ev_join, 0), "hipStreamWaitEvent");
+    for (int p = 1; p < c->n_parts; p++) {
+        hip_check(hipEventRecord(c->part_join[p], c->part_stream[p]), "hipEventRecord");
+        hip_check(hipStreamWaitEvent(c->stream, c->part_join[p], 0), "hipStreamWaitEvent");
+    }
     launch(c, "mean_pool", [&] { return launch_mean_pool(c->stream, w.out, w.seqs, c->staged_seqs, m.out_dims, w.pooled); });
 }
 
 void run_forward(ge_ctx* c, double* gpu_seconds) {
     if (c->staged_tokens < 0) fail(GE_ERR_STATE, "no batch is staged");
     hip_check(hipEventRecord(c->ev_start, c->stream), "hipEventRecord");
-    if (c->split_row > 0 && !c->prof)
+    if (c->n_parts > 1 && !c->prof)
         encode_split(c);
     else
         encode(c, nullptr);
@@ -1094,11 +1123,15 @@ int ge_create(int device, ge_ctx** out) {
     c->device = device;
     int rc = guarded(c.get(), [&] {
         ge::hip_check(hipStreamCreateWithFlags(&c->stream, hipStreamNonBlocking), "hipStreamCreate");
-        ge::hip_check(hipStreamCreateWithFlags(&c->stream2, hipStreamNonBlocking), "hipStreamCreate");
+        c->part_stream[0] = c->stream;
+        for (int p = 1; p < ge::kMaxParts; p++) {
+            ge::hip_check(hipStreamCreateWithFlags(&c->part_stream[p], hipStreamNonBlocking), "hipStreamCreate");
+            ge::hip_check(hipEventCreateWithFlags(&c->part_join[p], hipEventDisableTiming), "hipEventCreate");
+        }
         ge::hip_check(hipEventCreate(&c->ev_start), "hipEventCreate");
         ge::hip_check(hipEventCreate(&c->ev_stop), "hipEventCreate");
         ge::hip_check(hipEventCreateWithFlags(&c->ev_fork, hipEventDisableTiming), "hipEventCreate");
-        ge::hip_check(hipEventCreateWithFlags(&c->ev_join, hipEventDisableTiming), "hipEventCreate");
+
         hipDeviceProp_t prop;
         ge::hip_check(hipGetDeviceProperties(&prop, device), "hipGetDeviceProperties");
         c->name = std::string(prop.name) + " (" + prop.gcnArchName + ")";
@@ -1109,7 +1142,11 @@ int ge_create(int device, ge_ctx** out) {
     if (rc != GE_OK) {
         ge::g_create_error = c->err;
         if (c->stream) (void)hipStreamDestroy(c->stream);
-        if (c->stream2) (void)hipStreamDestroy(c->stream2);
+        for (int p = 1; p < ge::kMaxParts; p++) {
+            if (c->part_stream[p]) (void)hipStreamDestroy(c->part_stream[p]);
+            if (c->part_join[p]) (void)hipEventDestroy(c->part_join[p]);
+        }
+        if (c->ev_fork) (void)hipEventDestroy(c->ev_fork);
         return rc;
     }
     *out = c.release();
@@ -1130,10 +1167,12 @@ void ge_destroy(ge_ctx* c) {
     if (c->ev_start) (void)hipEventDestroy(c->ev_start);
     if (c->ev_stop) (void)hipEventDestroy(c->ev_stop);
     if (c->ev_fork) (void)hipEventDestroy(c->ev_fork);
-    if (c->ev_join) (void)hipEventDestroy(c->ev_join);
-    if (c->stream2) (void)hipStreamSynchronize(c->stream2);
+    for (int p = 1; p < ge::kMaxParts; p++) {
+        if (c->part_stream[p]) (void)hipStreamSynchronize(c->part_stream[p]);
+        if (c->part_stream[p]) (void)hipStreamDestroy(c->part_stream[p]);
+        if (c->part_join[p]) (void)hipEventDestroy(c->part_join[p]);
+    }
     if (c->stream) (void)hipStreamDestroy(c->stream);
-    if (c->stream2) (void)hipStreamDestroy(c->stream2);
     delete c;
 }
 

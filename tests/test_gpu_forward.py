@@ -106,6 +106,30 @@ def test_config2_per_layer_vs_oracle(c2_model, c2_oracle, config2_batch):
     print(f"worst l_out max_rel {worst:.3e}", flush=True)
 
 
+def test_split_batch_matches_single_stream(c2_model, config2_batch):
+    """A pack of >= 4096 tokens runs as two halves of whole sequences on two streams; with
+    profiling on, the same pack runs on one stream. Same kernels on the same rows: the vectors
+    must be identical."""
+    ctx = c2_model.context
+    print("config2 pack of 16384: two streams vs one", flush=True)
+    split, _ = ctx.forward(config2_batch)
+    ctx.profile_enable("")
+    try:
+        single, _ = ctx.forward(config2_batch)
+    finally:
+        ctx.profile_disable()
+    assert np.array_equal(split, single)
+    # an odd number of uneven sequences: the cut lands at a sequence start near the middle
+    uneven = [t[: 100 + 61 * i] for i, t in enumerate(config2_batch[:13])]
+    split, _ = ctx.forward(uneven)
+    ctx.profile_enable("")
+    try:
+        single, _ = ctx.forward(uneven)
+    finally:
+        ctx.profile_disable()
+    assert np.array_equal(split, single)
+
+
 def test_packing_invariance_and_determinism(c2_model, config2_batch):
     batch = config2_batch[:8]
     a = c2_model.embed_tokens(batch)
