@@ -498,6 +498,226 @@ __global__ __launch_bounds__(2 * G * 64) void attention_v2_kernel(const uint16_t
         }
 }
 
+// ============================================================================ attention, 16-query waves
+//
+// The same work item (64 query rows of one sequence, one KV head) and the same K / V^T stream as
+// attention_v2_kernel, with 4 G waves of 16 queries each (wave w: query head kvh * G + w % G,
+// rows q0 + 16 (w / G) .. + 15) on v_mfma_f32_16x16x32_f16. A wave's accumulators shrink to
+// 16 queries x hd (64 registers at hd 256) and its queries' fragments fit in registers (32),
+// so nothing but K and V^T lives in LDS and G = 3 gives 12 waves, three per SIMD: while one
+// wave is in its softmax, the SIMD's other waves keep the MFMA pipe busy.
+//
+// LDS per stage (one block of 32 keys), in fragment order (1 KB chunk = one operand fragment,
+// lane l's 16 bytes at 16 l):
+//   K chunk (ks, m), m = 0, 1: A operand of S^T tile m over head dims 32 ks .. + 31; lane l
+//     holds key 8 ((l % 16) / 4) + 4 m + l % 4, head dims 32 ks + 8 (l / 16) + [0, 8);
+//   V^T chunk dt: A operand of O^T rows 16 dt .. + 15; lane l holds head dim 16 dt + l % 16,
+//     keys 8 (l / 16) + [0, 8).
+// With that key order, lane l's accumulators of the two S^T tiles (rows 4 (l / 16) + r) are
+// keys 8 (l / 16) + [0, 8) of query l % 16: exactly the B operand of the P.V product, so P
+// goes from the S accumulators to the MFMA with only the fp16 conversion. A query's 32 scores
+// sit in lanes q, q + 16, q + 32, q + 48; its softmax reductions are two lane exchanges.
+namespace attn3 {
+constexpr int NS = 2;     // key blocks in LDS
+constexpr int BKV = 32;   // keys per block
+}  // namespace attn3
+
+template <int HD>
+constexpr int attention_v3_lds_bytes() { return attn3::NS * 2 * attn3::BKV * HD * 2; }
+
+template <int HD, int G>
+__global__ __launch_bounds__(4 * G * 64) void attention_v3_kernel(const uint16_t* __restrict__ Qg,
+                                                                  const uint16_t* __restrict__ Kg,
+                                                                  const uint16_t* __restrict__ VTg,
+                                                                  uint16_t* __restrict__ Og,
+                                                                  const AttnWork* __restrict__ work, int H, int KV,
+                                                                  int vt_cols, int hw, float scale_log2) {
+    using namespace attn3;
+    constexpr int QB = 64, NW = 4 * G, KS = HD / 32, DT = HD / 16;
+    constexpr int K_BYTES = BKV * HD * 2, STAGE = 2 * K_BYTES;
+    constexpr int KCH = K_BYTES / 1024, CH = 2 * KCH;  // K chunks (ks, m), then V^T chunks dt
+    static_assert(KCH == 2 * KS && KCH == DT, "chunk counts");
+    constexpr int CPW = (CH + NW - 1) / NW;  // copies per wave per block (some waves repeat one)
+    extern __shared__ __attribute__((aligned(1024))) unsigned char ldsa[];
+
+    // XCD-aware order, as in attention_v2_kernel.
+    const int nb = int(gridDim.x), full = nb / 8 * 8, bx = int(blockIdx.x);
+    const int widx = bx < full ? (bx % 8) * (full / 8) + bx / 8 : bx;
+    const int seq_start = __builtin_amdgcn_readfirstlane(int(work[widx].seq_start));
+    const int len = __builtin_amdgcn_readfirstlane(int(work[widx].seq_len));
+    const int wq0 = __builtin_amdgcn_readfirstlane(int(work[widx].q0));
+    const int vt_start = __builtin_amdgcn_readfirstlane(int(work[widx].vt_start));
+    const int kvh = blockIdx.y;
+    const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(int(threadIdx.x >> 6));
+    const int h = kvh * G + wave % G;
+    const int q0 = wq0 + (wave / G) * 16;
+    const int l16 = lane & 15, g4 = lane >> 4;  // query column, lane group
+    const int qi = q0 + l16;
+    const int qStride = H * HD, kvStride = KV * HD;
+
+    int kstart = 0, kend = len;
+    if (hw > 0) {
+        kstart = max(wq0 - hw, 0);
+        kend = min(wq0 + QB + hw, len);
+    }
+    kstart = kstart / BKV * BKV;
+    const int nblocks = (kend - kstart + BKV - 1) / BKV;
+
+    // Buffer resources over the sequence's rows of the KV head and over the head's V^T rows from
+    // the sequence's first column on: copies past them read zeros.
+    const __amdgpu_buffer_rsrc_t kr =
+        buffer_rsrc(Kg + (size_t)seq_start * kvStride + kvh * HD, uint32_t(((len - 1) * kvStride + HD) * 2));
+    const __amdgpu_buffer_rsrc_t vr = buffer_rsrc(VTg + (size_t)kvh * HD * vt_cols + vt_start,
+                                                  uint32_t(((HD - 1) * vt_cols + (vt_cols - vt_start)) * 2));
+    const uint32_t klane = uint32_t(((8 * (l16 >> 2) + (lane & 3)) * kvStride + 8 * g4) * 2);
+    const uint32_t vlane = uint32_t((l16 * vt_cols + 8 * g4) * 2);
+    // Every wave issues CPW copies per block (the waves past the last chunk repeat their first
+    // one), so one vmcnt count fits every wave.
+#define A3_ISSUE(kb, b)                                                                                    \
+    do {                                                                                                   \
+        _Pragma("unroll") for (int i = 0; i < CPW; i++) {                                                  \
+            int c = wave + i * NW;                                                                         \
+            if (c >= CH) c = wave;                                                                         \
+            unsigned char* dst_ = ldsa + (b) * STAGE + c * 1024;                                           \
+            if (c < KCH) {                                                                                 \
+                const int ks_ = c >> 1, m_ = c & 1;                                                        \
+                lds_copy16(kr, dst_, klane + uint32_t(((kb) + 4 * m_) * kvStride * 2 + ks_ * 64), 0);      \
+            } else {                                                                                       \
+                lds_copy16(vr, dst_, vlane + uint32_t((c - KCH) * 16 * vt_cols * 2 + (kb) * 2), 0);        \
+            }                                                                                              \
+        }                                                                                                  \
+    } while (0)
+
+    // This wave's query fragments (B operand of S^T = K Q^T): lane l: query qi (rows past the
+    // sequence re-read its last row; their outputs are never stored), head dims 32 ks + 8 (l / 16).
+    half8_t qa[KS];
+    {
+        const __amdgpu_buffer_rsrc_t qr =
+            buffer_rsrc(Qg + (size_t)seq_start * qStride + h * HD, uint32_t(((len - 1) * qStride + HD) * 2));
+        const uint32_t qo = uint32_t((min(qi, len - 1) * qStride + 8 * g4) * 2);
+#pragma unroll
+        for (int ks = 0; ks < KS; ks++)
+            qa[ks] = __builtin_bit_cast(half8_t, __builtin_amdgcn_raw_buffer_load_b128(qr, qo + ks * 64, 0, 0));
+    }
+
+    float4_t o[DT];
+#pragma unroll
+    for (int i = 0; i < DT; i++) o[i] = float4_t{0.0f, 0.0f, 0.0f, 0.0f};
+    float m_run = -INFINITY, l_run = 0.0f;
+
+#pragma unroll
+    for (int s = 0; s < NS - 1; s++)
+        if (s < nblocks) A3_ISSUE(kstart + s * BKV, s);
+    int b = 0;
+    for (int it = 0; it < nblocks; it++) {
+        const int kb = kstart + it * BKV;
+        // Block it has landed once at most the later blocks' copies are in flight; the barrier
+        // then covers every wave's copies, and (after each wave's LDS reads) frees the buffer
+        // the next copies overwrite.
+        static_assert(NS == 2, "the wait below assumes two stages");
+        wait_vmcnt<0>();
+        wait_lgkmcnt0();
+        workgroup_barrier();
+        if (it + NS - 1 < nblocks) A3_ISSUE(kstart + (it + NS - 1) * BKV, b ^ 1);
+        const unsigned char* const kf = ldsa + b * STAGE + lane * 16;
+        const unsigned char* const vf = kf + K_BYTES;
+        // S^T tiles m = 0, 1 over the head dims; K fragments read PF k-steps ahead
+        constexpr int PF = 2, RING = PF + 1;
+        float4_t s0 = {0.0f, 0.0f, 0.0f, 0.0f}, s1 = {0.0f, 0.0f, 0.0f, 0.0f};
+        half8_t ka[RING][2];
+#pragma unroll
+        for (int f = 0; f < PF; f++) {
+            ka[f][0] = *reinterpret_cast<const half8_t*>(kf + (2 * f) * 1024);
+            ka[f][1] = *reinterpret_cast<const half8_t*>(kf + (2 * f + 1) * 1024);
+        }
+#pragma unroll
+        for (int ks = 0; ks < KS; ks++) {
+            if (ks + PF < KS) {
+                ka[(ks + PF) % RING][0] = *reinterpret_cast<const half8_t*>(kf + (2 * (ks + PF)) * 1024);
+                ka[(ks + PF) % RING][1] = *reinterpret_cast<const half8_t*>(kf + (2 * (ks + PF) + 1) * 1024);
+            }
+            // keep the reads ahead of the MFMAs (the scheduler would otherwise sink them)
+            __builtin_amdgcn_sched_barrier(0);
+            s0 = __builtin_amdgcn_mfma_f32_16x16x32_f16(ka[ks % RING][0], qa[ks], s0, 0, 0, 0);
+            s1 = __builtin_amdgcn_mfma_f32_16x16x32_f16(ka[ks % RING][1], qa[ks], s1, 0, 0, 0);
+        }
+        // the first V^T fragments are read while the softmax runs
+        half8_t va[RING];
+#pragma unroll
+        for (int f = 0; f < PF; f++) va[f] = *reinterpret_cast<const half8_t*>(vf + f * 1024);
+        // this lane's scores: keys kb + 8 g4 + e, e = 0..7
+        float sc[8] = {s0[0], s0[1], s0[2], s0[3], s1[0], s1[1], s1[2], s1[3]};
+        const bool inside = kb + BKV <= len && (hw == 0 || (kb >= q0 + 15 - hw && kb + BKV - 1 <= q0 + hw));
+        if (!inside) {
+            // keys past the sequence, and (sliding window) keys farther than hw from the query
+            const int lim = hw > 0 ? hw : 1 << 30;
+#pragma unroll
+            for (int e = 0; e < 8; e++) {
+                const int key = kb + 8 * g4 + e;
+                const bool valid = (key < len) & (abs(qi - key) <= lim);
+                sc[e] = valid ? sc[e] : -INFINITY;
+            }
+        }
+        // max in the raw score domain (scale > 0), then scaled to log2 units
+        float bmax = fmaxf(fmaxf(fmaxf(sc[0], sc[1]), fmaxf(sc[2], sc[3])), fmaxf(fmaxf(sc[4], sc[5]), fmaxf(sc[6], sc[7])));
+        bmax = fmaxf(bmax, __shfl_xor(bmax, 16, 64));
+        bmax = fmaxf(bmax, __shfl_xor(bmax, 32, 64)) * scale_log2;
+        // Lazy rescaling, as in attention_v2_kernel: the reference point moves only when a
+        // score exceeds it by more than 2^8, so P stays below 256.
+        if (__builtin_amdgcn_ballot_w64(bmax > m_run + 8.0f)) {
+            const float m_new = fmaxf(m_run, bmax);
+            const float alpha = m_new == -INFINITY ? 1.0f : __builtin_amdgcn_exp2f(m_run - m_new);
+            l_run *= alpha;
+#pragma unroll
+            for (int i = 0; i < DT; i++) o[i] *= alpha;
+            m_run = m_new;
+        }
+        const float m_ref = m_run == -INFINITY ? 0.0f : m_run;
+        float sum = 0.0f;
+        half8_t pb;
+#pragma unroll
+        for (int e = 0; e < 8; e++) {
+            const float p = __builtin_amdgcn_exp2f(__builtin_fmaf(sc[e], scale_log2, -m_ref));
+            sum += p;
+            pb[e] = _Float16(p);
+        }
+        sum += __shfl_xor(sum, 16, 64);
+        sum += __shfl_xor(sum, 32, 64);
+        l_run += sum;
+        // O^T += V^T P^T: head-dim tiles dt of 16 rows, the block's 32 keys as one k-step
+#pragma unroll
+        for (int dt = 0; dt < DT; dt++) {
+            if (dt + PF < DT) va[(dt + PF) % RING] = *reinterpret_cast<const half8_t*>(vf + (dt + PF) * 1024);
+            __builtin_amdgcn_sched_barrier(0);
+            o[dt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(va[dt % RING], pb, o[dt], 0, 0, 0);
+        }
+        b ^= 1;
+    }
+#undef A3_ISSUE
+    wait_vmcnt<0>();
+    if (qi >= len) return;
+    const float inv = l_run > 0.0f ? 1.0f / l_run : 0.0f;
+    // o[dt], lane l: head dims 16 dt + 4 (l / 16) + r of query qi
+    _Float16* op = reinterpret_cast<_Float16*>(Og) + (size_t)(seq_start + qi) * qStride + h * HD + 4 * g4;
+#pragma unroll
+    for (int dt = 0; dt < DT; dt++) {
+        half4_t v4;
+#pragma unroll
+        for (int r = 0; r < 4; r++) v4[r] = _Float16(o[dt][r] * inv);
+        *reinterpret_cast<half4_t*>(op + dt * 16) = v4;
+    }
+}
+
+template <int HD, int G>
+static hipError_t attention_v3_dispatch(hipStream_t s, const uint16_t* q, const uint16_t* k, const uint16_t* vt,
+                                        int vt_cols, uint16_t* o, const AttnWork* work, int n_work, int H, int KV, int hw,
+                                        float scale) {
+    const float scale_log2 = scale * 1.4426950408889634f;
+    launch_kernel(attention_v3_kernel<HD, G>, dim3(n_work, KV), dim3(4 * G * 64), uint32_t(attention_v3_lds_bytes<HD>()), s,
+                  q, k, vt, o, work, H, KV, vt_cols, hw, scale_log2);
+    return hipGetLastError();
+}
+
 template <int HD, int G>
 static hipError_t attention_v2_dispatch(hipStream_t s, const uint16_t* q, const uint16_t* k, const uint16_t* vt,
                                         int vt_cols, uint16_t* o, const AttnWork* work, int n_work, int H, int KV, int hw,
@@ -513,9 +733,10 @@ static hipError_t attention_v2_dispatch_g(hipStream_t s, const uint16_t* q, cons
                                           int vt_cols, uint16_t* o, const AttnWork* work, int n_work, int H, int KV,
                                           int hw, float scale) {
     switch (H / KV) {
-    case 1: return attention_v2_dispatch<HD, 1>(s, q, k, vt, vt_cols, o, work, n_work, H, KV, hw, scale);
-    case 2: return attention_v2_dispatch<HD, 2>(s, q, k, vt, vt_cols, o, work, n_work, H, KV, hw, scale);
-    case 3: return attention_v2_dispatch<HD, 3>(s, q, k, vt, vt_cols, o, work, n_work, H, KV, hw, scale);
+    // groups of up to 3 query heads: 16-query waves (4 G waves, at most 3 per SIMD)
+    case 1: return attention_v3_dispatch<HD, 1>(s, q, k, vt, vt_cols, o, work, n_work, H, KV, hw, scale);
+    case 2: return attention_v3_dispatch<HD, 2>(s, q, k, vt, vt_cols, o, work, n_work, H, KV, hw, scale);
+    case 3: return attention_v3_dispatch<HD, 3>(s, q, k, vt, vt_cols, o, work, n_work, H, KV, hw, scale);
     case 4:
         if constexpr (attention_v2_lds_bytes<HD, 4>() <= 160 * 1024)
             return attention_v2_dispatch<HD, 4>(s, q, k, vt, vt_cols, o, work, n_work, H, KV, hw, scale);
@@ -600,6 +821,12 @@ static hipError_t attention_v2_configure() {
                                hipFuncAttributeMaxDynamicSharedMemorySize, attention_v2_lds_bytes<HD, G>());
 }
 
+template <int HD, int G>
+static hipError_t attention_v3_configure() {
+    return hipFuncSetAttribute(reinterpret_cast<const void*>(&attention_v3_kernel<HD, G>),
+                               hipFuncAttributeMaxDynamicSharedMemorySize, attention_v3_lds_bytes<HD>());
+}
+
 hipError_t configure_kernels() {
     hipError_t e = gemm_configure();
     if (e == hipSuccess) e = attention_configure_all<128, 128>();
@@ -610,6 +837,12 @@ hipError_t configure_kernels() {
     if (e == hipSuccess) e = attention_v2_configure<256, 1>();
     if (e == hipSuccess) e = attention_v2_configure<256, 2>();
     if (e == hipSuccess) e = attention_v2_configure<256, 3>();
+    if (e == hipSuccess) e = attention_v3_configure<128, 1>();
+    if (e == hipSuccess) e = attention_v3_configure<128, 2>();
+    if (e == hipSuccess) e = attention_v3_configure<128, 3>();
+    if (e == hipSuccess) e = attention_v3_configure<256, 1>();
+    if (e == hipSuccess) e = attention_v3_configure<256, 2>();
+    if (e == hipSuccess) e = attention_v3_configure<256, 3>();
     if (e == hipSuccess) e = attention_configure_all<256, 256>();
     if (e == hipSuccess) e = attention_configure_all<512, 256>();
     return e;

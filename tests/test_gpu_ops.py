@@ -128,6 +128,7 @@ ATTN_CASES = [  # (lengths, H, KV, hd, half_window): the reference's packed-leng
     ([300, 31], 4, 1, 512, 0),
     ([96, 40], 2, 1, 128, 8),
     ([257], 4, 4, 128, 0),
+    ([130, 64], 4, 1, 128, 32),  # four query heads per KV head: the 32-query-wave kernel
 ]
 
 
