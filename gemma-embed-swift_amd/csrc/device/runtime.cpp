@@ -919,7 +919,8 @@ void encode_split(ge_ctx* c) {
         halves.push_back(Half{c->part_stream[p], c->part_row[p], c->part_row[p + 1] - c->part_row[p],
                               w.work2 + c->part_work[p], c->part_work[p + 1] - c->part_work[p]});
     hip_check(hipEventRecord(c->ev_fork, c->stream), "hipEventRecord");
-    for (int p = 1; p < c->n_parts; p++) hip_check(hipStreamWaitEvent(c->part_stream[p], c->ev_fork, 0), "hipStreamWaitEvent");
+    for (int p = 0; p < c->n_parts; p++)
+        if (c->part_stream[p] != c->stream) hip_check(hipStreamWaitEvent(c->part_stream[p], c->ev_fork, 0), "hipStreamWaitEvent");
     uint16_t* t16 = reinterpret_cast<uint16_t*>(w.t);
     for (const Half& H : halves)
         launch(c, "embed_norm", [&] {
@@ -983,10 +984,11 @@ void encode_split(ge_ctx* c) {
         launch(c, "gemm_output", [&] {
             return launch_gemm_q8(H.s, m.output, w.h + (size_t)H.r0 * D, H.T, w.out + (size_t)H.r0 * m.out_dims, kEpiF32);
         });
-    for (int p = 1; p < c->n_parts; p++) {
-        hip_check(hipEventRecord(c->part_join[p], c->part_stream[p]), "hipEventRecord");
-        hip_check(hipStreamWaitEvent(c->stream, c->part_join[p], 0), "hipStreamWaitEvent");
-    }
+    for (int p = 0; p < c->n_parts; p++)
+        if (c->part_stream[p] != c->stream) {
+            hip_check(hipEventRecord(c->part_join[p], c->part_stream[p]), "hipEventRecord");
+            hip_check(hipStreamWaitEvent(c->stream, c->part_join[p], 0), "hipStreamWaitEvent");
+        }
     launch(c, "mean_pool", [&] { return launch_mean_pool(c->stream, w.out, w.seqs, c->staged_seqs, m.out_dims, w.pooled); });
 }
 
@@ -1124,8 +1126,8 @@ int ge_create(int device, ge_ctx** out) {
     int rc = guarded(c.get(), [&] {
         ge::hip_check(hipStreamCreateWithFlags(&c->stream, hipStreamNonBlocking), "hipStreamCreate");
         c->part_stream[0] = c->stream;
-        for (int p = 1; p < ge::kMaxParts; p++) {
-            ge::hip_check(hipStreamCreateWithFlags(&c->part_stream[p], hipStreamNonBlocking), "hipStreamCreate");
+        for (int p = 0; p < ge::kMaxParts; p++) {
+            if (p > 0) ge::hip_check(hipStreamCreateWithFlags(&c->part_stream[p], hipStreamNonBlocking), "hipStreamCreate");
             ge::hip_check(hipEventCreateWithFlags(&c->part_join[p], hipEventDisableTiming), "hipEventCreate");
         }
         ge::hip_check(hipEventCreate(&c->ev_start), "hipEventCreate");
@@ -1141,11 +1143,11 @@ int ge_create(int device, ge_ctx** out) {
     });
     if (rc != GE_OK) {
         ge::g_create_error = c->err;
-        if (c->stream) (void)hipStreamDestroy(c->stream);
-        for (int p = 1; p < ge::kMaxParts; p++) {
-            if (c->part_stream[p]) (void)hipStreamDestroy(c->part_stream[p]);
+        for (int p = 0; p < ge::kMaxParts; p++) {
+            if (c->part_stream[p] && c->part_stream[p] != c->stream) (void)hipStreamDestroy(c->part_stream[p]);
             if (c->part_join[p]) (void)hipEventDestroy(c->part_join[p]);
         }
+        if (c->stream) (void)hipStreamDestroy(c->stream);
         if (c->ev_fork) (void)hipEventDestroy(c->ev_fork);
         return rc;
     }
@@ -1167,9 +1169,11 @@ void ge_destroy(ge_ctx* c) {
     if (c->ev_start) (void)hipEventDestroy(c->ev_start);
     if (c->ev_stop) (void)hipEventDestroy(c->ev_stop);
     if (c->ev_fork) (void)hipEventDestroy(c->ev_fork);
-    for (int p = 1; p < ge::kMaxParts; p++) {
-        if (c->part_stream[p]) (void)hipStreamSynchronize(c->part_stream[p]);
-        if (c->part_stream[p]) (void)hipStreamDestroy(c->part_stream[p]);
+    for (int p = 0; p < ge::kMaxParts; p++) {
+        if (c->part_stream[p] && c->part_stream[p] != c->stream) {
+            (void)hipStreamSynchronize(c->part_stream[p]);
+            (void)hipStreamDestroy(c->part_stream[p]);
+        }
         if (c->part_join[p]) (void)hipEventDestroy(c->part_join[p]);
     }
     if (c->stream) (void)hipStreamDestroy(c->stream);
