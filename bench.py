@@ -32,7 +32,6 @@ sys.path.insert(0, os.path.join(ROOT, "gemma-embed-swift_amd"))
 METRIC = "embedded tokens/sec, 24L Q8_0 encoder 32×512 @1 GPU; Q8 GEMM % MFMA peak"
 PEAK_FP16_TFLOPS = 2500.0  # MI355X dense fp16/bf16 MFMA
 HBM_PEAK_GBS = 8000.0
-COPY_ELEMS = 1 << 28  # calibration kernel of the --probe run: reads 512 MiB, writes 1 GiB
 TEXTS, TOKENS = 32, 512
 D, FF, OUT, HD, H, KV, LAYERS = 768, 1152, 768, 256, 3, 1, 24
 
@@ -79,9 +78,10 @@ def attention_flops(lengths, window=512, pattern=(1, 1, 1, 1, 1, 0) * 4):
 
 
 def measured_traffic(label: str):
-    """HBM bytes per launch of `label` at this workload, from the committed rocprofv3 summary of two
-    counter runs of `bench.py --probe` (FETCH_SIZE, then WRITE_SIZE, each scaled by what the same
-    counter reads for a conversion kernel of known size). Returns (bytes, kernel) or (None, None)."""
+    """HBM bytes per launch of `label` at this workload, from the committed rocprofv3 summary of
+    counter runs of the standalone probe `gemma-embed-swift_amd/ge_probe` over the same kernel at
+    the same shape (FETCH_SIZE, then WRITE_SIZE, each scaled by what the same counter reads for a
+    conversion kernel of known size). Returns (bytes, kernel) or (None, None)."""
     import re
     path = os.path.join(ROOT, "profiles", f"{label}_config2_traffic.md")
     try:
@@ -91,6 +91,77 @@ def measured_traffic(label: str):
         return None, None
     m = re.search(rf"traffic_bytes_per_launch {label} (.+) grid (\d+): (\d+)", text)
     return (int(m.group(3)), m.group(1)) if m else (None, None)
+
+
+def library_gemm_comparison(reps: int = 30):
+    """This library's Q8_0 GEMM (`ge_op_gemm_q8`, fp16 activations in, fp16 out) against hipBLASLt
+    (through torch.matmul: the same activations times a dense fp16 weight, fp16 out) on the
+    forward's four projection shapes at config 2's M = 16384. The library's time per launch is
+    the mean of its dispatch events over `reps` synchronous calls; hipBLASLt is timed the same
+    way (events around each call, a synchronisation after it) and also back to back."""
+    import numpy as np
+    import torch
+    import gemma_embed as ge
+
+    m = TEXTS * TOKENS
+    shapes = (("qkv", (H + 2 * KV) * HD, D), ("o", D, H * HD), ("gate_up", 2 * FF, D), ("down", D, FF))
+    rng = np.random.default_rng(5)
+    ctx = ge.Context.create(0)
+    rows = []
+    try:
+        for name, n, k in shapes:
+            raw = rng.integers(0, 256, size=(n, k // 32, 34), dtype=np.uint8)
+            raw[:, :, 0:2] = np.frombuffer(np.full(n * (k // 32), 0.001, np.float16).tobytes(),
+                                           np.uint8).reshape(n, k // 32, 2)
+            x = (rng.standard_normal((m, k)) * 0.5).astype(np.float16)
+            w = ctx.q8_create(raw, n, k)
+            dx, dy = ctx.alloc(x.nbytes), ctx.alloc(m * n * 2)
+            try:
+                ctx.upload(dx, x)
+                ctx.gemm_q8(w, dx, m, dy, True)
+                ctx.profile_reset()
+                ctx.profile_enable("gemm")
+                for _ in range(reps):
+                    ctx.gemm_q8(w, dx, m, dy, True)
+                launches, total_ms = ctx.profile_stats()["gemm"]
+                ctx.profile_disable()
+            finally:
+                ctx.free(dx)
+                ctx.free(dy)
+                ctx.q8_destroy(w)
+            ours_us = total_ms * 1e3 / launches
+            tx = torch.from_numpy(x).cuda()
+            tw = torch.randn(n, k, device="cuda", dtype=torch.float16) * 0.01
+            for _ in range(3):
+                torch.matmul(tx, tw.t())
+            torch.cuda.synchronize()
+            # one call at a time with a synchronisation after each, as ge_op_gemm_q8 does
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            lib_ms = 0.0
+            for _ in range(reps):
+                e0.record()
+                torch.matmul(tx, tw.t())
+                e1.record()
+                torch.cuda.synchronize()
+                lib_ms += e0.elapsed_time(e1)
+            lib_us = lib_ms * 1e3 / reps
+            # and back to back
+            e0.record()
+            for _ in range(reps):
+                torch.matmul(tx, tw.t())
+            e1.record()
+            torch.cuda.synchronize()
+            lib_b2b_us = e0.elapsed_time(e1) * 1e3 / reps
+            flops = 2.0 * m * n * k
+            rows.append({"gemm": name, "M": m, "N": n, "K": k,
+                         "q8_us": round(ours_us, 2), "q8_frac": round(flops / ours_us * 1e-6 / PEAK_FP16_TFLOPS, 4),
+                         "hipblaslt_fp16_us": round(lib_us, 2), "hipblaslt_fp16_back_to_back_us": round(lib_b2b_us, 2),
+                         "hipblaslt_frac": round(flops / lib_us * 1e-6 / PEAK_FP16_TFLOPS, 4)})
+            log(f"{name}: q8 {ours_us:.2f} us, hipBLASLt fp16 {lib_us:.2f} us ({lib_b2b_us:.2f} back to back)")
+            del tx, tw
+    finally:
+        ctx.close()
+    return rows
 
 
 def cpu_baseline(model_path: str, batch, budget_s: float = 12.0):
@@ -126,14 +197,17 @@ def main():
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU oracle baseline")
     ap.add_argument("--model", default=None, help="existing config-2 GGUF (default: generate one)")
-    ap.add_argument("--probe", action="store_true",
-                    help="counter-collection run: a known-size conversion kernel (the calibration for HBM "
-                         "byte counters), then the warmup and timed steps only")
+    ap.add_argument("--library-gemm", action="store_true",
+                    help="only compare the Q8_0 GEMM with hipBLASLt (torch.matmul) on the forward's projection "
+                         "shapes and print that as one JSON line")
     args = ap.parse_args()
     if args.gpus != 1:
         print(json.dumps({"error": "this build runs on one GPU; --gpus above 1 is not supported "
                                    "(the forward shards as pure data parallelism, one context per GPU)"}))
         sys.exit(2)
+    if args.library_gemm:
+        print(json.dumps({"library_gemm": library_gemm_comparison(), "peak_tflops": PEAK_FP16_TFLOPS}))
+        return
 
     import numpy as np
     import gemma_embed as ge
@@ -151,14 +225,6 @@ def main():
     model = ge.EmbeddingModel.load(path, batch_token_budget=16384)
     ctx = model.context
     log(f"loaded on {model.info.device_name.decode()}")
-
-    if args.probe:
-        # fp16 -> fp32 conversion of COPY_ELEMS values: reads 2 and writes 4 bytes per value.
-        src, dst = ctx.alloc(2 * COPY_ELEMS), ctx.alloc(4 * COPY_ELEMS)
-        ctx.f16_to_f32(src, dst, COPY_ELEMS)
-        ctx.free(src)
-        ctx.free(dst)
-        log(f"calibration conversion of {COPY_ELEMS} values done")
 
     # ---- main measurement: one resident 16384-token pack per step
     ctx.batch_stage(batch)
@@ -187,10 +253,6 @@ def main():
     ms_per_step = elapsed * 1e3 / args.steps
     value = n_tokens / (elapsed / args.steps)
     log(f"resident pack: {ms_per_step:.3f} ms/step, {value:,.0f} tokens/s")
-    if args.probe:
-        model.close()
-        print(json.dumps({"probe": True, "ms_per_step": round(ms_per_step, 4), "value": round(value, 1)}))
-        return
 
     flops = gemm_flops(n_tokens)
     step_gemm_flops = LAYERS * (flops["gemm_qkv"] + flops["gemm_o"] + flops["gemm_gate_up"] + flops["gemm_down"]) \

@@ -1,0 +1,104 @@
+// ge_probe: a small standalone program for profilers (rocprofv3 kernel traces and counters).
+//
+// It runs one kernel of the forward at its config-2 shape through the C-ABI, with no Python and
+// no model file, so a profiler sees a short program with few dispatches:
+//
+//   ge_probe gate_up [reps]   the gate/up GEMM with the GeGLU epilogue (ge_op_gemm_q8_geglu:
+//                             M = 16384 tokens, K = 768, F = 1152 gate and 1152 up rows), the
+//                             forward's dominant kernel (Kernels.gemm with the geglu epilogue,
+//                             Metal/MetalForward.swift:524-557; Shaders/GEMM.metal:41-67)
+//   ge_probe calibrate        fp16 -> fp32 conversion of 2^28 values (reads 512 MiB, writes 1 GiB):
+//                             the known-size kernel that scales the HBM byte counters
+//
+// Inputs are synthetic: Q8_0 rows with random int8 quants and fp16 scales, activations uniform
+// in [-0.5, 0.5). Each call of the GeGLU entry point also interleaves the two matrices and builds
+// their fragment-order copy; a profile reads the GEMM kernel's own rows.
+#include <cstdint>
+#include <cstdio>
+#include <cstdlib>
+#include <cstring>
+#include <vector>
+
+#include "gemmaembed.h"
+#include "halfconv.hpp"
+#include "prng.hpp"
+
+namespace {
+
+int fail(ge_ctx* c, const char* what) {
+    std::fprintf(stderr, "ge_probe: %s: %s\n", what, c ? ge_last_error(c) : ge_create_error());
+    if (c) ge_destroy(c);
+    return 1;
+}
+
+// Q8_0 rows: per 32 values an fp16 scale then 32 int8 quants (34 bytes).
+std::vector<uint8_t> synth_q8(uint64_t seed, int rows, int cols) {
+    ge::SeededRandom rng(seed);
+    std::vector<uint8_t> raw((size_t)rows * (cols / 32) * 34);
+    for (size_t b = 0; b < raw.size() / 34; b++) {
+        uint8_t* blk = raw.data() + b * 34;
+        const uint16_t s = ge::float_to_half(float(0.0005 + 0.001 * rng.unit()));
+        std::memcpy(blk, &s, 2);
+        for (int i = 0; i < 32; i++) blk[2 + i] = uint8_t(int8_t(int(rng.next() % 255) - 127));
+    }
+    return raw;
+}
+
+int probe_gate_up(ge_ctx* c, int reps) {
+    const int M = 16384, K = 768, F = 1152;
+    ge_q8_matrix *gate = nullptr, *up = nullptr;
+    const std::vector<uint8_t> g = synth_q8(11, F, K), u = synth_q8(12, F, K);
+    if (ge_op_q8_create(c, g.data(), F, K, &gate) != 0) return fail(c, "q8_create");
+    if (ge_op_q8_create(c, u.data(), F, K, &up) != 0) return fail(c, "q8_create");
+    std::vector<uint16_t> x((size_t)M * K);
+    ge::SeededRandom rng(13);
+    for (auto& v : x) v = ge::float_to_half(float(rng.unit() - 0.5));
+    void* dx = ge_dev_alloc(c, x.size() * 2);
+    void* da = ge_dev_alloc(c, (size_t)M * F * 2);
+    if (!dx || !da) return fail(c, "dev_alloc");
+    if (ge_dev_upload(c, dx, x.data(), x.size() * 2) != 0) return fail(c, "dev_upload");
+    for (int r = 0; r < reps; r++)
+        if (ge_op_gemm_q8_geglu(c, gate, up, dx, M, da) != 0) return fail(c, "gemm_q8_geglu");
+    std::printf("ge_probe gate_up: %d launches of M=%d K=%d F=%d done\n", reps, M, K, F);
+    std::fflush(stdout);
+    ge_dev_free(c, dx);
+    ge_dev_free(c, da);
+    ge_op_q8_destroy(c, gate);
+    ge_op_q8_destroy(c, up);
+    return 0;
+}
+
+int probe_calibrate(ge_ctx* c) {
+    const size_t n = size_t(1) << 28;
+    void* src = ge_dev_alloc(c, 2 * n);
+    void* dst = ge_dev_alloc(c, 4 * n);
+    if (!src || !dst) return fail(c, "dev_alloc");
+    if (ge_op_f16_to_f32(c, src, dst, n) != 0) return fail(c, "f16_to_f32");
+    std::printf("ge_probe calibrate: converted %zu values (reads %zu, writes %zu bytes)\n", n, 2 * n, 4 * n);
+    std::fflush(stdout);
+    ge_dev_free(c, src);
+    ge_dev_free(c, dst);
+    return 0;
+}
+
+}  // namespace
+
+int main(int argc, char** argv) {
+    const char* what = argc > 1 ? argv[1] : "gate_up";
+    const int reps = argc > 2 ? std::atoi(argv[2]) : 20;
+    if (std::strcmp(what, "gate_up") != 0 && std::strcmp(what, "calibrate") != 0) {
+        std::fprintf(stderr, "usage: ge_probe gate_up [reps] | ge_probe calibrate\n");
+        return 2;
+    }
+    if (reps < 1 || reps > 10000) {
+        std::fprintf(stderr, "ge_probe: reps must be in [1, 10000]\n");
+        return 2;
+    }
+    ge_ctx* c = nullptr;
+    if (ge_create(0, &c) != 0) return fail(nullptr, "create");
+    std::printf("ge_probe on %s\n", ge_device_name(c));
+    std::fflush(stdout);
+    const int rc = std::strcmp(what, "calibrate") == 0 ? probe_calibrate(c) : probe_gate_up(c, reps);
+    if (rc == 0) ge_destroy(c);
+    return rc;
+}
