@@ -276,23 +276,39 @@ struct QkvStage {
 };
 
 template <int HD>
-__global__ __launch_bounds__(GemmWide::NT) void gemm_qkv_kernel(const uint16_t* __restrict__ X,
+__global__ __launch_bounds__(GemmWide::NT) __attribute__((amdgpu_waves_per_eu(4))) void gemm_qkv_kernel(const uint16_t* __restrict__ X,
                                                                  const uint16_t* __restrict__ Fh, int M, int N, int K,
                                                                  int tiles_n, int tiles, QkvEpilogue a) {
     using C = GemmWide;
     static_assert(C::BM == 128 && C::BN == 256 && 256 % HD == 0, "heads per tile");
     static_assert(QkvStage::BYTES <= C::LDS, "staging fits the stage buffers");
-    constexpr int LPH = HD / 4;  // lanes per head in the row pass
     extern __shared__ __attribute__((aligned(1024))) unsigned char lds[];
     const int tile = xcd_tile(blockIdx.x, tiles);
     const int m0 = (tile / tiles_n) * C::BM, n0 = (tile % tiles_n) * C::BN;
     asm volatile("" ::"s"(a.q_norm), "s"(a.k_norm), "s"(a.positions), "s"(a.rope), "s"(a.q), "s"(a.k), "s"(a.v),
                  "s"(a.vcol), "s"(a.vt), "s"(a.scale), "s"(a.eps), "s"(a.vt_cols), "s"(a.heads), "s"(a.kv_heads));
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int wm = wave / C::WN, wn = wave % C::WN;
+    // Row pass over (row, head) units: a unit is one token's HD values of one head of the tile.
+    // LPR lanes take a unit; lane k of them holds dims [8k, 8k + 8) and their NeoX partners
+    // [HD/2 + 8k, HD/2 + 8k + 8), so the rotation needs no other lane, and its RoPE table entries
+    // (pairs 8k .. 8k + 7, 64 contiguous bytes) and its q / k stores are contiguous across the
+    // unit's lanes. Units u = (it * UPI + lane / LPR) * NW + wave.
+    const int H = a.heads, KV = a.kv_heads, S = N / HD;
+    constexpr int LPR = HD / 16, UPI = 64 / LPR, UNITS = C::BM * (256 / HD), NIT = UNITS / (UPI * C::NW);
+    static_assert(NIT * UPI * C::NW == UNITS, "units per wave");
+    const int k8 = (lane % LPR) * 8, ug = lane / LPR;
+    // The units' positions are loaded before the main loop and their RoPE table entries right
+    // after the staging writes, so neither latency is paid in the row pass.
+    int upos[NIT];
+#pragma unroll
+    for (int it = 0; it < NIT; it++) {
+        const int u = (it * UPI + ug) * C::NW + wave, t = m0 + u % C::BM;
+        upos[it] = t < M ? a.positions[t] : 0;
+    }
     float16_t acc[C::FM][C::FN];
     gemm_mainloop<C, true>(X, Fh, M, N, K, m0, n0, lds, acc);
 
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    const int wm = wave / C::WN, wn = wave % C::WN;
     wait_lgkmcnt0();
     workgroup_barrier();  // every wave's last fragment reads are done: the stages become the tile
 #pragma unroll
@@ -307,86 +323,75 @@ __global__ __launch_bounds__(GemmWide::NT) void gemm_qkv_kernel(const uint16_t* 
                 const int r = wm * C::TM + i * 32 + (lane & 31), c = wn * (C::TN / 8) + j * 4 + g;
                 *reinterpret_cast<half4_t*>(lds + QkvStage::off(r, c) + (lane >> 5) * 8) = h;
             }
+    float4_t cs[NIT][4];
+#pragma unroll
+    for (int it = 0; it < NIT; it++) {
+        const int slot = n0 / HD + ((it * UPI + ug) * C::NW + wave) / C::BM;
+        if (slot < H + KV) {
+            const float* trow = a.rope + (size_t)upos[it] * HD + 2 * k8;
+#pragma unroll
+            for (int q = 0; q < 4; q++) cs[it][q] = *reinterpret_cast<const float4_t*>(trow + 4 * q);
+        }
+    }
     wait_lgkmcnt0();
     workgroup_barrier();
 
-    const int H = a.heads, KV = a.kv_heads, S = N / HD;
-    const int hl = lane / LPH, cl = (lane % LPH) * 4;  // head within the tile, first column within it
-    const int slot = n0 / HD + hl;
-    const bool valid = slot < S, isq = slot < H, isk = !isq && slot < H + KV, isv = valid && !isq && !isk;
-    const bool lo = cl < HD / 2;  // holds the first half of the NeoX pairs
-    float w[4] = {1.0f, 1.0f, 1.0f, 1.0f};
-    if (valid && (isq || isk)) {
-        const float4_t wv = *reinterpret_cast<const float4_t*>((isq ? a.q_norm : a.k_norm) + cl);
 #pragma unroll
-        for (int e = 0; e < 4; e++) w[e] = wv[e];
-    }
-    uint16_t* dst = isq ? a.q : (isk ? a.k : a.v);
-    const int dst_heads = isq ? H : KV, dst_slot = isq ? slot : (isk ? slot - H : slot - H - KV);
-    // Rows r = wave + NW k; lane k holds row k's position. Four rows at a time; the RoPE table
-    // entries of the next four rows are loaded while the current ones are processed, so the
-    // table's latency is paid once per wave rather than once per batch.
-    constexpr int RPW = C::BM / C::NW, RBATCH = 4, NB = RPW / RBATCH;
-    const int my_row = wave + C::NW * lane;
-    const int my_pos = lane < RPW && m0 + my_row < M ? a.positions[m0 + my_row] : 0;
-    const bool rope = isq || isk;
-    const int tcol = (lo ? cl : cl - HD / 2) * 2;  // this lane's first (cos, sin) pair in a table row
-    float4_t cs[2][RBATCH][2];
-#define QKV_TABLE(buf, b)                                                                                   \
-    do {                                                                                                    \
-        _Pragma("unroll") for (int k = 0; k < RBATCH; k++) {                                                \
-            const float* row_ = a.rope + (size_t)__shfl(my_pos, (b) * RBATCH + k, 64) * HD + tcol;          \
-            cs[buf][k][0] = *reinterpret_cast<const float4_t*>(row_);                                       \
-            cs[buf][k][1] = *reinterpret_cast<const float4_t*>(row_ + 4);                                   \
-        }                                                                                                   \
-    } while (0)
-    if (rope) QKV_TABLE(0, 0);
+    for (int it = 0; it < NIT; it++) {
+        const int u = (it * UPI + ug) * C::NW + wave, hh = u / C::BM, r = u % C::BM, t = m0 + r;
+        const int slot = n0 / HD + hh;
+        const bool valid = slot < S && t < M, isq = slot < H, isk = !isq && slot < H + KV;
+        const bool isv = valid && !isq && !isk, rope = isq || isk;
+        const half8_t x0 = *reinterpret_cast<const half8_t*>(lds + QkvStage::off(r, (hh * HD + k8) / 8));
+        const half8_t x1 = *reinterpret_cast<const half8_t*>(lds + QkvStage::off(r, (hh * HD + HD / 2 + k8) / 8));
+        float f0[8], f1[8], ss = 0.0f;
 #pragma unroll
-    for (int b = 0; b < NB; b++) {
-        if (rope && b + 1 < NB) QKV_TABLE((b + 1) & 1, b + 1);
-        float f[RBATCH][4], ss[RBATCH];
-#pragma unroll
-        for (int k = 0; k < RBATCH; k++) {
-            const int r = wave + C::NW * (b * RBATCH + k);
-            const half4_t x = *reinterpret_cast<const half4_t*>(lds + QkvStage::off(r, lane >> 1) + (lane & 1) * 8);
-            ss[k] = 0.0f;
-#pragma unroll
-            for (int e = 0; e < 4; e++) {
-                f[k][e] = float(x[e]);
-                ss[k] += f[k][e] * f[k][e];
-            }
+        for (int e = 0; e < 8; e++) {
+            f0[e] = float(x0[e]);
+            f1[e] = float(x1[e]);
+            ss += f0[e] * f0[e] + f1[e] * f1[e];
         }
 #pragma unroll
-        for (int m = LPH / 2; m >= 1; m >>= 1)
+        for (int m = LPR / 2; m >= 1; m >>= 1) ss += __shfl_xor(ss, m, 64);
+        const float inv = 1.0f / sqrtf(ss / float(HD) + a.eps);
+        half8_t o0, o1;
+        if (rope) {
+            const float* wn_ = (isq ? a.q_norm : a.k_norm);
+            const float4_t w00 = *reinterpret_cast<const float4_t*>(wn_ + k8);
+            const float4_t w01 = *reinterpret_cast<const float4_t*>(wn_ + k8 + 4);
+            const float4_t w10 = *reinterpret_cast<const float4_t*>(wn_ + HD / 2 + k8);
+            const float4_t w11 = *reinterpret_cast<const float4_t*>(wn_ + HD / 2 + k8 + 4);
+            const float wa[8] = {w00[0], w00[1], w00[2], w00[3], w01[0], w01[1], w01[2], w01[3]};
+            const float wb[8] = {w10[0], w10[1], w10[2], w10[3], w11[0], w11[1], w11[2], w11[3]};
 #pragma unroll
-            for (int k = 0; k < RBATCH; k++) ss[k] += __shfl_xor(ss[k], m, 64);
-#pragma unroll
-        for (int k = 0; k < RBATCH; k++) {
-            const int r = wave + C::NW * (b * RBATCH + k), t = m0 + r;
-            const float inv = 1.0f / sqrtf(ss[k] / float(HD) + a.eps);
-            half4_t o;
-            if (rope) {
-                const float4_t c01 = cs[b & 1][k][0], c23 = cs[b & 1][k][1];
-                const float cr[8] = {c01[0], c01[1], c01[2], c01[3], c23[0], c23[1], c23[2], c23[3]};
-#pragma unroll
-                for (int e = 0; e < 4; e++) {
-                    const float mine = f[k][e] * inv * w[e];
-                    const float other = __shfl_xor(mine, LPH / 2, 64);
-                    const float c = cr[2 * e], sn = cr[2 * e + 1];
-                    // (a, b) = (first, second) half of the pair: a' = a c - b s, b' = a s + b c
-                    o[e] = _Float16(lo ? mine * c - other * sn : other * sn + mine * c);
-                }
-            } else {
-#pragma unroll
-                for (int e = 0; e < 4; e++) o[e] = _Float16(f[k][e] * inv);
+            for (int e = 0; e < 8; e++) {
+                // (a, b) = (first, second) half of pair k8 + e: a' = a c - b s, b' = a s + b c
+                const float av = f0[e] * inv * wa[e], bv = f1[e] * inv * wb[e];
+                const float c = cs[it][e / 2][2 * (e % 2)], sn = cs[it][e / 2][2 * (e % 2) + 1];
+                o0[e] = _Float16(av * c - bv * sn);
+                o1[e] = _Float16(bv * c + av * sn);
             }
-            if (valid && t < M) {
-                if (dst) *reinterpret_cast<half4_t*>(dst + ((size_t)t * dst_heads + dst_slot) * HD + cl) = o;
-                if (isv && a.vt) *reinterpret_cast<half4_t*>(lds + QkvStage::off(r, lane >> 1) + (lane & 1) * 8) = o;
+        } else {
+#pragma unroll
+            for (int e = 0; e < 8; e++) {
+                o0[e] = _Float16(f0[e] * inv);
+                o1[e] = _Float16(f1[e] * inv);
+            }
+        }
+        if (valid) {
+            uint16_t* dst = isq ? a.q : (isk ? a.k : a.v);
+            const int dst_heads = isq ? H : KV, dst_slot = isq ? slot : (isk ? slot - H : slot - H - KV);
+            if (dst) {
+                uint16_t* drow = dst + ((size_t)t * dst_heads + dst_slot) * HD;
+                *reinterpret_cast<half8_t*>(drow + k8) = o0;
+                *reinterpret_cast<half8_t*>(drow + HD / 2 + k8) = o1;
+            }
+            if (isv && a.vt) {
+                *reinterpret_cast<half8_t*>(lds + QkvStage::off(r, (hh * HD + k8) / 8)) = o0;
+                *reinterpret_cast<half8_t*>(lds + QkvStage::off(r, (hh * HD + HD / 2 + k8) / 8)) = o1;
             }
         }
     }
-#undef QKV_TABLE
     if (!a.vt) return;
     // V^T rows: vt[(slot - H - KV) * HD + d][vcol[t]] for this tile's V heads.
     const int first_v = H + KV, tile_slot0 = n0 / HD;
@@ -398,6 +403,7 @@ __global__ __launch_bounds__(GemmWide::NT) void gemm_qkv_kernel(const uint16_t* 
     for (int hh = 0; hh < 256 / HD; hh++) {
         const int sl = tile_slot0 + hh;
         if (sl < first_v || sl >= S) continue;
+#pragma unroll 8
         for (int d = wave; d < HD; d += C::NW) {
             const int col = hh * HD + d;
             uint16_t* row = a.vt + (size_t)((sl - first_v) * HD + d) * a.vt_cols;
