@@ -517,6 +517,23 @@ __global__ __launch_bounds__(2 * G * 64) void attention_v2_kernel(const uint16_t
 // keys 8 (l / 16) + [0, 8) of query l % 16: exactly the B operand of the P.V product, so P
 // goes from the S accumulators to the MFMA with only the fp16 conversion. A query's 32 scores
 // sit in lanes q, q + 16, q + 32, q + 48; its softmax reductions are two lane exchanges.
+// Max and sum over lanes l, l ^ 16, l ^ 32 and l ^ 48 (the four key groups of a query in the
+// 16x16 MFMA layouts) with the gfx950 row-swap instructions: VALU operations, where a shuffle
+// would be an LDS round trip.
+__device__ __forceinline__ float max_over_key_groups(float v) {
+    const auto a = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    v = fmaxf(__uint_as_float(a[0]), __uint_as_float(a[1]));
+    const auto b = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    return fmaxf(__uint_as_float(b[0]), __uint_as_float(b[1]));
+}
+
+__device__ __forceinline__ float sum_over_key_groups(float v) {
+    const auto a = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    v = __uint_as_float(a[0]) + __uint_as_float(a[1]);
+    const auto b = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    return __uint_as_float(b[0]) + __uint_as_float(b[1]);
+}
+
 namespace attn3 {
 constexpr int NS = 2;     // key blocks in LDS
 constexpr int BKV = 32;   // keys per block
@@ -611,14 +628,20 @@ __global__ __launch_bounds__(4 * G * 64) void attention_v3_kernel(const uint16_t
     int b = 0;
     for (int it = 0; it < nblocks; it++) {
         const int kb = kstart + it * BKV;
-        // Block it has landed once at most the later blocks' copies are in flight; the barrier
-        // then covers every wave's copies, and (after each wave's LDS reads) frees the buffer
-        // the next copies overwrite.
-        static_assert(NS == 2, "the wait below assumes two stages");
-        wait_vmcnt<0>();
+        // Block it has landed once at most the later blocks' copies are in flight (min(NS - 2,
+        // blocks left) of them, CPW copies each); the barrier then covers every wave's copies,
+        // and (after each wave's LDS reads) frees the buffer the next copies overwrite.
+        static_assert(NS >= 2 && NS <= 4, "the waits below cover two to four stages");
+        const int ahead = min(NS - 2, nblocks - 1 - it);
+        if (ahead >= 2)
+            wait_vmcnt<2 * CPW>();
+        else if (ahead == 1)
+            wait_vmcnt<CPW>();
+        else
+            wait_vmcnt<0>();
         wait_lgkmcnt0();
         workgroup_barrier();
-        if (it + NS - 1 < nblocks) A3_ISSUE(kstart + (it + NS - 1) * BKV, b ^ 1);
+        if (it + NS - 1 < nblocks) A3_ISSUE(kstart + (it + NS - 1) * BKV, b == 0 ? NS - 1 : b - 1);
         const unsigned char* const kf = ldsa + b * STAGE + lane * 16;
         const unsigned char* const vf = kf + K_BYTES;
         // S^T tiles m = 0, 1 over the head dims; K fragments read PF k-steps ahead
@@ -658,13 +681,15 @@ __global__ __launch_bounds__(4 * G * 64) void attention_v3_kernel(const uint16_t
                 sc[e] = valid ? sc[e] : -INFINITY;
             }
         }
-        // max in the raw score domain (scale > 0), then scaled to log2 units
-        float bmax = fmaxf(fmaxf(fmaxf(sc[0], sc[1]), fmaxf(sc[2], sc[3])), fmaxf(fmaxf(sc[4], sc[5]), fmaxf(sc[6], sc[7])));
-        bmax = fmaxf(bmax, __shfl_xor(bmax, 16, 64));
-        bmax = fmaxf(bmax, __shfl_xor(bmax, 32, 64)) * scale_log2;
+        // this lane's max in the raw score domain (scale > 0)
+        const float lmax =
+            fmaxf(fmaxf(fmaxf(sc[0], sc[1]), fmaxf(sc[2], sc[3])), fmaxf(fmaxf(sc[4], sc[5]), fmaxf(sc[6], sc[7])));
         // Lazy rescaling, as in attention_v2_kernel: the reference point moves only when a
-        // score exceeds it by more than 2^8, so P stays below 256.
-        if (__builtin_amdgcn_ballot_w64(bmax > m_run + 8.0f)) {
+        // score exceeds it by more than 2^8, so P stays below 256. A lane's own scores decide
+        // whether the wave takes the update; the query's block max (over its four key groups)
+        // is formed only then.
+        if (__builtin_amdgcn_ballot_w64(lmax * scale_log2 > m_run + 8.0f)) {
+            const float bmax = max_over_key_groups(lmax) * scale_log2;
             const float m_new = fmaxf(m_run, bmax);
             const float alpha = m_new == -INFINITY ? 1.0f : __builtin_amdgcn_exp2f(m_run - m_new);
             l_run *= alpha;
@@ -681,9 +706,7 @@ __global__ __launch_bounds__(4 * G * 64) void attention_v3_kernel(const uint16_t
             sum += p;
             pb[e] = _Float16(p);
         }
-        sum += __shfl_xor(sum, 16, 64);
-        sum += __shfl_xor(sum, 32, 64);
-        l_run += sum;
+        l_run += sum;  // this lane's keys only; the key groups are summed once, at the end
         // O^T += V^T P^T: head-dim tiles dt of 16 rows, the block's 32 keys as one k-step
 #pragma unroll
         for (int dt = 0; dt < DT; dt++) {
@@ -691,10 +714,11 @@ __global__ __launch_bounds__(4 * G * 64) void attention_v3_kernel(const uint16_t
             __builtin_amdgcn_sched_barrier(0);
             o[dt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(va[dt % RING], pb, o[dt], 0, 0, 0);
         }
-        b ^= 1;
+        b = b + 1 == NS ? 0 : b + 1;
     }
 #undef A3_ISSUE
     wait_vmcnt<0>();
+    l_run = sum_over_key_groups(l_run);
     if (qi >= len) return;
     const float inv = l_run > 0.0f ? 1.0f / l_run : 0.0f;
     // o[dt], lane l: head dims 16 dt + 4 (l / 16) + r of query qi
