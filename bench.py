@@ -12,8 +12,8 @@ Also reported on the same JSON line:
                 the timed steps, against MI355X's dense fp16 MFMA peak (2.5 PFLOP/s);
   gemm_all      the same for all Q8_0 GEMM launches together;
   variants      the reference's default 8192-token budget (two packs per step, restaged each
-                time) and the full host API path (token ids in host memory -> normalised vectors,
-                PCIe included);
+                time), the full host API path (token ids in host memory -> normalised vectors,
+                PCIe included) and BASELINE config 4 (4 texts x 8192 tokens, one resident pack);
   cpu_baseline  the CPU oracle (a C restatement of the reference's CPUReference.swift) on a
                 bounded sample of the same workload, on this host's cores.
 """
@@ -294,6 +294,24 @@ def main():
         model.embed(batch, opts)
     api_rate = n_tokens * reps / (time.perf_counter() - t0)
     log(f"default budget {default_budget:,.0f} tok/s; embed API {api_rate:,.0f} tok/s")
+    # ---- variant: BASELINE config 4, 4 texts x 8192 tokens as one resident 32768-token pack
+    long_texts, long_len = 4, 8192
+    long_batch = [r.tolist() for r in ge.synth_tokens(8, 2, 262144, long_texts * long_len).reshape(long_texts, long_len)]
+    ctx.batch_stage(long_batch)
+    ctx.batch_run()
+    ctx.sync()
+    long_reps = 3
+    t0 = time.perf_counter()
+    for _ in range(long_reps):
+        ctx.batch_run()
+    ctx.sync()
+    long_ms = (time.perf_counter() - t0) * 1e3 / long_reps
+    long_rate = long_texts * long_len / (long_ms * 1e-3)
+    if not np.all(np.isfinite(ctx.batch_read())):
+        raise SystemExit("non-finite pooled output (config 4)")
+    long_flops = LAYERS * sum(gemm_flops(long_texts * long_len)[k] for k in ("gemm_qkv", "gemm_o", "gemm_gate_up", "gemm_down")) \
+        + gemm_flops(long_texts * long_len)["gemm_output"] + attention_flops([long_len] * long_texts)
+    log(f"config 4 (4 x 8192): {long_ms:.2f} ms/step, {long_rate:,.0f} tok/s")
 
     total_flops = step_gemm_flops + attention_flops([TOKENS] * TEXTS)
     traffic, traffic_kernel = measured_traffic(dom)
@@ -324,7 +342,9 @@ def main():
         "end_to_end_roofline_frac": round(total_flops / (ms_per_step * 1e-3) / 1e12 / PEAK_FP16_TFLOPS, 4),
         "kernels": per_kernel,
         "variants": {"default_budget_8192_tokens_per_s": round(default_budget, 1),
-                     "embed_api_pcie_inclusive_tokens_per_s": round(api_rate, 1)},
+                     "embed_api_pcie_inclusive_tokens_per_s": round(api_rate, 1),
+                     "config4_4x8192": {"tokens_per_s": round(long_rate, 1), "ms_per_step": round(long_ms, 3),
+                                        "tflops": round(long_flops / (long_ms * 1e-3) / 1e12, 1)}},
     }
     model.close()
     if not args.no_cpu:

@@ -202,6 +202,42 @@ def test_config3_ragged_vs_oracle(c2_model, c2_oracle):
         assert cosine(out[i].vector, w) >= COSINE_BAR, i
 
 
+@pytest.fixture(scope="module")
+def config4_texts():
+    # 4 texts x 8192 tokens, ids uniform in [2, 262144)
+    toks = ge.synth_tokens(8, 2, 262144, 4 * 8192).reshape(4, 8192)
+    return [t.tolist() for t in toks]
+
+
+def test_config4_long_context_vs_oracle(config2_gguf, c2_oracle, config4_texts):
+    """the 24-layer encoder over 4 texts of 8192 tokens (sliding window 512 on
+    local layers, full 8192 x 8192 attention on the global layers 5, 11, 17, 23), as one
+    32768-token pack. The last text against the oracle: pooled cosine and per-layer error at a
+    global and the last layer; the same text alone must give the same bits."""
+    m = ge.EmbeddingModel.load(config2_gguf, batch_token_budget=32768)
+    try:
+        ctx = m.context
+        print("config4 forward 4 x 8192 (one pack of 32768)", flush=True)
+        pooled, secs = ctx.forward(config4_texts)
+        print(f"gpu forward {secs * 1e3:.2f} ms", flush=True)
+        assert pooled.shape == (4, 768) and np.all(np.isfinite(pooled))
+        alone, _ = ctx.forward([config4_texts[3]])
+        assert np.array_equal(alone[0], pooled[3])
+        print("oracle forward of one 8192-token text (about half a minute)", flush=True)
+        keep = [("l_out", 5), ("l_out", 23)]
+        want, tr = c2_oracle.forward(config4_texts[3], keep=keep)
+        c = cosine(pooled[3], want)
+        print(f"text 3 cosine {c:.9f} max_rel {max_rel(pooled[3], want):.3e}", flush=True)
+        assert c >= COSINE_BAR
+        for name, layer in keep:
+            got = ctx.trace([config4_texts[3]], name, layer)
+            r = max_rel(got, tr[(name, layer)].reshape(8192, -1))
+            print(f"{name}-{layer}: max_rel {r:.3e}", flush=True)
+            assert r <= PER_LAYER_TOL, (name, layer)
+    finally:
+        m.close()
+
+
 def test_rejects_bad_batches(c2_model):
     ctx = c2_model.context
     with pytest.raises(ge.GemmaEmbedError) as e:
