@@ -666,7 +666,9 @@ void ensure_workspace(ge_ctx* c, int tokens, int seqs, int work, int work2, int 
     // read from them are masked, so they contribute exact zeros.
     if (m.any_v2 && (vt_cols > w.vt_cap || !w.vt)) {
         if (w.vt) (void)hipFree(w.vt);
-        w.vt_cap = std::max(vt_cols, w.vt_cap + w.vt_cap / 2);
+        // grow by half, in whole 64-column steps: the copies and the kernels' checks need
+        // 16-byte aligned rows (a multiple of 8 columns)
+        w.vt_cap = (std::max(vt_cols, w.vt_cap + w.vt_cap / 2) + 63) / 64 * 64;
         w.vt = ws_alloc<uint16_t>(size_t(m.max_kvd), size_t(w.vt_cap), "transposed v");
     }
 }

@@ -238,6 +238,23 @@ def test_config4_long_context_vs_oracle(config2_gguf, c2_oracle, config4_texts):
         m.close()
 
 
+def test_growing_batches_in_one_context(config2_gguf, c2_oracle):
+    """Batches that grow from one short text (the workspace and the transposed-V buffer grow
+    between calls; a grown V^T row length must stay a multiple of 8 columns), each against the
+    oracle."""
+    m = ge.EmbeddingModel.load(config2_gguf, batch_token_budget=8192)
+    try:
+        for lengths in ([8], [16], [40], [8, 200], [1000], [3, 5, 7]):
+            texts = [ge.synth_tokens(20 + n, 2, 262144, n).tolist() for n in lengths]
+            print(f"lengths {lengths}", flush=True)
+            pooled, _ = m.context.forward(texts)
+            for i, t in enumerate(texts):
+                want, _ = c2_oracle.forward(t)
+                assert cosine(pooled[i], want) >= COSINE_BAR, (lengths, i)
+    finally:
+        m.close()
+
+
 def test_rejects_bad_batches(c2_model):
     ctx = c2_model.context
     with pytest.raises(ge.GemmaEmbedError) as e:
