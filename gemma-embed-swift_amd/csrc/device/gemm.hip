@@ -256,6 +256,88 @@ __global__ __launch_bounds__(C::NT) void gemm_kernel(const uint16_t* __restrict_
                                        out_scale);
 }
 
+
+// ============================================================================ skinny GEMM
+//
+// For short batches (a few dozen tokens) the tiled kernel has a handful of workgroups. Here each
+// wave computes one block of 32 rows by 32 * NJ columns over the whole of K on its own: the
+// fragments come straight from global memory into registers (activations through a buffer
+// resource whose range check returns zeros past row M, weights in fragment order, 1 KB per
+// fragment), SK k-steps in flight, no LDS and no barrier. The MFMA, its operand order and the
+// order of the k-steps are those of the tiled kernel, so every output has the same bits there
+// and here, whichever the batch size selects. TR: the transposed accumulation of the QKV kernel,
+// stored as its fp16 staging (acc * out_scale, row-major [M][N]) for the separate row pass.
+constexpr int kSkinnySteps = 8;  // k-steps in flight per wave; K must be a multiple of 16 * 8
+
+template <int EPI, bool TR, int NJ>
+__global__ __launch_bounds__(256) void gemm_skinny_kernel(const uint16_t* __restrict__ X,
+                                                          const uint16_t* __restrict__ Fh, void* __restrict__ Y,
+                                                          int M, int N, int K, float out_scale) {
+    constexpr int SK = kSkinnySteps;
+    const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(int(threadIdx.x >> 6));
+    const int groups = N / (32 * NJ), items = (M + 31) / 32 * groups;
+    const int item = blockIdx.x * 4 + wave;
+    if (item >= items) return;
+    const int rt = item / groups, cg = item % groups;
+    const int KT = K / 16;
+    asm volatile("" ::"s"(Y), "s"(out_scale));
+    const __amdgpu_buffer_rsrc_t xr = buffer_rsrc(X, uint32_t(M) * uint32_t(K) * 2u);
+    const __amdgpu_buffer_rsrc_t fr = buffer_rsrc(Fh, uint32_t(N) * uint32_t(K) * 2u);
+    // lane l: activation row rt * 32 + l % 32, k-step columns 8 (l / 32) .. + 8; weight fragment
+    // bytes 16 l of the 1 KB chunk (jb, t)
+    const uint32_t aoff = uint32_t(((rt * 32 + (lane & 31)) * K + 8 * (lane >> 5)) * 2);
+    uint32_t boff[NJ];
+#pragma unroll
+    for (int j = 0; j < NJ; j++) boff[j] = uint32_t(((cg * NJ + j) * KT * 512 + lane * 8) * 2);
+    half8_t a[SK], b[SK][NJ];
+#define SK_LOAD(u, t)                                                                                   \
+    do {                                                                                                \
+        a[u] = __builtin_bit_cast(half8_t, __builtin_amdgcn_raw_buffer_load_b128(xr, aoff + (t) * 32, 0, 0)); \
+        _Pragma("unroll") for (int j = 0; j < NJ; j++) b[u][j] =                                        \
+            __builtin_bit_cast(half8_t, __builtin_amdgcn_raw_buffer_load_b128(fr, boff[j] + (t) * 1024, 0, 0)); \
+    } while (0)
+    float16_t acc[1][NJ];
+#pragma unroll
+    for (int j = 0; j < NJ; j++)
+#pragma unroll
+        for (int r = 0; r < 16; r++) acc[0][j][r] = 0.0f;
+#pragma unroll
+    for (int u = 0; u < SK; u++) SK_LOAD(u, u);
+    for (int t0 = 0; t0 < KT; t0 += SK) {
+#pragma unroll
+        for (int u = 0; u < SK; u++) {
+            const half8_t av = a[u];
+            half8_t bv[NJ];
+#pragma unroll
+            for (int j = 0; j < NJ; j++) bv[j] = b[u][j];
+            if (t0 + SK < KT) SK_LOAD(u, t0 + SK + u);
+#pragma unroll
+            for (int j = 0; j < NJ; j++)
+                acc[0][j] = TR ? __builtin_amdgcn_mfma_f32_32x32x16_f16(bv[j], av, acc[0][j], 0, 0, 0)
+                               : __builtin_amdgcn_mfma_f32_32x32x16_f16(av, bv[j], acc[0][j], 0, 0, 0);
+        }
+    }
+#undef SK_LOAD
+    if constexpr (TR) {
+        // register 4 g + e of acc[j]: row rt * 32 + lane % 32, column 32 (cg NJ + j) + 8 g + 4 (lane / 32) + e
+        const int row = rt * 32 + (lane & 31);
+        if (row < M) {
+            _Float16* yrow = static_cast<_Float16*>(Y) + (size_t)row * N + 32 * cg * NJ + 4 * (lane >> 5);
+#pragma unroll
+            for (int j = 0; j < NJ; j++)
+#pragma unroll
+                for (int g = 0; g < 4; g++) {
+                    half4_t h;
+#pragma unroll
+                    for (int e = 0; e < 4; e++) h[e] = _Float16(acc[0][j][4 * g + e] * out_scale);
+                    *reinterpret_cast<half4_t*>(yrow + 32 * j + 8 * g) = h;
+                }
+        }
+    } else {
+        gemm_store_tile<1, NJ, EPI>(acc, Y, M, N, rt * 32, 32 * cg * NJ, lane, out_scale);
+    }
+}
+
 // ============================================================================ QKV + norms + RoPE
 //
 // The QKV projection with the per-head RMSNorms, NeoX RoPE and the V transpose of the attention
@@ -267,6 +349,53 @@ __global__ __launch_bounds__(C::NT) void gemm_kernel(const uint16_t* __restrict_
 // squares is a butterfly over its HD / 4 lanes, and the NeoX partner of column j (j + HD / 2) sits
 // HD / 8 lanes away. Normalised V rows go back into LDS for the transposed write, one V^T row
 // (128 tokens) per wave instruction pair.
+// One (token, head) unit of the QKV epilogue. The unit's hd/16 lanes each hold dims [k8, k8 + 8)
+// (x0) and their NeoX partners [hd/2 + k8, hd/2 + k8 + 8) (x1) of the projection (fp16, scaled by
+// c), and the RoPE table entries of pairs k8 .. k8 + 7 (cs: cos, sin interleaved). Returns the
+// RMS-normalised values (eps already scaled by c^2), weighted and rotated when `rope` (q and k),
+// plain for v. The arithmetic (explicit fused multiply-adds, no contraction beyond them) is the
+// same wherever it is inlined, so the fused epilogue and the separate row pass give the same bits.
+// Every lane of the unit must take part (the sum of squares is a butterfly over them).
+template <int HD>
+__device__ __forceinline__ void qkv_unit(const half8_t x0, const half8_t x1, const float4_t (&cs)[4], bool rope,
+                                         const float* __restrict__ wnorm, int k8, float eps, half8_t& o0,
+                                         half8_t& o1) {
+#pragma clang fp contract(off)
+    constexpr int LPR = HD / 16;
+    float f0[8], f1[8], ss = 0.0f;
+#pragma unroll
+    for (int e = 0; e < 8; e++) {
+        f0[e] = float(x0[e]);
+        f1[e] = float(x1[e]);
+        ss = __builtin_fmaf(f1[e], f1[e], __builtin_fmaf(f0[e], f0[e], ss));
+    }
+#pragma unroll
+    for (int m = LPR / 2; m >= 1; m >>= 1) ss += __shfl_xor(ss, m, 64);
+    const float inv = 1.0f / sqrtf(ss / float(HD) + eps);
+    if (rope) {
+        const float4_t w00 = *reinterpret_cast<const float4_t*>(wnorm + k8);
+        const float4_t w01 = *reinterpret_cast<const float4_t*>(wnorm + k8 + 4);
+        const float4_t w10 = *reinterpret_cast<const float4_t*>(wnorm + HD / 2 + k8);
+        const float4_t w11 = *reinterpret_cast<const float4_t*>(wnorm + HD / 2 + k8 + 4);
+        const float wa[8] = {w00[0], w00[1], w00[2], w00[3], w01[0], w01[1], w01[2], w01[3]};
+        const float wb[8] = {w10[0], w10[1], w10[2], w10[3], w11[0], w11[1], w11[2], w11[3]};
+#pragma unroll
+        for (int e = 0; e < 8; e++) {
+            // (a, b) = (first, second) half of pair k8 + e: a' = a c - b s, b' = a s + b c
+            const float av = f0[e] * inv * wa[e], bv = f1[e] * inv * wb[e];
+            const float c = cs[e / 2][2 * (e % 2)], sn = cs[e / 2][2 * (e % 2) + 1];
+            o0[e] = _Float16(__builtin_fmaf(av, c, -(bv * sn)));
+            o1[e] = _Float16(__builtin_fmaf(bv, c, av * sn));
+        }
+    } else {
+#pragma unroll
+        for (int e = 0; e < 8; e++) {
+            o0[e] = _Float16(f0[e] * inv);
+            o1[e] = _Float16(f1[e] * inv);
+        }
+    }
+}
+
 struct QkvStage {
     static constexpr int RB = 512;  // bytes per staged row (256 halves)
     // 16-byte chunk c of row r at chunk c ^ (r % 16): the transposed fragment writes of one
@@ -344,40 +473,8 @@ __global__ __launch_bounds__(GemmWide::NT) __attribute__((amdgpu_waves_per_eu(4)
         const bool isv = valid && !isq && !isk, rope = isq || isk;
         const half8_t x0 = *reinterpret_cast<const half8_t*>(lds + QkvStage::off(r, (hh * HD + k8) / 8));
         const half8_t x1 = *reinterpret_cast<const half8_t*>(lds + QkvStage::off(r, (hh * HD + HD / 2 + k8) / 8));
-        float f0[8], f1[8], ss = 0.0f;
-#pragma unroll
-        for (int e = 0; e < 8; e++) {
-            f0[e] = float(x0[e]);
-            f1[e] = float(x1[e]);
-            ss += f0[e] * f0[e] + f1[e] * f1[e];
-        }
-#pragma unroll
-        for (int m = LPR / 2; m >= 1; m >>= 1) ss += __shfl_xor(ss, m, 64);
-        const float inv = 1.0f / sqrtf(ss / float(HD) + a.eps);
         half8_t o0, o1;
-        if (rope) {
-            const float* wn_ = (isq ? a.q_norm : a.k_norm);
-            const float4_t w00 = *reinterpret_cast<const float4_t*>(wn_ + k8);
-            const float4_t w01 = *reinterpret_cast<const float4_t*>(wn_ + k8 + 4);
-            const float4_t w10 = *reinterpret_cast<const float4_t*>(wn_ + HD / 2 + k8);
-            const float4_t w11 = *reinterpret_cast<const float4_t*>(wn_ + HD / 2 + k8 + 4);
-            const float wa[8] = {w00[0], w00[1], w00[2], w00[3], w01[0], w01[1], w01[2], w01[3]};
-            const float wb[8] = {w10[0], w10[1], w10[2], w10[3], w11[0], w11[1], w11[2], w11[3]};
-#pragma unroll
-            for (int e = 0; e < 8; e++) {
-                // (a, b) = (first, second) half of pair k8 + e: a' = a c - b s, b' = a s + b c
-                const float av = f0[e] * inv * wa[e], bv = f1[e] * inv * wb[e];
-                const float c = cs[it][e / 2][2 * (e % 2)], sn = cs[it][e / 2][2 * (e % 2) + 1];
-                o0[e] = _Float16(av * c - bv * sn);
-                o1[e] = _Float16(bv * c + av * sn);
-            }
-        } else {
-#pragma unroll
-            for (int e = 0; e < 8; e++) {
-                o0[e] = _Float16(f0[e] * inv);
-                o1[e] = _Float16(f1[e] * inv);
-            }
-        }
+        qkv_unit<HD>(x0, x1, cs[it], rope, isq ? a.q_norm : a.k_norm, k8, a.eps, o0, o1);
         if (valid) {
             uint16_t* dst = isq ? a.q : (isk ? a.k : a.v);
             const int dst_heads = isq ? H : KV, dst_slot = isq ? slot : (isk ? slot - H : slot - H - KV);
@@ -411,6 +508,53 @@ __global__ __launch_bounds__(GemmWide::NT) __attribute__((amdgpu_waves_per_eu(4)
             const uint16_t v1 = *reinterpret_cast<const uint16_t*>(lds + QkvStage::off(64 + lane, col >> 3) + (col & 7) * 2);
             if (vc0 >= 0) row[vc0] = v0;
             if (vc1 >= 0) row[vc1] = v1;
+        }
+    }
+}
+
+
+// The QKV epilogue as its own pass over the skinny GEMM's fp16 staging [M][N] (short batches):
+// the fused kernel's units and arithmetic (qkv_unit), so the same bits; units u = (token, head)
+// in token-major order, hd/16 lanes each. V^T is written straight from registers.
+template <int HD>
+__global__ __launch_bounds__(256) void qkv_rowpass_kernel(const uint16_t* __restrict__ stage, int M, int N,
+                                                          QkvEpilogue a) {
+    constexpr int LPR = HD / 16, UPI = 64 / LPR;
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int S = N / HD, H = a.heads, KV = a.kv_heads;
+    const int gu = (blockIdx.x * 4 + wave) * UPI + lane / LPR, k8 = (lane % LPR) * 8;
+    const bool live = gu < M * S;  // the same for all lanes of a unit
+    const int t = live ? gu / S : 0, slot = live ? gu % S : 0;
+    const bool isq = slot < H, isk = !isq && slot < H + KV, isv = !isq && !isk, rope = isq || isk;
+    float4_t cs[4];
+    half8_t x0 = {}, x1 = {};
+    if (live) {
+        if (rope) {
+            const float* trow = a.rope + (size_t)a.positions[t] * HD + 2 * k8;
+#pragma unroll
+            for (int q = 0; q < 4; q++) cs[q] = *reinterpret_cast<const float4_t*>(trow + 4 * q);
+        }
+        const uint16_t* srow = stage + (size_t)t * N + slot * HD;
+        x0 = *reinterpret_cast<const half8_t*>(srow + k8);
+        x1 = *reinterpret_cast<const half8_t*>(srow + HD / 2 + k8);
+    }
+    half8_t o0, o1;
+    qkv_unit<HD>(x0, x1, cs, live && rope, isq ? a.q_norm : a.k_norm, k8, a.eps, o0, o1);
+    if (!live) return;
+    uint16_t* dst = isq ? a.q : (isk ? a.k : a.v);
+    const int dst_heads = isq ? H : KV, dst_slot = isq ? slot : (isk ? slot - H : slot - H - KV);
+    if (dst) {
+        uint16_t* drow = dst + ((size_t)t * dst_heads + dst_slot) * HD;
+        *reinterpret_cast<half8_t*>(drow + k8) = o0;
+        *reinterpret_cast<half8_t*>(drow + HD / 2 + k8) = o1;
+    }
+    if (isv && a.vt) {
+        const int vc = a.vcol[t];
+        _Float16* vt = reinterpret_cast<_Float16*>(a.vt) + (size_t)(slot - H - KV) * HD * a.vt_cols + vc;
+#pragma unroll
+        for (int e = 0; e < 8; e++) {
+            vt[(size_t)(k8 + e) * a.vt_cols] = o0[e];
+            vt[(size_t)(HD / 2 + k8 + e) * a.vt_cols] = o1[e];
         }
     }
 }
@@ -488,10 +632,28 @@ hipError_t launch_q8_fragments(hipStream_t s, const Q8Dev& w, uint16_t* fh) {
     return hipGetLastError();
 }
 
+template <int EPI, bool TR, int NJ>
+hipError_t gemm_skinny_launch(hipStream_t s, const Q8Dev& w, const uint16_t* x, int M, void* y, float out_scale) {
+    const int items = (M + 31) / 32 * (w.rows / (32 * NJ));
+    launch_kernel(gemm_skinny_kernel<EPI, TR, NJ>, dim3((items + 3) / 4), dim3(256), 0, s, x, w.fh, y, M, w.rows, w.cols,
+                  out_scale);
+    return hipGetLastError();
+}
+
+bool skinny_ok(const Q8Dev& w, int M) { return M <= kSkinnyMaxRows && w.cols % (16 * kSkinnySteps) == 0; }
+
 hipError_t launch_gemm_q8(hipStream_t s, const Q8Dev& w, const uint16_t* x, int M, void* y, GemmEpilogue epi,
                           float out_scale) {
     if (!gemm_operands_ok(w, x, M, y)) return hipErrorInvalidValue;
     if (M == 0) return hipSuccess;
+    if (skinny_ok(w, M)) {
+        switch (epi) {
+        case kEpiF32: return gemm_skinny_launch<kEpiF32, false, 1>(s, w, x, M, y, out_scale);
+        case kEpiF16: return gemm_skinny_launch<kEpiF16, false, 1>(s, w, x, M, y, out_scale);
+        case kEpiGeglu: return gemm_skinny_launch<kEpiGeglu, false, 2>(s, w, x, M, y, out_scale);
+        default: return hipErrorInvalidValue;
+        }
+    }
     if (w.rows <= 1024 && w.cols % GemmSquare::BK == 0) return gemm_launch<GemmSquare>(s, w, x, M, y, epi, out_scale);
     return gemm_launch<GemmWide>(s, w, x, M, y, epi, out_scale);
 }
@@ -504,6 +666,19 @@ hipError_t launch_gemm_qkv(hipStream_t s, const Q8Dev& w, const uint16_t* x, int
         (e.vt && (!e.vcol || e.vt_cols <= 0)))
         return hipErrorInvalidValue;
     if (M == 0) return hipSuccess;
+    if (e.stage && skinny_ok(w, M)) {
+        // short batch: the skinny GEMM's fp16 staging, then the row pass (same bits as fused)
+        hipError_t r = gemm_skinny_launch<kEpiF16, true, 1>(s, w, x, M, e.stage, e.scale);
+        if (r != hipSuccess) return r;
+        const int units = M * (w.rows / hd), per_block = 4 * (64 / (hd / 16));
+        if (hd == 128)
+            launch_kernel(qkv_rowpass_kernel<128>, dim3((units + per_block - 1) / per_block), dim3(256), 0, s, e.stage, M,
+                          w.rows, e);
+        else
+            launch_kernel(qkv_rowpass_kernel<256>, dim3((units + per_block - 1) / per_block), dim3(256), 0, s, e.stage, M,
+                          w.rows, e);
+        return hipGetLastError();
+    }
     using C = GemmWide;
     const int N = w.rows, K = w.cols;
     const int tiles_m = (M + C::BM - 1) / C::BM, tiles_n = (N + C::BN - 1) / C::BN, tiles = tiles_m * tiles_n;

@@ -50,6 +50,9 @@ enum GemmEpilogue { kEpiF32 = 0, kEpiF16 = 1, kEpiGeglu = 2 };
 // K of 32. kEpiGeglu expects W's rows
 // interleaved in 32-row gate/up groups and writes fp16 act[M][N / 2] = gelu_tanh(gate) * up *
 // out_scale. out_scale is a power of two wherever the forward uses it, so it is exact.
+// Batches of at most kSkinnyMaxRows rows (and K a multiple of 128) run on the skinny kernel,
+// one wave per 32-row block; the results are bitwise those of the tiled kernel.
+constexpr int kSkinnyMaxRows = 64;
 hipError_t launch_gemm_q8(hipStream_t s, const Q8Dev& w, const uint16_t* x, int M, void* y, GemmEpilogue epi,
                           float out_scale = 1.0f);
 
@@ -74,6 +77,9 @@ struct QkvEpilogue {
     int vt_cols = 0;
     int heads = 0;
     int kv_heads = 0;
+    // fp16 scratch of at least M * N halves: lets short batches (M <= kSkinnyMaxRows) take the
+    // skinny GEMM and a separate row pass, with the same results; null = always the fused kernel
+    uint16_t* stage = nullptr;
 };
 bool gemm_qkv_supported(int hd, int H, int KV);
 hipError_t launch_gemm_qkv(hipStream_t s, const Q8Dev& w, const uint16_t* x, int M, int hd, const QkvEpilogue& e);

@@ -846,6 +846,7 @@ void encode(ge_ctx* c, StopPoint* sp) {
                 e.eps = m.eps * L.qkv_c * L.qkv_c;
                 e.heads = m.heads;
                 e.kv_heads = L.kv_heads;
+                e.stage = reinterpret_cast<uint16_t*>(w.qkv);  // [rows][max_qkv] fp32: room for fp16 [T][N]
                 return launch_gemm_qkv(s, L.wqkv, w.h, T, L.head_dim, e);
             });
         } else {

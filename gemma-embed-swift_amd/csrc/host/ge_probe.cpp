@@ -7,6 +7,9 @@
 //                             M = 16384 tokens, K = 768, F = 1152 gate and 1152 up rows), the
 //                             forward's dominant kernel (Kernels.gemm with the geglu epilogue,
 //                             Metal/MetalForward.swift:524-557; Shaders/GEMM.metal:41-67)
+//   ge_probe attention [reps] the attention of a sliding-window layer (ge_op_attention: 32
+//                             sequences of 512 tokens, 3 query heads, 1 KV head, head dim 256,
+//                             half window 256; Kernels.attention, Metal/MetalForward.swift:669-694)
 //   ge_probe calibrate        fp16 -> fp32 conversion of 2^28 values (reads 512 MiB, writes 1 GiB):
 //                             the known-size kernel that scales the HBM byte counters
 //
@@ -68,6 +71,41 @@ int probe_gate_up(ge_ctx* c, int reps) {
     return 0;
 }
 
+int probe_attention(ge_ctx* c, int reps) {
+    const int S = 32, L = 512, T = S * L, H = 3, KV = 1, HD = 256, slack = 64;
+    ge::SeededRandom rng(14);
+    auto rand_f16 = [&](size_t n, double amp) {
+        std::vector<uint16_t> v(n);
+        for (auto& x : v) x = ge::float_to_half(float(amp * (rng.unit() - 0.5)));
+        return v;
+    };
+    const std::vector<uint16_t> q = rand_f16((size_t)(T + slack) * H * HD, 3.0);
+    const std::vector<uint16_t> k = rand_f16((size_t)(T + slack) * KV * HD, 2.0);
+    const std::vector<uint16_t> v = rand_f16((size_t)(T + slack) * KV * HD, 2.0);
+    std::vector<ge_attention_work> work;
+    const int qpw = ge_attention_queries();
+    for (int s = 0; s < S; s++)
+        for (int q0 = 0; q0 < L; q0 += qpw) work.push_back(ge_attention_work{uint32_t(s * L), uint32_t(L), uint32_t(q0)});
+    void* dq = ge_dev_alloc(c, q.size() * 2);
+    void* dk = ge_dev_alloc(c, k.size() * 2);
+    void* dv = ge_dev_alloc(c, v.size() * 2);
+    void* dout = ge_dev_alloc(c, q.size() * 2);
+    void* dw = ge_dev_alloc(c, work.size() * sizeof(ge_attention_work));
+    if (!dq || !dk || !dv || !dout || !dw) return fail(c, "dev_alloc");
+    if (ge_dev_upload(c, dq, q.data(), q.size() * 2) != 0 || ge_dev_upload(c, dk, k.data(), k.size() * 2) != 0 ||
+        ge_dev_upload(c, dv, v.data(), v.size() * 2) != 0 ||
+        ge_dev_upload(c, dw, work.data(), work.size() * sizeof(ge_attention_work)) != 0)
+        return fail(c, "dev_upload");
+    for (int r = 0; r < reps; r++)
+        if (ge_op_attention(c, dq, dk, dv, dout, dw, int32_t(work.size()), H, KV, HD, 256, 1.0f) != 0)
+            return fail(c, "attention");
+    std::printf("ge_probe attention: %d launches of %d x %d tokens, H=%d KV=%d hd=%d, half window 256 done\n", reps, S,
+                L, H, KV, HD);
+    std::fflush(stdout);
+    for (void* p : {dq, dk, dv, dout, dw}) ge_dev_free(c, p);
+    return 0;
+}
+
 int probe_calibrate(ge_ctx* c) {
     const size_t n = size_t(1) << 28;
     void* src = ge_dev_alloc(c, 2 * n);
@@ -86,8 +124,8 @@ int probe_calibrate(ge_ctx* c) {
 int main(int argc, char** argv) {
     const char* what = argc > 1 ? argv[1] : "gate_up";
     const int reps = argc > 2 ? std::atoi(argv[2]) : 20;
-    if (std::strcmp(what, "gate_up") != 0 && std::strcmp(what, "calibrate") != 0) {
-        std::fprintf(stderr, "usage: ge_probe gate_up [reps] | ge_probe calibrate\n");
+    if (std::strcmp(what, "gate_up") != 0 && std::strcmp(what, "attention") != 0 && std::strcmp(what, "calibrate") != 0) {
+        std::fprintf(stderr, "usage: ge_probe gate_up [reps] | ge_probe attention [reps] | ge_probe calibrate\n");
         return 2;
     }
     if (reps < 1 || reps > 10000) {
@@ -98,7 +136,9 @@ int main(int argc, char** argv) {
     if (ge_create(0, &c) != 0) return fail(nullptr, "create");
     std::printf("ge_probe on %s\n", ge_device_name(c));
     std::fflush(stdout);
-    const int rc = std::strcmp(what, "calibrate") == 0 ? probe_calibrate(c) : probe_gate_up(c, reps);
+    const int rc = std::strcmp(what, "calibrate") == 0   ? probe_calibrate(c)
+                   : std::strcmp(what, "attention") == 0 ? probe_attention(c, reps)
+                                                         : probe_gate_up(c, reps);
     if (rc == 0) ge_destroy(c);
     return rc;
 }

@@ -142,6 +142,26 @@ def test_packing_invariance_and_determinism(c2_model, config2_batch):
     assert np.array_equal(mixed[1], a[1])
 
 
+def test_short_texts_alone_match_larger_packs(c2_model, config2_batch):
+    """A short pack (at most 64 tokens) runs its GEMMs on the skinny kernel and the QKV epilogue as
+    a separate row pass; inside a larger pack the same text runs on the tiled kernels. The vector
+    must have the same bits either way (MetalForwardTests.swift:95-120: counts around the tile
+    boundaries, alone and between a 19- and a 97-token text)."""
+    body = config2_batch[7]
+    ctx = c2_model.context
+    for count in (1, 2, 13, 15, 16, 17, 31, 32, 33, 63, 64, 65):
+        subject = body[:count]
+        packed, _ = ctx.forward([config2_batch[3][:19], subject, config2_batch[4][:97]])
+        alone, _ = ctx.forward([subject])
+        assert np.array_equal(alone[0], packed[1]), count
+    for lengths in ([5, 8], [8, 8], [8, 9], [30, 34]):
+        small = [config2_batch[9 + i][:n] for i, n in enumerate(lengths)]
+        got, _ = ctx.forward(small)
+        want, _ = ctx.forward(small + [config2_batch[20][:97]])
+        for i in range(len(lengths)):
+            assert np.array_equal(got[i], want[i]), (lengths, i)
+
+
 def test_embed_api_options(c2_model, config2_batch):
     texts = [t[: 20 + 37 * i] for i, t in enumerate(config2_batch[:10])]
     full = c2_model.embed(texts, ge.EmbedOptions(normalise=False))

@@ -97,6 +97,45 @@ def test_gemm_f16_output_and_row_independence(ctx, c2):
     assert np.array_equal(y32[131:140], y_part)
 
 
+@pytest.mark.parametrize("name,y_f16", [("blk.1.attn_q.weight", False), ("blk.1.ffn_down.weight", True),
+                                         ("output.weight", False)])
+def test_gemm_short_batches_match_tiled_rows(ctx, c2, name, y_f16):
+    """Up to 64 rows run on the skinny kernel; the same rows inside a 300-row batch run on the
+    tiled kernel. Same MFMA, operand order and k order: the same bits."""
+    shape, _, _ = c2.tensors[name]
+    cols, rows = shape
+    raw = np.asarray(c2.raw(name))
+    x16 = f16_round(RNG.standard_normal((300, cols)))
+    full = run_gemm(ctx, raw, rows, cols, x16, y_f16)
+    for lo, n in ((0, 1), (5, 7), (100, 32), (200, 33), (236, 64)):
+        part = run_gemm(ctx, raw, rows, cols, x16[lo:lo + n].copy(), y_f16)
+        assert np.array_equal(full[lo:lo + n], part), (lo, n)
+
+
+def test_gemm_geglu_short_batch_matches_tiled_rows(ctx, c2):
+    M = 300
+    x16 = f16_round(RNG.standard_normal((M, 768)) * 0.05)
+    g = ctx.q8_create(np.asarray(c2.raw("blk.4.ffn_gate.weight")), 1152, 768)
+    u = ctx.q8_create(np.asarray(c2.raw("blk.4.ffn_up.weight")), 1152, 768)
+
+    def geglu(x):
+        dx, da = ctx.alloc(x.nbytes), ctx.alloc(x.shape[0] * 1152 * 2)
+        try:
+            ctx.upload(dx, x)
+            ctx.gemm_q8_geglu(g, u, dx, x.shape[0], da)
+            return ctx.download(da, (x.shape[0], 1152), np.float16)
+        finally:
+            ctx.free(dx)
+            ctx.free(da)
+    try:
+        full = geglu(x16)
+        for lo, n in ((0, 3), (40, 64), (250, 50)):
+            assert np.array_equal(full[lo:lo + n], geglu(x16[lo:lo + n].copy())), (lo, n)
+    finally:
+        ctx.q8_destroy(g)
+        ctx.q8_destroy(u)
+
+
 def test_gemm_geglu_vs_oracle(ctx, c2):
     M = 333
     x16 = f16_round(RNG.standard_normal((M, 768)) * 0.05)
