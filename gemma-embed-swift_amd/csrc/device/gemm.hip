@@ -267,13 +267,16 @@ __global__ __launch_bounds__(C::NT) void gemm_kernel(const uint16_t* __restrict_
 // order of the k-steps are those of the tiled kernel, so every output has the same bits there
 // and here, whichever the batch size selects. TR: the transposed accumulation of the QKV kernel,
 // stored as its fp16 staging (acc * out_scale, row-major [M][N]) for the separate row pass.
-constexpr int kSkinnySteps = 8;  // k-steps in flight per wave; K must be a multiple of 16 * 8
+// k-steps in flight per wave (a short batch's GEMM is bound by the latency of its weight reads:
+// few waves, each streaming 32 or 64 weight rows); K must be a multiple of 16 times this
+template <int NJ>
+constexpr int skinny_steps() { return NJ == 1 ? 24 : 12; }
 
 template <int EPI, bool TR, int NJ>
 __global__ __launch_bounds__(256) void gemm_skinny_kernel(const uint16_t* __restrict__ X,
                                                           const uint16_t* __restrict__ Fh, void* __restrict__ Y,
                                                           int M, int N, int K, float out_scale) {
-    constexpr int SK = kSkinnySteps;
+    constexpr int SK = skinny_steps<NJ>();
     const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(int(threadIdx.x >> 6));
     const int groups = N / (32 * NJ), items = (M + 31) / 32 * groups;
     const int item = blockIdx.x * 4 + wave;
@@ -640,7 +643,9 @@ hipError_t gemm_skinny_launch(hipStream_t s, const Q8Dev& w, const uint16_t* x, 
     return hipGetLastError();
 }
 
-bool skinny_ok(const Q8Dev& w, int M) { return M <= kSkinnyMaxRows && w.cols % (16 * kSkinnySteps) == 0; }
+bool skinny_ok(const Q8Dev& w, int M) {
+    return M <= kSkinnyMaxRows && w.cols % (16 * skinny_steps<1>()) == 0 && w.cols % (16 * skinny_steps<2>()) == 0;
+}
 
 hipError_t launch_gemm_q8(hipStream_t s, const Q8Dev& w, const uint16_t* x, int M, void* y, GemmEpilogue epi,
                           float out_scale) {

@@ -50,7 +50,7 @@ enum GemmEpilogue { kEpiF32 = 0, kEpiF16 = 1, kEpiGeglu = 2 };
 // K of 32. kEpiGeglu expects W's rows
 // interleaved in 32-row gate/up groups and writes fp16 act[M][N / 2] = gelu_tanh(gate) * up *
 // out_scale. out_scale is a power of two wherever the forward uses it, so it is exact.
-// Batches of at most kSkinnyMaxRows rows (and K a multiple of 128) run on the skinny kernel,
+// Batches of at most kSkinnyMaxRows rows (and K a multiple of 384) run on the skinny kernel,
 // one wave per 32-row block; the results are bitwise those of the tiled kernel.
 constexpr int kSkinnyMaxRows = 64;
 hipError_t launch_gemm_q8(hipStream_t s, const Q8Dev& w, const uint16_t* x, int M, void* y, GemmEpilogue epi,
