@@ -542,15 +542,15 @@ constexpr int BKV = 32;   // keys per block
 template <int HD>
 constexpr int attention_v3_lds_bytes() { return attn3::NS * 2 * attn3::BKV * HD * 2; }
 
-template <int HD, int G>
-__global__ __launch_bounds__(4 * G * 64) void attention_v3_kernel(const uint16_t* __restrict__ Qg,
+template <int HD, int G, int QW>
+__global__ __launch_bounds__(QW * G * 64) void attention_v3_kernel(const uint16_t* __restrict__ Qg,
                                                                   const uint16_t* __restrict__ Kg,
                                                                   const uint16_t* __restrict__ VTg,
                                                                   uint16_t* __restrict__ Og,
                                                                   const AttnWork* __restrict__ work, int H, int KV,
                                                                   int vt_cols, int hw, float scale_log2) {
     using namespace attn3;
-    constexpr int QB = 64, NW = 4 * G, KS = HD / 32, DT = HD / 16;
+    constexpr int QB = 16 * QW, NW = QW * G, KS = HD / 32, DT = HD / 16;
     constexpr int K_BYTES = BKV * HD * 2, STAGE = 2 * K_BYTES;
     constexpr int KCH = K_BYTES / 1024, CH = 2 * KCH;  // K chunks (ks, m), then V^T chunks dt
     static_assert(KCH == 2 * KS && KCH == DT, "chunk counts");
@@ -735,10 +735,14 @@ __global__ __launch_bounds__(4 * G * 64) void attention_v3_kernel(const uint16_t
 template <int HD, int G>
 static hipError_t attention_v3_dispatch(hipStream_t s, const uint16_t* q, const uint16_t* k, const uint16_t* vt,
                                         int vt_cols, uint16_t* o, const AttnWork* work, int n_work, int H, int KV, int hw,
-                                        float scale) {
+                                        float scale, int item_queries) {
     const float scale_log2 = scale * 1.4426950408889634f;
-    launch_kernel(attention_v3_kernel<HD, G>, dim3(n_work, KV), dim3(4 * G * 64), uint32_t(attention_v3_lds_bytes<HD>()), s,
-                  q, k, vt, o, work, H, KV, vt_cols, hw, scale_log2);
+    if (item_queries == 32)
+        launch_kernel(attention_v3_kernel<HD, G, 2>, dim3(n_work, KV), dim3(2 * G * 64), uint32_t(attention_v3_lds_bytes<HD>()),
+                      s, q, k, vt, o, work, H, KV, vt_cols, hw, scale_log2);
+    else
+        launch_kernel(attention_v3_kernel<HD, G, 4>, dim3(n_work, KV), dim3(4 * G * 64), uint32_t(attention_v3_lds_bytes<HD>()),
+                      s, q, k, vt, o, work, H, KV, vt_cols, hw, scale_log2);
     return hipGetLastError();
 }
 
@@ -755,13 +759,14 @@ static hipError_t attention_v2_dispatch(hipStream_t s, const uint16_t* q, const 
 template <int HD>
 static hipError_t attention_v2_dispatch_g(hipStream_t s, const uint16_t* q, const uint16_t* k, const uint16_t* vt,
                                           int vt_cols, uint16_t* o, const AttnWork* work, int n_work, int H, int KV,
-                                          int hw, float scale) {
+                                          int hw, float scale, int item_queries) {
     switch (H / KV) {
-    // groups of up to 3 query heads: 16-query waves (4 G waves, at most 3 per SIMD)
-    case 1: return attention_v3_dispatch<HD, 1>(s, q, k, vt, vt_cols, o, work, n_work, H, KV, hw, scale);
-    case 2: return attention_v3_dispatch<HD, 2>(s, q, k, vt, vt_cols, o, work, n_work, H, KV, hw, scale);
-    case 3: return attention_v3_dispatch<HD, 3>(s, q, k, vt, vt_cols, o, work, n_work, H, KV, hw, scale);
+    // groups of up to 3 query heads: 16-query waves (item_queries / 16 per head)
+    case 1: return attention_v3_dispatch<HD, 1>(s, q, k, vt, vt_cols, o, work, n_work, H, KV, hw, scale, item_queries);
+    case 2: return attention_v3_dispatch<HD, 2>(s, q, k, vt, vt_cols, o, work, n_work, H, KV, hw, scale, item_queries);
+    case 3: return attention_v3_dispatch<HD, 3>(s, q, k, vt, vt_cols, o, work, n_work, H, KV, hw, scale, item_queries);
     case 4:
+        if (item_queries != 64) return hipErrorInvalidValue;
         if constexpr (attention_v2_lds_bytes<HD, 4>() <= 160 * 1024)
             return attention_v2_dispatch<HD, 4>(s, q, k, vt, vt_cols, o, work, n_work, H, KV, hw, scale);
         return hipErrorInvalidValue;
@@ -777,12 +782,14 @@ bool attention_v2_supported(int hd, int H, int KV) {
 
 hipError_t launch_attention_v2(hipStream_t s, const uint16_t* q, const uint16_t* k, const uint16_t* vt, int vt_cols,
                                uint16_t* o, const AttnWork* work, int n_work, int H, int KV, int hd, int half_window,
-                               float scale) {
-    if (n_work < 0 || !attention_v2_supported(hd, H, KV) || half_window < 0 || vt_cols <= 0 || vt_cols % 8)
+                               float scale, int item_queries) {
+    if (n_work < 0 || !attention_v2_supported(hd, H, KV) || half_window < 0 || vt_cols <= 0 || vt_cols % 8 ||
+        (item_queries != 64 && !(item_queries == 32 && H / KV <= 3)))
         return hipErrorInvalidValue;
     if (n_work == 0) return hipSuccess;
-    if (hd == 128) return attention_v2_dispatch_g<128>(s, q, k, vt, vt_cols, o, work, n_work, H, KV, half_window, scale);
-    return attention_v2_dispatch_g<256>(s, q, k, vt, vt_cols, o, work, n_work, H, KV, half_window, scale);
+    if (hd == 128)
+        return attention_v2_dispatch_g<128>(s, q, k, vt, vt_cols, o, work, n_work, H, KV, half_window, scale, item_queries);
+    return attention_v2_dispatch_g<256>(s, q, k, vt, vt_cols, o, work, n_work, H, KV, half_window, scale, item_queries);
 }
 
 // V [T][KV][hd] fp16 -> V^T [KV * hd][vt_cols] at column vcol[t]. A workgroup transposes 64
@@ -847,7 +854,10 @@ static hipError_t attention_v2_configure() {
 
 template <int HD, int G>
 static hipError_t attention_v3_configure() {
-    return hipFuncSetAttribute(reinterpret_cast<const void*>(&attention_v3_kernel<HD, G>),
+    hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&attention_v3_kernel<HD, G, 4>),
+                                       hipFuncAttributeMaxDynamicSharedMemorySize, attention_v3_lds_bytes<HD>());
+    if (e != hipSuccess) return e;
+    return hipFuncSetAttribute(reinterpret_cast<const void*>(&attention_v3_kernel<HD, G, 2>),
                                hipFuncAttributeMaxDynamicSharedMemorySize, attention_v3_lds_bytes<HD>());
 }
 

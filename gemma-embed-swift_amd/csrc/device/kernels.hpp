@@ -115,13 +115,15 @@ hipError_t launch_attention(hipStream_t s, const uint16_t* q, const uint16_t* k,
                             const AttnWork* work, int n_work, int H, int KV, int hd, int half_window, float scale);
 
 // Attention with K/V copied straight into LDS (head dims 128 and 256, at most 4 query heads per
-// KV head): work items of kAttnQueriesV2 query rows; V given transposed, vt [KV * hd][vt_cols],
-// each sequence's keys starting at its work items' vt_start.
+// KV head): work items of item_queries query rows (kAttnQueriesV2, or 32 for up to 3 query heads
+// per KV head: twice the workgroups for a small batch; a query's result is the same either way);
+// V given transposed, vt [KV * hd][vt_cols], each sequence's keys starting at its work items'
+// vt_start.
 constexpr int kAttnQueriesV2 = 64;
 bool attention_v2_supported(int hd, int H, int KV);
 hipError_t launch_attention_v2(hipStream_t s, const uint16_t* q, const uint16_t* k, const uint16_t* vt, int vt_cols,
                                uint16_t* o, const AttnWork* work, int n_work, int H, int KV, int hd, int half_window,
-                               float scale);
+                               float scale, int item_queries = kAttnQueriesV2);
 
 // v [T][width] fp16 -> vt [width][vt_cols] with token t at column vcol[t]; width a multiple of 64.
 hipError_t launch_v_transpose(hipStream_t s, const uint16_t* v, int T, int width, const int32_t* vcol, int vt_cols,

@@ -97,9 +97,10 @@ struct DevModel {
     Q8Dev tok_embd, output;
     float* out_norm = nullptr;
     std::vector<DevLayer> layer;
-    int max_qd = 0, max_kvd = 0, max_qkv = 0;
+    int max_qd = 0, max_kvd = 0, max_qkv = 0, max_kv_heads = 1;
     bool all_fused = true;  // every layer: fused QKV epilogue and the LDS-copy attention
     bool any_v2 = false;
+    bool items32_ok = true;  // every LDS-copy attention layer takes 32-query work items (<= 3 heads per KV head)
 };
 
 struct Workspace {
@@ -162,6 +163,7 @@ struct ge_ctx {
     ge::Workspace ws;
     // staged batch
     int staged_tokens = -1, staged_seqs = 0, staged_work = 0, staged_work2 = 0, staged_vt_cols = 0;
+    int attn_items = ge::kAttnQueriesV2;  // query rows per LDS-copy attention work item of the staged batch
     // Split batch: part p is rows [part_row[p], part_row[p + 1]) with work2 items
     // [part_work[p], part_work[p + 1]); n_parts 1 = not split.
     int n_parts = 1;
@@ -591,11 +593,13 @@ void upload(ge_ctx* c, const ge_model_desc* d, const void* base, size_t len) {
         L.rope = rope_table(c, hd, L.rope_base, m.max_tokens);
         m.max_qd = std::max(m.max_qd, L.qd);
         m.max_kvd = std::max(m.max_kvd, L.kvd);
+        m.max_kv_heads = std::max(m.max_kv_heads, L.kv_heads);
         L.attn_v2 = attention_v2_supported(L.head_dim, m.heads, L.kv_heads);
         L.qkv_gn = qkv_norm_rope_vt_supported(L.head_dim, m.heads, L.kv_heads);
         L.qkv_fused = L.qkv_gn && gemm_qkv_supported(L.head_dim, m.heads, L.kv_heads);
         m.all_fused = m.all_fused && L.qkv_fused && L.attn_v2;
         m.any_v2 = m.any_v2 || L.attn_v2;
+        if (L.attn_v2 && m.heads / L.kv_heads > 3) m.items32_ok = false;
         m.max_qkv = std::max(m.max_qkv, L.qd + 2 * L.kvd);
         m.layer.push_back(L);
     }
@@ -675,6 +679,10 @@ void ensure_workspace(ge_ctx* c, int tokens, int seqs, int work, int work2, int 
 
 // Batches of at least this many tokens are split into two halves on two streams.
 constexpr int kSplitMinTokens = 4096;
+// Below this many 64-query workgroups (one per CU), use 32-query items. Measured at config 2's
+// sliding layers: a 8192-token pack (128 items) 36.5 -> 31.0 us per attention launch; a 16384-token
+// pack (256 items) 41.0 -> 57.0 us, so it keeps 64-query items.
+constexpr int kAttnSmallItems = 256;
 
 // Transposed-V layout of a packed batch: each sequence's keys start at a column that is a
 // multiple of 8 (16-byte aligned copies); vt_cols leaves a key block of slack past the end.
@@ -737,10 +745,17 @@ void stage(ge_ctx* c, const int32_t* tokens, const int32_t* positions, int n, co
     }
     std::vector<AttnWork> work2;
     VtLayout vl;
+    int items = kAttnQueriesV2;
     if (m.any_v2) {
         vl = vt_layout(n, seqs, n_seqs);
+        // A batch whose 64-query items would give fewer than kAttnSmallItems workgroups (a pack of
+        // 8192 tokens: 128) takes 32-query items: twice the workgroups, the same results (a query's
+        // wave sees the same key blocks; blocks outside its window add exact zeros).
+        int64_t items64 = 0;
+        for (int s = 0; s < n_seqs; s++) items64 += (seqs[s].length + kAttnQueriesV2 - 1) / kAttnQueriesV2;
+        if (m.items32_ok && items64 * m.max_kv_heads < kAttnSmallItems) items = 32;
         for (int s = 0; s < n_seqs; s++)
-            for (uint32_t q0 = 0; q0 < seqs[s].length; q0 += kAttnQueriesV2)
+            for (uint32_t q0 = 0; q0 < seqs[s].length; q0 += uint32_t(items))
                 work2.push_back(AttnWork{seqs[s].start, seqs[s].length, q0, vl.start[size_t(s)]});
     }
     // Split a large batch of several sequences into parts of whole sequences, cut at the
@@ -796,6 +811,7 @@ void stage(ge_ctx* c, const int32_t* tokens, const int32_t* positions, int n, co
     c->staged_work = int(work.size());
     c->staged_work2 = int(work2.size());
     c->staged_vt_cols = vl.cols;
+    c->attn_items = items;
     c->n_parts = n_parts;
     std::copy(part_row, part_row + kMaxParts + 1, c->part_row);
     std::copy(part_work, part_work + kMaxParts + 1, c->part_work);
@@ -872,7 +888,7 @@ void encode(ge_ctx* c, StopPoint* sp) {
             if (!fused_vt) launch(c, "v_transpose", [&] { return launch_v_transpose(s, w.v, T, L.kvd, w.vcol, w.vt_cap, w.vt); });
             launch(c, "attention", [&] {
                 return launch_attention_v2(s, w.q, w.k, w.vt, w.vt_cap, w.attn, w.work2, c->staged_work2, m.heads, L.kv_heads,
-                                           L.head_dim, hw, 1.0f);
+                                           L.head_dim, hw, 1.0f, c->attn_items);
             });
         } else {
             launch(c, "attention", [&] {
@@ -955,7 +971,7 @@ void encode_split(ge_ctx* c) {
         for (const Half& H : halves)
             launch(c, "attention", [&] {
                 return launch_attention_v2(H.s, w.q, w.k, w.vt, w.vt_cap, w.attn, H.work, H.n_work, m.heads, L.kv_heads,
-                                           L.head_dim, hw, 1.0f);
+                                           L.head_dim, hw, 1.0f, c->attn_items);
             });
         for (const Half& H : halves)
             launch(c, "gemm_o", [&] {

@@ -130,6 +130,17 @@ def test_split_batch_matches_single_stream(c2_model, config2_batch):
     assert np.array_equal(split, single)
 
 
+def test_attention_item_size_does_not_change_results(c2_model, config2_batch):
+    """A pack of 16384 tokens (256 work items of 64 queries) and one of 8192 tokens (fewer than one
+    64-query item per CU: 32-query items) give the same texts the same bits."""
+    ctx = c2_model.context
+    full, _ = ctx.forward(config2_batch)
+    half, _ = ctx.forward(config2_batch[:16])
+    assert np.array_equal(full[:16], half)
+    quarter, _ = ctx.forward(config2_batch[20:24])
+    assert np.array_equal(full[20:24], quarter)
+
+
 def test_packing_invariance_and_determinism(c2_model, config2_batch):
     batch = config2_batch[:8]
     a = c2_model.embed_tokens(batch)
