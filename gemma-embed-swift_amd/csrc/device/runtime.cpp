@@ -155,6 +155,13 @@ struct ge_ctx {
     hipStream_t part_stream[ge::kMaxParts] = {};
     hipEvent_t part_join[ge::kMaxParts] = {};
     hipEvent_t ev_start = nullptr, ev_stop = nullptr, ev_fork = nullptr;
+    // Pinned host staging of a batch's small arrays (ids, positions, ranges, work lists, V^T
+    // columns): their uploads are asynchronous, and the next batch waits for staged_copy before
+    // writing the buffer again.
+    void* pinned = nullptr;
+    size_t pinned_cap = 0;
+    hipEvent_t staged_copy = nullptr;
+    bool staged_copy_recorded = false;
     std::string err, name;
     bool has_model = false;
     ge::DevModel model;
@@ -616,6 +623,15 @@ T* ws_alloc(size_t rows, size_t width, const char* what) {
     return static_cast<T*>(p);
 }
 
+// Whether ensure_workspace would reallocate any buffer for a batch of this size.
+bool workspace_grows(const ge_ctx* c, int tokens, int seqs, int work, int work2, int vt_cols) {
+    const Workspace& w = c->ws;
+    const DevModel& m = c->model;
+    const int rows = (tokens + 63) / 64 * 64 + kRowSlack;
+    return rows > w.rows || seqs > w.seq_cap || !w.seqs || work > w.work_cap || !w.work ||
+           (m.any_v2 && (work2 > w.work2_cap || !w.work2 || vt_cols > w.vt_cap || !w.vt));
+}
+
 void ensure_workspace(ge_ctx* c, int tokens, int seqs, int work, int work2, int vt_cols) {
     Workspace& w = c->ws;
     const DevModel& m = c->model;
@@ -794,18 +810,45 @@ void stage(ge_ctx* c, const int32_t* tokens, const int32_t* positions, int n, co
                 if (part_work[p + 1] == part_work[p]) n_parts = 1;  // a part without work: do not split
         }
     }
+    // The workspace may be reallocated below: nothing queued may still use it.
+    if (workspace_grows(c, n, n_seqs, int(work.size()), int(work2.size()), vl.cols))
+        hip_check(hipStreamSynchronize(c->stream), "hipStreamSynchronize");
     ensure_workspace(c, n, n_seqs, int(work.size()), int(work2.size()), vl.cols);
     Workspace& w = c->ws;
-    hip_check(hipMemcpyAsync(w.tokens, tokens, size_t(n) * 4, hipMemcpyHostToDevice, c->stream), "upload tokens");
-    hip_check(hipMemcpyAsync(w.positions, positions, size_t(n) * 4, hipMemcpyHostToDevice, c->stream), "upload positions");
-    hip_check(hipMemcpyAsync(w.seqs, sr.data(), sr.size() * sizeof(SeqRange), hipMemcpyHostToDevice, c->stream), "upload sequences");
-    if (!work.empty())
-        hip_check(hipMemcpyAsync(w.work, work.data(), work.size() * sizeof(AttnWork), hipMemcpyHostToDevice, c->stream), "upload work");
-    if (!work2.empty()) {
-        hip_check(hipMemcpyAsync(w.work2, work2.data(), work2.size() * sizeof(AttnWork), hipMemcpyHostToDevice, c->stream), "upload work");
-        hip_check(hipMemcpyAsync(w.vcol, vl.vcol.data(), size_t(n) * 4, hipMemcpyHostToDevice, c->stream), "upload columns");
+    // The small arrays go through one pinned buffer: asynchronous copies, no wait for them here
+    // (the forward's kernels follow them on the same stream).
+    struct Piece {
+        void* dst;
+        const void* src;
+        size_t bytes;
+    };
+    const Piece pieces[] = {{w.tokens, tokens, size_t(n) * 4},
+                            {w.positions, positions, size_t(n) * 4},
+                            {w.seqs, sr.data(), sr.size() * sizeof(SeqRange)},
+                            {w.work, work.data(), work.size() * sizeof(AttnWork)},
+                            {w.work2, work2.data(), work2.size() * sizeof(AttnWork)},
+                            {w.vcol, vl.vcol.data(), work2.empty() ? 0 : size_t(n) * 4}};
+    size_t total = 0;
+    for (const Piece& pc : pieces) total += (pc.bytes + 255) / 256 * 256;
+    if (c->staged_copy_recorded) hip_check(hipEventSynchronize(c->staged_copy), "hipEventSynchronize");
+    if (total > c->pinned_cap) {
+        if (c->pinned) hip_check(hipHostFree(c->pinned), "hipHostFree");
+        c->pinned = nullptr;
+        c->pinned_cap = 0;
+        const size_t cap = std::max(total, size_t(1) << 20);
+        hip_check(hipHostMalloc(&c->pinned, cap, hipHostMallocDefault), "hipHostMalloc");
+        c->pinned_cap = cap;
     }
-    hip_check(hipStreamSynchronize(c->stream), "hipStreamSynchronize");
+    size_t off = 0;
+    for (const Piece& pc : pieces) {
+        if (pc.bytes == 0) continue;
+        unsigned char* h = static_cast<unsigned char*>(c->pinned) + off;
+        std::memcpy(h, pc.src, pc.bytes);
+        hip_check(hipMemcpyAsync(pc.dst, h, pc.bytes, hipMemcpyHostToDevice, c->stream), "upload batch");
+        off += (pc.bytes + 255) / 256 * 256;
+    }
+    hip_check(hipEventRecord(c->staged_copy, c->stream), "hipEventRecord");
+    c->staged_copy_recorded = true;
     c->staged_tokens = n;
     c->staged_seqs = n_seqs;
     c->staged_work = int(work.size());
@@ -1152,6 +1195,7 @@ int ge_create(int device, ge_ctx** out) {
         ge::hip_check(hipEventCreate(&c->ev_start), "hipEventCreate");
         ge::hip_check(hipEventCreate(&c->ev_stop), "hipEventCreate");
         ge::hip_check(hipEventCreateWithFlags(&c->ev_fork, hipEventDisableTiming), "hipEventCreate");
+        ge::hip_check(hipEventCreateWithFlags(&c->staged_copy, hipEventDisableTiming), "hipEventCreate");
 
         hipDeviceProp_t prop;
         ge::hip_check(hipGetDeviceProperties(&prop, device), "hipGetDeviceProperties");
@@ -1167,7 +1211,8 @@ int ge_create(int device, ge_ctx** out) {
             if (c->part_join[p]) (void)hipEventDestroy(c->part_join[p]);
         }
         if (c->stream) (void)hipStreamDestroy(c->stream);
-        if (c->ev_fork) (void)hipEventDestroy(c->ev_fork);
+        for (hipEvent_t e : {c->ev_start, c->ev_stop, c->ev_fork, c->staged_copy})
+            if (e) (void)hipEventDestroy(e);
         return rc;
     }
     *out = c.release();
@@ -1188,6 +1233,8 @@ void ge_destroy(ge_ctx* c) {
     if (c->ev_start) (void)hipEventDestroy(c->ev_start);
     if (c->ev_stop) (void)hipEventDestroy(c->ev_stop);
     if (c->ev_fork) (void)hipEventDestroy(c->ev_fork);
+    if (c->staged_copy) (void)hipEventDestroy(c->staged_copy);
+    if (c->pinned) (void)hipHostFree(c->pinned);
     for (int p = 0; p < ge::kMaxParts; p++) {
         if (c->part_stream[p] && c->part_stream[p] != c->stream) {
             (void)hipStreamSynchronize(c->part_stream[p]);
