@@ -120,6 +120,7 @@ struct GemmCfg {
 // K in stages of 64, two stages (128 KB) for the 768-wide ones (attention output, down).
 using GemmWide = GemmCfg<128, 256, 2, 4, 32, 3>;
 using GemmSquare = GemmCfg<256, 256, 4, 4, 64, 2>;
+using GemmSmall = GemmCfg<128, 128, 2, 2, 64, 2>;
 
 // Workgroup b's tile: workgroups are dealt to the 8 XCDs round robin (b runs on XCD b % 8), and
 // tile (b % 8) * (T / 8) + b / 8 gives each XCD a contiguous, M-major run of tiles.
@@ -579,6 +580,7 @@ hipError_t gemm_configure_shape() {
 hipError_t gemm_configure() {
     hipError_t e = gemm_configure_shape<GemmWide>();
     if (e == hipSuccess) e = gemm_configure_shape<GemmSquare>();
+    if (e == hipSuccess) e = gemm_configure_shape<GemmSmall>();
     if (e == hipSuccess) e = set_lds_limit(gemm_qkv_kernel<128>, GemmWide::LDS);
     if (e == hipSuccess) e = set_lds_limit(gemm_qkv_kernel<256>, GemmWide::LDS);
     return e;
@@ -659,7 +661,14 @@ hipError_t launch_gemm_q8(hipStream_t s, const Q8Dev& w, const uint16_t* x, int 
         default: return hipErrorInvalidValue;
         }
     }
-    if (w.rows <= 1024 && w.cols % GemmSquare::BK == 0) return gemm_launch<GemmSquare>(s, w, x, M, y, epi, out_scale);
+    // The 768-wide projections (o, down, output) by batch rows, from a sweep of the tile shapes
+    // (the timed config-2 forward launches them at M = 8192, two at a time): 256 x 256 tiles from
+    // 12288 rows, 128 x 256 from 6144, 128 x 128 (K in stages of 64) below. The tile shape does
+    // not change the results: every shape runs the same MFMA over the same k order.
+    if (w.rows <= 1024 && w.cols % GemmSquare::BK == 0) {
+        if (M >= 12288) return gemm_launch<GemmSquare>(s, w, x, M, y, epi, out_scale);
+        if (M < 6144) return gemm_launch<GemmSmall>(s, w, x, M, y, epi, out_scale);
+    }
     return gemm_launch<GemmWide>(s, w, x, M, y, epi, out_scale);
 }
 
