@@ -106,6 +106,30 @@ def test_config2_per_layer_vs_oracle(c2_model, c2_oracle, config2_batch):
     print(f"worst l_out max_rel {worst:.3e}", flush=True)
 
 
+@pytest.mark.parametrize("lengths", [(100, 37, 64), (20, 25, 10)], ids=["tiled", "short"])
+def test_every_trace_tensor_vs_oracle(c2_model, c2_oracle, config2_batch, lengths):
+    """Every named intermediate the C-ABI traces (llama.cpp names), at a sliding (0) and a global (5)
+    layer, against the oracle on the middle text of a pack: the embedding, the norms, the raw and
+    the normed/rotated projections, attention, the GeGLU product, the FFN output, the layer output
+    and the final norm and projection. A pack of at most 64 tokens runs the short-batch kernels."""
+    batch = [config2_batch[2 + 4 * i][:n] for i, n in enumerate(lengths)]
+    idx, lo = 1, lengths[0]
+    per_layer = ["attn_norm", "Qcur", "Kcur", "Vcur", "Qcur_pos", "Kcur_pos", "Vcur_normed", "kqv_out",
+                 "attn_out", "ffn_norm", "ffn_geglu", "ffn_out", "pe_in", "l_out"]
+    names = [("inp_scaled", -1), ("result_norm", -1), ("result_embd", -1)] + \
+        [(n, l) for l in (0, 5) for n in per_layer]
+    _, tr = c2_oracle.forward(batch[idx], keep=names)
+    n = len(batch[idx])
+    for name, layer in names:
+        got = c2_model.context.trace(batch, name, layer)[lo:lo + n]
+        want = tr[(name, layer)].reshape(n, -1)
+        if name == "ffn_geglu":  # stored scaled by a power of two; compare the shape-invariant ratio
+            got = got * (np.abs(want).max() / max(np.abs(got).max(), 1e-30))
+        r = max_rel(got, want)
+        print(f"{name}-{layer}: max_rel {r:.3e}", flush=True)
+        assert r <= PER_LAYER_TOL, (name, layer)
+
+
 def test_split_batch_matches_single_stream(c2_model, config2_batch):
     """A pack of >= 4096 tokens runs as two halves of whole sequences on two streams; with
     profiling on, the same pack runs on one stream. Same kernels on the same rows: the vectors
