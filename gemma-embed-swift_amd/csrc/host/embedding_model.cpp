@@ -68,6 +68,9 @@ void finish(const float* v, int dims, bool normalise, float* out) {
     }
 }
 
+// Largest device pack that consecutive planned batches are merged into (tokens).
+constexpr int64_t kRunTokens = 32768;
+
 int model_fail(ge_model* m, int code, const std::string& msg) {
     m->err = msg;
     return code;
@@ -216,23 +219,39 @@ int ge_model_embed(ge_model* m, const int32_t* tokens, const int32_t* lengths, i
     int completed_texts = 0;
     int64_t completed_tokens = 0;
     std::vector<float> pooled;
-    for (size_t r = 0; r + 1 < starts.size(); r++) {
-        std::vector<std::vector<int32_t>> batch(prepared.begin() + starts[r], prepared.begin() + starts[r + 1]);
-        int rc = ge::run_batch(m, batch, &pooled);
+    auto batch_tokens = [&](size_t r) {
+        int64_t t = 0;
+        for (int i = starts[r]; i < starts[r + 1]; i++) t += costs[size_t(i)];
+        return t;
+    };
+    // Consecutive planned batches run on the device as one pack of up to kRunTokens tokens. A
+    // text's vector does not depend on the pack around it (every kernel gives the same bits for
+    // its rows whatever the pack), so only the time changes: an 8192-token pack (the default
+    // budget) uses the GPU less well than a larger one. Progress and cancellation still follow
+    // the planned batches.
+    for (size_t r = 0; r + 1 < starts.size();) {
+        size_t r_end = r + 1;
+        int64_t tok = batch_tokens(r);
+        while (r_end + 1 < starts.size() && tok + batch_tokens(r_end) <= ge::kRunTokens) tok += batch_tokens(r_end++);
+        std::vector<std::vector<int32_t>> pack(prepared.begin() + starts[r], prepared.begin() + starts[r_end]);
+        int rc = ge::run_batch(m, pack, &pooled);
         if (rc != GE_OK) return rc;
-        for (int i = starts[r]; i < starts[r + 1]; i++) {
-            const size_t j = size_t(i - starts[r]);
-            ge::finish(pooled.data() + j * size_t(m->cfg.out_dims), opt.dimensions, opt.normalise != 0,
-                       out + size_t(i) * size_t(opt.dimensions));
-            if (token_counts) token_counts[i] = costs[size_t(i)];
-            if (truncated) truncated[i] = cut[size_t(i)];
-            completed_tokens += costs[size_t(i)];
+        for (size_t q = r; q < r_end; q++) {
+            for (int i = starts[q]; i < starts[q + 1]; i++) {
+                const size_t j = size_t(i - starts[r]);
+                ge::finish(pooled.data() + j * size_t(m->cfg.out_dims), opt.dimensions, opt.normalise != 0,
+                           out + size_t(i) * size_t(opt.dimensions));
+                if (token_counts) token_counts[i] = costs[size_t(i)];
+                if (truncated) truncated[i] = cut[size_t(i)];
+                completed_tokens += costs[size_t(i)];
+            }
+            completed_texts = starts[q + 1];
+            // EmbeddingProgress after every batch; a non-zero return cancels before the next one
+            // (Task.checkCancellation, EmbeddingModel.swift:162).
+            if (progress && progress(user, completed_texts, n, completed_tokens) != 0 && q + 2 < starts.size())
+                return ge::model_fail(m, GE_ERR_CANCELLED, "embedding was cancelled");
         }
-        completed_texts = starts[r + 1];
-        // EmbeddingProgress after every batch; a non-zero return cancels before the next one
-        // (Task.checkCancellation, EmbeddingModel.swift:162).
-        if (progress && progress(user, completed_texts, n, completed_tokens) != 0 && r + 2 < starts.size())
-            return ge::model_fail(m, GE_ERR_CANCELLED, "embedding was cancelled");
+        r = r_end;
     }
     return GE_OK;
 }

@@ -10,12 +10,17 @@
 //   ge_probe attention [reps] the attention of a sliding-window layer (ge_op_attention: 32
 //                             sequences of 512 tokens, 3 query heads, 1 KV head, head dim 256,
 //                             half window 256; Kernels.attention, Metal/MetalForward.swift:669-694)
+//   ge_probe embed [reps]     the host API end to end on config 2 (a synthetic 24-layer model
+//                             written to a temporary GGUF; 32 texts x 512 ids): the time per
+//                             call of ge_model_embed at the 8192- and 16384-token budgets, and
+//                             of the resident pack (ge_batch_run) for comparison
 //   ge_probe calibrate        fp16 -> fp32 conversion of 2^28 values (reads 512 MiB, writes 1 GiB):
 //                             the known-size kernel that scales the HBM byte counters
 //
 // Inputs are synthetic: Q8_0 rows with random int8 quants and fp16 scales, activations uniform
 // in [-0.5, 0.5). Each call of the GeGLU entry point also interleaves the two matrices and builds
 // their fragment-order copy; a profile reads the GEMM kernel's own rows.
+#include <chrono>
 #include <cstdint>
 #include <cstdio>
 #include <cstdlib>
@@ -106,6 +111,75 @@ int probe_attention(ge_ctx* c, int reps) {
     return 0;
 }
 
+int probe_embed(int reps) {
+    // BASELINE config 2's model shape (the Python package's CONFIG2)
+    uint8_t pattern[24];
+    for (int l = 0; l < 24; l++) pattern[l] = (l % 6 == 5) ? 0 : 1;
+    ge_synth_spec spec{};
+    spec.layers = 24, spec.hidden = 768, spec.heads = 3, spec.feed_forward = 1152, spec.out_dims = 768;
+    spec.per_layer_input = 0, spec.vocab = 262144, spec.sliding_window = 512;
+    spec.head_dim_swa = 256, spec.head_dim_global = 256, spec.kv_heads_swa = 1, spec.kv_heads_global = 1;
+    spec.eps = 1e-6f, spec.rope_base = 1e6f, spec.rope_base_swa = 1e4f, spec.pattern = pattern, spec.seed = 4;
+    char err[512] = {0};
+    const char* path = "/tmp/ge_probe_config2.gguf";
+    if (ge_synth_write_gguf(path, &spec, err, sizeof err) != 0) {
+        std::fprintf(stderr, "ge_probe: synth: %s\n", err);
+        return 1;
+    }
+    const int texts = 32, len = 512;
+    std::vector<int32_t> ids(size_t(texts) * len), lengths(texts, len);
+    ge_synth_tokens(3, 2, 262144, texts * len, ids.data());
+    std::vector<float> out(size_t(texts) * 768);
+    for (int budget : {8192, 16384}) {
+        ge_load_options lo{0, budget, 1};
+        ge_model* m = nullptr;
+        if (ge_model_load(path, &lo, &m, err, sizeof err) != 0) {
+            std::fprintf(stderr, "ge_probe: load: %s\n", err);
+            return 1;
+        }
+        ge_embed_options eo{2048, 768, 1, 0};
+        auto call = [&] {
+            return ge_model_embed(m, ids.data(), lengths.data(), texts, &eo, out.data(), nullptr, nullptr, nullptr, nullptr);
+        };
+        for (int r = 0; r < 2; r++)
+            if (call() != 0) return std::fprintf(stderr, "ge_probe: embed: %s\n", ge_model_last_error(m)), 1;
+        const auto t0 = std::chrono::steady_clock::now();
+        for (int r = 0; r < reps; r++)
+            if (call() != 0) return std::fprintf(stderr, "ge_probe: embed: %s\n", ge_model_last_error(m)), 1;
+        const double ms = std::chrono::duration<double, std::milli>(std::chrono::steady_clock::now() - t0).count() / reps;
+        std::printf("ge_model_embed, budget %d: %.3f ms per call of %d x %d ids, %.0f tokens/s\n", budget, ms, texts, len,
+                    texts * len / (ms * 1e-3));
+        if (budget == 16384) {
+            ge_ctx* c = ge_model_context(m);
+            std::vector<int32_t> pos(ids.size());
+            std::vector<ge_seq> seqs(texts);
+            for (int t = 0; t < texts; t++) {
+                seqs[t] = ge_seq{uint32_t(t * len), uint32_t(len)};
+                for (int i = 0; i < len; i++) pos[size_t(t) * len + i] = i;
+            }
+            if (ge_batch_stage(c, ids.data(), pos.data(), int32_t(ids.size()), seqs.data(), texts) != 0) return fail(c, "stage");
+            for (int r = 0; r < 2; r++) ge_batch_run(c);
+            ge_sync(c);
+            const auto t1 = std::chrono::steady_clock::now();
+            for (int r = 0; r < reps; r++) ge_batch_run(c);
+            ge_sync(c);
+            const double rms = std::chrono::duration<double, std::milli>(std::chrono::steady_clock::now() - t1).count() / reps;
+            const auto t2 = std::chrono::steady_clock::now();
+            for (int r = 0; r < reps; r++) {
+                ge_batch_stage(c, ids.data(), pos.data(), int32_t(ids.size()), seqs.data(), texts);
+                ge_batch_run(c);
+                ge_batch_read(c, out.data());
+            }
+            const double sms = std::chrono::duration<double, std::milli>(std::chrono::steady_clock::now() - t2).count() / reps;
+            std::printf("resident pack: %.3f ms per forward; stage + run + read: %.3f ms\n", rms, sms);
+        }
+        std::fflush(stdout);
+        ge_model_free(m);
+    }
+    std::remove(path);
+    return 0;
+}
+
 int probe_calibrate(ge_ctx* c) {
     const size_t n = size_t(1) << 28;
     void* src = ge_dev_alloc(c, 2 * n);
@@ -124,8 +198,9 @@ int probe_calibrate(ge_ctx* c) {
 int main(int argc, char** argv) {
     const char* what = argc > 1 ? argv[1] : "gate_up";
     const int reps = argc > 2 ? std::atoi(argv[2]) : 20;
+    if (std::strcmp(what, "embed") == 0) return reps < 1 || reps > 10000 ? 2 : probe_embed(reps);
     if (std::strcmp(what, "gate_up") != 0 && std::strcmp(what, "attention") != 0 && std::strcmp(what, "calibrate") != 0) {
-        std::fprintf(stderr, "usage: ge_probe gate_up [reps] | ge_probe attention [reps] | ge_probe calibrate\n");
+        std::fprintf(stderr, "usage: ge_probe gate_up|attention|embed [reps] | ge_probe calibrate\n");
         return 2;
     }
     if (reps < 1 || reps > 10000) {
