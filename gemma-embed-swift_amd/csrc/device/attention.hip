@@ -542,7 +542,9 @@ constexpr int BKV = 32;   // keys per block
 template <int HD>
 constexpr int attention_v3_lds_bytes() { return attn3::NS * 2 * attn3::BKV * HD * 2; }
 
-template <int HD, int G, int QW>
+// HO: head dims stored per head (the first HO of HD; the rest are zero padding of Q, K and V^T, as
+// for the image tower's 72-wide heads held in 96), output row stride H * HO.
+template <int HD, int G, int QW, int HO = HD>
 __global__ __launch_bounds__(QW * G * 64) void attention_v3_kernel(const uint16_t* __restrict__ Qg,
                                                                   const uint16_t* __restrict__ Kg,
                                                                   const uint16_t* __restrict__ VTg,
@@ -551,6 +553,8 @@ __global__ __launch_bounds__(QW * G * 64) void attention_v3_kernel(const uint16_
                                                                   int vt_cols, int hw, float scale_log2) {
     using namespace attn3;
     constexpr int QB = 16 * QW, NW = QW * G, KS = HD / 32, DT = HD / 16;
+    constexpr int DTO = (HO + 15) / 16;  // head-dim tiles of O that hold stored dims
+    static_assert(HO <= HD && HO % 8 == 0, "stored head dims");
     constexpr int K_BYTES = BKV * HD * 2, STAGE = 2 * K_BYTES;
     constexpr int KCH = K_BYTES / 1024, CH = 2 * KCH;  // K chunks (ks, m), then V^T chunks dt
     static_assert(KCH == 2 * KS && KCH == DT, "chunk counts");
@@ -709,8 +713,8 @@ __global__ __launch_bounds__(QW * G * 64) void attention_v3_kernel(const uint16_
         l_run += sum;  // this lane's keys only; the key groups are summed once, at the end
         // O^T += V^T P^T: head-dim tiles dt of 16 rows, the block's 32 keys as one k-step
 #pragma unroll
-        for (int dt = 0; dt < DT; dt++) {
-            if (dt + PF < DT) va[(dt + PF) % RING] = *reinterpret_cast<const half8_t*>(vf + (dt + PF) * 1024);
+        for (int dt = 0; dt < DTO; dt++) {
+            if (dt + PF < DTO) va[(dt + PF) % RING] = *reinterpret_cast<const half8_t*>(vf + (dt + PF) * 1024);
             __builtin_amdgcn_sched_barrier(0);
             o[dt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(va[dt % RING], pb, o[dt], 0, 0, 0);
         }
@@ -722,9 +726,10 @@ __global__ __launch_bounds__(QW * G * 64) void attention_v3_kernel(const uint16_
     if (qi >= len) return;
     const float inv = l_run > 0.0f ? 1.0f / l_run : 0.0f;
     // o[dt], lane l: head dims 16 dt + 4 (l / 16) + r of query qi
-    _Float16* op = reinterpret_cast<_Float16*>(Og) + (size_t)(seq_start + qi) * qStride + h * HD + 4 * g4;
+    _Float16* op = reinterpret_cast<_Float16*>(Og) + (size_t)(seq_start + qi) * (H * HO) + h * HO + 4 * g4;
 #pragma unroll
-    for (int dt = 0; dt < DT; dt++) {
+    for (int dt = 0; dt < DTO; dt++) {
+        if (HO < HD && 16 * dt + 4 * g4 >= HO) continue;
         half4_t v4;
 #pragma unroll
         for (int r = 0; r < 4; r++) v4[r] = _Float16(o[dt][r] * inv);
@@ -790,6 +795,20 @@ hipError_t launch_attention_v2(hipStream_t s, const uint16_t* q, const uint16_t*
     if (hd == 128)
         return attention_v2_dispatch_g<128>(s, q, k, vt, vt_cols, o, work, n_work, H, KV, half_window, scale, item_queries);
     return attention_v2_dispatch_g<256>(s, q, k, vt, vt_cols, o, work, n_work, H, KV, half_window, scale, item_queries);
+}
+
+bool attention_padded_supported(int hp, int hd, int H, int KV) { return hp == 96 && hd == 72 && H > 0 && KV == H; }
+
+hipError_t launch_attention_padded(hipStream_t s, const uint16_t* q, const uint16_t* k, const uint16_t* vt, int vt_cols,
+                                   uint16_t* o, const AttnWork* work, int n_work, int H, int KV, int hp, int hd,
+                                   int half_window, float scale) {
+    if (n_work < 0 || !attention_padded_supported(hp, hd, H, KV) || half_window < 0 || vt_cols <= 0 || vt_cols % 8)
+        return hipErrorInvalidValue;
+    if (n_work == 0) return hipSuccess;
+    const float scale_log2 = scale * 1.4426950408889634f;
+    launch_kernel(attention_v3_kernel<96, 1, 4, 72>, dim3(n_work, KV), dim3(4 * 64), uint32_t(attention_v3_lds_bytes<96>()), s,
+                  q, k, vt, o, work, H, KV, vt_cols, half_window, scale_log2);
+    return hipGetLastError();
 }
 
 // V [T][KV][hd] fp16 -> V^T [KV * hd][vt_cols] at column vcol[t]. A workgroup transposes 64

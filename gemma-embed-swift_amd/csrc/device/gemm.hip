@@ -22,7 +22,8 @@ __device__ __forceinline__ half8_t dequant8(uint32_t a, uint32_t b, _Float16 d) 
 // GUARD false: the caller has checked that every row and column is inside Y.
 template <int FM, int FN, int EPI, bool GUARD>
 __device__ __forceinline__ void gemm_store_tile_impl(const float16_t (&acc)[FM][FN], void* __restrict__ Y, int M, int N,
-                                                     int row0, int cbase, int lane, float out_scale) {
+                                                     int row0, int cbase, int lane, float out_scale,
+                                                     const GemmEpiArgs& ea) {
     const int rbase = row0 + (lane >> 5) * 4;
     if constexpr (EPI == kEpiGeglu) {
         static_assert(FN % 2 == 0, "geglu pairs tiles");
@@ -49,12 +50,26 @@ __device__ __forceinline__ void gemm_store_tile_impl(const float16_t (&acc)[FM][
             for (int j = 0; j < FN; j++) {
                 const int col = cbase + j * 32 + (lane & 31);
                 if (GUARD && col >= N) continue;
+                float bias = 0.0f;
+                _Float16* hdst = nullptr;
+                size_t hstride = 0;
+                if constexpr (EPI == kEpiGeluBias || EPI == kEpiHeads) bias = ea.bias[col];
+                if constexpr (EPI == kEpiHeads) {
+                    // column -> (part, head, e) of the head-padded outputs
+                    const int g = col / ea.hd, e = col - g * ea.hd, part = g / ea.heads, head = g - part * ea.heads;
+                    hdst = reinterpret_cast<_Float16*>(ea.dst[part]) + head * ea.hp + e;
+                    hstride = size_t(ea.heads) * ea.hp;
+                }
 #pragma unroll
                 for (int r = 0; r < 16; r++) {
                     const int row = rbase + i * 32 + (r >> 2) * 8 + (r & 3);
                     if (GUARD && row >= M) continue;
                     if constexpr (EPI == kEpiF32)
                         static_cast<float*>(Y)[(size_t)row * N + col] = acc[i][j][r] * out_scale;
+                    else if constexpr (EPI == kEpiGeluBias)
+                        static_cast<_Float16*>(Y)[(size_t)row * N + col] = _Float16(gelu_tanh(acc[i][j][r] + bias) * out_scale);
+                    else if constexpr (EPI == kEpiHeads)
+                        hdst[(size_t)row * hstride] = _Float16((acc[i][j][r] + bias) * out_scale);
                     else
                         static_cast<_Float16*>(Y)[(size_t)row * N + col] = _Float16(acc[i][j][r] * out_scale);
                 }
@@ -64,11 +79,11 @@ __device__ __forceinline__ void gemm_store_tile_impl(const float16_t (&acc)[FM][
 
 template <int FM, int FN, int EPI>
 __device__ __forceinline__ void gemm_store_tile(const float16_t (&acc)[FM][FN], void* __restrict__ Y, int M, int N,
-                                                int row0, int cbase, int lane, float out_scale) {
+                                                int row0, int cbase, int lane, float out_scale, const GemmEpiArgs& ea) {
     if (row0 + FM * 32 <= M && cbase + FN * 32 <= N)
-        gemm_store_tile_impl<FM, FN, EPI, false>(acc, Y, M, N, row0, cbase, lane, out_scale);
+        gemm_store_tile_impl<FM, FN, EPI, false>(acc, Y, M, N, row0, cbase, lane, out_scale, ea);
     else
-        gemm_store_tile_impl<FM, FN, EPI, true>(acc, Y, M, N, row0, cbase, lane, out_scale);
+        gemm_store_tile_impl<FM, FN, EPI, true>(acc, Y, M, N, row0, cbase, lane, out_scale, ea);
 }
 
 // ============================================================================ GEMM
@@ -243,7 +258,7 @@ __device__ __forceinline__ void gemm_mainloop(const uint16_t* __restrict__ X, co
 template <class C, int EPI>
 __global__ __launch_bounds__(C::NT) void gemm_kernel(const uint16_t* __restrict__ X, const uint16_t* __restrict__ Fh,
                                                       void* __restrict__ Y, int M, int N, int K, float out_scale,
-                                                      int tiles_n, int tiles) {
+                                                      int tiles_n, int tiles, GemmEpiArgs ea) {
     extern __shared__ __attribute__((aligned(1024))) unsigned char lds[];
     const int tile = xcd_tile(blockIdx.x, tiles);
     const int m0 = (tile / tiles_n) * C::BM, n0 = (tile % tiles_n) * C::BN;
@@ -254,7 +269,7 @@ __global__ __launch_bounds__(C::NT) void gemm_kernel(const uint16_t* __restrict_
     gemm_mainloop<C, false>(X, Fh, M, N, K, m0, n0, lds, acc);
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     gemm_store_tile<C::FM, C::FN, EPI>(acc, Y, M, N, m0 + (wave / C::WN) * C::TM, n0 + (wave % C::WN) * C::TN, lane,
-                                       out_scale);
+                                       out_scale, ea);
 }
 
 
@@ -276,7 +291,7 @@ constexpr int skinny_steps() { return NJ == 1 ? 24 : 12; }
 template <int EPI, bool TR, int NJ>
 __global__ __launch_bounds__(256) void gemm_skinny_kernel(const uint16_t* __restrict__ X,
                                                           const uint16_t* __restrict__ Fh, void* __restrict__ Y,
-                                                          int M, int N, int K, float out_scale) {
+                                                          int M, int N, int K, float out_scale, GemmEpiArgs ea) {
     constexpr int SK = skinny_steps<NJ>();
     const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(int(threadIdx.x >> 6));
     const int groups = N / (32 * NJ), items = (M + 31) / 32 * groups;
@@ -338,7 +353,7 @@ __global__ __launch_bounds__(256) void gemm_skinny_kernel(const uint16_t* __rest
                 }
         }
     } else {
-        gemm_store_tile<1, NJ, EPI>(acc, Y, M, N, rt * 32, 32 * cg * NJ, lane, out_scale);
+        gemm_store_tile<1, NJ, EPI>(acc, Y, M, N, rt * 32, 32 * cg * NJ, lane, out_scale, ea);
     }
 }
 
@@ -574,6 +589,8 @@ hipError_t gemm_configure_shape() {
     hipError_t e = set_lds_limit(gemm_kernel<C, kEpiF32>, C::LDS);
     if (e == hipSuccess) e = set_lds_limit(gemm_kernel<C, kEpiF16>, C::LDS);
     if (e == hipSuccess) e = set_lds_limit(gemm_kernel<C, kEpiGeglu>, C::LDS);
+    if (e == hipSuccess) e = set_lds_limit(gemm_kernel<C, kEpiGeluBias>, C::LDS);
+    if (e == hipSuccess) e = set_lds_limit(gemm_kernel<C, kEpiHeads>, C::LDS);
     return e;
 }
 
@@ -588,19 +605,25 @@ hipError_t gemm_configure() {
 
 template <class C>
 hipError_t gemm_launch(hipStream_t s, const Q8Dev& w, const uint16_t* x, int M, void* y, GemmEpilogue epi,
-                       float out_scale) {
+                       float out_scale, const GemmEpiArgs& ea) {
     const int N = w.rows, K = w.cols;
     const int tiles_m = (M + C::BM - 1) / C::BM, tiles_n = (N + C::BN - 1) / C::BN, tiles = tiles_m * tiles_n;
     const dim3 grid(tiles), block(C::NT);
     switch (epi) {
     case kEpiF32:
-        launch_kernel(gemm_kernel<C, kEpiF32>, grid, block, C::LDS, s, x, w.fh, y, M, N, K, out_scale, tiles_n, tiles);
+        launch_kernel(gemm_kernel<C, kEpiF32>, grid, block, C::LDS, s, x, w.fh, y, M, N, K, out_scale, tiles_n, tiles, ea);
         break;
     case kEpiF16:
-        launch_kernel(gemm_kernel<C, kEpiF16>, grid, block, C::LDS, s, x, w.fh, y, M, N, K, out_scale, tiles_n, tiles);
+        launch_kernel(gemm_kernel<C, kEpiF16>, grid, block, C::LDS, s, x, w.fh, y, M, N, K, out_scale, tiles_n, tiles, ea);
         break;
     case kEpiGeglu:
-        launch_kernel(gemm_kernel<C, kEpiGeglu>, grid, block, C::LDS, s, x, w.fh, y, M, N, K, out_scale, tiles_n, tiles);
+        launch_kernel(gemm_kernel<C, kEpiGeglu>, grid, block, C::LDS, s, x, w.fh, y, M, N, K, out_scale, tiles_n, tiles, ea);
+        break;
+    case kEpiGeluBias:
+        launch_kernel(gemm_kernel<C, kEpiGeluBias>, grid, block, C::LDS, s, x, w.fh, y, M, N, K, out_scale, tiles_n, tiles, ea);
+        break;
+    case kEpiHeads:
+        launch_kernel(gemm_kernel<C, kEpiHeads>, grid, block, C::LDS, s, x, w.fh, y, M, N, K, out_scale, tiles_n, tiles, ea);
         break;
     default: return hipErrorInvalidValue;
     }
@@ -638,10 +661,11 @@ hipError_t launch_q8_fragments(hipStream_t s, const Q8Dev& w, uint16_t* fh) {
 }
 
 template <int EPI, bool TR, int NJ>
-hipError_t gemm_skinny_launch(hipStream_t s, const Q8Dev& w, const uint16_t* x, int M, void* y, float out_scale) {
+hipError_t gemm_skinny_launch(hipStream_t s, const Q8Dev& w, const uint16_t* x, int M, void* y, float out_scale,
+                              const GemmEpiArgs& ea = GemmEpiArgs{}) {
     const int items = (M + 31) / 32 * (w.rows / (32 * NJ));
     launch_kernel(gemm_skinny_kernel<EPI, TR, NJ>, dim3((items + 3) / 4), dim3(256), 0, s, x, w.fh, y, M, w.rows, w.cols,
-                  out_scale);
+                  out_scale, ea);
     return hipGetLastError();
 }
 
@@ -650,7 +674,16 @@ bool skinny_ok(const Q8Dev& w, int M) {
 }
 
 hipError_t launch_gemm_q8(hipStream_t s, const Q8Dev& w, const uint16_t* x, int M, void* y, GemmEpilogue epi,
-                          float out_scale) {
+                          float out_scale, const GemmEpiArgs* eap) {
+    const GemmEpiArgs ea = eap ? *eap : GemmEpiArgs{};
+    if (epi == kEpiHeads) {
+        if (!ea.bias || !ea.dst[0] || !ea.dst[1] || !ea.dst[2] || ea.hd <= 0 || ea.hp < ea.hd || ea.heads <= 0 ||
+            w.rows != 3 * ea.heads * ea.hd)
+            return hipErrorInvalidValue;
+        y = ea.dst[0];
+    } else if (epi == kEpiGeluBias && !ea.bias) {
+        return hipErrorInvalidValue;
+    }
     if (!gemm_operands_ok(w, x, M, y)) return hipErrorInvalidValue;
     if (M == 0) return hipSuccess;
     if (skinny_ok(w, M)) {
@@ -658,6 +691,8 @@ hipError_t launch_gemm_q8(hipStream_t s, const Q8Dev& w, const uint16_t* x, int 
         case kEpiF32: return gemm_skinny_launch<kEpiF32, false, 1>(s, w, x, M, y, out_scale);
         case kEpiF16: return gemm_skinny_launch<kEpiF16, false, 1>(s, w, x, M, y, out_scale);
         case kEpiGeglu: return gemm_skinny_launch<kEpiGeglu, false, 2>(s, w, x, M, y, out_scale);
+        case kEpiGeluBias: return gemm_skinny_launch<kEpiGeluBias, false, 1>(s, w, x, M, y, out_scale, ea);
+        case kEpiHeads: return gemm_skinny_launch<kEpiHeads, false, 1>(s, w, x, M, y, out_scale, ea);
         default: return hipErrorInvalidValue;
         }
     }
@@ -666,10 +701,10 @@ hipError_t launch_gemm_q8(hipStream_t s, const Q8Dev& w, const uint16_t* x, int 
     // 12288 rows, 128 x 256 from 6144, 128 x 128 (K in stages of 64) below. The tile shape does
     // not change the results: every shape runs the same MFMA over the same k order.
     if (w.rows <= 1024 && w.cols % GemmSquare::BK == 0) {
-        if (M >= 12288) return gemm_launch<GemmSquare>(s, w, x, M, y, epi, out_scale);
-        if (M < 6144) return gemm_launch<GemmSmall>(s, w, x, M, y, epi, out_scale);
+        if (M >= 12288) return gemm_launch<GemmSquare>(s, w, x, M, y, epi, out_scale, ea);
+        if (M < 6144) return gemm_launch<GemmSmall>(s, w, x, M, y, epi, out_scale, ea);
     }
-    return gemm_launch<GemmWide>(s, w, x, M, y, epi, out_scale);
+    return gemm_launch<GemmWide>(s, w, x, M, y, epi, out_scale, ea);
 }
 
 bool gemm_qkv_supported(int hd, int H, int KV) { return (hd == 128 || hd == 256) && H > 0 && KV > 0; }

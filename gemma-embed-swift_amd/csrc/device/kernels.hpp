@@ -44,7 +44,17 @@ struct Q8Dev {
 // halves; rows a multiple of 32).
 hipError_t launch_q8_fragments(hipStream_t s, const Q8Dev& w, uint16_t* fh);
 
-enum GemmEpilogue { kEpiF32 = 0, kEpiF16 = 1, kEpiGeglu = 2 };
+enum GemmEpilogue { kEpiF32 = 0, kEpiF16 = 1, kEpiGeglu = 2, kEpiGeluBias = 3, kEpiHeads = 4 };
+
+// Operands of the bias epilogues of the image tower. kEpiGeluBias: fp16
+// y[M][N] = gelu_tanh(acc + bias) * out_scale. kEpiHeads: fp16 (acc + bias) * out_scale into three
+// head-padded buffers: column n = (part * heads + head) * hd + e of the product goes to dst[part]
+// at [row][head][e], row stride heads * hp; columns hd .. hp of each head are not written.
+struct GemmEpiArgs {
+    const float* bias = nullptr;
+    uint16_t* dst[3] = {nullptr, nullptr, nullptr};
+    int hd = 0, hp = 0, heads = 0;
+};
 
 // y[M][N] = (x[M][K] (fp16) * W[N][K]^T (Q8_0, through W.fh)) * out_scale; N a multiple of 64,
 // K of 32. kEpiGeglu expects W's rows
@@ -53,8 +63,9 @@ enum GemmEpilogue { kEpiF32 = 0, kEpiF16 = 1, kEpiGeglu = 2 };
 // Batches of at most kSkinnyMaxRows rows (and K a multiple of 384) run on the skinny kernel,
 // one wave per 32-row block; the results are bitwise those of the tiled kernel.
 constexpr int kSkinnyMaxRows = 64;
+// kEpiGeluBias and kEpiHeads take their operands from ea (y is then unused by kEpiHeads).
 hipError_t launch_gemm_q8(hipStream_t s, const Q8Dev& w, const uint16_t* x, int M, void* y, GemmEpilogue epi,
-                          float out_scale = 1.0f);
+                          float out_scale = 1.0f, const GemmEpiArgs* ea = nullptr);
 
 // The QKV projection with the per-head norms and RoPE in its epilogue: the GEMM's fp32 result,
 // rounded to fp16 as qkv * scale (scale a power of two; eps is eps_model * scale^2), then the
@@ -125,12 +136,35 @@ hipError_t launch_attention_v2(hipStream_t s, const uint16_t* q, const uint16_t*
                                uint16_t* o, const AttnWork* work, int n_work, int H, int KV, int hd, int half_window,
                                float scale, int item_queries = kAttnQueriesV2);
 
+// The same attention over heads stored padded: q [T][H][hp], k [T][KV][hp] and vt [KV * hp][vt_cols]
+// hold hd real dims per head and zeros past them; out [T][H][hd]. Supported: hp 96 with hd 72
+// (the image tower's heads), one query head per KV head, 64-query work items.
+bool attention_padded_supported(int hp, int hd, int H, int KV);
+hipError_t launch_attention_padded(hipStream_t s, const uint16_t* q, const uint16_t* k, const uint16_t* vt, int vt_cols,
+                                   uint16_t* o, const AttnWork* work, int n_work, int H, int KV, int hp, int hd,
+                                   int half_window, float scale);
+
 // v [T][width] fp16 -> vt [width][vt_cols] with token t at column vcol[t]; width a multiple of 64.
 hipError_t launch_v_transpose(hipStream_t s, const uint16_t* v, int T, int width, const int32_t* vcol, int vt_cols,
                               uint16_t* vt);
 
 // pooled[s] = mean of the sequence's rows of x [*][width].
 hipError_t launch_mean_pool(hipStream_t s, const float* x, const SeqRange* seqs, int n_seqs, int width, float* pooled);
+
+// ---- image tower row kernels (vision.hip); widths a multiple of 4, at most kVitMaxWidth.
+constexpr int kVitMaxWidth = 2048;
+// x = ((t + bias) + pos[px]) + pos[npos + py] (fp32 [T][d]), h = LayerNorm(x) * w + b (fp16).
+hipError_t launch_vit_embed(hipStream_t s, const float* t, const float* bias, const float* pos, int npos,
+                            const int32_t* px, const int32_t* py, int T, int d, const float* w, const float* b, float eps,
+                            float* x, uint16_t* h);
+// x = x + (t + bias); if w: h = LayerNorm(x) * w + b (fp16).
+hipError_t launch_vit_residual_ln(hipStream_t s, float* x, const float* t, const float* bias, const float* w,
+                                  const float* b, float eps, int T, int d, uint16_t* h);
+// Token i: the mean of LayerNorm(x) * pw + pb over rows row0[i] + dy gx[i] + dx (dy, dx < merge)
+// into pooled (fp32 [n][d]), and RMSNorm(mean) * nw into out (fp16 [n][d]).
+hipError_t launch_vit_pool(hipStream_t s, const float* x, const int32_t* row0, const int32_t* gx, int n_tokens, int merge,
+                           int d, const float* pw, const float* pb, float eps, const float* nw, float* pooled,
+                           uint16_t* out);
 
 // Per-device kernel attributes (dynamic LDS limits); call once per device before launching.
 hipError_t configure_kernels();

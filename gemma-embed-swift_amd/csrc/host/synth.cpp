@@ -9,6 +9,7 @@
 //  - fp32 norm weights and layer_output_scale: 1 + 0.1 N(0, 1);
 //  - bf16 per_layer_model_proj: bf16(0.02 N(0, 1));
 //  - every tensor draws from its own SplitMix64 stream seeded by (seed, tensor name).
+#include <cmath>
 #include <cstdio>
 #include <cstring>
 #include <memory>
@@ -68,6 +69,9 @@ struct TensorSpec {
     std::vector<int64_t> shape;
     int type;
     uint64_t offset = 0;
+    // value rule: Q8_0 block scales from |N(0, scale)|; F32 offset + scale N(0, 1); F16 and BF16
+    // scale N(0, 1)
+    double scale = -1, offset_f = 1;
     size_t bytes() const {
         int64_t n = 1;
         for (auto d : shape) n *= d;
@@ -116,20 +120,27 @@ void write_tensor_data(Writer& w, const TensorSpec& t, uint64_t seed) {
                 block[2 + j] = uint8_t(int8_t(q));
                 maxq = std::max(maxq, q < 0 ? -q : q);
             }
-            const double z = 0.02 * rng.gaussian();
+            const double z = (t.scale > 0 ? t.scale : 0.02) * rng.gaussian();
             const uint16_t d = float_to_half(float(std::fabs(z) * double(maxq) / 127.0));
             block[0] = uint8_t(d & 0xff);
             block[1] = uint8_t(d >> 8);
             w.bytes(block, 34);
         }
     } else if (t.type == GE_TYPE_F32) {
-        for (int64_t i = 0; i < n; i++) w.put<float>(float(1.0 + 0.1 * rng.gaussian()));
+        const double sc = t.scale >= 0 ? t.scale : 0.1;
+        for (int64_t i = 0; i < n; i++) w.put<float>(float(t.offset_f + sc * rng.gaussian()));
     } else if (t.type == GE_TYPE_BF16) {
-        for (int64_t i = 0; i < n; i++) w.put<uint16_t>(float_to_bf16(float(0.02 * rng.gaussian())));
+        const double sc = t.scale > 0 ? t.scale : 0.02;
+        for (int64_t i = 0; i < n; i++) w.put<uint16_t>(float_to_bf16(float(sc * rng.gaussian())));
+    } else if (t.type == GE_TYPE_F16) {
+        const double sc = t.scale > 0 ? t.scale : 0.02;
+        for (int64_t i = 0; i < n; i++) w.put<uint16_t>(float_to_half(float(sc * rng.gaussian())));
     } else {
         throw Error(GE_ERR_INVALID, "internal: tensor type");
     }
 }
+
+void write_file(const std::string& path, const std::vector<KV>& kvs, std::vector<TensorSpec>& ts, uint64_t seed);
 
 void synth_write(const std::string& path, const ge_synth_spec& s) {
     if (s.layers <= 0 || s.hidden <= 0 || s.heads <= 0 || s.feed_forward <= 0 || s.out_dims <= 0 || s.vocab <= 2 ||
@@ -223,6 +234,11 @@ void synth_write(const std::string& path, const ge_synth_spec& s) {
             add(b + "proj.weight", {pl, d}, GE_TYPE_Q8_0);
         }
     }
+    write_file(path, kvs, ts, s.seed);
+}
+
+// GGUF v3: header, metadata, tensor directory, then the data section with 32-byte alignment.
+void write_file(const std::string& path, const std::vector<KV>& kvs, std::vector<TensorSpec>& ts, uint64_t seed) {
     uint64_t off = 0;
     for (auto& t : ts) {
         t.offset = off;
@@ -248,12 +264,87 @@ void synth_write(const std::string& path, const ge_synth_spec& s) {
     const uint64_t data0 = w.written;
     for (const auto& t : ts) {
         while (w.written - data0 < t.offset) w.put<uint8_t>(0);
-        write_tensor_data(w, t, s.seed);
+        write_tensor_data(w, t, seed);
     }
     w.pad(32);
     w.flush();
 }
 
+
+// An image-encoder GGUF ("clip" architecture, projector "gemma3") for BASELINE config 5's tower,
+// in the tensor layout ge_upload_vision reads. Values: Q8_0 matrices as the text model's but with
+// z ~ N(0, 1 / (64 sqrt(K))) (K: the row width), so each projection keeps its input's scale;
+// ffn_down F16 N(0, 1) / sqrt(K); LayerNorm and RMSNorm weights 1 + 0.1 N(0, 1); biases
+// 0.1 N(0, 1); position rows 0.5 N(0, 1).
+void synth_vision_write(const std::string& path, const ge_synth_vision_spec& s) {
+    if (s.layers <= 0 || s.hidden <= 0 || s.heads <= 0 || s.feed_forward <= 0 || s.patch_size <= 0 || s.merge <= 0 ||
+        s.proj_dims <= 0 || s.positions <= 0)
+        throw Error(GE_ERR_INVALID, "synthetic image encoder spec has a non-positive size");
+    const int64_t d = s.hidden, ff = s.feed_forward, area = 3 * int64_t(s.patch_size) * s.patch_size;
+    if (d % 32 || area % 32) throw Error(GE_ERR_INVALID, "Q8_0 rows need widths that are multiples of 32");
+    const int down_type = s.ffn_down_type ? s.ffn_down_type : GE_TYPE_F16;
+    if (down_type == GE_TYPE_Q8_0 && ff % 32) throw Error(GE_ERR_INVALID, "a Q8_0 ffn_down needs feed_forward % 32 == 0");
+    if (down_type != GE_TYPE_Q8_0 && down_type != GE_TYPE_F16) throw Error(GE_ERR_INVALID, "ffn_down type must be F16 or Q8_0");
+    const std::string a = "clip.vision.";
+    std::vector<KV> kvs;
+    auto u32 = [&](const std::string& k, uint64_t v) { KV x; x.key = k; x.type = 4; x.u = v; kvs.push_back(x); };
+    auto f32 = [&](const std::string& k, float v) { KV x; x.key = k; x.type = 6; x.f = v; kvs.push_back(x); };
+    auto str = [&](const std::string& k, const std::string& v) { KV x; x.key = k; x.type = 8; x.s = v; kvs.push_back(x); };
+    str("general.architecture", "clip");
+    str("general.name", "synthetic-vit");
+    u32("general.alignment", 32);
+    str(a + "projector_type", "gemma3");
+    u32(a + "block_count", uint64_t(s.layers));
+    u32(a + "embedding_length", uint64_t(d));
+    u32(a + "attention.head_count", uint64_t(s.heads));
+    u32(a + "feed_forward_length", uint64_t(ff));
+    u32(a + "patch_size", uint64_t(s.patch_size));
+    u32(a + "projection_dim", uint64_t(s.proj_dims));
+    u32(a + "projector.scale_factor", uint64_t(s.merge));
+    f32(a + "attention.layer_norm_epsilon", s.eps);
+
+    std::vector<TensorSpec> ts;
+    auto q8 = [&](const std::string& n, int64_t cols, int64_t rows) {
+        TensorSpec t{n, {cols, rows}, GE_TYPE_Q8_0, 0};
+        t.scale = 1.0 / (64.0 * std::sqrt(double(cols)));
+        ts.push_back(t);
+    };
+    auto vec = [&](const std::string& n, std::vector<int64_t> shape, double offset, double scale) {
+        TensorSpec t{n, shape, GE_TYPE_F32, 0};
+        t.offset_f = offset;
+        t.scale = scale;
+        ts.push_back(t);
+    };
+    q8("v.patch_embd.weight", area, d);
+    vec("v.patch_embd.bias", {d}, 0, 0.1);
+    vec("v.position_embd.weight", {d, s.positions, 2}, 0, 0.5);
+    for (int i = 0; i < s.layers; i++) {
+        const std::string b = "v.blk." + std::to_string(i) + ".";
+        vec(b + "ln1.weight", {d}, 1, 0.1);
+        vec(b + "ln1.bias", {d}, 0, 0.1);
+        for (const char* p : {"attn_q", "attn_k", "attn_v", "attn_out"}) {
+            q8(b + p + ".weight", d, d);
+            vec(b + p + ".bias", {d}, 0, 0.1);
+        }
+        vec(b + "ln2.weight", {d}, 1, 0.1);
+        vec(b + "ln2.bias", {d}, 0, 0.1);
+        q8(b + "ffn_up.weight", d, ff);
+        vec(b + "ffn_up.bias", {ff}, 0, 0.1);
+        if (down_type == GE_TYPE_Q8_0) {
+            q8(b + "ffn_down.weight", ff, d);
+        } else {
+            TensorSpec t{b + "ffn_down.weight", {ff, d}, GE_TYPE_F16, 0};
+            t.scale = 1.0 / std::sqrt(double(ff));
+            ts.push_back(t);
+        }
+        vec(b + "ffn_down.bias", {d}, 0, 0.1);
+    }
+    vec("v.post_ln.weight", {d}, 1, 0.1);
+    vec("v.post_ln.bias", {d}, 0, 0.1);
+    vec("mm.soft_emb_norm.weight", {d}, 1, 0.1);
+    q8("mm.input_projection.weight", d, s.proj_dims);
+    write_file(path, kvs, ts, s.seed);
+}
 }  // namespace
 }  // namespace ge
 
@@ -275,5 +366,26 @@ extern "C" int ge_synth_tokens(uint64_t seed, int32_t lo, int32_t hi, int32_t co
     if (!out || count < 0 || hi <= lo) return GE_ERR_INVALID;
     ge::SeededRandom rng(seed);
     for (int32_t i = 0; i < count; i++) out[i] = int32_t(rng.uniform_int(lo, hi));
+    return GE_OK;
+}
+
+extern "C" int ge_synth_write_vision_gguf(const char* path, const ge_synth_vision_spec* spec, char* err, size_t errlen) {
+    try {
+        if (!path || !spec) throw ge::Error(GE_ERR_INVALID, "null argument");
+        ge::synth_vision_write(path, *spec);
+        return GE_OK;
+    } catch (const ge::Error& e) {
+        if (err && errlen) std::snprintf(err, errlen, "%s", e.what());
+        return e.code;
+    } catch (const std::exception& e) {
+        if (err && errlen) std::snprintf(err, errlen, "%s", e.what());
+        return GE_ERR_INVALID;
+    }
+}
+
+extern "C" int ge_synth_uniform(uint64_t seed, float lo, float hi, int64_t count, float* out) {
+    if (!out || count < 0 || !(hi > lo)) return GE_ERR_INVALID;
+    ge::SeededRandom rng(seed);
+    for (int64_t i = 0; i < count; i++) out[i] = float(lo + (hi - lo) * rng.unit());
     return GE_OK;
 }

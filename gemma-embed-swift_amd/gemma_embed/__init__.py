@@ -11,7 +11,7 @@ from __future__ import annotations
 import ctypes as C
 import os
 from dataclasses import dataclass
-from typing import Callable, Iterable, List, Optional, Sequence
+from typing import Callable, Iterable, List, Optional, Sequence, Tuple
 
 import numpy as np
 
@@ -29,6 +29,8 @@ ERRORS = {
     7: "cancelled",
     8: "noDevice",
 }
+(GE_ERR_INVALID, GE_ERR_GGUF, GE_ERR_MODEL, GE_ERR_GPU, GE_ERR_OPTIONS, GE_ERR_STATE, GE_ERR_CANCELLED,
+ GE_ERR_NO_DEVICE) = range(1, 9)
 GE_TYPE_F32, GE_TYPE_F16, GE_TYPE_Q8_0, GE_TYPE_BF16 = 0, 1, 8, 30
 
 
@@ -73,6 +75,17 @@ class ge_synth_spec(C.Structure):
                 ("head_dim_global", C.c_int32), ("kv_heads_swa", C.c_int32), ("kv_heads_global", C.c_int32),
                 ("eps", C.c_float), ("rope_base", C.c_float), ("rope_base_swa", C.c_float),
                 ("pattern", C.POINTER(C.c_uint8)), ("seed", C.c_uint64)]
+
+
+class ge_synth_vision_spec(C.Structure):
+    _fields_ = [("layers", C.c_int32), ("hidden", C.c_int32), ("heads", C.c_int32),
+                ("feed_forward", C.c_int32), ("patch_size", C.c_int32), ("merge", C.c_int32),
+                ("proj_dims", C.c_int32), ("positions", C.c_int32), ("eps", C.c_float),
+                ("ffn_down_type", C.c_int32), ("seed", C.c_uint64)]
+
+
+class ge_image_grid(C.Structure):
+    _fields_ = [("grid_x", C.c_int32), ("grid_y", C.c_int32)]
 
 
 PROGRESS_FN = C.CFUNCTYPE(C.c_int, C.c_void_p, C.c_int32, C.c_int32, C.c_int64)
@@ -125,6 +138,17 @@ SIGNATURES = {
     "ge_finish": (_I, [_PF, C.c_int32, C.c_int32, C.c_int32, _PF]),
     "ge_synth_write_gguf": (_I, [C.c_char_p, C.POINTER(ge_synth_spec), C.c_char_p, C.c_size_t]),
     "ge_synth_tokens": (_I, [C.c_uint64, C.c_int32, C.c_int32, C.c_int32, _PI32]),
+    "ge_synth_uniform": (_I, [C.c_uint64, C.c_float, C.c_float, C.c_int64, _PF]),
+    "ge_synth_write_vision_gguf": (_I, [C.c_char_p, C.POINTER(ge_synth_vision_spec), C.c_char_p, C.c_size_t]),
+    "ge_upload_vision": (_I, [_P, _P, _P, C.c_size_t]),
+    "ge_vision_load": (_I, [_P, C.c_char_p, C.c_char_p, C.c_size_t]),
+    "ge_vision_encode": (_I, [_P, _PF, C.c_int32, C.POINTER(ge_image_grid), C.c_int32, _PF, C.POINTER(C.c_double)]),
+    "ge_vision_stage": (_I, [_P, _PF, C.c_int32, C.POINTER(ge_image_grid), C.c_int32]),
+    "ge_vision_run": (_I, [_P]),
+    "ge_vision_read": (_I, [_P, _PF]),
+    "ge_vision_tokens": (C.c_int32, [_P]),
+    "ge_vision_trace": (_I, [_P, _PF, C.c_int32, C.POINTER(ge_image_grid), C.c_int32, C.c_char_p, C.c_int32, _PF,
+                             C.c_size_t, C.POINTER(C.c_size_t)]),
 }
 
 
@@ -220,6 +244,48 @@ def synth_write_gguf(path: str, **spec) -> str:
     return path
 
 
+# BASELINE config 5's image tower, and a two-layer version of it with small grids for tests.
+CONFIG5_VISION = dict(layers=16, hidden=1152, heads=16, feed_forward=4304, patch_size=16, merge=3, proj_dims=768,
+                      positions=48, eps=1e-6, ffn_down_type=0, seed=5)
+TINY_VISION = dict(CONFIG5_VISION, layers=2, positions=12, seed=11)
+
+
+def synth_write_vision_gguf(path: str, **spec) -> str:
+    """Writes a seeded synthetic image-encoder GGUF (see ge_synth_write_vision_gguf)."""
+    s = ge_synth_vision_spec()
+    for k in ("layers", "hidden", "heads", "feed_forward", "patch_size", "merge", "proj_dims", "positions",
+              "ffn_down_type"):
+        setattr(s, k, int(spec.get(k, 0)))
+    s.eps = float(spec["eps"])
+    s.seed = int(spec["seed"])
+    err = C.create_string_buffer(512)
+    rc = lib.ge_synth_write_vision_gguf(path.encode(), C.byref(s), err, 512)
+    if rc != GE_OK:
+        raise GemmaEmbedError(rc, err.value.decode())
+    return path
+
+
+def synth_uniform(seed: int, lo: float, hi: float, count: int) -> np.ndarray:
+    out = np.zeros(count, dtype=np.float32)
+    rc = lib.ge_synth_uniform(seed, lo, hi, count, _ptr(out, C.c_float))
+    if rc != GE_OK:
+        raise GemmaEmbedError(rc, "ge_synth_uniform")
+    return out
+
+
+def image_patches(seed: int, grids: Sequence[Tuple[int, int]], area: int) -> np.ndarray:
+    """Synthetic pixels uniform in [-1, 1) as patch rows [sum(gx * gy), area]."""
+    n = sum(gx * gy for gx, gy in grids)
+    return synth_uniform(seed, -1.0, 1.0, n * area).reshape(n, area)
+
+
+def _grid_array(grids) -> C.Array:
+    arr = (ge_image_grid * max(len(grids), 1))()
+    for i, (gx, gy) in enumerate(grids):
+        arr[i].grid_x, arr[i].grid_y = int(gx), int(gy)
+    return arr
+
+
 # ---------------------------------------------------------------------------- device context
 
 def pack(sequences: Sequence[Sequence[int]]):
@@ -290,6 +356,48 @@ class Context:
                                          len(seqs), name.encode(), layer, _ptr(out, C.c_float), out.size,
                                          C.byref(need)), "ge_forward_trace")
         return out.reshape(len(toks), -1)
+
+    # ---- image tower
+    def vision_load(self, path: str):
+        err = C.create_string_buffer(512)
+        rc = lib.ge_vision_load(self.handle, path.encode(), err, 512)
+        if rc != GE_OK:
+            raise GemmaEmbedError(rc, err.value.decode())
+
+    def vision_encode(self, patches: np.ndarray, grids: Sequence[Tuple[int, int]], proj_dims: int, merge: int = 3):
+        """Patches [P, area] of images with the given grids -> (vectors [tokens, proj_dims], gpu_seconds)."""
+        p = np.ascontiguousarray(patches, dtype=np.float32)
+        tokens = sum((gx // merge) * (gy // merge) for gx, gy in grids)
+        out = np.zeros((tokens, proj_dims), dtype=np.float32)
+        secs = C.c_double(0)
+        self._check(lib.ge_vision_encode(self.handle, _ptr(p, C.c_float), p.shape[0], _grid_array(grids), len(grids),
+                                         _ptr(out, C.c_float), C.byref(secs)), "ge_vision_encode")
+        return out, secs.value
+
+    def vision_trace(self, patches: np.ndarray, grids: Sequence[Tuple[int, int]], name: str, layer: int = -1):
+        p = np.ascontiguousarray(patches, dtype=np.float32)
+        ga = _grid_array(grids)
+        need = C.c_size_t(0)
+        self._check(lib.ge_vision_trace(self.handle, _ptr(p, C.c_float), p.shape[0], ga, len(grids), name.encode(),
+                                        layer, None, 0, C.byref(need)), "ge_vision_trace")
+        out = np.zeros(need.value, dtype=np.float32)
+        self._check(lib.ge_vision_trace(self.handle, _ptr(p, C.c_float), p.shape[0], ga, len(grids), name.encode(),
+                                        layer, _ptr(out, C.c_float), out.size, C.byref(need)), "ge_vision_trace")
+        return out
+
+    def vision_stage(self, patches: np.ndarray, grids: Sequence[Tuple[int, int]]):
+        p = np.ascontiguousarray(patches, dtype=np.float32)
+        self._check(lib.ge_vision_stage(self.handle, _ptr(p, C.c_float), p.shape[0], _grid_array(grids), len(grids)),
+                    "ge_vision_stage")
+
+    def vision_run(self):
+        self._check(lib.ge_vision_run(self.handle), "ge_vision_run")
+
+    def vision_read(self, proj_dims: int) -> np.ndarray:
+        n = lib.ge_vision_tokens(self.handle)
+        out = np.zeros((max(n, 0), proj_dims), dtype=np.float32)
+        self._check(lib.ge_vision_read(self.handle, _ptr(out, C.c_float)), "ge_vision_read")
+        return out
 
     def batch_stage(self, sequences: Sequence[Sequence[int]]):
         toks, pos, seqs = pack(sequences)

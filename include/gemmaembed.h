@@ -173,6 +173,51 @@ int ge_op_attention(ge_ctx* ctx, const void* q, const void* k, const void* v, vo
                     int32_t n_work, int32_t heads, int32_t kv_heads, int32_t head_dim, int32_t half_window,
                     float scale);
 
+/* ---- image tower, on the same context as the text encoder.
+ * Replaces Metal/VisionTower.swift (VisionTower.upload :109-138, encode :140-185) for a
+ * pre-LayerNorm ViT: per layer x += attn_out(attn(LN1(x))) + b, x += down(gelu_tanh(up(LN2(x)))),
+ * heads of hidden / heads dims (72, 128 or 256), then a final LayerNorm, merge x merge mean pooling,
+ * a weighted RMSNorm and a Q8_0 projection. Tensors (GGUF names, ne order):
+ *   v.patch_embd.weight Q8_0 [3 p^2, hidden] (patch element c p^2 + ky p + kx), v.patch_embd.bias,
+ *   v.position_embd.weight F32 [hidden, positions, 2] (column rows, then row rows),
+ *   v.blk.N.{ln1,ln2}.{weight,bias}, v.blk.N.attn_{q,k,v,out}.{weight Q8_0, bias},
+ *   v.blk.N.ffn_up.{weight Q8_0 [hidden, ff], bias}, v.blk.N.ffn_down.{weight F16/F32/BF16/Q8_0 [ff, hidden], bias},
+ *   v.post_ln.{weight,bias}, mm.soft_emb_norm.weight, mm.input_projection.weight Q8_0 [hidden, proj_dims];
+ * vectors F32. */
+typedef struct ge_vision_desc {
+    int32_t layers, hidden, heads, feed_forward, patch_size, merge, proj_dims, positions;
+    float eps;
+    const ge_tensor_desc* tensors;
+    int32_t n_tensors;
+} ge_vision_desc;
+int ge_upload_vision(ge_ctx* ctx, const ge_vision_desc* desc, const void* file_base, size_t len);
+
+/* One image of a batch: its patch grid (PreparedImage.gridX / gridY, Image/ImagePreprocessor.swift:6-61),
+ * both multiples of the merge size. Images follow each other as patch rows (row-major over the
+ * grid) and as pooled tokens ((grid_x / merge) * (grid_y / merge) each, row-major). */
+typedef struct ge_image_grid {
+    int32_t grid_x, grid_y;
+} ge_image_grid;
+
+/* VisionTower.upload + encode + read back: patches fp32 [n_patches][3 p^2] -> vectors fp32
+ * [tokens][proj_dims] (caller-owned; tokens = sum of the images' pooled tokens). Synchronous. */
+int ge_vision_encode(ge_ctx* ctx, const float* patches, int32_t n_patches, const ge_image_grid* grids, int32_t n_images,
+                     float* vectors, double* gpu_seconds);
+/* Device-resident image batches (as ge_batch_*): stage uploads the patches and descriptors, run
+ * enqueues the tower without waiting, read waits and copies the vectors out. */
+int ge_vision_stage(ge_ctx* ctx, const float* patches, int32_t n_patches, const ge_image_grid* grids, int32_t n_images);
+int ge_vision_run(ge_ctx* ctx);
+int ge_vision_read(ge_ctx* ctx, float* vectors);
+/* Pooled tokens of the staged image batch, or -1 when none is staged. */
+int32_t ge_vision_tokens(ge_ctx* ctx);
+/* Per-layer parity (CPUVisionReference.forward's trace, Model/CPUVisionReference.swift:89-165):
+ * stages the batch, runs up to the named tensor and copies it out as fp32. Names (layer -1): inp
+ * (patch projection, no bias), pos_embd, pooled, pooled_normed, projected; per layer:
+ * layer_inp_normed, Qcur, Kcur, Vcur (with bias, [patches][heads][hd]), kqv_out, attn_out (no
+ * bias), ffn_inp, ffn_inp_normed, ffn_gelu, ffn_out (no bias), layer_out. */
+int ge_vision_trace(ge_ctx* ctx, const float* patches, int32_t n_patches, const ge_image_grid* grids, int32_t n_images,
+                    const char* tensor_name, int32_t layer, float* out, size_t out_count, size_t* needed);
+
 /* ===================================================================== host mirror */
 
 typedef struct ge_model ge_model;
@@ -255,9 +300,28 @@ typedef struct ge_synth_spec {
 } ge_synth_spec;
 int ge_synth_write_gguf(const char* path, const ge_synth_spec* spec, char* err, size_t errlen);
 
+/* Synthetic image-encoder GGUF ("clip" architecture, projector "gemma3") in the layout
+ * ge_upload_vision reads (no reference counterpart). Q8_0 matrices as above but with
+ * z ~ N(0, 1 / (64 sqrt(K))) for rows of K elements; ffn_down F16 N(0, 1) / sqrt(ff) (or Q8_0 when
+ * ffn_down_type is GE_TYPE_Q8_0 and ff % 32 == 0); norm weights 1 + 0.1 N(0, 1); biases
+ * 0.1 N(0, 1); position rows 0.5 N(0, 1). */
+typedef struct ge_synth_vision_spec {
+    int32_t layers, hidden, heads, feed_forward, patch_size, merge, proj_dims, positions;
+    float eps;
+    int32_t ffn_down_type; /* 0 = F16 */
+    uint64_t seed;
+} ge_synth_vision_spec;
+int ge_synth_write_vision_gguf(const char* path, const ge_synth_vision_spec* spec, char* err, size_t errlen);
+
+/* Loads an image-encoder GGUF (VisionConfig.init, Model/VisionConfig.swift:40-90, and the
+ * weight directory, Model/VisionWeights.swift) onto the context through ge_upload_vision. */
+int ge_vision_load(ge_ctx* ctx, const char* path, char* err, size_t errlen);
+
 /* SplitMix64 helpers shared by tests and the bench (the reference tests' SeededRandom,
  * Tests/GemmaEmbedTests/KernelTests.swift:9-26): `count` ids uniform in [lo, hi). */
 int ge_synth_tokens(uint64_t seed, int32_t lo, int32_t hi, int32_t count, int32_t* out);
+/* `count` floats uniform in [lo, hi) from SplitMix64 (53-bit uniforms), e.g. pixel values. */
+int ge_synth_uniform(uint64_t seed, float lo, float hi, int64_t count, float* out);
 
 #ifdef __cplusplus
 }

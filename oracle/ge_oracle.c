@@ -875,3 +875,256 @@ done:
     free(o); free(on); free(gate); free(up); free(per_layer); free(g);
     return rc;
 }
+
+/* ================================================================ image tower (config 5)
+ *
+ * BASELINE config 5's encoder, restated the way CPUVisionReference.forward
+ * (Model/CPUVisionReference.swift:89-165) runs the reference's gemma4v tower: the same stage
+ * order (patch projection, position rows, per-layer attention and MLP blocks with residual adds,
+ * pooling over merge x merge windows, a norm and the projection), the same position-table layout
+ * (column rows, then row rows, :99-107) and trace names. Config 5's architecture differs from
+ * gemma4v where BASELINE says so: LayerNorm with bias (pre-LN), biased projections, a non-gated
+ * gelu_tanh MLP of width feed_forward, scaled dot-product attention (1 / sqrt(hd), no q/k norms,
+ * no RoPE), a final LayerNorm before pooling, and the projector's weighted RMSNorm. */
+
+#define ORA_VIT_MAX_LAYERS 64
+
+typedef struct {
+    const float *ln1_w, *ln1_b, *ln2_w, *ln2_b, *bq, *bk, *bv, *bo, *bup, *bdown;
+    float *wq, *wk, *wv, *wo, *wup, *wdown; /* dequantised [rows][cols] */
+} ora_vit_layer;
+
+struct ora_vision {
+    ora_model* file; /* the mapping and its parsed directory */
+    int layers, hidden, heads, ff, patch, merge, proj, npos;
+    float eps;
+    float *patch_w, *proj_w;
+    const float *patch_b, *pos, *post_w, *post_b, *norm_w;
+    ora_vit_layer layer[ORA_VIT_MAX_LAYERS];
+};
+
+/* LayerNorm per row: mean, then the mean of squared deviations, out = (x - mean) * rstd * w + b
+ * with rstd = 1 / sqrt(var + eps), sums in element order. */
+void ora_layernorm(const float* x, int rows, int width, const float* w, const float* b, float eps, float* out) {
+    for (int r = 0; r < rows; r++) {
+        const float* xr = x + (size_t)r * width;
+        float* o = out + (size_t)r * width;
+        float s = 0;
+        for (int i = 0; i < width; i++) s += xr[i];
+        const float mean = s / (float)width;
+        float ss = 0;
+        for (int i = 0; i < width; i++) {
+            const float t = xr[i] - mean;
+            ss += t * t;
+        }
+        const float rstd = 1.0f / sqrtf(ss / (float)width + eps);
+        for (int i = 0; i < width; i++) o[i] = (xr[i] - mean) * rstd * w[i] + b[i];
+    }
+}
+
+/* Mean of each merge x merge window of a grid_x x grid_y grid of rows (CPUVisionReference.pool):
+ * token oy * (grid_x / merge) + ox sums rows (merge oy + dy) * grid_x + merge ox + dx in (dy, dx)
+ * order, then scales by 1 / merge^2. */
+void ora_pool(const float* x, int grid_x, int grid_y, int merge, int width, float* out) {
+    const int tx = grid_x / merge, ty = grid_y / merge;
+    const float inv = 1.0f / (float)(merge * merge);
+    for (int oy = 0; oy < ty; oy++)
+        for (int ox = 0; ox < tx; ox++) {
+            float* o = out + ((size_t)oy * tx + ox) * width;
+            for (int i = 0; i < width; i++) o[i] = 0;
+            for (int dy = 0; dy < merge; dy++)
+                for (int dx = 0; dx < merge; dx++) {
+                    const float* xr = x + ((size_t)(merge * oy + dy) * grid_x + merge * ox + dx) * width;
+                    for (int i = 0; i < width; i++) o[i] += xr[i];
+                }
+            for (int i = 0; i < width; i++) o[i] *= inv;
+        }
+}
+
+static int vmeta_int(const ora_model* m, const char* key, int* out, char* err, int errlen) {
+    const ora_kv* kv = find_kv(m, key);
+    if (!kv || !kv_is_int(kv)) { set_err(err, errlen, "image encoder file lacks metadata key %s", key); return -1; }
+    *out = (int)kv->ival;
+    return 0;
+}
+
+ora_vision* ora_vision_open(const char* path, char* err, int errlen) {
+    int fd = open(path, O_RDONLY);
+    if (fd < 0) { set_err(err, errlen, "cannot read %s", path); return NULL; }
+    struct stat st;
+    if (fstat(fd, &st) != 0 || st.st_size < 24) { close(fd); set_err(err, errlen, "invalid GGUF file: too short"); return NULL; }
+    void* p = mmap(NULL, (size_t)st.st_size, PROT_READ, MAP_SHARED, fd, 0);
+    close(fd);
+    if (p == MAP_FAILED) { set_err(err, errlen, "cannot map %s", path); return NULL; }
+    ora_vision* v = (ora_vision*)calloc(1, sizeof(ora_vision));
+    v->file = (ora_model*)calloc(1, sizeof(ora_model));
+    v->file->map = (uint8_t*)p;
+    v->file->size = (size_t)st.st_size;
+    ora_model* m = v->file;
+    if (parse(m, err, errlen) != 0) { ora_vision_close(v); return NULL; }
+    const ora_kv* arch = find_kv(m, "general.architecture");
+    if (!arch || arch->vtype != 8 || strcmp(arch->sval, "clip") != 0) {
+        set_err(err, errlen, "image encoder architecture is not clip"); ora_vision_close(v); return NULL;
+    }
+    const ora_kv* pt = find_kv(m, "clip.vision.projector_type");
+    if (!pt || pt->vtype != 8 || strcmp(pt->sval, "gemma3") != 0) {
+        set_err(err, errlen, "image projector is not gemma3"); ora_vision_close(v); return NULL;
+    }
+    const ora_kv* eps = find_kv(m, "clip.vision.attention.layer_norm_epsilon");
+    if (vmeta_int(m, "clip.vision.block_count", &v->layers, err, errlen) ||
+        vmeta_int(m, "clip.vision.embedding_length", &v->hidden, err, errlen) ||
+        vmeta_int(m, "clip.vision.attention.head_count", &v->heads, err, errlen) ||
+        vmeta_int(m, "clip.vision.feed_forward_length", &v->ff, err, errlen) ||
+        vmeta_int(m, "clip.vision.patch_size", &v->patch, err, errlen) ||
+        vmeta_int(m, "clip.vision.projection_dim", &v->proj, err, errlen) ||
+        vmeta_int(m, "clip.vision.projector.scale_factor", &v->merge, err, errlen) || !eps) {
+        if (!eps) set_err(err, errlen, "image encoder file lacks metadata key clip.vision.attention.layer_norm_epsilon");
+        ora_vision_close(v);
+        return NULL;
+    }
+    v->eps = (eps->vtype == 6 || eps->vtype == 12) ? (float)eps->fval : (float)eps->ival;
+    if (v->layers > ORA_VIT_MAX_LAYERS || v->hidden % v->heads) { set_err(err, errlen, "bad image encoder shape"); ora_vision_close(v); return NULL; }
+    const int d = v->hidden, area = 3 * v->patch * v->patch;
+    const ora_tensor* pos = find_tensor(m, "v.position_embd.weight");
+    if (!pos || pos->ndim != 3 || pos->shape[0] != d || pos->shape[2] != 2 || pos->type != ORA_F32) {
+        set_err(err, errlen, "image encoder file lacks a [hidden, positions, 2] F32 v.position_embd.weight");
+        ora_vision_close(v);
+        return NULL;
+    }
+    v->npos = (int)pos->shape[1];
+    v->pos = (const float*)tensor_data(m, pos);
+    int failed = 0;
+    char nm[96];
+#define VT_(name, c, r, f32) (tensor_checked(m, name, c, r, f32, 0, err, errlen, &failed))
+    const ora_tensor *pw = VT_("v.patch_embd.weight", area, d, 0), *pb = VT_("v.patch_embd.bias", d, 1, 1),
+                     *qw = VT_("mm.input_projection.weight", d, v->proj, 0), *nw = VT_("mm.soft_emb_norm.weight", d, 1, 1),
+                     *plw = VT_("v.post_ln.weight", d, 1, 1), *plb = VT_("v.post_ln.bias", d, 1, 1);
+    if (failed) { ora_vision_close(v); return NULL; }
+    v->patch_w = dequant(m, pw);
+    v->proj_w = dequant(m, qw);
+    v->patch_b = (const float*)tensor_data(m, pb);
+    v->norm_w = (const float*)tensor_data(m, nw);
+    v->post_w = (const float*)tensor_data(m, plw);
+    v->post_b = (const float*)tensor_data(m, plb);
+    for (int l = 0; l < v->layers && !failed; l++) {
+        ora_vit_layer* L = &v->layer[l];
+#define VL_(suffix, c, r, f32) (snprintf(nm, sizeof(nm), "v.blk.%d." suffix, l), VT_(nm, c, r, f32))
+        const ora_tensor *l1w = VL_("ln1.weight", d, 1, 1), *l1b = VL_("ln1.bias", d, 1, 1), *l2w = VL_("ln2.weight", d, 1, 1),
+                         *l2b = VL_("ln2.bias", d, 1, 1), *wq = VL_("attn_q.weight", d, d, 0), *wk = VL_("attn_k.weight", d, d, 0),
+                         *wv = VL_("attn_v.weight", d, d, 0), *wo = VL_("attn_out.weight", d, d, 0),
+                         *bq = VL_("attn_q.bias", d, 1, 1), *bk = VL_("attn_k.bias", d, 1, 1), *bv = VL_("attn_v.bias", d, 1, 1),
+                         *bo = VL_("attn_out.bias", d, 1, 1), *wu = VL_("ffn_up.weight", d, v->ff, 0),
+                         *bu = VL_("ffn_up.bias", v->ff, 1, 1), *wd = VL_("ffn_down.weight", v->ff, d, 0),
+                         *bd = VL_("ffn_down.bias", d, 1, 1);
+#undef VL_
+        if (failed) break;
+        L->ln1_w = (const float*)tensor_data(m, l1w); L->ln1_b = (const float*)tensor_data(m, l1b);
+        L->ln2_w = (const float*)tensor_data(m, l2w); L->ln2_b = (const float*)tensor_data(m, l2b);
+        L->bq = (const float*)tensor_data(m, bq); L->bk = (const float*)tensor_data(m, bk);
+        L->bv = (const float*)tensor_data(m, bv); L->bo = (const float*)tensor_data(m, bo);
+        L->bup = (const float*)tensor_data(m, bu); L->bdown = (const float*)tensor_data(m, bd);
+        L->wq = dequant(m, wq); L->wk = dequant(m, wk); L->wv = dequant(m, wv); L->wo = dequant(m, wo);
+        L->wup = dequant(m, wu); L->wdown = dequant(m, wd);
+    }
+#undef VT_
+    if (failed) { ora_vision_close(v); return NULL; }
+    return v;
+}
+
+void ora_vision_close(ora_vision* v) {
+    if (!v) return;
+    for (int l = 0; l < ORA_VIT_MAX_LAYERS; l++) {
+        ora_vit_layer* L = &v->layer[l];
+        free(L->wq); free(L->wk); free(L->wv); free(L->wo); free(L->wup); free(L->wdown);
+    }
+    free(v->patch_w);
+    free(v->proj_w);
+    ora_close(v->file);
+    free(v);
+}
+
+int ora_vision_hidden(const ora_vision* v) { return v->hidden; }
+int ora_vision_proj_dims(const ora_vision* v) { return v->proj; }
+int ora_vision_merge(const ora_vision* v) { return v->merge; }
+int ora_vision_patch_area(const ora_vision* v) { return 3 * v->patch * v->patch; }
+int ora_vision_layers(const ora_vision* v) { return v->layers; }
+
+/* One image: patches [gx * gy][3 p^2] (patch i at column i % gx, row i / gx) -> vectors
+ * [(gx / merge) * (gy / merge)][proj]. */
+int ora_vision_forward(ora_vision* v, const float* patches, int grid_x, int grid_y, float* vectors, ora_trace_fn trace,
+                       void* user, int threads) {
+    if (grid_x <= 0 || grid_y <= 0 || grid_x % v->merge || grid_y % v->merge || grid_x > v->npos || grid_y > v->npos)
+        return -1;
+    const int P = grid_x * grid_y, d = v->hidden, H = v->heads, hd = d / H, ff = v->ff, area = 3 * v->patch * v->patch;
+    const int T = (grid_x / v->merge) * (grid_y / v->merge);
+    const size_t Pd = (size_t)P * d;
+    float* x = (float*)malloc(Pd * sizeof(float));
+    float* h = (float*)malloc(Pd * sizeof(float));
+    float* q = (float*)malloc(Pd * sizeof(float));
+    float* k = (float*)malloc(Pd * sizeof(float));
+    float* vv = (float*)malloc(Pd * sizeof(float));
+    float* attn = (float*)malloc(Pd * sizeof(float));
+    float* o = (float*)malloc(Pd * sizeof(float));
+    float* u = (float*)malloc((size_t)P * ff * sizeof(float));
+    float* pooled = (float*)malloc((size_t)T * d * sizeof(float));
+    float* pn = (float*)malloc((size_t)T * d * sizeof(float));
+
+    ora_matmul(patches, P, area, v->patch_w, d, x, threads);
+    trace_emit(trace, user, "inp", -1, x, Pd);
+    for (int t = 0; t < P; t++) {
+        const float* rx = v->pos + (size_t)(t % grid_x) * d;
+        const float* ry = v->pos + (size_t)(v->npos + t / grid_x) * d;
+        float* xr = x + (size_t)t * d;
+        for (int i = 0; i < d; i++) xr[i] = ((xr[i] + v->patch_b[i]) + rx[i]) + ry[i];
+    }
+    trace_emit(trace, user, "pos_embd", -1, x, Pd);
+    const float scale = 1.0f / sqrtf((float)hd);
+    for (int l = 0; l < v->layers; l++) {
+        const ora_vit_layer* L = &v->layer[l];
+        ora_layernorm(x, P, d, L->ln1_w, L->ln1_b, v->eps, h);
+        trace_emit(trace, user, "layer_inp_normed", l, h, Pd);
+        ora_matmul(h, P, d, L->wq, d, q, threads);
+        ora_matmul(h, P, d, L->wk, d, k, threads);
+        ora_matmul(h, P, d, L->wv, d, vv, threads);
+        for (int t = 0; t < P; t++)
+            for (int i = 0; i < d; i++) {
+                const size_t idx = (size_t)t * d + i;
+                q[idx] += L->bq[i];
+                k[idx] += L->bk[i];
+                vv[idx] += L->bv[i];
+            }
+        trace_emit(trace, user, "Qcur", l, q, Pd);
+        trace_emit(trace, user, "Kcur", l, k, Pd);
+        trace_emit(trace, user, "Vcur", l, vv, Pd);
+        ora_attention(q, k, vv, P, H, H, hd, scale, 0, attn, threads);
+        trace_emit(trace, user, "kqv_out", l, attn, Pd);
+        ora_matmul(attn, P, d, L->wo, d, o, threads);
+        trace_emit(trace, user, "attn_out", l, o, Pd);
+        for (int t = 0; t < P; t++)
+            for (int i = 0; i < d; i++) x[(size_t)t * d + i] += o[(size_t)t * d + i] + L->bo[i];
+        trace_emit(trace, user, "ffn_inp", l, x, Pd);
+        ora_layernorm(x, P, d, L->ln2_w, L->ln2_b, v->eps, h);
+        trace_emit(trace, user, "ffn_inp_normed", l, h, Pd);
+        ora_matmul(h, P, d, L->wup, ff, u, threads);
+        for (int t = 0; t < P; t++)
+            for (int i = 0; i < ff; i++) {
+                const size_t idx = (size_t)t * ff + i;
+                u[idx] = ora_gelu_tanh(u[idx] + L->bup[i]);
+            }
+        trace_emit(trace, user, "ffn_gelu", l, u, (size_t)P * ff);
+        ora_matmul(u, P, ff, L->wdown, d, o, threads);
+        trace_emit(trace, user, "ffn_out", l, o, Pd);
+        for (int t = 0; t < P; t++)
+            for (int i = 0; i < d; i++) x[(size_t)t * d + i] += o[(size_t)t * d + i] + L->bdown[i];
+        trace_emit(trace, user, "layer_out", l, x, Pd);
+    }
+    ora_layernorm(x, P, d, v->post_w, v->post_b, v->eps, h);
+    ora_pool(h, grid_x, grid_y, v->merge, d, pooled);
+    trace_emit(trace, user, "pooled", -1, pooled, (size_t)T * d);
+    ora_rmsnorm(pooled, T, d, v->norm_w, v->eps, 1.0f, pn);
+    trace_emit(trace, user, "pooled_normed", -1, pn, (size_t)T * d);
+    ora_matmul(pn, T, d, v->proj_w, v->proj, vectors, threads);
+    trace_emit(trace, user, "projected", -1, vectors, (size_t)T * v->proj);
+    free(x); free(h); free(q); free(k); free(vv); free(attn); free(o); free(u); free(pooled); free(pn);
+    return 0;
+}

@@ -56,6 +56,21 @@ void ora_rope(float* x, int tokens, int heads, int head_dim, const float* table,
 void ora_attention(const float* q, const float* k, const float* v, int tokens, int heads, int kv_heads,
                    int head_dim, float scale, int window, float* out, int threads);
 
+/* ---- image tower, Model/CPUVisionReference.swift:89-165 in structure. */
+typedef struct ora_vision ora_vision;
+ora_vision* ora_vision_open(const char* path, char* err, int errlen);
+void ora_vision_close(ora_vision* v);
+int ora_vision_hidden(const ora_vision* v);
+int ora_vision_proj_dims(const ora_vision* v);
+int ora_vision_merge(const ora_vision* v);
+int ora_vision_patch_area(const ora_vision* v);
+int ora_vision_layers(const ora_vision* v);
+/* One image's patches [gx * gy][3 p^2] -> vectors [(gx / merge) (gy / merge)][proj]. */
+int ora_vision_forward(ora_vision* v, const float* patches, int grid_x, int grid_y, float* vectors, ora_trace_fn trace,
+                       void* user, int threads);
+void ora_layernorm(const float* x, int rows, int width, const float* w, const float* b, float eps, float* out);
+void ora_pool(const float* x, int grid_x, int grid_y, int merge, int width, float* out);
+
 #ifdef __cplusplus
 }
 #endif

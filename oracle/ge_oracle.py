@@ -33,6 +33,16 @@ _SIG = {
     "ora_rope_table": (None, [C.c_int, C.c_float, C.c_int, _F]),
     "ora_rope": (None, [_F, C.c_int, C.c_int, C.c_int, _F, C.POINTER(C.c_int32)]),
     "ora_attention": (None, [_F, _F, _F, C.c_int, C.c_int, C.c_int, C.c_int, C.c_float, C.c_int, _F, C.c_int]),
+    "ora_vision_open": (C.c_void_p, [C.c_char_p, C.c_char_p, C.c_int]),
+    "ora_vision_close": (None, [C.c_void_p]),
+    "ora_vision_hidden": (C.c_int, [C.c_void_p]),
+    "ora_vision_proj_dims": (C.c_int, [C.c_void_p]),
+    "ora_vision_merge": (C.c_int, [C.c_void_p]),
+    "ora_vision_patch_area": (C.c_int, [C.c_void_p]),
+    "ora_vision_layers": (C.c_int, [C.c_void_p]),
+    "ora_vision_forward": (C.c_int, [C.c_void_p, _F, C.c_int, C.c_int, _F, TRACE_FN, C.c_void_p, C.c_int]),
+    "ora_layernorm": (None, [_F, C.c_int, C.c_int, _F, _F, C.c_float, _F]),
+    "ora_pool": (None, [_F, C.c_int, C.c_int, C.c_int, C.c_int, _F]),
 }
 
 
@@ -101,6 +111,67 @@ class OracleModel:
         if rc != 0:
             raise ValueError(f"ora_forward failed ({rc})")
         return pooled, traces
+
+
+class VisionOracle:
+    """An image-encoder GGUF opened by the oracle (the config-5 tower, ora_vision_*)."""
+
+    def __init__(self, path: str):
+        err = C.create_string_buffer(512)
+        h = lib.ora_vision_open(path.encode(), err, 512)
+        if not h:
+            raise ValueError(err.value.decode())
+        self.h = C.c_void_p(h)
+        self.hidden = lib.ora_vision_hidden(self.h)
+        self.proj_dims = lib.ora_vision_proj_dims(self.h)
+        self.merge = lib.ora_vision_merge(self.h)
+        self.area = lib.ora_vision_patch_area(self.h)
+        self.layers = lib.ora_vision_layers(self.h)
+
+    def close(self):
+        if self.h:
+            lib.ora_vision_close(self.h)
+            self.h = None
+
+    def __enter__(self):
+        return self
+
+    def __exit__(self, *a):
+        self.close()
+
+    def forward(self, patches, grid_x: int, grid_y: int, keep: Optional[Iterable[Tuple[str, int]]] = None,
+                threads: int = 0):
+        """One image -> (vectors [tokens, proj_dims], {(name, layer): array})."""
+        p = f32(patches)
+        tokens = (grid_x // self.merge) * (grid_y // self.merge)
+        out = np.zeros((tokens, self.proj_dims), dtype=np.float32)
+        want = set(keep or [])
+        traces: Dict[Tuple[str, int], np.ndarray] = {}
+
+        def cb(_u, name, layer, data, count):
+            key = (name.decode(), int(layer))
+            if key in want:
+                traces[key] = np.ctypeslib.as_array(data, shape=(count,)).copy()
+
+        fn = TRACE_FN(cb)
+        rc = lib.ora_vision_forward(self.h, _f(p), grid_x, grid_y, _f(out), fn if want else TRACE_FN(), None, threads)
+        if rc != 0:
+            raise ValueError(f"ora_vision_forward failed ({rc})")
+        return out, traces
+
+
+def layernorm(x: np.ndarray, width: int, weight: np.ndarray, bias: np.ndarray, eps: float = 1e-6) -> np.ndarray:
+    x, w, b = f32(x), f32(weight), f32(bias)
+    out = np.zeros_like(x)
+    lib.ora_layernorm(_f(x), x.size // width, width, _f(w), _f(b), eps, _f(out))
+    return out
+
+
+def pool(x: np.ndarray, grid_x: int, grid_y: int, merge: int, width: int) -> np.ndarray:
+    x = f32(x)
+    out = np.zeros(((grid_x // merge) * (grid_y // merge), width), dtype=np.float32)
+    lib.ora_pool(_f(x), grid_x, grid_y, merge, width, _f(out))
+    return out
 
 
 def dequant_row(type_: int, row: bytes, cols: int) -> np.ndarray:

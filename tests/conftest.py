@@ -31,3 +31,15 @@ def tiny_gguf(model_dir):
 def config2_gguf(model_dir):
     import gemma_embed as ge
     return ge.synth_write_gguf(os.path.join(model_dir, "config2.gguf"), **ge.CONFIG2)
+
+
+@pytest.fixture(scope="session")
+def tiny_vision_gguf(model_dir):
+    import gemma_embed as ge
+    return ge.synth_write_vision_gguf(os.path.join(model_dir, "tiny_vision.gguf"), **ge.TINY_VISION)
+
+
+@pytest.fixture(scope="session")
+def config5_vision_gguf(model_dir):
+    import gemma_embed as ge
+    return ge.synth_write_vision_gguf(os.path.join(model_dir, "config5_vision.gguf"), **ge.CONFIG5_VISION)

@@ -204,3 +204,76 @@ def forward(g: Gguf, tokens: np.ndarray, keep: Tuple = ()) -> Tuple[np.ndarray, 
     y = rmsnorm(x, g.tensor("output_norm.weight"), eps) @ g.tensor("output.weight").T
     tr("result_embd", -1, y)
     return y.mean(axis=0), traces
+
+
+# ---------------------------------------------------------------------------- image tower
+
+def layernorm(x: np.ndarray, w: np.ndarray, b: np.ndarray, eps: float) -> np.ndarray:
+    mu = x.mean(axis=-1, keepdims=True)
+    var = ((x - mu) ** 2).mean(axis=-1, keepdims=True)
+    return (x - mu) / np.sqrt(var + eps) * w + b
+
+
+def vision_forward(g: Gguf, patches: np.ndarray, gx: int, gy: int, keep: Tuple = ()) -> Tuple[np.ndarray, Dict]:
+    """BASELINE config 5's tower for one image, float64: pre-LayerNorm blocks with biased
+    projections, softmax(q k^T / sqrt(hd)) attention over all patches, gelu_tanh MLP, final
+    LayerNorm, merge x merge mean pooling (as a reshape), weighted RMSNorm and projection."""
+    a = "clip.vision."
+    m = g.meta
+    L, d, H = m[a + "block_count"], m[a + "embedding_length"], m[a + "attention.head_count"]
+    eps, merge = m[a + "attention.layer_norm_epsilon"], m[a + "projector.scale_factor"]
+    hd = d // H
+    P = gx * gy
+    traces = {}
+
+    def tr(name, layer, val):
+        if (name, layer) in keep:
+            traces[(name, layer)] = np.array(val, dtype=np.float64).reshape(-1)
+
+    def lin(x, name):
+        return x @ g.tensor(name + ".weight").T
+
+    x = np.asarray(patches, dtype=np.float64) @ g.tensor("v.patch_embd.weight").T
+    tr("inp", -1, x)
+    shape, _, _ = g.tensors["v.position_embd.weight"]
+    npos = shape[1]
+    table = g.tensor("v.position_embd.weight")  # [2 npos, d]
+    col, row = np.arange(P) % gx, np.arange(P) // gx
+    x = x + g.tensor("v.patch_embd.bias") + table[col] + table[npos + row]
+    tr("pos_embd", -1, x)
+    for l in range(L):
+        b = f"v.blk.{l}."
+        h = layernorm(x, g.tensor(b + "ln1.weight"), g.tensor(b + "ln1.bias"), eps)
+        tr("layer_inp_normed", l, h)
+        q = lin(h, b + "attn_q") + g.tensor(b + "attn_q.bias")
+        k = lin(h, b + "attn_k") + g.tensor(b + "attn_k.bias")
+        v = lin(h, b + "attn_v") + g.tensor(b + "attn_v.bias")
+        tr("Qcur", l, q)
+        tr("Kcur", l, k)
+        tr("Vcur", l, v)
+        s = np.einsum("ihd,jhd->hij", q.reshape(P, H, hd), k.reshape(P, H, hd)) / np.sqrt(hd)
+        s = s - s.max(axis=-1, keepdims=True)
+        p = np.exp(s)
+        p /= p.sum(axis=-1, keepdims=True)
+        att = np.einsum("hij,jhd->ihd", p, v.reshape(P, H, hd)).reshape(P, d)
+        tr("kqv_out", l, att)
+        o = lin(att, b + "attn_out")
+        tr("attn_out", l, o)
+        x = x + o + g.tensor(b + "attn_out.bias")
+        tr("ffn_inp", l, x)
+        f = layernorm(x, g.tensor(b + "ln2.weight"), g.tensor(b + "ln2.bias"), eps)
+        tr("ffn_inp_normed", l, f)
+        u = gelu_tanh(lin(f, b + "ffn_up") + g.tensor(b + "ffn_up.bias"))
+        tr("ffn_gelu", l, u)
+        o = lin(u, b + "ffn_down")
+        tr("ffn_out", l, o)
+        x = x + o + g.tensor(b + "ffn_down.bias")
+        tr("layer_out", l, x)
+    y = layernorm(x, g.tensor("v.post_ln.weight"), g.tensor("v.post_ln.bias"), eps)
+    pooled = y.reshape(gy // merge, merge, gx // merge, merge, d).mean(axis=(1, 3)).reshape(-1, d)
+    tr("pooled", -1, pooled)
+    pn = rmsnorm(pooled, g.tensor("mm.soft_emb_norm.weight"), eps)
+    tr("pooled_normed", -1, pn)
+    out = pn @ g.tensor("mm.input_projection.weight").T
+    tr("projected", -1, out)
+    return out, traces
