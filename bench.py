@@ -13,8 +13,9 @@ Also reported on the same JSON line:
   gemm_all      the same for all Q8_0 GEMM launches together;
   variants      two device packs of 8192 tokens per step (the reference's default budget),
                 restaged each time; the full host API path at the reference's default options
-                (token ids in host memory -> normalised vectors, PCIe included); and BASELINE
-                config 4 (4 texts x 8192 tokens, one resident pack);
+                (token ids in host memory -> normalised vectors, PCIe included); BASELINE
+                config 4 (4 texts x 8192 tokens, one resident pack); and BASELINE config 5 (the
+                16-layer image tower over 8 resident 768 x 768 images);
   cpu_baseline  the CPU oracle (a C restatement of the reference's CPUReference.swift) on a
                 bounded sample of the same workload, on this host's cores.
 """
@@ -76,6 +77,71 @@ def attention_flops(lengths, window=512, pattern=(1, 1, 1, 1, 1, 0) * 4):
                 pairs = n * n
             total += 4 * HD * H * pairs
     return total
+
+
+VIT = dict(images=8, grid=48, area=768, d=1152, ff=4304, heads=16, hd=72, layers=16, proj=768, merge=3)
+
+
+def vision_flops():
+    """Algorithmic FLOPs of one config-5 batch at the tower's true widths (the padding of the
+    heads to 96 and of the MLP to 4352 columns is not counted): 2 M N K per GEMM and
+    4 hd H P^2 per image and layer for the attention."""
+    v = VIT
+    P = v["images"] * v["grid"] ** 2
+    d, ff = v["d"], v["ff"]
+    gemm = 2 * P * v["area"] * d + v["layers"] * 2 * P * d * (3 * d + d + 2 * ff) \
+        + 2 * (P // v["merge"] ** 2) * d * v["proj"]
+    attn = v["layers"] * v["images"] * 4 * v["hd"] * v["heads"] * (v["grid"] ** 2) ** 2
+    return gemm, attn
+
+
+def vision_variant(tmp: str, reps: int):
+    """8 synthetic 768 x 768 images (48 x 48 patches of 16 x 16 x 3 fp32 pixels
+    uniform in [-1, 1]) through the 16-layer tower, pooled 3 x 3 to 256 tokens each and projected
+    to 768: patches resident in HBM, one batch per step."""
+    import numpy as np
+    import gemma_embed as ge
+    path = os.path.join(tmp, "config5_vision.gguf")
+    ge.synth_write_vision_gguf(path, **ge.CONFIG5_VISION)
+    v = VIT
+    grids = [(v["grid"], v["grid"])] * v["images"]
+    patches = ge.image_patches(51, grids, v["area"])
+    ctx = ge.Context.create(0)
+    try:
+        ctx.vision_load(path)
+        ctx.vision_stage(patches, grids)
+        for _ in range(2):
+            ctx.vision_run()
+        ctx.sync()
+        t0 = time.perf_counter()
+        for _ in range(reps):
+            ctx.vision_run()
+        ctx.sync()
+        ms = (time.perf_counter() - t0) * 1e3 / reps
+        out = ctx.vision_read(v["proj"])
+        if out.shape != (v["images"] * 256, v["proj"]) or not np.all(np.isfinite(out)):
+            raise SystemExit("bad config-5 output")
+        ctx.profile_reset()
+        ctx.profile_enable("")
+        ctx.vision_run()
+        ctx.sync()
+        stats = ctx.profile_stats()
+        ctx.profile_disable()
+    finally:
+        ctx.close()
+    gemm, attn = vision_flops()
+    kernels = {k: {"launches": n, "avg_us": round(t / max(n, 1) * 1e3, 2), "ms": round(t, 4)} for k, (n, t) in stats.items()}
+    gemm_ms = sum(t for k, (n, t) in stats.items() if k.startswith("vit_gemm"))
+    attn_ms = stats.get("vit_attention", (0, 0.0))[1]
+    return {"workload": "config5: 16-layer ViT (width 1152, 16 heads of 72, MLP 4304, Q8_0), 8 images x 2304 patches, "
+                        "3x3 pooled to 256 tokens each, projected to 768",
+            "images_per_s": round(v["images"] / (ms * 1e-3), 2), "ms_per_batch": round(ms, 3),
+            "patches_per_s": round(v["images"] * v["grid"] ** 2 / (ms * 1e-3), 1),
+            "tflops": round((gemm + attn) / (ms * 1e-3) / 1e12, 1),
+            "frac": round((gemm + attn) / (ms * 1e-3) / 1e12 / PEAK_FP16_TFLOPS, 4),
+            "gemm_tflops": round(gemm / (gemm_ms * 1e-3) / 1e12, 1) if gemm_ms else None,
+            "attention_tflops": round(attn / (attn_ms * 1e-3) / 1e12, 1) if attn_ms else None,
+            "algorithmic_flops": gemm + attn, "kernels": kernels}
 
 
 def measured_traffic(label: str):
@@ -319,6 +385,10 @@ def main():
         + gemm_flops(long_texts * long_len)["gemm_output"] + attention_flops([long_len] * long_texts)
     log(f"config 4 (4 x 8192): {long_ms:.2f} ms/step, {long_rate:,.0f} tok/s")
 
+    vision = vision_variant(tmp, max(3, args.steps // 2))
+    log(f"config 5 (8 images): {vision['ms_per_batch']:.2f} ms/batch, {vision['images_per_s']:.1f} images/s, "
+        f"{vision['tflops']} TFLOP/s")
+
     total_flops = step_gemm_flops + attention_flops([TOKENS] * TEXTS)
     traffic, traffic_kernel = measured_traffic(dom)
     result = {
@@ -350,7 +420,8 @@ def main():
         "variants": {"packs_of_8192_tokens_per_s": round(default_budget, 1),
                      "embed_api_default_options_pcie_inclusive_tokens_per_s": round(api_rate, 1),
                      "config4_4x8192": {"tokens_per_s": round(long_rate, 1), "ms_per_step": round(long_ms, 3),
-                                        "tflops": round(long_flops / (long_ms * 1e-3) / 1e12, 1)}},
+                                        "tflops": round(long_flops / (long_ms * 1e-3) / 1e12, 1)},
+                     "config5_vision_8_images": vision},
     }
     model.close()
     if not args.no_cpu:

@@ -542,9 +542,7 @@ constexpr int BKV = 32;   // keys per block
 template <int HD>
 constexpr int attention_v3_lds_bytes() { return attn3::NS * 2 * attn3::BKV * HD * 2; }
 
-// HO: head dims stored per head (the first HO of HD; the rest are zero padding of Q, K and V^T, as
-// for the image tower's 72-wide heads held in 96), output row stride H * HO.
-template <int HD, int G, int QW, int HO = HD>
+template <int HD, int G, int QW>
 __global__ __launch_bounds__(QW * G * 64) void attention_v3_kernel(const uint16_t* __restrict__ Qg,
                                                                   const uint16_t* __restrict__ Kg,
                                                                   const uint16_t* __restrict__ VTg,
@@ -553,12 +551,11 @@ __global__ __launch_bounds__(QW * G * 64) void attention_v3_kernel(const uint16_
                                                                   int vt_cols, int hw, float scale_log2) {
     using namespace attn3;
     constexpr int QB = 16 * QW, NW = QW * G, KS = HD / 32, DT = HD / 16;
-    constexpr int DTO = (HO + 15) / 16;  // head-dim tiles of O that hold stored dims
-    static_assert(HO <= HD && HO % 8 == 0, "stored head dims");
     constexpr int K_BYTES = BKV * HD * 2, STAGE = 2 * K_BYTES;
     constexpr int KCH = K_BYTES / 1024, CH = 2 * KCH;  // K chunks (ks, m), then V^T chunks dt
     static_assert(KCH == 2 * KS && KCH == DT, "chunk counts");
     constexpr int CPW = (CH + NW - 1) / NW;  // copies per wave per block (some waves repeat one)
+    static_assert(NW <= CH, "a wave past the last chunk repeats its own chunk index");
     extern __shared__ __attribute__((aligned(1024))) unsigned char ldsa[];
 
     // XCD-aware order, as in attention_v2_kernel.
@@ -713,8 +710,8 @@ __global__ __launch_bounds__(QW * G * 64) void attention_v3_kernel(const uint16_
         l_run += sum;  // this lane's keys only; the key groups are summed once, at the end
         // O^T += V^T P^T: head-dim tiles dt of 16 rows, the block's 32 keys as one k-step
 #pragma unroll
-        for (int dt = 0; dt < DTO; dt++) {
-            if (dt + PF < DTO) va[(dt + PF) % RING] = *reinterpret_cast<const half8_t*>(vf + (dt + PF) * 1024);
+        for (int dt = 0; dt < DT; dt++) {
+            if (dt + PF < DT) va[(dt + PF) % RING] = *reinterpret_cast<const half8_t*>(vf + (dt + PF) * 1024);
             __builtin_amdgcn_sched_barrier(0);
             o[dt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(va[dt % RING], pb, o[dt], 0, 0, 0);
         }
@@ -726,10 +723,9 @@ __global__ __launch_bounds__(QW * G * 64) void attention_v3_kernel(const uint16_
     if (qi >= len) return;
     const float inv = l_run > 0.0f ? 1.0f / l_run : 0.0f;
     // o[dt], lane l: head dims 16 dt + 4 (l / 16) + r of query qi
-    _Float16* op = reinterpret_cast<_Float16*>(Og) + (size_t)(seq_start + qi) * (H * HO) + h * HO + 4 * g4;
+    _Float16* op = reinterpret_cast<_Float16*>(Og) + (size_t)(seq_start + qi) * qStride + h * HD + 4 * g4;
 #pragma unroll
-    for (int dt = 0; dt < DTO; dt++) {
-        if (HO < HD && 16 * dt + 4 * g4 >= HO) continue;
+    for (int dt = 0; dt < DT; dt++) {
         half4_t v4;
 #pragma unroll
         for (int r = 0; r < 4; r++) v4[r] = _Float16(o[dt][r] * inv);
@@ -797,17 +793,206 @@ hipError_t launch_attention_v2(hipStream_t s, const uint16_t* q, const uint16_t*
     return attention_v2_dispatch_g<256>(s, q, k, vt, vt_cols, o, work, n_work, H, KV, half_window, scale, item_queries);
 }
 
+// The image tower's attention: one query head per KV head, no window, heads stored padded (HD
+// dims of which the first HO are real). As attention_v3_kernel (the same K/V^T ring in LDS, the
+// same MFMAs and softmax), but each wave owns QT tiles of 16 queries, so every K and V^T fragment
+// read from LDS feeds QT MFMAs: at head dim 72 the LDS reads, not the MFMAs, set the pace.
+template <int HD, int QW, int QT, int HO>
+__global__ __launch_bounds__(QW * 64) void attention_mq_kernel(const uint16_t* __restrict__ Qg,
+                                                               const uint16_t* __restrict__ Kg,
+                                                               const uint16_t* __restrict__ VTg,
+                                                               uint16_t* __restrict__ Og,
+                                                               const AttnWork* __restrict__ work, int H, int vt_cols,
+                                                               float scale_log2) {
+    using namespace attn3;
+    constexpr int NW = QW, KS = HD / 32, DT = HD / 16, DTO = (HO + 15) / 16;
+    constexpr int K_BYTES = BKV * HD * 2, STAGE = 2 * K_BYTES;
+    constexpr int KCH = K_BYTES / 1024, CH = 2 * KCH;  // K chunks (ks, m), then V^T chunks dt
+    static_assert(KCH == 2 * KS && KCH == DT, "chunk counts");
+    static_assert(HO <= HD && HO % 8 == 0, "stored head dims");
+    static_assert(NW <= CH, "a wave past the last chunk repeats its own chunk index");
+    constexpr int CPW = (CH + NW - 1) / NW;
+    extern __shared__ __attribute__((aligned(1024))) unsigned char ldsa[];
+
+    const int nb = int(gridDim.x), full = nb / 8 * 8, bx = int(blockIdx.x);
+    const int widx = bx < full ? (bx % 8) * (full / 8) + bx / 8 : bx;
+    const int seq_start = __builtin_amdgcn_readfirstlane(int(work[widx].seq_start));
+    const int len = __builtin_amdgcn_readfirstlane(int(work[widx].seq_len));
+    const int wq0 = __builtin_amdgcn_readfirstlane(int(work[widx].q0));
+    const int vt_start = __builtin_amdgcn_readfirstlane(int(work[widx].vt_start));
+    const int h = blockIdx.y;
+    const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(int(threadIdx.x >> 6));
+    const int qbase = wq0 + wave * 16 * QT;  // tile t: queries qbase + 16 t + lane % 16
+    const int l16 = lane & 15, g4 = lane >> 4;
+    const int stride = H * HD;
+    const int nblocks = (len + BKV - 1) / BKV;
+
+    const __amdgpu_buffer_rsrc_t kr =
+        buffer_rsrc(Kg + (size_t)seq_start * stride + h * HD, uint32_t(((len - 1) * stride + HD) * 2));
+    const __amdgpu_buffer_rsrc_t vr = buffer_rsrc(VTg + (size_t)h * HD * vt_cols + vt_start,
+                                                  uint32_t(((HD - 1) * vt_cols + (vt_cols - vt_start)) * 2));
+    const uint32_t klane = uint32_t(((8 * (l16 >> 2) + (lane & 3)) * stride + 8 * g4) * 2);
+    const uint32_t vlane = uint32_t((l16 * vt_cols + 8 * g4) * 2);
+#define MQ_ISSUE(kb, b)                                                                                    \
+    do {                                                                                                   \
+        _Pragma("unroll") for (int i = 0; i < CPW; i++) {                                                  \
+            int c = wave + i * NW;                                                                         \
+            if (c >= CH) c = wave;                                                                         \
+            unsigned char* dst_ = ldsa + (b) * STAGE + c * 1024;                                           \
+            if (c < KCH) {                                                                                 \
+                const int ks_ = c >> 1, m_ = c & 1;                                                        \
+                lds_copy16(kr, dst_, klane + uint32_t(((kb) + 4 * m_) * stride * 2 + ks_ * 64), 0);        \
+            } else {                                                                                       \
+                lds_copy16(vr, dst_, vlane + uint32_t((c - KCH) * 16 * vt_cols * 2 + (kb) * 2), 0);        \
+            }                                                                                              \
+        }                                                                                                  \
+    } while (0)
+
+    half8_t qa[QT][KS];
+    {
+        const __amdgpu_buffer_rsrc_t qr =
+            buffer_rsrc(Qg + (size_t)seq_start * stride + h * HD, uint32_t(((len - 1) * stride + HD) * 2));
+#pragma unroll
+        for (int t = 0; t < QT; t++) {
+            const uint32_t qo = uint32_t((min(qbase + 16 * t + l16, len - 1) * stride + 8 * g4) * 2);
+#pragma unroll
+            for (int ks = 0; ks < KS; ks++)
+                qa[t][ks] = __builtin_bit_cast(half8_t, __builtin_amdgcn_raw_buffer_load_b128(qr, qo + ks * 64, 0, 0));
+        }
+    }
+    float4_t o[QT][DTO];
+    float m_run[QT], l_run[QT];
+#pragma unroll
+    for (int t = 0; t < QT; t++) {
+#pragma unroll
+        for (int i = 0; i < DTO; i++) o[t][i] = float4_t{0.0f, 0.0f, 0.0f, 0.0f};
+        m_run[t] = -INFINITY;
+        l_run[t] = 0.0f;
+    }
+
+#pragma unroll
+    for (int s = 0; s < NS - 1; s++)
+        if (s < nblocks) MQ_ISSUE(s * BKV, s);
+    int b = 0;
+    for (int it = 0; it < nblocks; it++) {
+        const int kb = it * BKV;
+        static_assert(NS >= 2 && NS <= 4, "the waits below cover two to four stages");
+        const int ahead = min(NS - 2, nblocks - 1 - it);
+        if (ahead >= 2)
+            wait_vmcnt<2 * CPW>();
+        else if (ahead == 1)
+            wait_vmcnt<CPW>();
+        else
+            wait_vmcnt<0>();
+        wait_lgkmcnt0();
+        workgroup_barrier();
+        if (it + NS - 1 < nblocks) MQ_ISSUE((it + NS - 1) * BKV, b == 0 ? NS - 1 : b - 1);
+        const unsigned char* const kf = ldsa + b * STAGE + lane * 16;
+        const unsigned char* const vf = kf + K_BYTES;
+        constexpr int PF = 2, RING = PF + 1;
+        float4_t s[QT][2];
+#pragma unroll
+        for (int t = 0; t < QT; t++) s[t][0] = s[t][1] = float4_t{0.0f, 0.0f, 0.0f, 0.0f};
+        half8_t ka[RING][2];
+#pragma unroll
+        for (int f = 0; f < PF; f++) {
+            ka[f][0] = *reinterpret_cast<const half8_t*>(kf + (2 * f) * 1024);
+            ka[f][1] = *reinterpret_cast<const half8_t*>(kf + (2 * f + 1) * 1024);
+        }
+#pragma unroll
+        for (int ks = 0; ks < KS; ks++) {
+            if (ks + PF < KS) {
+                ka[(ks + PF) % RING][0] = *reinterpret_cast<const half8_t*>(kf + (2 * (ks + PF)) * 1024);
+                ka[(ks + PF) % RING][1] = *reinterpret_cast<const half8_t*>(kf + (2 * (ks + PF) + 1) * 1024);
+            }
+            __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+            for (int t = 0; t < QT; t++) {
+                s[t][0] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ka[ks % RING][0], qa[t][ks], s[t][0], 0, 0, 0);
+                s[t][1] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ka[ks % RING][1], qa[t][ks], s[t][1], 0, 0, 0);
+            }
+        }
+        half8_t va[RING];
+#pragma unroll
+        for (int f = 0; f < PF; f++) va[f] = *reinterpret_cast<const half8_t*>(vf + f * 1024);
+        const bool inside = kb + BKV <= len;
+        half8_t pb[QT];
+#pragma unroll
+        for (int t = 0; t < QT; t++) {
+            float sc[8] = {s[t][0][0], s[t][0][1], s[t][0][2], s[t][0][3], s[t][1][0], s[t][1][1], s[t][1][2], s[t][1][3]};
+            if (!inside) {
+#pragma unroll
+                for (int e = 0; e < 8; e++) sc[e] = kb + 8 * g4 + e < len ? sc[e] : -INFINITY;
+            }
+            const float lmax =
+                fmaxf(fmaxf(fmaxf(sc[0], sc[1]), fmaxf(sc[2], sc[3])), fmaxf(fmaxf(sc[4], sc[5]), fmaxf(sc[6], sc[7])));
+            // lazy rescaling, as in attention_v3_kernel
+            if (__builtin_amdgcn_ballot_w64(lmax * scale_log2 > m_run[t] + 8.0f)) {
+                const float bmax = max_over_key_groups(lmax) * scale_log2;
+                const float m_new = fmaxf(m_run[t], bmax);
+                const float alpha = m_new == -INFINITY ? 1.0f : __builtin_amdgcn_exp2f(m_run[t] - m_new);
+                l_run[t] *= alpha;
+#pragma unroll
+                for (int i = 0; i < DTO; i++) o[t][i] *= alpha;
+                m_run[t] = m_new;
+            }
+            const float m_ref = m_run[t] == -INFINITY ? 0.0f : m_run[t];
+            float sum = 0.0f;
+#pragma unroll
+            for (int e = 0; e < 8; e++) {
+                const float p = __builtin_amdgcn_exp2f(__builtin_fmaf(sc[e], scale_log2, -m_ref));
+                sum += p;
+                pb[t][e] = _Float16(p);
+            }
+            l_run[t] += sum;
+        }
+#pragma unroll
+        for (int dt = 0; dt < DTO; dt++) {
+            if (dt + PF < DTO) va[(dt + PF) % RING] = *reinterpret_cast<const half8_t*>(vf + (dt + PF) * 1024);
+            __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+            for (int t = 0; t < QT; t++) o[t][dt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(va[dt % RING], pb[t], o[t][dt], 0, 0, 0);
+        }
+        b = b + 1 == NS ? 0 : b + 1;
+    }
+#undef MQ_ISSUE
+    wait_vmcnt<0>();
+#pragma unroll
+    for (int t = 0; t < QT; t++) l_run[t] = sum_over_key_groups(l_run[t]);
+#pragma unroll
+    for (int t = 0; t < QT; t++) {
+        const int qi = qbase + 16 * t + l16;
+        if (qi >= len) continue;
+        const float inv = l_run[t] > 0.0f ? 1.0f / l_run[t] : 0.0f;
+        _Float16* op = reinterpret_cast<_Float16*>(Og) + (size_t)(seq_start + qi) * (H * HO) + h * HO + 4 * g4;
+#pragma unroll
+        for (int dt = 0; dt < DTO; dt++) {
+            if (HO < HD && 16 * dt + 4 * g4 >= HO) continue;
+            half4_t v4;
+#pragma unroll
+            for (int r = 0; r < 4; r++) v4[r] = _Float16(o[t][dt][r] * inv);
+            *reinterpret_cast<half4_t*>(op + dt * 16) = v4;
+        }
+    }
+}
+
 bool attention_padded_supported(int hp, int hd, int H, int KV) { return hp == 96 && hd == 72 && H > 0 && KV == H; }
 
 hipError_t launch_attention_padded(hipStream_t s, const uint16_t* q, const uint16_t* k, const uint16_t* vt, int vt_cols,
                                    uint16_t* o, const AttnWork* work, int n_work, int H, int KV, int hp, int hd,
-                                   int half_window, float scale) {
-    if (n_work < 0 || !attention_padded_supported(hp, hd, H, KV) || half_window < 0 || vt_cols <= 0 || vt_cols % 8)
+                                   int half_window, float scale, int item_queries) {
+    if (n_work < 0 || !attention_padded_supported(hp, hd, H, KV) || half_window != 0 || vt_cols <= 0 || vt_cols % 8 ||
+        (item_queries != 64 && item_queries != 256))
         return hipErrorInvalidValue;
     if (n_work == 0) return hipSuccess;
     const float scale_log2 = scale * 1.4426950408889634f;
-    launch_kernel(attention_v3_kernel<96, 1, 4, 72>, dim3(n_work, KV), dim3(4 * 64), uint32_t(attention_v3_lds_bytes<96>()), s,
-                  q, k, vt, o, work, H, KV, vt_cols, half_window, scale_log2);
+    // 256-query items: eight waves of two 16-query tiles share each K/V block copied into LDS
+    if (item_queries == 256)
+        launch_kernel(attention_mq_kernel<96, 8, 2, 72>, dim3(n_work, KV), dim3(8 * 64), uint32_t(attention_v3_lds_bytes<96>()),
+                      s, q, k, vt, o, work, H, vt_cols, scale_log2);
+    else
+        launch_kernel(attention_mq_kernel<96, 4, 1, 72>, dim3(n_work, KV), dim3(4 * 64), uint32_t(attention_v3_lds_bytes<96>()),
+                      s, q, k, vt, o, work, H, vt_cols, scale_log2);
     return hipGetLastError();
 }
 

@@ -138,11 +138,12 @@ hipError_t launch_attention_v2(hipStream_t s, const uint16_t* q, const uint16_t*
 
 // The same attention over heads stored padded: q [T][H][hp], k [T][KV][hp] and vt [KV * hp][vt_cols]
 // hold hd real dims per head and zeros past them; out [T][H][hd]. Supported: hp 96 with hd 72
-// (the image tower's heads), one query head per KV head, 64-query work items.
+// (the image tower's heads), one query head per KV head, no window (half_window 0), work items
+// of 64 or 256 queries (a query's result is the same either way).
 bool attention_padded_supported(int hp, int hd, int H, int KV);
 hipError_t launch_attention_padded(hipStream_t s, const uint16_t* q, const uint16_t* k, const uint16_t* vt, int vt_cols,
                                    uint16_t* o, const AttnWork* work, int n_work, int H, int KV, int hp, int hd,
-                                   int half_window, float scale);
+                                   int half_window, float scale, int item_queries);
 
 // v [T][width] fp16 -> vt [width][vt_cols] with token t at column vcol[t]; width a multiple of 64.
 hipError_t launch_v_transpose(hipStream_t s, const uint16_t* v, int T, int width, const int32_t* vcol, int vt_cols,

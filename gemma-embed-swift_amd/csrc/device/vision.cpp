@@ -42,9 +42,13 @@ struct VisionState {
     AttnWork* work = nullptr;
     // staged batch
     int staged_patches = -1, staged_tokens = 0, staged_work = 0;
+    int items = kAttnQueriesV2;  // query rows per attention work item of the staged batch
 };
 
 namespace {
+
+// Smallest count of 256-query attention workgroups for which a batch takes them (one per CU).
+constexpr int64_t kVitWideItems = 256;
 
 VisionState& vision_of(ge_ctx* c) {
     if (!c->vision) fail(GE_ERR_STATE, "no image encoder has been uploaded");
@@ -354,6 +358,12 @@ void vision_stage(ge_ctx* c, const float* patches, int n_patches, const ge_image
     std::vector<AttnWork> work;
     int64_t P = 0;
     uint32_t col = 0;
+    // 256-query work items when they still give at least kVitWideItems workgroups (eight waves
+    // of two query tiles share a K/V block: a quarter of the L2 reads per query, half the LDS
+    // reads); 64 for small batches. Same results either way.
+    int64_t items256 = 0;
+    for (int i = 0; i < n_images; i++) items256 += (int64_t(grids[i].grid_x) * grids[i].grid_y + 255) / 256;
+    const int items = v.hp != v.hd && items256 * v.heads >= kVitWideItems ? 256 : kAttnQueriesV2;
     for (int i = 0; i < n_images; i++) {
         const int gx = grids[i].grid_x, gy = grids[i].grid_y;
         if (gx <= 0 || gy <= 0 || gx % v.merge || gy % v.merge)
@@ -367,7 +377,7 @@ void vision_stage(ge_ctx* c, const float* patches, int n_patches, const ge_image
             py.push_back(p / gx);
             vcol.push_back(int32_t(col + uint32_t(p)));
         }
-        for (uint32_t q0 = 0; q0 < uint32_t(n); q0 += uint32_t(kAttnQueriesV2))
+        for (uint32_t q0 = 0; q0 < uint32_t(n); q0 += uint32_t(items))
             work.push_back(AttnWork{uint32_t(P), uint32_t(n), q0, col});
         for (int oy = 0; oy < gy / v.merge; oy++)
             for (int ox = 0; ox < gx / v.merge; ox++) {
@@ -399,6 +409,7 @@ void vision_stage(ge_ctx* c, const float* patches, int n_patches, const ge_image
     v.staged_patches = n_patches;
     v.staged_tokens = tokens;
     v.staged_work = int(work.size());
+    v.items = items;
 }
 
 // ---------------------------------------------------------------- forward
@@ -450,7 +461,7 @@ void vision_encode(ge_ctx* c, VitStop* sp) {
             const float sc = att_scale / (L.qkv_c * L.qkv_c);
             if (v.hp != v.hd)
                 return launch_attention_padded(s, v.q, v.k, v.vt, v.vt_cap, v.attn, v.work, v.staged_work, v.heads, v.heads,
-                                               v.hp, v.hd, 0, sc);
+                                               v.hp, v.hd, 0, sc, v.items);
             return launch_attention_v2(s, v.q, v.k, v.vt, v.vt_cap, v.attn, v.work, v.staged_work, v.heads, v.heads, v.hd, 0,
                                        sc);
         });

@@ -14,6 +14,9 @@
 //                             written to a temporary GGUF; 32 texts x 512 ids): the time per
 //                             call of ge_model_embed at the 8192- and 16384-token budgets, and
 //                             of the resident pack (ge_batch_run) for comparison
+//   ge_probe vision [reps]    BASELINE config 5: the synthetic 16-layer image tower (written to a
+//                             temporary GGUF) over 8 resident images of 48 x 48 patches
+//                             (ge_vision_run), the time per batch
 //   ge_probe calibrate        fp16 -> fp32 conversion of 2^28 values (reads 512 MiB, writes 1 GiB):
 //                             the known-size kernel that scales the HBM byte counters
 //
@@ -180,6 +183,41 @@ int probe_embed(int reps) {
     return 0;
 }
 
+int probe_vision(ge_ctx* c, int reps) {
+    ge_synth_vision_spec spec{};
+    spec.layers = 16, spec.hidden = 1152, spec.heads = 16, spec.feed_forward = 4304, spec.patch_size = 16;
+    spec.merge = 3, spec.proj_dims = 768, spec.positions = 48, spec.eps = 1e-6f, spec.ffn_down_type = 0, spec.seed = 5;
+    char err[512] = {0};
+    const char* path = "/tmp/ge_probe_config5_vision.gguf";
+    if (ge_synth_write_vision_gguf(path, &spec, err, sizeof err) != 0) {
+        std::fprintf(stderr, "ge_probe: synth: %s\n", err);
+        return 1;
+    }
+    if (ge_vision_load(c, path, err, sizeof err) != 0) {
+        std::fprintf(stderr, "ge_probe: vision load: %s\n", err);
+        return 1;
+    }
+    std::remove(path);
+    const int images = 8, grid = 48, area = 768;
+    std::vector<float> patches(size_t(images) * grid * grid * area);
+    ge_synth_uniform(51, -1.0f, 1.0f, int64_t(patches.size()), patches.data());
+    std::vector<ge_image_grid> grids(images, ge_image_grid{grid, grid});
+    if (ge_vision_stage(c, patches.data(), images * grid * grid, grids.data(), images) != 0) return fail(c, "vision stage");
+    for (int r = 0; r < 2; r++)
+        if (ge_vision_run(c) != 0) return fail(c, "vision run");
+    ge_sync(c);
+    const auto t0 = std::chrono::steady_clock::now();
+    for (int r = 0; r < reps; r++)
+        if (ge_vision_run(c) != 0) return fail(c, "vision run");
+    ge_sync(c);
+    const double ms = std::chrono::duration<double, std::milli>(std::chrono::steady_clock::now() - t0).count() / reps;
+    std::vector<float> out(size_t(images) * 256 * 768);
+    if (ge_vision_read(c, out.data()) != 0) return fail(c, "vision read");
+    std::printf("config 5 image tower: %.3f ms per batch of %d images, %.1f images/s\n", ms, images, images / (ms * 1e-3));
+    std::fflush(stdout);
+    return 0;
+}
+
 int probe_calibrate(ge_ctx* c) {
     const size_t n = size_t(1) << 28;
     void* src = ge_dev_alloc(c, 2 * n);
@@ -199,8 +237,9 @@ int main(int argc, char** argv) {
     const char* what = argc > 1 ? argv[1] : "gate_up";
     const int reps = argc > 2 ? std::atoi(argv[2]) : 20;
     if (std::strcmp(what, "embed") == 0) return reps < 1 || reps > 10000 ? 2 : probe_embed(reps);
-    if (std::strcmp(what, "gate_up") != 0 && std::strcmp(what, "attention") != 0 && std::strcmp(what, "calibrate") != 0) {
-        std::fprintf(stderr, "usage: ge_probe gate_up|attention|embed [reps] | ge_probe calibrate\n");
+    if (std::strcmp(what, "gate_up") != 0 && std::strcmp(what, "attention") != 0 && std::strcmp(what, "calibrate") != 0 &&
+        std::strcmp(what, "vision") != 0) {
+        std::fprintf(stderr, "usage: ge_probe gate_up|attention|embed|vision [reps] | ge_probe calibrate\n");
         return 2;
     }
     if (reps < 1 || reps > 10000) {
@@ -213,6 +252,7 @@ int main(int argc, char** argv) {
     std::fflush(stdout);
     const int rc = std::strcmp(what, "calibrate") == 0   ? probe_calibrate(c)
                    : std::strcmp(what, "attention") == 0 ? probe_attention(c, reps)
+                   : std::strcmp(what, "vision") == 0    ? probe_vision(c, reps)
                                                          : probe_gate_up(c, reps);
     if (rc == 0) ge_destroy(c);
     return rc;
