@@ -1,7 +1,7 @@
 // The image tower on the device: weight upload from an image-encoder GGUF's tensor directory,
 // staging of a batch of images (patches plus pool grids), the forward and named-tensor traces.
-// Plays the role of the reference's Metal/VisionTower.swift (VisionBatch :7-33, VisionWorkspace
-// :37-83, upload :109-138, encode :140-185) for BASELINE config 5's encoder: LayerNorm with bias
+// Plays the role of the reference's Metal/VisionTower.swift (VisionBatch :8-34, VisionWorkspace
+// :38-82, upload :113-140, encode :143-185) for BASELINE config 5's encoder: LayerNorm with bias
 // before attention and MLP, biased projections, a non-gated gelu_tanh MLP, heads of 72, learned
 // column and row position tables (the reference's table layout), a final LayerNorm, 3x3 mean
 // pooling, the projector's weighted RMSNorm and a Q8_0 projection into the text space.
@@ -347,7 +347,7 @@ void ensure_vision_workspace(ge_ctx* c, VisionState& v, int patches, int tokens,
     v.work = vws_alloc<AttnWork>(size_t(wc), 1, "attention work");
 }
 
-// VisionBatch.init (VisionTower.swift:16-30) and VisionTower.upload (:109-138): images back to
+// VisionBatch.init (VisionTower.swift:17-33) and VisionTower.upload (:113-140): images back to
 // back as patch rows (patch i of an image at column i % gx, row i / gx), each image one attention
 // sequence, pooled tokens back to back in (oy, ox) order.
 void vision_stage(ge_ctx* c, const float* patches, int n_patches, const ge_image_grid* grids, int n_images) {
@@ -425,7 +425,7 @@ struct VitStop {
     }
 };
 
-// VisionTower.encode (VisionTower.swift:141-185) for config 5's encoder: 8 launches per layer.
+// VisionTower.encode (VisionTower.swift:143-185) for config 5's encoder: 8 launches per layer.
 void vision_encode(ge_ctx* c, VitStop* sp) {
     VisionState& v = vision_of(c);
     if (v.staged_patches < 0) fail(GE_ERR_STATE, "no image batch is staged");

@@ -2,8 +2,9 @@
 // 3x3 pooling and a projection into the text space). One wave per row; lane l owns elements
 // c * 256 + 4 l .. + 3 of every 256-wide chunk c. The GEMMs (patch embedding, QKV, output, MLP,
 // projection) and the attention are the text path's kernels. Counterparts in the reference's
-// gemma4v tower: position rows (Shaders/Elementwise.metal:146-240, VisionTower.swift:152-155),
-// fused residual norms (:299-354) and the pooling (CPUVisionReference.swift:60-83).
+// gemma4v tower: position rows (Shaders/Elementwise.metal:207-222, Metal/VisionTower.swift:153-154),
+// fused residual norms (Shaders/Elementwise.metal:300-350) and the pooling (:223-242,
+// Model/CPUVisionReference.swift:67-83).
 #include "common.hpp"
 #include "kernels.hpp"
 

@@ -1,5 +1,5 @@
 // Image-encoder GGUF loading for the device library: VisionConfig.init's metadata reads
-// (Model/VisionConfig.swift:40-90) and the weight directory (Model/VisionWeights.swift), turned
+// (Model/VisionConfig.swift:44-81) and the weight directory (Model/VisionWeights.swift), turned
 // into the ge_vision_desc that ge_upload_vision takes.
 #include <cstdio>
 #include <string>

@@ -174,7 +174,7 @@ int ge_op_attention(ge_ctx* ctx, const void* q, const void* k, const void* v, vo
                     float scale);
 
 /* ---- image tower, on the same context as the text encoder.
- * Replaces Metal/VisionTower.swift (VisionTower.upload :109-138, encode :140-185) for a
+ * Replaces Metal/VisionTower.swift (VisionTower.upload :113-140, encode :143-185) for a
  * pre-LayerNorm ViT: per layer x += attn_out(attn(LN1(x))) + b, x += down(gelu_tanh(up(LN2(x)))),
  * heads of hidden / heads dims (72, 128 or 256), then a final LayerNorm, merge x merge mean pooling,
  * a weighted RMSNorm and a Q8_0 projection. Tensors (GGUF names, ne order):
@@ -313,7 +313,7 @@ typedef struct ge_synth_vision_spec {
 } ge_synth_vision_spec;
 int ge_synth_write_vision_gguf(const char* path, const ge_synth_vision_spec* spec, char* err, size_t errlen);
 
-/* Loads an image-encoder GGUF (VisionConfig.init, Model/VisionConfig.swift:40-90, and the
+/* Loads an image-encoder GGUF (VisionConfig.init, Model/VisionConfig.swift:44-81, and the
  * weight directory, Model/VisionWeights.swift) onto the context through ge_upload_vision. */
 int ge_vision_load(ge_ctx* ctx, const char* path, char* err, size_t errlen);
 
