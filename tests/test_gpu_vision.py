@@ -168,3 +168,31 @@ def test_config5_batch_of_eight_bitwise(config5):
     for i in (0, 5):
         alone, _ = c.vision_encode(patches[i * 2304:(i + 1) * 2304], [(48, 48)], o.proj_dims)
         assert np.array_equal(alone, batch[i * 256:(i + 1) * 256]), i
+
+
+def test_tower_with_128_wide_heads_and_q8_down(tmp_path):
+    """The other head path (head dim 128 through the text path's LDS-copy attention, no padding)
+    and a Q8_0 ffn_down, on a small tower with a 2 x 2 merge."""
+    spec = dict(layers=2, hidden=256, heads=2, feed_forward=1024, patch_size=16, merge=2, proj_dims=128, positions=16,
+                eps=1e-6, ffn_down_type=ge.GE_TYPE_Q8_0, seed=13)
+    path = ge.synth_write_vision_gguf(str(tmp_path / "small_vision.gguf"), **spec)
+    grids = [(8, 6), (4, 4), (16, 2)]
+    c = ge.Context.create(0)
+    try:
+        c.vision_load(path)
+        with ora.VisionOracle(path) as o:
+            patches = ge.image_patches(41, grids, o.area)
+            vecs, _ = c.vision_encode(patches, grids, o.proj_dims, merge=2)
+            rows = split_rows(vecs, [(gx // 2) * (gy // 2) for gx, gy in grids])
+            pats = split_rows(patches, [gx * gy for gx, gy in grids])
+            for i, (gx, gy) in enumerate(grids):
+                want, tr = o.forward(pats[i], gx, gy, keep=[("kqv_out", 1), ("layer_out", 1)])
+                assert max_rel(rows[i], want) <= TOL, i
+                assert min(cosine(rows[i][t], want[t]) for t in range(want.shape[0])) >= COSINE_BAR, i
+            for name in ("kqv_out", "layer_out"):
+                got = c.vision_trace(patches, grids, name, 1).reshape(patches.shape[0], -1)
+                for i, ((gx, gy), part) in enumerate(zip(grids, split_rows(got, [gx * gy for gx, gy in grids]))):
+                    _, tr = o.forward(pats[i], gx, gy, keep=[(name, 1)])
+                    assert max_rel(part, tr[(name, 1)].reshape(part.shape)) <= TOL, (name, i)
+    finally:
+        c.close()
