@@ -326,7 +326,14 @@ double max_abs(const ge_model_desc* d, const std::string& name, int n, const voi
     return m;
 }
 
+void drop_graphs(ge_ctx* c) {
+    for (ShortGraph& g : c->graphs)
+        if (g.exec) (void)hipGraphExecDestroy(g.exec);
+    c->graphs.clear();
+}
+
 void free_model(ge_ctx* c) {
+    drop_graphs(c);
     for (void* p : c->weight_allocs) (void)hipFree(p);
     c->weight_allocs.clear();
     c->rope_tables.clear();
@@ -335,6 +342,7 @@ void free_model(ge_ctx* c) {
 }
 
 void free_workspace(ge_ctx* c) {
+    drop_graphs(c);
     Workspace& w = c->ws;
     void* ps[] = {w.x, w.qkv, w.t, w.out, w.h, w.q, w.k, w.v, w.attn, w.act, w.tokens, w.positions, w.seqs, w.work, w.pooled,
                   w.vt, w.vcol, w.work2};
@@ -473,6 +481,7 @@ bool workspace_grows(const ge_ctx* c, int tokens, int seqs, int work, int work2,
 }
 
 void ensure_workspace(ge_ctx* c, int tokens, int seqs, int work, int work2, int vt_cols) {
+    if (workspace_grows(c, tokens, seqs, work, work2, vt_cols)) drop_graphs(c);
     Workspace& w = c->ws;
     const DevModel& m = c->model;
     const int rows = (tokens + 63) / 64 * 64 + kRowSlack;
@@ -894,11 +903,58 @@ void encode_split(ge_ctx* c) {
     launch(c, "mean_pool", [&] { return launch_mean_pool(c->stream, w.out, w.seqs, c->staged_seqs, m.out_dims, w.pooled); });
 }
 
+// Packs of at most this many tokens replay their forward as a HIP graph from the second run of
+// the same shape on.
+constexpr int kGraphMaxTokens = 64;
+constexpr size_t kMaxGraphs = 32;
+
+// A short pack's forward is ~170 launches of a few microseconds of work each, so launch latency,
+// not the kernels, sets its time. The first run of a pack shape is eager and records the shape;
+// the second captures the launches (encode) into a graph, which that run and every later one
+// replays with one launch. The key holds everything the launches' arguments depend on besides
+// the workspace and model addresses, and every graph is dropped when those change.
+void run_graph(ge_ctx* c) {
+    const int key[6] = {c->staged_tokens, c->staged_seqs, c->staged_work, c->staged_work2, c->ws.vt_cap, c->attn_items};
+    ShortGraph* g = nullptr;
+    for (ShortGraph& x : c->graphs)
+        if (std::equal(key, key + 6, x.key)) g = &x;
+    if (!g) {
+        if (c->graphs.size() >= kMaxGraphs) {
+            if (c->graphs.front().exec) (void)hipGraphExecDestroy(c->graphs.front().exec);
+            c->graphs.erase(c->graphs.begin());
+        }
+        ShortGraph n;
+        std::copy(key, key + 6, n.key);
+        c->graphs.push_back(n);
+        encode(c, nullptr);
+        return;
+    }
+    if (!g->exec) {
+        hipGraph_t graph = nullptr;
+        hip_check(hipStreamBeginCapture(c->stream, hipStreamCaptureModeThreadLocal), "hipStreamBeginCapture");
+        try {
+            encode(c, nullptr);
+        } catch (...) {
+            (void)hipStreamEndCapture(c->stream, &graph);
+            if (graph) (void)hipGraphDestroy(graph);
+            throw;
+        }
+        hip_check(hipStreamEndCapture(c->stream, &graph), "hipStreamEndCapture");
+        const hipError_t e = hipGraphInstantiate(&g->exec, graph, nullptr, nullptr, 0);
+        (void)hipGraphDestroy(graph);
+        if (e != hipSuccess) g->exec = nullptr;
+        hip_check(e, "hipGraphInstantiate");
+    }
+    hip_check(hipGraphLaunch(g->exec, c->stream), "hipGraphLaunch");
+}
+
 void run_forward(ge_ctx* c, double* gpu_seconds) {
     if (c->staged_tokens < 0) fail(GE_ERR_STATE, "no batch is staged");
     hip_check(hipEventRecord(c->ev_start, c->stream), "hipEventRecord");
     if (c->n_parts > 1 && !c->prof)
         encode_split(c);
+    else if (!c->prof && c->staged_tokens <= kGraphMaxTokens)
+        run_graph(c);
     else
         encode(c, nullptr);
     hip_check(hipEventRecord(c->ev_stop, c->stream), "hipEventRecord");

@@ -97,6 +97,13 @@ struct StopPoint {
 
 constexpr int kMaxParts = 4;  // streams a large batch is split over (measured 2, 3, 4: 5.93, 5.93, 5.85 ms at config 2)
 
+// A short pack's forward captured as a HIP graph, keyed by everything its launches' arguments
+// depend on (see run_graph); exec is null while the shape has been seen only once.
+struct ShortGraph {
+    int key[6] = {};
+    hipGraphExec_t exec = nullptr;
+};
+
 struct VisionState;
 // Frees the image tower's weights and workspace (vision.cpp).
 void free_vision(ge_ctx* c);
@@ -136,6 +143,9 @@ struct ge_ctx {
     std::vector<std::pair<std::string, ge::ProfStat>> prof_stats;
     std::vector<ge::PendingEvent> prof_pending;
     std::vector<hipEvent_t> event_pool;
+    // short packs replayed as HIP graphs (run_graph); dropped whenever the workspace or the
+    // model changes, since the graphs hold their addresses
+    std::vector<ge::ShortGraph> graphs;
     // the image tower, when one is uploaded (vision.cpp)
     ge::VisionState* vision = nullptr;
 };

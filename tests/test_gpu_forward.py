@@ -197,6 +197,29 @@ def test_short_texts_alone_match_larger_packs(c2_model, config2_batch):
             assert np.array_equal(got[i], want[i]), (lengths, i)
 
 
+def test_short_pack_graph_replays_match_eager(c2_model, config2_batch, c2_oracle):
+    """Packs of at most 64 tokens replay their forward as a HIP graph from the second run of a
+    shape on. Every replay, with other shapes and eager work queued between replays, must equal
+    the shape's first (eager) run bitwise; new ids in a known shape must give their own vectors."""
+    ctx = c2_model.context
+    a = [config2_batch[11][:9]]
+    b = [config2_batch[12][:20], config2_batch[13][:5]]
+    first_a, _ = ctx.forward(a)
+    first_b, _ = ctx.forward(b)
+    for i in range(4):
+        got, _ = ctx.forward(a)
+        assert np.array_equal(got, first_a), i
+        ctx.forward([config2_batch[14 + i][:300]])
+        got, _ = ctx.forward(b)
+        assert np.array_equal(got, first_b), i
+    a2 = [config2_batch[15][:9]]
+    replayed, _ = ctx.forward(a2)
+    packed, _ = ctx.forward([a2[0], config2_batch[16][:100]])
+    assert np.array_equal(replayed[0], packed[0])
+    want, _ = c2_oracle.forward(a2[0])
+    assert cosine(replayed[0], want) >= COSINE_BAR
+
+
 def test_embed_api_options(c2_model, config2_batch):
     texts = [t[: 20 + 37 * i] for i, t in enumerate(config2_batch[:10])]
     full = c2_model.embed(texts, ge.EmbedOptions(normalise=False))
