@@ -480,8 +480,22 @@ bool workspace_grows(const ge_ctx* c, int tokens, int seqs, int work, int work2,
            (m.any_v2 && (work2 > w.work2_cap || !w.work2 || vt_cols > w.vt_cap || !w.vt));
 }
 
+void ensure_workspace_impl(ge_ctx* c, int tokens, int seqs, int work, int work2, int vt_cols);
+
+// Grows the workspace for a batch. If an allocation fails, the whole workspace is freed before
+// the error propagates, so no capacity is ever recorded for a buffer that does not exist.
 void ensure_workspace(ge_ctx* c, int tokens, int seqs, int work, int work2, int vt_cols) {
-    if (workspace_grows(c, tokens, seqs, work, work2, vt_cols)) drop_graphs(c);
+    if (!workspace_grows(c, tokens, seqs, work, work2, vt_cols)) return;
+    drop_graphs(c);
+    try {
+        ensure_workspace_impl(c, tokens, seqs, work, work2, vt_cols);
+    } catch (...) {
+        free_workspace(c);
+        throw;
+    }
+}
+
+void ensure_workspace_impl(ge_ctx* c, int tokens, int seqs, int work, int work2, int vt_cols) {
     Workspace& w = c->ws;
     const DevModel& m = c->model;
     const int rows = (tokens + 63) / 64 * 64 + kRowSlack;

@@ -311,6 +311,8 @@ T* vws_alloc(size_t rows, size_t width, const char* what) {
     return static_cast<T*>(p);
 }
 
+void alloc_vision_workspace(VisionState& v, int r, int tr, int wc, int vc);
+
 void ensure_vision_workspace(ge_ctx* c, VisionState& v, int patches, int tokens, int work, int vt_cols) {
     const int rows = (patches + 63) / 64 * 64 + kRowSlack, tok_rows = (tokens + 63) / 64 * 64 + kRowSlack;
     const bool grow = rows > v.rows || tok_rows > v.tok_rows || work > v.work_cap || vt_cols > v.vt_cap;
@@ -319,11 +321,20 @@ void ensure_vision_workspace(ge_ctx* c, VisionState& v, int patches, int tokens,
     const int r = std::max(rows, v.rows), tr = std::max(tok_rows, v.tok_rows), wc = std::max(std::max(work, 1), v.work_cap);
     const int vc = (std::max(vt_cols, v.vt_cap + v.vt_cap / 2) + 63) / 64 * 64;
     free_vision_workspace(v);
-    const size_t D = size_t(v.hidden), HP = size_t(v.heads) * v.hp;
+    try {
+        alloc_vision_workspace(v, r, tr, wc, vc);
+    } catch (...) {
+        free_vision_workspace(v);  // no capacity is recorded for buffers that do not exist
+        throw;
+    }
     v.rows = r;
     v.tok_rows = tr;
     v.work_cap = wc;
     v.vt_cap = vc;
+}
+
+void alloc_vision_workspace(VisionState& v, int r, int tr, int wc, int vc) {
+    const size_t D = size_t(v.hidden), HP = size_t(v.heads) * v.hp;
     v.patches32 = vws_alloc<float>(r, v.area, "patches");
     v.patches16 = vws_alloc<uint16_t>(r, v.area, "patches");
     v.x = vws_alloc<float>(r, D, "x");
