@@ -152,6 +152,20 @@ hipError_t launch_v_transpose(hipStream_t s, const uint16_t* v, int T, int width
 // pooled[s] = mean of the sequence's rows of x [*][width].
 hipError_t launch_mean_pool(hipStream_t s, const float* x, const SeqRange* seqs, int n_seqs, int width, float* pooled);
 
+// ---- per-layer-input branch (ple.hip); widths a multiple of 4, at most 1024.
+// out[r] = rmsnorm(in[r] * mul * rscale[r / per_scale]) * w for rows of `width` (in may be out).
+hipError_t launch_ple_rmsnorm(hipStream_t s, const float* in, int rows, int width, float mul, const float* rscale,
+                              int per_scale, const float* w, float eps, float* out);
+// x16[r] = fp16(x[r] / s_r), rscale[r] = s_r: the power of two >= 1 that brings ||x[r]||_2 under 2^14.
+hipError_t launch_ple_input(hipStream_t s, const float* x, int T, int d, uint16_t* x16, float* rscale);
+// g = gelu_tanh(graw[r] * rscale[r]) * ple[r][layer] (ple fp32 [T][layers][pl]); g16 = fp16(g / s2_r),
+// rscale2[r] = s2_r, chosen as in launch_ple_input.
+hipError_t launch_ple_gate(hipStream_t s, const float* graw, const float* rscale, const float* ple, int layer, int layers,
+                           int T, int pl, uint16_t* g16, float* rscale2);
+// x = (x + rmsnorm(praw[r] * rscale2[r]) * w) * out_scale; if next_w: h = rmsnorm(x) * next_w (fp16).
+hipError_t launch_ple_residual_norm(hipStream_t s, float* x, const float* praw, const float* rscale2, const float* w,
+                                    float out_scale, const float* next_w, float eps, int T, int d, uint16_t* h);
+
 // ---- image tower row kernels (vision.hip); widths a multiple of 4, at most kVitMaxWidth.
 constexpr int kVitMaxWidth = 2048;
 // x = ((t + bias) + pos[px]) + pos[npos + py] (fp32 [T][d]), h = LayerNorm(x) * w + b (fp16).

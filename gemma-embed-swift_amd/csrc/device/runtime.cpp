@@ -209,6 +209,69 @@ Q8Dev upload_q8(ge_ctx* c, const HostQ8& h, const char* what, bool gemm_weight) 
     return d;
 }
 
+float half_bits_to_float(uint16_t b) { return float(__builtin_bit_cast(_Float16, b)); }
+
+// A [cols, rows] weight of any accepted type as fp16 MFMA fragments (Q8Dev::fh order) with the
+// columns zero-padded to cols_pad: values are rounded to fp16 once (Q8_0: fp16 of q * d, as the
+// device dequantisation does; F16 as stored; F32 and BF16 rounded to nearest even).
+Q8Dev upload_fragments(const ge_tensor_desc* t, int64_t cols, int64_t rows, int cols_pad, const void* base, size_t len,
+                       std::vector<void*>& allocs) {
+    check_shape(t, cols, rows);
+    if (rows % 32 || cols_pad % 32 || cols_pad < cols) fail(GE_ERR_MODEL, "tensor %s: shape does not tile", t->name);
+    const uint8_t* p = tensor_ptr(t, base, len);
+    std::vector<float> row(size_t(cols), 0.0f);
+    std::vector<uint16_t> dense(size_t(rows) * cols_pad, 0);
+    for (int64_t r = 0; r < rows; r++) {
+        switch (t->type) {
+        case GE_TYPE_F32: std::memcpy(row.data(), p + size_t(r) * cols * 4, size_t(cols) * 4); break;
+        case GE_TYPE_F16:
+            for (int64_t i = 0; i < cols; i++) {
+                uint16_t b;
+                std::memcpy(&b, p + (size_t(r) * cols + i) * 2, 2);
+                row[size_t(i)] = half_bits_to_float(b);
+            }
+            break;
+        case GE_TYPE_BF16:
+            for (int64_t i = 0; i < cols; i++) {
+                uint16_t b;
+                std::memcpy(&b, p + (size_t(r) * cols + i) * 2, 2);
+                const uint32_t bits = uint32_t(b) << 16;
+                std::memcpy(&row[size_t(i)], &bits, 4);
+            }
+            break;
+        case GE_TYPE_Q8_0: {
+            if (cols % 32) fail(GE_ERR_MODEL, "tensor %s: Q8_0 rows must be a multiple of 32 wide", t->name);
+            const uint8_t* rp = p + size_t(r) * (cols / 32) * 34;
+            for (int64_t b = 0; b < cols / 32; b++) {
+                const float sc = half_bits_to_float(uint16_t(rp[b * 34] | (rp[b * 34 + 1] << 8)));
+                for (int e = 0; e < 32; e++) row[size_t(b * 32 + e)] = sc * float(int8_t(rp[b * 34 + 2 + e]));
+            }
+            break;
+        }
+        default: fail(GE_ERR_MODEL, "tensor %s uses unsupported storage type %d", t->name, t->type);
+        }
+        for (int64_t i = 0; i < cols; i++)
+            dense[size_t(r) * cols_pad + i] = __builtin_bit_cast(uint16_t, _Float16(row[size_t(i)]));
+    }
+    // fragment order: 32-row block j, 16-wide k-step s: 512 halves, lane l's 8 halves are row
+    // 32 j + l % 32, columns 16 s + 8 (l / 32) + [0, 8)
+    const int KT = cols_pad / 16;
+    std::vector<uint16_t> fh(dense.size());
+    for (int64_t j = 0; j < rows / 32; j++)
+        for (int s = 0; s < KT; s++)
+            for (int l = 0; l < 64; l++)
+                for (int e = 0; e < 8; e++)
+                    fh[((size_t(j) * KT + s) * 64 + l) * 8 + e] =
+                        dense[size_t(32 * j + l % 32) * cols_pad + 16 * s + 8 * (l / 32) + e];
+    Q8Dev m;
+    m.rows = int(rows);
+    m.cols = cols_pad;
+    m.fh = static_cast<uint16_t*>(dev_alloc(fh.size() * 2, t->name));
+    allocs.push_back(m.fh);
+    hip_check(hipMemcpy(m.fh, fh.data(), fh.size() * 2, hipMemcpyHostToDevice), "hipMemcpy weights");
+    return m;
+}
+
 const uint8_t* q8_tensor(const ge_model_desc* d, const std::string& name, int64_t cols, int64_t rows, const void* base,
                          size_t len) {
     const ge_tensor_desc* t = find(d, name);
@@ -345,7 +408,7 @@ void free_workspace(ge_ctx* c) {
     drop_graphs(c);
     Workspace& w = c->ws;
     void* ps[] = {w.x, w.qkv, w.t, w.out, w.h, w.q, w.k, w.v, w.attn, w.act, w.tokens, w.positions, w.seqs, w.work, w.pooled,
-                  w.vt, w.vcol, w.work2};
+                  w.vt, w.vcol, w.work2, w.ple, w.ple_t, w.rs, w.rs2, w.x16, w.g16};
     for (void* p : ps)
         if (p) (void)hipFree(p);
     c->ws = Workspace{};
@@ -356,8 +419,8 @@ void upload(ge_ctx* c, const ge_model_desc* d, const void* base, size_t len) {
     if (!d || !base) fail(GE_ERR_INVALID, "null model descriptor or file base");
     if (d->layers <= 0 || d->hidden <= 0 || d->heads <= 0 || d->feed_forward <= 0 || d->out_dims <= 0 || d->vocab <= 0)
         fail(GE_ERR_MODEL, "model descriptor has a non-positive size");
-    if (d->per_layer_input > 0)
-        fail(GE_ERR_MODEL, "the per-layer-input branch (per_layer_model_proj) is not supported on the GPU path yet");
+    if (d->per_layer_input < 0 || d->per_layer_input % 64 || d->per_layer_input > 1024)
+        fail(GE_ERR_MODEL, "per-layer input width %d: the kernels need a multiple of 64 up to 1024", d->per_layer_input);
     if (d->hidden % 64 || d->hidden > 1024) fail(GE_ERR_MODEL, "hidden size %d: the kernels need a multiple of 64 up to 1024", d->hidden);
     if (d->feed_forward % 32) fail(GE_ERR_MODEL, "feed_forward_length %d is not a multiple of 32", d->feed_forward);
     if (d->out_dims % 64) fail(GE_ERR_MODEL, "embedding_length_out %d is not a multiple of 64", d->out_dims);
@@ -389,6 +452,12 @@ void upload(ge_ctx* c, const ge_model_desc* d, const void* base, size_t len) {
         m.output = upload_q8(c, h, "output");
     }
     m.out_norm = upload_f32(c, d, "output_norm.weight", D, base, len);
+    if (m.pl > 0) {
+        // per_layer_model_proj (BF16 in the reference's file) as fp16 fragments
+        m.pl_proj = upload_fragments(find(d, "per_layer_model_proj.weight"), D, int64_t(m.pl) * m.layers, D, base, len,
+                                     c->weight_allocs);
+        m.pl_norm = upload_f32(c, d, "per_layer_proj_norm.weight", m.pl, base, len);
+    }
     for (int i = 0; i < m.layers; i++) {
         DevLayer L;
         L.sliding = d->sliding[i] != 0;
@@ -446,13 +515,22 @@ void upload(ge_ctx* c, const ge_model_desc* d, const void* base, size_t len) {
         L.ffn_norm = upload_f32(c, d, b + "ffn_norm.weight", D, base, len);
         L.post_ffw = upload_f32(c, d, b + "post_ffw_norm.weight", D, base, len);
         L.rope = rope_table(c, hd, L.rope_base, m.max_tokens);
+        if (m.pl > 0) {
+            HostQ8 g = host_q8(m.pl, D);
+            repack_rows(q8_tensor(d, b + "inp_gate.weight", D, m.pl, base, len), m.pl, D, &g, 0);
+            L.inp_gate = upload_q8(c, g, "inp_gate");
+            HostQ8 pj = host_q8(D, m.pl);
+            repack_rows(q8_tensor(d, b + "proj.weight", m.pl, D, base, len), D, m.pl, &pj, 0);
+            L.proj = upload_q8(c, pj, "proj");
+            L.post_norm = upload_f32(c, d, b + "post_norm.weight", D, base, len);
+        }
         m.max_qd = std::max(m.max_qd, L.qd);
         m.max_kvd = std::max(m.max_kvd, L.kvd);
         m.max_kv_heads = std::max(m.max_kv_heads, L.kv_heads);
         L.attn_v2 = attention_v2_supported(L.head_dim, m.heads, L.kv_heads);
         L.qkv_gn = qkv_norm_rope_vt_supported(L.head_dim, m.heads, L.kv_heads);
         L.qkv_fused = L.qkv_gn && gemm_qkv_supported(L.head_dim, m.heads, L.kv_heads);
-        m.all_fused = m.all_fused && L.qkv_fused && L.attn_v2;
+        m.all_fused = m.all_fused && L.qkv_fused && L.attn_v2 && m.pl == 0;
         m.any_v2 = m.any_v2 || L.attn_v2;
         if (L.attn_v2 && m.heads / L.kv_heads > 3) m.items32_ok = false;
         m.max_qkv = std::max(m.max_qkv, L.qd + 2 * L.kvd);
@@ -518,6 +596,14 @@ void ensure_workspace_impl(ge_ctx* c, int tokens, int seqs, int work, int work2,
         w.tokens = ws_alloc<int32_t>(rows, 1, "tokens");
         w.positions = ws_alloc<int32_t>(rows, 1, "positions");
         w.vcol = ws_alloc<int32_t>(rows, 1, "vt columns");
+        if (m.pl > 0) {
+            w.ple = ws_alloc<float>(rows, size_t(m.layers) * m.pl, "per-layer inputs");
+            w.ple_t = ws_alloc<float>(rows, size_t(std::max(m.pl, m.hidden)), "per-layer projection");
+            w.rs = ws_alloc<float>(rows, 1, "row scales");
+            w.rs2 = ws_alloc<float>(rows, 1, "row scales");
+            w.x16 = ws_alloc<uint16_t>(rows, m.hidden, "scaled residual");
+            w.g16 = ws_alloc<uint16_t>(rows, m.pl, "per-layer gate");
+        }
         w.seqs = nullptr;
         w.work = nullptr;
         w.pooled = nullptr;
@@ -746,6 +832,15 @@ void encode(ge_ctx* c, StopPoint* sp) {
         return launch_embed_norm(s, m.tok_embd, w.tokens, T, m.emb_scale, m.layer[0].attn_norm, m.eps, w.x, w.h);
     });
     if (at(sp, "inp_scaled", -1) || at(sp, "attn_norm", 0)) return;
+    if (m.pl > 0) {
+        // CPUReference.swift:206-210: the per-layer inputs from the scaled embedding rows
+        launch(c, "ple_input", [&] { return launch_ple_input(s, w.x, T, D, w.x16, w.rs); });
+        launch(c, "gemm_ple_model_proj", [&] { return launch_gemm_q8(s, m.pl_proj, w.x16, T, w.ple, kEpiF32); });
+        launch(c, "ple_norm", [&] {
+            return launch_ple_rmsnorm(s, w.ple, T * m.layers, m.pl, m.pl_scale, w.rs, m.layers, m.pl_norm, m.eps, w.ple);
+        });
+        if (at(sp, "inp_per_layer", -1)) return;
+    }
     for (int l = 0; l < m.layers; l++) {
         const DevLayer& L = m.layer[size_t(l)];
         // The raw projection (trace points Qcur / Kcur / Vcur) only exists on the unfused path.
@@ -813,6 +908,24 @@ void encode(ge_ctx* c, StopPoint* sp) {
         launch(c, "gemm_down", [&] { return launch_gemm_q8(s, L.wd, w.act, T, t16, kEpiF16, L.down_scale * L.down_c); });
         if (at(sp, "ffn_out", l)) return;
         const float* next = l + 1 < m.layers ? m.layer[size_t(l) + 1].attn_norm : m.out_norm;
+        if (m.pl > 0) {
+            // CPUReference.swift:259-269: x += rmsnorm(proj(gelu(inp_gate(x)) * ple_l), post_norm), then
+            // the layer output scale; the unnormalised inputs of both projections go row-scaled
+            launch(c, "residual_norm", [&] {
+                return launch_residual_norm(s, w.x, t16, m.eps * L.down_c * L.down_c, L.post_ffw, 1.0f, nullptr, m.eps, T, D,
+                                            nullptr);
+            });
+            if (at(sp, "pe_in", l)) return;
+            launch(c, "ple_input", [&] { return launch_ple_input(s, w.x, T, D, w.x16, w.rs); });
+            launch(c, "gemm_ple_gate", [&] { return launch_gemm_q8(s, L.inp_gate, w.x16, T, w.ple_t, kEpiF32); });
+            launch(c, "ple_gate", [&] { return launch_ple_gate(s, w.ple_t, w.rs, w.ple, l, m.layers, T, m.pl, w.g16, w.rs2); });
+            launch(c, "gemm_ple_proj", [&] { return launch_gemm_q8(s, L.proj, w.g16, T, w.ple_t, kEpiF32); });
+            launch(c, "ple_residual_norm", [&] {
+                return launch_ple_residual_norm(s, w.x, w.ple_t, w.rs2, L.post_norm, L.out_scale, next, m.eps, T, D, w.h);
+            });
+            if (at(sp, "l_out", l) || at(sp, "attn_norm", l + 1)) return;
+            continue;
+        }
         launch(c, "residual_norm", [&] {
             return launch_residual_norm(s, w.x, t16, m.eps * L.down_c * L.down_c, L.post_ffw, L.out_scale, next, m.eps, T, D,
                                         w.h);
@@ -1056,6 +1169,8 @@ void trace(ge_ctx* c, const char* name, int layer, float* out, size_t cap, size_
         unscale = 1.0f / L->down_c;
     } else if (n == "result_embd") {
         buf = w.out; stride = width = m.out_dims;
+    } else if (n == "inp_per_layer" && m.pl > 0) {
+        buf = w.ple; stride = width = m.layers * m.pl;
     } else {
         fail(GE_ERR_INVALID, "unknown trace tensor %s", name);
     }
@@ -1063,7 +1178,8 @@ void trace(ge_ctx* c, const char* name, int layer, float* out, size_t cap, size_
     if (needed) *needed = count;
     if (!out) return;
     if (cap < count) fail(GE_ERR_INVALID, "trace buffer holds %zu floats, %s needs %zu", cap, name, count);
-    StopPoint sp{n, (n == "inp_scaled" || n == "result_norm" || n == "result_embd") ? -1 : layer, false};
+    StopPoint sp{n, (n == "inp_scaled" || n == "result_norm" || n == "result_embd" || n == "inp_per_layer") ? -1 : layer,
+                 false};
     encode(c, &sp);
     if (!sp.hit) fail(GE_ERR_INVALID, "tensor %s at layer %d is not produced by this forward", name, layer);
     copy_out(c, buf, f16, T, stride, col0, width, out);

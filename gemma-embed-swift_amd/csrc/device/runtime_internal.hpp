@@ -44,6 +44,8 @@ struct DevLayer {
     // 1 / act_scale. Both are powers of two, so the round trip is exact.
     float act_scale = 1, down_scale = 1;
     Q8Dev wqkv, wo, wgu, wd;  // wqkv rows: q | k | v; wgu rows: gate/up interleaved in 32-row groups
+    Q8Dev inp_gate, proj;     // per-layer-input branch (per_layer_input > 0)
+    float* post_norm = nullptr;
     float *attn_norm = nullptr, *q_norm = nullptr, *k_norm = nullptr, *post_attn = nullptr, *ffn_norm = nullptr,
           *post_ffw = nullptr;
     const float* rope = nullptr;
@@ -53,6 +55,8 @@ struct DevModel {
     int layers = 0, hidden = 0, heads = 0, ff = 0, out_dims = 0, pl = 0, vocab = 0, window = 0, max_tokens = 8192;
     float eps = 1e-6f, emb_scale = 1, pl_scale = 1;
     Q8Dev tok_embd, output;
+    Q8Dev pl_proj;  // per_layer_model_proj as fp16 fragments [layers * pl][hidden] (per_layer_input > 0)
+    float* pl_norm = nullptr;
     float* out_norm = nullptr;
     std::vector<DevLayer> layer;
     int max_qd = 0, max_kvd = 0, max_qkv = 0, max_kv_heads = 1;
@@ -77,6 +81,11 @@ struct Workspace {
     uint16_t* vt = nullptr;
     int32_t* vcol = nullptr;
     AttnWork* work2 = nullptr;
+    // per-layer-input branch: the per-layer inputs fp32 [T][layers][pl], row-scaled fp16 GEMM
+    // inputs (x16 [T][hidden], g16 [T][pl]) with their row scales, and an fp32 GEMM output
+    // [T][max(pl, hidden)]
+    float *ple = nullptr, *ple_t = nullptr, *rs = nullptr, *rs2 = nullptr;
+    uint16_t *x16 = nullptr, *g16 = nullptr;
 };
 
 struct ProfStat {
@@ -210,6 +219,11 @@ void repack_rows(const uint8_t* src, int rows, int cols, HostQ8* dst, int dst_ro
 HostQ8 host_q8(int rows, int cols);
 // Quant and scale planes, plus (for GEMM weights) the dequantised fragment-order copy.
 Q8Dev upload_q8(ge_ctx* c, const HostQ8& h, const char* what, bool gemm_weight = true);
+// A [cols, rows] weight tensor of any accepted type (F32, F16, BF16, Q8_0) as fp16 MFMA fragments
+// (Q8Dev::fh order only, no quant planes), columns zero-padded to cols_pad; the allocation is
+// appended to allocs.
+Q8Dev upload_fragments(const ge_tensor_desc* t, int64_t cols, int64_t rows, int cols_pad, const void* base, size_t len,
+                       std::vector<void*>& allocs);
 // max_j ||W_j||_2 of repacked Q8_0 rows.
 double max_row_norm(const HostQ8& h);
 // The power of two c <= 1 that brings `bound` under 2^15 (half of fp16's largest finite value).

@@ -118,68 +118,10 @@ HostQ8 q8_rows(const ge_vision_desc* d, const std::string& name, int64_t cols, i
     return h;
 }
 
-float half_bits_to_float(uint16_t b) { return float(__builtin_bit_cast(_Float16, b)); }
-
-// A [cols, rows] weight of any accepted type as fp16 MFMA fragments (Q8Dev::fh order) with the
-// columns zero-padded to cols_pad: values are rounded to fp16 once (Q8_0: fp16 of q * d, as the
-// device dequantisation does; F16 as stored; F32 and BF16 rounded to nearest even).
+// A [cols, rows] weight of any accepted type as fp16 MFMA fragments, columns zero-padded.
 Q8Dev fragments_any(VisionState& v, const ge_vision_desc* d, const std::string& name, int64_t cols, int64_t rows,
                     int cols_pad, const void* base, size_t len) {
-    const ge_tensor_desc* t = vfind(d, name);
-    check_shape(t, cols, rows);
-    if (rows % 32 || cols_pad % 32 || cols_pad < cols) fail(GE_ERR_MODEL, "tensor %s: shape does not tile", t->name);
-    const uint8_t* p = tensor_ptr(t, base, len);
-    std::vector<float> row(size_t(cols), 0.0f);
-    std::vector<uint16_t> dense(size_t(rows) * cols_pad, 0);
-    for (int64_t r = 0; r < rows; r++) {
-        switch (t->type) {
-        case GE_TYPE_F32: std::memcpy(row.data(), p + size_t(r) * cols * 4, size_t(cols) * 4); break;
-        case GE_TYPE_F16:
-            for (int64_t i = 0; i < cols; i++) {
-                uint16_t b;
-                std::memcpy(&b, p + (size_t(r) * cols + i) * 2, 2);
-                row[size_t(i)] = half_bits_to_float(b);
-            }
-            break;
-        case GE_TYPE_BF16:
-            for (int64_t i = 0; i < cols; i++) {
-                uint16_t b;
-                std::memcpy(&b, p + (size_t(r) * cols + i) * 2, 2);
-                const uint32_t bits = uint32_t(b) << 16;
-                std::memcpy(&row[size_t(i)], &bits, 4);
-            }
-            break;
-        case GE_TYPE_Q8_0: {
-            if (cols % 32) fail(GE_ERR_MODEL, "tensor %s: Q8_0 rows must be a multiple of 32 wide", t->name);
-            const uint8_t* rp = p + size_t(r) * (cols / 32) * 34;
-            for (int64_t b = 0; b < cols / 32; b++) {
-                const float sc = half_bits_to_float(uint16_t(rp[b * 34] | (rp[b * 34 + 1] << 8)));
-                for (int e = 0; e < 32; e++) row[size_t(b * 32 + e)] = sc * float(int8_t(rp[b * 34 + 2 + e]));
-            }
-            break;
-        }
-        default: fail(GE_ERR_MODEL, "tensor %s uses unsupported storage type %d", t->name, t->type);
-        }
-        for (int64_t i = 0; i < cols; i++)
-            dense[size_t(r) * cols_pad + i] = __builtin_bit_cast(uint16_t, _Float16(row[size_t(i)]));
-    }
-    // fragment order: 32-row block j, 16-wide k-step s: 512 halves, lane l's 8 halves are row
-    // 32 j + l % 32, columns 16 s + 8 (l / 32) + [0, 8)
-    const int KT = cols_pad / 16;
-    std::vector<uint16_t> fh(dense.size());
-    for (int64_t j = 0; j < rows / 32; j++)
-        for (int s = 0; s < KT; s++)
-            for (int l = 0; l < 64; l++)
-                for (int e = 0; e < 8; e++)
-                    fh[((size_t(j) * KT + s) * 64 + l) * 8 + e] =
-                        dense[size_t(32 * j + l % 32) * cols_pad + 16 * s + 8 * (l / 32) + e];
-    Q8Dev m;
-    m.rows = int(rows);
-    m.cols = cols_pad;
-    m.fh = static_cast<uint16_t*>(dev_alloc(fh.size() * 2, t->name));
-    v.weights.push_back(m.fh);
-    hip_check(hipMemcpy(m.fh, fh.data(), fh.size() * 2, hipMemcpyHostToDevice), "hipMemcpy weights");
-    return m;
+    return upload_fragments(vfind(d, name), cols, rows, cols_pad, base, len, v.weights);
 }
 
 Q8Dev upload_vision_q8(ge_ctx* c, VisionState& v, const HostQ8& h, const char* what) {

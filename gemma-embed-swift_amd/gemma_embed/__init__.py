@@ -225,6 +225,15 @@ CONFIG2 = dict(layers=24, hidden=768, heads=3, feed_forward=1152, out_dims=768, 
 TINY = dict(layers=2, hidden=128, heads=2, feed_forward=256, out_dims=128, per_layer_input=0, vocab=512,
             sliding_window=16, head_dim_swa=128, head_dim_global=128, kv_heads_swa=1, kv_heads_global=1,
             eps=1e-6, rope_base=1e6, rope_base_swa=1e4, pattern=[1, 0], seed=7)
+# The same with the per-layer-input branch (64-wide per-layer inputs).
+TINY_PLE = dict(TINY, per_layer_input=64, heads=2, kv_heads_swa=1, kv_heads_global=1, seed=9)
+# The reference's real architecture (Model/Architecture.md:7-9, Fixtures/model.json): d 512, 4 query
+# heads, sliding layers of 2 KV heads of 256 (window 1024, RoPE 1e4), global layers 5, 11, 17, 23 of
+# 1 KV head of 512 (RoPE 1e6), GeGLU 2048, per-layer inputs of 512, output 768; synthetic weights.
+REAL_SHAPES = dict(layers=24, hidden=512, heads=4, feed_forward=2048, out_dims=768, per_layer_input=512,
+                   vocab=262144, sliding_window=1024, head_dim_swa=256, head_dim_global=512, kv_heads_swa=2,
+                   kv_heads_global=1, eps=1e-6, rope_base=1e6, rope_base_swa=1e4,
+                   pattern=[1, 1, 1, 1, 1, 0] * 4, seed=12)
 
 
 def synth_write_gguf(path: str, **spec) -> str:

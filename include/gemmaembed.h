@@ -104,7 +104,8 @@ int ge_forward(ge_ctx* ctx, const int32_t* tokens, const int32_t* positions, int
  * tensor at `layer` (-1 for inp_scaled, result_norm, result_embd) and copies it out as fp32
  * [n_tokens][width]. Names: inp_scaled, attn_norm, Qcur, Kcur, Vcur, Qcur_pos, Kcur_pos,
  * Vcur_normed, kqv_out, attn_out, ffn_norm, ffn_geglu, ffn_out, pe_in, l_out, result_norm,
- * result_embd, and with the per-layer-input branch inp_per_layer and per_layer_embd_out.
+ * result_embd, and with the per-layer-input branch inp_per_layer (pe_in is then the residual
+ * before the branch, l_out after it; the reference's per_layer_embd_out is not kept on the GPU).
  * `out_count` is the capacity of `out` in floats; the needed count is written to *needed. */
 int ge_forward_trace(ge_ctx* ctx, const int32_t* tokens, const int32_t* positions, int32_t n_tokens,
                      const ge_seq* seqs, int32_t n_seqs, const char* tensor_name, int32_t layer, float* out,

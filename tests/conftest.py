@@ -43,3 +43,15 @@ def tiny_vision_gguf(model_dir):
 def config5_vision_gguf(model_dir):
     import gemma_embed as ge
     return ge.synth_write_vision_gguf(os.path.join(model_dir, "config5_vision.gguf"), **ge.CONFIG5_VISION)
+
+
+@pytest.fixture(scope="session")
+def tiny_ple_gguf(model_dir):
+    import gemma_embed as ge
+    return ge.synth_write_gguf(os.path.join(model_dir, "tiny_ple.gguf"), **ge.TINY_PLE)
+
+
+@pytest.fixture(scope="session")
+def real_shapes_gguf(model_dir):
+    import gemma_embed as ge
+    return ge.synth_write_gguf(os.path.join(model_dir, "real_shapes.gguf"), **ge.REAL_SHAPES)

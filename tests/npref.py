@@ -167,6 +167,7 @@ def forward(g: Gguf, tokens: np.ndarray, keep: Tuple = ()) -> Tuple[np.ndarray, 
         pl = m[a + "embedding_length_per_layer_input"]
         per = x @ g.tensor("per_layer_model_proj.weight").T / np.sqrt(d)
         per = rmsnorm(per.reshape(T, L, pl), g.tensor("per_layer_proj_norm.weight"), eps)
+        tr("inp_per_layer", -1, per)
     for l in range(L):
         b = f"blk.{l}."
         sw = bool(pattern[l])
@@ -193,10 +194,12 @@ def forward(g: Gguf, tokens: np.ndarray, keep: Tuple = ()) -> Tuple[np.ndarray, 
         act = gelu_tanh(f @ g.tensor(b + "ffn_gate.weight").T) * (f @ g.tensor(b + "ffn_up.weight").T)
         tr("ffn_geglu", l, act)
         x = x + rmsnorm(act @ g.tensor(b + "ffn_down.weight").T, g.tensor(b + "post_ffw_norm.weight"), eps)
+        tr("pe_in", l, x)
         scale = float(g.tensor(b + "layer_output_scale.weight")[0]) if b + "layer_output_scale.weight" in g.tensors else 1.0
         if ple:
             gg = gelu_tanh(x @ g.tensor(b + "inp_gate.weight").T) * per[:, l, :]
             p = rmsnorm(gg @ g.tensor(b + "proj.weight").T, g.tensor(b + "post_norm.weight"), eps)
+            tr("per_layer_embd_out", l, p)
             x = (x + p) * scale
         else:
             x = x * scale

@@ -342,3 +342,62 @@ def test_rejects_bad_batches(c2_model):
         ctx.forward([[]])
     with pytest.raises(ge.GemmaEmbedError):
         ctx.forward([list(range(2, 8200))])  # longer than the 8192-token context
+
+
+def _split(a, lengths):
+    out, r = [], 0
+    for n in lengths:
+        out.append(a[r:r + n])
+        r += n
+    return out
+
+
+def test_per_layer_inputs_every_trace_vs_oracle(tiny_ple_gguf):
+    """The per-layer-input branch (CPUReference.swift:206-210, :259-269) on the GPU: the per-layer
+    inputs, the residual before and after the branch, and the pooled vectors."""
+    m = ge.EmbeddingModel.load(tiny_ple_gguf)
+    try:
+        seqs = [ge.synth_tokens(s, 2, 512, n).tolist() for s, n in ((31, 40), (32, 7), (33, 64), (34, 100))]
+        lengths = [len(x) for x in seqs]
+        pooled = m.embed_tokens(seqs)
+        names = [("inp_per_layer", -1)] + [(n, l) for l in range(2) for n in ("pe_in", "l_out")] + [("attn_norm", 1)]
+        with ora.OracleModel(tiny_ple_gguf) as o:
+            want = [o.forward(sq, keep=names) for sq in seqs]
+            for i in range(len(seqs)):
+                assert cosine(pooled[i], want[i][0]) >= COSINE_BAR, i
+            for name, layer in names:
+                got = m.context.trace(seqs, name, layer)
+                for i, part in enumerate(_split(got, lengths)):
+                    assert max_rel(part, want[i][1][(name, layer)].reshape(part.shape)) <= PER_LAYER_TOL, (name, layer, i)
+        # a short text alone (the graph-replayed short path) has the bits it has inside the pack
+        for _ in range(3):
+            alone, _ = m.context.forward([seqs[1]])
+            assert np.array_equal(alone[0], pooled[1])
+    finally:
+        m.close()
+
+
+@pytest.mark.timeout(300)
+def test_reference_real_architecture_vs_oracle(real_shapes_gguf):
+    """The reference's real architecture at its real shapes (Model/Architecture.md:7-9): d 512,
+    4 query heads, sliding layers with 2 KV heads of 256 and window 1024, global layers with 1 KV
+    head of 512, GeGLU 2048, per-layer inputs of 512; synthetic weights."""
+    m = ge.EmbeddingModel.load(real_shapes_gguf)
+    try:
+        seqs = [ge.synth_tokens(s, 2, 262144, n).tolist() for s, n in ((41, 9), (42, 300), (43, 1500))]
+        lengths = [len(x) for x in seqs]
+        pooled = m.embed_tokens(seqs)
+        layers = (0, 5, 11, 23)
+        keep = [("l_out", l) for l in layers]
+        with ora.OracleModel(real_shapes_gguf) as o:
+            want = [o.forward(sq, keep=keep) for sq in seqs]
+        for i in range(len(seqs)):
+            c = cosine(pooled[i], want[i][0])
+            print(f"real shapes: text {i} ({lengths[i]} tokens) cosine {c:.8f}", flush=True)
+            assert c >= COSINE_BAR, i
+        for l in layers:
+            got = m.context.trace(seqs, "l_out", l)
+            for i, part in enumerate(_split(got, lengths)):
+                assert max_rel(part, want[i][1][("l_out", l)].reshape(part.shape)) <= PER_LAYER_TOL, (l, i)
+    finally:
+        m.close()

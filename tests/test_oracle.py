@@ -236,6 +236,26 @@ def test_forward_config2_vs_float64(config2_gguf):
     assert cos > 0.9999999
 
 
+def test_forward_per_layer_inputs_vs_float64(tiny_ple_gguf):
+    """The per-layer-input branch (CPUReference.swift:206-210, :259-269) against float64."""
+    import gemma_embed as ge
+    g = npref.Gguf(tiny_ple_gguf)
+    keep = [(n, l) for n in ("pe_in", "l_out", "per_layer_embd_out") for l in range(2)] + \
+           [("inp_per_layer", -1), ("result_embd", -1)]
+    with ora.OracleModel(tiny_ple_gguf) as m:
+        for seed, T in ((21, 40), (22, 3), (23, 64)):
+            toks = ge.synth_tokens(seed, 2, m.vocab, T)
+            pooled, tr = m.forward(toks, keep=keep)
+            want, wtr = npref.forward(g, toks, keep=tuple(keep))
+            assert np.abs(pooled - want).max() < 2e-4 * np.abs(want).max(), seed
+            for key in keep:
+                a, b = tr[key], wtr[key]
+                assert a.shape == b.shape, key
+                assert np.abs(a - b).max() < 2e-4 * np.abs(b).max(), (seed, key)
+            # the branch changes the result: without it the layer outputs differ
+            assert not np.allclose(tr[("pe_in", 1)], tr[("l_out", 1)])
+
+
 def test_forward_rejects_bad_tokens(tiny_gguf):
     with ora.OracleModel(tiny_gguf) as m:
         with pytest.raises(ValueError):
