@@ -15,7 +15,10 @@ Also reported on the same JSON line:
                 restaged each time; the full host API path at the reference's default options
                 (token ids in host memory -> normalised vectors, PCIe included); BASELINE
                 config 4 (4 texts x 8192 tokens, one resident pack); and BASELINE config 5 (the
-                16-layer image tower over 8 resident 768 x 768 images);
+                16-layer image tower over 8 resident 768 x 768 images); and the reference's own
+                architecture at its real shapes on the shapes of its published benchmarks, through
+                the host API, beside the reference's published M3 Max times (context only: a
+                different chip and real weights);
   cpu_baseline  the CPU oracle (a C restatement of the reference's CPUReference.swift) on a
                 bounded sample of the same workload, on this host's cores.
 """
@@ -142,6 +145,43 @@ def vision_variant(tmp: str, reps: int):
             "gemm_tflops": round(gemm / (gemm_ms * 1e-3) / 1e12, 1) if gemm_ms else None,
             "attention_tflops": round(attn / (attn_ms * 1e-3) / 1e12, 1) if attn_ms else None,
             "algorithmic_flops": gemm + attn, "kernels": kernels}
+
+
+def reference_shapes_variant(tmp: str, reps: int):
+    """The reference's own architecture at its real shapes (d 512, per-layer inputs; synthetic
+    weights) on the shapes of its published benchmarks (an 8 x 1024-token pack in
+    0.4078 s median, a 1 x 64-token call in 6.18 ms, on an Apple M3 Max with the real model),
+    through the host API: token ids in host memory -> normalised vectors, the reference's own
+    boundary (COMPARISON.md:57-60)."""
+    import numpy as np
+    import gemma_embed as ge
+    path = os.path.join(tmp, "real_shapes.gguf")
+    ge.synth_write_gguf(path, **ge.REAL_SHAPES)
+    model = ge.EmbeddingModel.load(path)
+    try:
+        opts = ge.EmbedOptions()
+        pack = [r.tolist() for r in ge.synth_tokens(81, 2, 262144, 8 * 1024).reshape(8, 1024)]
+        one = [ge.synth_tokens(82, 2, 262144, 64).tolist()]
+        for _ in range(2):
+            model.embed(pack, opts)
+            model.embed(one, opts)
+        t0 = time.perf_counter()
+        for _ in range(reps):
+            out = model.embed(pack, opts)
+        pack_s = (time.perf_counter() - t0) / reps
+        t0 = time.perf_counter()
+        for _ in range(reps * 4):
+            model.embed(one, opts)
+        one_s = (time.perf_counter() - t0) / (reps * 4)
+        if not all(np.all(np.isfinite(e.vector)) for e in out):
+            raise SystemExit("non-finite output (reference shapes)")
+    finally:
+        model.close()
+    return {"model": "reference architecture at its real shapes: d 512, 4 heads, KV 2x256 sliding / 1x512 global, "
+                     "GeGLU 2048, per-layer inputs 512, 24 layers; synthetic Q8_0 weights",
+            "pack_8x1024_s": round(pack_s, 5), "pack_8x1024_tokens_per_s": round(8 * 1024 / pack_s, 1),
+            "reference_m3max_pack_8x1024_s": 0.4078,
+            "call_1x64_ms": round(one_s * 1e3, 3), "reference_m3max_call_1x64_ms": 6.18}
 
 
 def measured_traffic(label: str):
@@ -386,6 +426,9 @@ def main():
     log(f"config 4 (4 x 8192): {long_ms:.2f} ms/step, {long_rate:,.0f} tok/s")
 
     vision = vision_variant(tmp, max(3, args.steps // 2))
+    ref_shapes = reference_shapes_variant(tmp, max(3, args.steps // 4))
+    log(f"reference shapes: 8 x 1024 in {ref_shapes['pack_8x1024_s'] * 1e3:.2f} ms "
+        f"({ref_shapes['pack_8x1024_tokens_per_s']:,.0f} tok/s), 1 x 64 call {ref_shapes['call_1x64_ms']:.2f} ms")
     log(f"config 5 (8 images): {vision['ms_per_batch']:.2f} ms/batch, {vision['images_per_s']:.1f} images/s, "
         f"{vision['tflops']} TFLOP/s")
 
@@ -421,7 +464,8 @@ def main():
                      "embed_api_default_options_pcie_inclusive_tokens_per_s": round(api_rate, 1),
                      "config4_4x8192": {"tokens_per_s": round(long_rate, 1), "ms_per_step": round(long_ms, 3),
                                         "tflops": round(long_flops / (long_ms * 1e-3) / 1e12, 1)},
-                     "config5_vision_8_images": vision},
+                     "config5_vision_8_images": vision,
+                     "reference_shapes_host_api": ref_shapes},
     }
     model.close()
     if not args.no_cpu:

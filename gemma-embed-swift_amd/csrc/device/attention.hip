@@ -563,7 +563,9 @@ __global__ __launch_bounds__(QW * G * 64) void attention_v3_kernel(const uint16_
     const int widx = bx < full ? (bx % 8) * (full / 8) + bx / 8 : bx;
     const int seq_start = __builtin_amdgcn_readfirstlane(int(work[widx].seq_start));
     const int len = __builtin_amdgcn_readfirstlane(int(work[widx].seq_len));
-    const int wq0 = __builtin_amdgcn_readfirstlane(int(work[widx].q0));
+    // grid z splits a work item into parts of QB queries (head dim 512: 32-query workgroups over
+    // 64-query items)
+    const int wq0 = __builtin_amdgcn_readfirstlane(int(work[widx].q0)) + int(blockIdx.z) * QB;
     const int vt_start = __builtin_amdgcn_readfirstlane(int(work[widx].vt_start));
     const int kvh = blockIdx.y;
     const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(int(threadIdx.x >> 6));
@@ -776,6 +778,7 @@ static hipError_t attention_v2_dispatch_g(hipStream_t s, const uint16_t* q, cons
 }
 
 bool attention_v2_supported(int hd, int H, int KV) {
+    if (hd == 512) return KV > 0 && H == 4 * KV;  // attention_v3_kernel<512, 4, 2>
     if (!((hd == 128 || hd == 256) && KV > 0 && H % KV == 0 && H / KV >= 1 && H / KV <= 4)) return false;
     const int G = H / KV;
     return 2 * G * 32 * hd * 2 + 2 * (2 * attn2::BKV * hd * 2) <= 160 * 1024;  // LDS of one workgroup
@@ -785,9 +788,17 @@ hipError_t launch_attention_v2(hipStream_t s, const uint16_t* q, const uint16_t*
                                uint16_t* o, const AttnWork* work, int n_work, int H, int KV, int hd, int half_window,
                                float scale, int item_queries) {
     if (n_work < 0 || !attention_v2_supported(hd, H, KV) || half_window < 0 || vt_cols <= 0 || vt_cols % 8 ||
-        (item_queries != 64 && !(item_queries == 32 && H / KV <= 3)))
+        (item_queries != 64 && !(item_queries == 32 && (H / KV <= 3 || hd == 512))))
         return hipErrorInvalidValue;
     if (n_work == 0) return hipSuccess;
+    if (hd == 512) {
+        // 8 waves (4 query heads x 2 query tiles) of 252 registers, K/V blocks of 64 KB in LDS: a
+        // workgroup takes 32 queries, grid z the halves of a 64-query item
+        const float scale_log2 = scale * 1.4426950408889634f;
+        launch_kernel(attention_v3_kernel<512, 4, 2>, dim3(n_work, KV, item_queries / 32), dim3(8 * 64),
+                      uint32_t(attention_v3_lds_bytes<512>()), s, q, k, vt, o, work, H, KV, vt_cols, half_window, scale_log2);
+        return hipGetLastError();
+    }
     if (hd == 128)
         return attention_v2_dispatch_g<128>(s, q, k, vt, vt_cols, o, work, n_work, H, KV, half_window, scale, item_queries);
     return attention_v2_dispatch_g<256>(s, q, k, vt, vt_cols, o, work, n_work, H, KV, half_window, scale, item_queries);
@@ -1081,6 +1092,9 @@ hipError_t configure_kernels() {
     if (e == hipSuccess) e = attention_v3_configure<256, 1>();
     if (e == hipSuccess) e = attention_v3_configure<256, 2>();
     if (e == hipSuccess) e = attention_v3_configure<256, 3>();
+    if (e == hipSuccess)
+        e = hipFuncSetAttribute(reinterpret_cast<const void*>(&attention_v3_kernel<512, 4, 2>),
+                                hipFuncAttributeMaxDynamicSharedMemorySize, attention_v3_lds_bytes<512>());
     if (e == hipSuccess) e = attention_configure_all<256, 256>();
     if (e == hipSuccess) e = attention_configure_all<512, 256>();
     return e;

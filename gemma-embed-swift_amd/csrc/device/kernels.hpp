@@ -125,8 +125,8 @@ hipError_t launch_qkv_norm_rope_vt(hipStream_t s, const uint16_t* qkv16, int T, 
 hipError_t launch_attention(hipStream_t s, const uint16_t* q, const uint16_t* k, const uint16_t* v, uint16_t* o,
                             const AttnWork* work, int n_work, int H, int KV, int hd, int half_window, float scale);
 
-// Attention with K/V copied straight into LDS (head dims 128 and 256, at most 4 query heads per
-// KV head): work items of item_queries query rows (kAttnQueriesV2, or 32 for up to 3 query heads
+// Attention with K/V copied straight into LDS (head dims 128 and 256 with at most 4 query heads
+// per KV head, and head dim 512 with exactly 4): work items of item_queries query rows (kAttnQueriesV2, or 32 for up to 3 query heads
 // per KV head: twice the workgroups for a small batch; a query's result is the same either way);
 // V given transposed, vt [KV * hd][vt_cols], each sequence's keys starting at its work items'
 // vt_start.

@@ -529,7 +529,10 @@ void upload(ge_ctx* c, const ge_model_desc* d, const void* base, size_t len) {
         m.max_kv_heads = std::max(m.max_kv_heads, L.kv_heads);
         L.attn_v2 = attention_v2_supported(L.head_dim, m.heads, L.kv_heads);
         L.qkv_gn = qkv_norm_rope_vt_supported(L.head_dim, m.heads, L.kv_heads);
-        L.qkv_fused = L.qkv_gn && gemm_qkv_supported(L.head_dim, m.heads, L.kv_heads);
+        // The fused epilogue stages one 128 x 256 tile in the GEMM's own LDS, so it also takes
+        // layouts the separate kernel's V^T staging cannot hold (2 KV heads of 256); a trace of the
+        // raw projection of such a layer runs the fp32 path.
+        L.qkv_fused = gemm_qkv_supported(L.head_dim, m.heads, L.kv_heads);
         m.all_fused = m.all_fused && L.qkv_fused && L.attn_v2 && m.pl == 0;
         m.any_v2 = m.any_v2 || L.attn_v2;
         if (L.attn_v2 && m.heads / L.kv_heads > 3) m.items32_ok = false;
@@ -881,8 +884,9 @@ void encode(ge_ctx* c, StopPoint* sp) {
                                            w.positions, L.rope, w.q, w.k, w.v);
             });
         }
-        // The fused kernels also write V^T for the LDS-copy attention.
-        const bool fused_vt = L.qkv_gn;
+        // The fused kernels also write V^T for the LDS-copy attention: the QKV GEMM's epilogue, or
+        // the fp16 path's norm kernel.
+        const bool fused_vt = (L.qkv_fused && !raw_qkv) || L.qkv_gn;
         if (at(sp, "Qcur_pos", l) || at(sp, "Kcur_pos", l) || at(sp, "Vcur_normed", l)) return;
         const int hw = L.sliding ? m.window / 2 : 0;  // halfWindow = slidingWindow / 2 (MetalForward.swift:399)
         if (L.attn_v2) {
