@@ -17,6 +17,11 @@
 //   ge_probe vision [reps]    BASELINE config 5: the synthetic 16-layer image tower (written to a
 //                             temporary GGUF) over 8 resident images of 48 x 48 patches
 //                             (ge_vision_run), the time per batch
+//   ge_probe reference_shapes [reps]
+//                             the reference's own architecture at its real shapes (d 512, 4 query
+//                             heads, KV 2 x 256 sliding / 1 x 512 global, GeGLU 2048, per-layer
+//                             inputs 512, 24 layers; synthetic weights): a resident 8 x 1024-token
+//                             pack and a 1 x 64-token pack (ge_batch_run), the time per forward
 //   ge_probe calibrate        fp16 -> fp32 conversion of 2^28 values (reads 512 MiB, writes 1 GiB):
 //                             the known-size kernel that scales the HBM byte counters
 //
@@ -218,6 +223,53 @@ int probe_vision(ge_ctx* c, int reps) {
     return 0;
 }
 
+int probe_reference_shapes(int reps) {
+    uint8_t pattern[24];
+    for (int i = 0; i < 24; i++) pattern[i] = (i % 6 == 5) ? 0 : 1;
+    ge_synth_spec spec{};
+    spec.layers = 24, spec.hidden = 512, spec.heads = 4, spec.feed_forward = 2048, spec.out_dims = 768;
+    spec.per_layer_input = 512, spec.vocab = 262144, spec.sliding_window = 1024;
+    spec.head_dim_swa = 256, spec.head_dim_global = 512, spec.kv_heads_swa = 2, spec.kv_heads_global = 1;
+    spec.eps = 1e-6f, spec.rope_base = 1e6f, spec.rope_base_swa = 1e4f, spec.pattern = pattern, spec.seed = 12;
+    char err[512] = {0};
+    const char* path = "/tmp/ge_probe_reference_shapes.gguf";
+    if (ge_synth_write_gguf(path, &spec, err, sizeof err) != 0) {
+        std::fprintf(stderr, "ge_probe: synth: %s\n", err);
+        return 1;
+    }
+    ge_load_options lo{0, 8192, 1};
+    ge_model* m = nullptr;
+    if (ge_model_load(path, &lo, &m, err, sizeof err) != 0) {
+        std::fprintf(stderr, "ge_probe: load: %s\n", err);
+        return 1;
+    }
+    std::remove(path);
+    ge_ctx* c = ge_model_context(m);
+    const int shapes[2][2] = {{8, 1024}, {1, 64}};
+    for (const auto& shape : shapes) {
+        const int texts = shape[0], len = shape[1];
+        std::vector<int32_t> ids(size_t(texts) * len), pos(ids.size());
+        std::vector<ge_seq> seqs(static_cast<size_t>(texts));
+        ge_synth_tokens(3, 2, 262144, int32_t(ids.size()), ids.data());
+        for (int t = 0; t < texts; t++) {
+            seqs[size_t(t)] = ge_seq{uint32_t(t * len), uint32_t(len)};
+            for (int i = 0; i < len; i++) pos[size_t(t) * len + i] = i;
+        }
+        if (ge_batch_stage(c, ids.data(), pos.data(), int32_t(ids.size()), seqs.data(), texts) != 0) return fail(c, "stage");
+        for (int r = 0; r < 3; r++) ge_batch_run(c);
+        ge_sync(c);
+        const auto t0 = std::chrono::steady_clock::now();
+        for (int r = 0; r < reps; r++) ge_batch_run(c);
+        ge_sync(c);
+        const double ms = std::chrono::duration<double, std::milli>(std::chrono::steady_clock::now() - t0).count() / reps;
+        std::printf("reference shapes, %d x %d tokens: %.3f ms per resident forward, %.0f tokens/s\n", texts, len, ms,
+                    texts * len / (ms * 1e-3));
+        std::fflush(stdout);
+    }
+    ge_model_free(m);
+    return 0;
+}
+
 int probe_calibrate(ge_ctx* c) {
     const size_t n = size_t(1) << 28;
     void* src = ge_dev_alloc(c, 2 * n);
@@ -237,9 +289,10 @@ int main(int argc, char** argv) {
     const char* what = argc > 1 ? argv[1] : "gate_up";
     const int reps = argc > 2 ? std::atoi(argv[2]) : 20;
     if (std::strcmp(what, "embed") == 0) return reps < 1 || reps > 10000 ? 2 : probe_embed(reps);
+    if (std::strcmp(what, "reference_shapes") == 0) return reps < 1 || reps > 10000 ? 2 : probe_reference_shapes(reps);
     if (std::strcmp(what, "gate_up") != 0 && std::strcmp(what, "attention") != 0 && std::strcmp(what, "calibrate") != 0 &&
         std::strcmp(what, "vision") != 0) {
-        std::fprintf(stderr, "usage: ge_probe gate_up|attention|embed|vision [reps] | ge_probe calibrate\n");
+        std::fprintf(stderr, "usage: ge_probe gate_up|attention|embed|vision|reference_shapes [reps] | ge_probe calibrate\n");
         return 2;
     }
     if (reps < 1 || reps > 10000) {
