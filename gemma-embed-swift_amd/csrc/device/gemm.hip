@@ -283,16 +283,14 @@ __global__ __launch_bounds__(C::NT) void gemm_kernel(const uint16_t* __restrict_
 // order of the k-steps are those of the tiled kernel, so every output has the same bits there
 // and here, whichever the batch size selects. TR: the transposed accumulation of the QKV kernel,
 // stored as its fp16 staging (acc * out_scale, row-major [M][N]) for the separate row pass.
-// k-steps in flight per wave (a short batch's GEMM is bound by the latency of its weight reads:
-// few waves, each streaming 32 or 64 weight rows); K must be a multiple of 16 times this
-template <int NJ>
-constexpr int skinny_steps() { return NJ == 1 ? 24 : 12; }
-
-template <int EPI, bool TR, int NJ>
+// SK: k-steps in flight per wave (a short batch's GEMM is bound by the latency of its weight reads:
+// few waves, each streaming 32 or 64 weight rows): the largest of 24, 16, 8 (12, 8, 4 for the
+// GeGLU pairs) that divides K / 16. It sets only how far the loads run ahead, not the order of
+// the MFMAs, so it does not change a bit of the result.
+template <int EPI, bool TR, int NJ, int SK>
 __global__ __launch_bounds__(256) void gemm_skinny_kernel(const uint16_t* __restrict__ X,
                                                           const uint16_t* __restrict__ Fh, void* __restrict__ Y,
                                                           int M, int N, int K, float out_scale, GemmEpiArgs ea) {
-    constexpr int SK = skinny_steps<NJ>();
     const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(int(threadIdx.x >> 6));
     const int groups = N / (32 * NJ), items = (M + 31) / 32 * groups;
     const int item = blockIdx.x * 4 + wave;
@@ -664,14 +662,22 @@ template <int EPI, bool TR, int NJ>
 hipError_t gemm_skinny_launch(hipStream_t s, const Q8Dev& w, const uint16_t* x, int M, void* y, float out_scale,
                               const GemmEpiArgs& ea = GemmEpiArgs{}) {
     const int items = (M + 31) / 32 * (w.rows / (32 * NJ));
-    launch_kernel(gemm_skinny_kernel<EPI, TR, NJ>, dim3((items + 3) / 4), dim3(256), 0, s, x, w.fh, y, M, w.rows, w.cols,
-                  out_scale, ea);
+    const dim3 grid((items + 3) / 4), block(256);
+    const int KT = w.cols / 16;
+    constexpr int S0 = NJ == 1 ? 24 : 12, S1 = NJ == 1 ? 16 : 8, S2 = NJ == 1 ? 8 : 4;
+    if (KT % S0 == 0)
+        launch_kernel(gemm_skinny_kernel<EPI, TR, NJ, S0>, grid, block, 0, s, x, w.fh, y, M, w.rows, w.cols, out_scale, ea);
+    else if (KT % S1 == 0)
+        launch_kernel(gemm_skinny_kernel<EPI, TR, NJ, S1>, grid, block, 0, s, x, w.fh, y, M, w.rows, w.cols, out_scale, ea);
+    else if (KT % S2 == 0)
+        launch_kernel(gemm_skinny_kernel<EPI, TR, NJ, S2>, grid, block, 0, s, x, w.fh, y, M, w.rows, w.cols, out_scale, ea);
+    else
+        return hipErrorInvalidValue;
     return hipGetLastError();
 }
 
-bool skinny_ok(const Q8Dev& w, int M) {
-    return M <= kSkinnyMaxRows && w.cols % (16 * skinny_steps<1>()) == 0 && w.cols % (16 * skinny_steps<2>()) == 0;
-}
+// K / 16 must be a multiple of 8 (of 4 would do for the GeGLU pairs).
+bool skinny_ok(const Q8Dev& w, int M) { return M <= kSkinnyMaxRows && w.cols % 128 == 0; }
 
 hipError_t launch_gemm_q8(hipStream_t s, const Q8Dev& w, const uint16_t* x, int M, void* y, GemmEpilogue epi,
                           float out_scale, const GemmEpiArgs* eap) {

@@ -60,7 +60,7 @@ struct GemmEpiArgs {
 // K of 32. kEpiGeglu expects W's rows
 // interleaved in 32-row gate/up groups and writes fp16 act[M][N / 2] = gelu_tanh(gate) * up *
 // out_scale. out_scale is a power of two wherever the forward uses it, so it is exact.
-// Batches of at most kSkinnyMaxRows rows (and K a multiple of 384) run on the skinny kernel,
+// Batches of at most kSkinnyMaxRows rows (and K a multiple of 128) run on the skinny kernel,
 // one wave per 32-row block; the results are bitwise those of the tiled kernel.
 constexpr int kSkinnyMaxRows = 64;
 // kEpiGeluBias and kEpiHeads take their operands from ea (y is then unused by kEpiHeads).

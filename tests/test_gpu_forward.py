@@ -395,6 +395,11 @@ def test_reference_real_architecture_vs_oracle(real_shapes_gguf):
             c = cosine(pooled[i], want[i][0])
             print(f"real shapes: text {i} ({lengths[i]} tokens) cosine {c:.8f}", flush=True)
             assert c >= COSINE_BAR, i
+        # the 9-token text alone runs the short-batch kernels (K of 512, 1024 and 2048: 8 or 16
+        # k-steps in flight) and must have the bits it has inside the pack
+        for _ in range(3):
+            alone, _ = m.context.forward([seqs[0]])
+            assert np.array_equal(alone[0], pooled[0])
         for l in layers:
             got = m.context.trace(seqs, "l_out", l)
             for i, part in enumerate(_split(got, lengths)):
