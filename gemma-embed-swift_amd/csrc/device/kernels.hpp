@@ -158,6 +158,9 @@ hipError_t launch_ple_rmsnorm(hipStream_t s, const float* in, int rows, int widt
                               int per_scale, const float* w, float eps, float* out);
 // x16[r] = fp16(x[r] / s_r), rscale[r] = s_r: the power of two >= 1 that brings ||x[r]||_2 under 2^14.
 hipError_t launch_ple_input(hipStream_t s, const float* x, int T, int d, uint16_t* x16, float* rscale);
+// x = x + rmsnorm(t16) * w (t16 = t * c, t_eps = eps * c^2), then x16 / rscale as launch_ple_input.
+hipError_t launch_ple_residual_input(hipStream_t s, float* x, const uint16_t* t16, float t_eps, const float* w, int T,
+                                     int d, uint16_t* x16, float* rscale);
 // g = gelu_tanh(graw[r] * rscale[r]) * ple[r][layer] (ple fp32 [T][layers][pl]); g16 = fp16(g / s2_r),
 // rscale2[r] = s2_r, chosen as in launch_ple_input.
 hipError_t launch_ple_gate(hipStream_t s, const float* graw, const float* rscale, const float* ple, int layer, int layers,

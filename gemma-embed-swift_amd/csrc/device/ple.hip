@@ -93,6 +93,60 @@ __global__ __launch_bounds__(256) void ple_input_kernel(const float* __restrict_
     }
 }
 
+// The FFN residual of a layer with the branch, fused with the branch's row-scaled input:
+// x = x + rmsnorm(t) * w (t as fp16 t * c with t_eps = eps * c^2, as residual_norm_kernel takes
+// it), then x16[r] = fp16(x[r] / s_r), rscale[r] = s_r.
+template <int CH>
+__global__ __launch_bounds__(256) void ple_residual_input_kernel(float* __restrict__ x, const uint16_t* __restrict__ t16,
+                                                                 float t_eps, const float* __restrict__ w, int T, int d,
+                                                                 uint16_t* __restrict__ x16, float* __restrict__ rscale) {
+    const int row = blockIdx.x * 4 + (threadIdx.x >> 6), lane = threadIdx.x & 63;
+    if (row >= T) return;
+    float tv[CH][4], xv[CH][4];
+    float ss = 0.0f;
+#pragma unroll
+    for (int c = 0; c < CH; c++) {
+        const int e = c * 256 + lane * 4;
+        if (e < d) {
+            const half4_t a = *reinterpret_cast<const half4_t*>(t16 + (size_t)row * d + e);
+#pragma unroll
+            for (int j = 0; j < 4; j++) {
+                tv[c][j] = float(a[j]);
+                ss += tv[c][j] * tv[c][j];
+            }
+        }
+    }
+    const float inv = 1.0f / sqrtf(wave_sum(ss) / float(d) + t_eps);
+    float ss2 = 0.0f;
+#pragma unroll
+    for (int c = 0; c < CH; c++) {
+        const int e = c * 256 + lane * 4;
+        if (e < d) {
+            float4* xp = reinterpret_cast<float4*>(x + (size_t)row * d + e);
+            const float4 a = *xp;
+            const float xa[4] = {a.x, a.y, a.z, a.w};
+#pragma unroll
+            for (int j = 0; j < 4; j++) {
+                xv[c][j] = xa[j] + tv[c][j] * inv * w[e + j];
+                ss2 += xv[c][j] * xv[c][j];
+            }
+            *xp = make_float4(xv[c][0], xv[c][1], xv[c][2], xv[c][3]);
+        }
+    }
+    const float sc = ple_row_scale(wave_sum(ss2)), is = 1.0f / sc;
+    if (lane == 0) rscale[row] = sc;
+#pragma unroll
+    for (int c = 0; c < CH; c++) {
+        const int e = c * 256 + lane * 4;
+        if (e < d) {
+            half4_t o;
+#pragma unroll
+            for (int j = 0; j < 4; j++) o[j] = _Float16(xv[c][j] * is);
+            *reinterpret_cast<half4_t*>(x16 + (size_t)row * d + e) = o;
+        }
+    }
+}
+
 // g = gelu_tanh(graw[r] * rscale[r]) * ple[r][layer]; g16[r] = fp16(g / s2_r), rscale2[r] = s2_r.
 template <int CH>
 __global__ __launch_bounds__(256) void ple_gate_kernel(const float* __restrict__ graw, const float* __restrict__ rscale,
@@ -214,6 +268,14 @@ hipError_t launch_ple_input(hipStream_t s, const float* x, int T, int d, uint16_
     if (T < 0 || !ple_width_ok(d) || !x || !x16 || !rscale) return hipErrorInvalidValue;
     if (T == 0) return hipSuccess;
     PLE_DISPATCH(ple_input_kernel, d, T, s, x, T, d, x16, rscale);
+    return hipGetLastError();
+}
+
+hipError_t launch_ple_residual_input(hipStream_t s, float* x, const uint16_t* t16, float t_eps, const float* w, int T,
+                                     int d, uint16_t* x16, float* rscale) {
+    if (T < 0 || !ple_width_ok(d) || !x || !t16 || !w || !x16 || !rscale) return hipErrorInvalidValue;
+    if (T == 0) return hipSuccess;
+    PLE_DISPATCH(ple_residual_input_kernel, d, T, s, x, t16, t_eps, w, T, d, x16, rscale);
     return hipGetLastError();
 }
 

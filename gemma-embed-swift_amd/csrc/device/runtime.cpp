@@ -915,12 +915,10 @@ void encode(ge_ctx* c, StopPoint* sp) {
         if (m.pl > 0) {
             // CPUReference.swift:259-269: x += rmsnorm(proj(gelu(inp_gate(x)) * ple_l), post_norm), then
             // the layer output scale; the unnormalised inputs of both projections go row-scaled
-            launch(c, "residual_norm", [&] {
-                return launch_residual_norm(s, w.x, t16, m.eps * L.down_c * L.down_c, L.post_ffw, 1.0f, nullptr, m.eps, T, D,
-                                            nullptr);
+            launch(c, "ple_residual_input", [&] {
+                return launch_ple_residual_input(s, w.x, t16, m.eps * L.down_c * L.down_c, L.post_ffw, T, D, w.x16, w.rs);
             });
             if (at(sp, "pe_in", l)) return;
-            launch(c, "ple_input", [&] { return launch_ple_input(s, w.x, T, D, w.x16, w.rs); });
             launch(c, "gemm_ple_gate", [&] { return launch_gemm_q8(s, L.inp_gate, w.x16, T, w.ple_t, kEpiF32); });
             launch(c, "ple_gate", [&] { return launch_ple_gate(s, w.ple_t, w.rs, w.ple, l, m.layers, T, m.pl, w.g16, w.rs2); });
             launch(c, "gemm_ple_proj", [&] { return launch_gemm_q8(s, L.proj, w.g16, T, w.ple_t, kEpiF32); });
