@@ -533,8 +533,8 @@ void upload(ge_ctx* c, const ge_model_desc* d, const void* base, size_t len) {
         // layouts the separate kernel's V^T staging cannot hold (2 KV heads of 256); a trace of the
         // raw projection of such a layer runs the fp32 path.
         L.qkv_fused = gemm_qkv_supported(L.head_dim, m.heads, L.kv_heads);
-        m.all_fused = m.all_fused && L.qkv_fused && L.attn_v2 && m.pl == 0;
         m.any_v2 = m.any_v2 || L.attn_v2;
+        m.all_v2 = m.all_v2 && L.attn_v2;
         if (L.attn_v2 && m.heads / L.kv_heads > 3) m.items32_ok = false;
         m.max_qkv = std::max(m.max_qkv, L.qd + 2 * L.kvd);
         m.layer.push_back(L);
@@ -731,7 +731,7 @@ void stage(ge_ctx* c, const int32_t* tokens, const int32_t* positions, int n, co
     // memory-bound kernels and its kernels' start and end phases overlap the others' work.
     int n_parts = 1;
     int part_row[kMaxParts + 1] = {0}, part_work[kMaxParts + 1] = {0};
-    if (m.all_fused && n >= kSplitMinTokens && n_seqs >= 2) {
+    if (m.all_v2 && n >= kSplitMinTokens && n_seqs >= 2) {
         const int want = kMaxParts;
         std::vector<int> starts;
         for (int s = 0; s < n_seqs; s++)
@@ -921,9 +921,10 @@ void encode(ge_ctx* c, StopPoint* sp) {
             if (at(sp, "pe_in", l)) return;
             launch(c, "gemm_ple_gate", [&] { return launch_gemm_q8(s, L.inp_gate, w.x16, T, w.ple_t, kEpiF32); });
             launch(c, "ple_gate", [&] { return launch_ple_gate(s, w.ple_t, w.rs, w.ple, l, m.layers, T, m.pl, w.g16, w.rs2); });
-            launch(c, "gemm_ple_proj", [&] { return launch_gemm_q8(s, L.proj, w.g16, T, w.ple_t, kEpiF32); });
+            // the projection (fp32 [T][hidden]) goes to t, free once the FFN residual has read it
+            launch(c, "gemm_ple_proj", [&] { return launch_gemm_q8(s, L.proj, w.g16, T, w.t, kEpiF32); });
             launch(c, "ple_residual_norm", [&] {
-                return launch_ple_residual_norm(s, w.x, w.ple_t, w.rs2, L.post_norm, L.out_scale, next, m.eps, T, D, w.h);
+                return launch_ple_residual_norm(s, w.x, w.t, w.rs2, L.post_norm, L.out_scale, next, m.eps, T, D, w.h);
             });
             if (at(sp, "l_out", l) || at(sp, "attn_norm", l + 1)) return;
             continue;
@@ -941,19 +942,19 @@ void encode(ge_ctx* c, StopPoint* sp) {
 }
 
 // The forward of a split batch (see stage()): every layer's kernels run for each part's rows
-// on the part's stream, launched part after part, so the parts' kernels overlap. Only layers
-// with the fused QKV epilogue and the LDS-copy attention.
+// on the part's stream, launched part after part, so the parts' kernels overlap. The same kernels
+// and arguments per row as encode(), so a token's values do not depend on the split; every layer
+// must use the LDS-copy attention, whose work list stage() orders by part.
 void encode_split(ge_ctx* c) {
     const DevModel& m = c->model;
     Workspace& w = c->ws;
-    const int T = c->staged_tokens, D = m.hidden;
+    const int D = m.hidden;
     struct Half {
         hipStream_t s;
         int r0, T;
         const AttnWork* work;
         int n_work;
     };
-    (void)T;
     std::vector<Half> halves;
     for (int p = 0; p < c->n_parts; p++)
         halves.push_back(Half{c->part_stream[p], c->part_row[p], c->part_row[p + 1] - c->part_row[p],
@@ -962,32 +963,78 @@ void encode_split(ge_ctx* c) {
     for (int p = 0; p < c->n_parts; p++)
         if (c->part_stream[p] != c->stream) hip_check(hipStreamWaitEvent(c->part_stream[p], c->ev_fork, 0), "hipStreamWaitEvent");
     uint16_t* t16 = reinterpret_cast<uint16_t*>(w.t);
+    auto rows = [](auto* base, int r0, size_t width) { return base + size_t(r0) * width; };
     for (const Half& H : halves)
         launch(c, "embed_norm", [&] {
             return launch_embed_norm(H.s, m.tok_embd, w.tokens + H.r0, H.T, m.emb_scale, m.layer[0].attn_norm, m.eps,
-                                     w.x + (size_t)H.r0 * D, w.h + (size_t)H.r0 * D);
+                                     rows(w.x, H.r0, D), rows(w.h, H.r0, D));
         });
+    if (m.pl > 0) {
+        const size_t LP = size_t(m.layers) * m.pl;
+        for (const Half& H : halves)
+            launch(c, "ple_input", [&] {
+                return launch_ple_input(H.s, rows(w.x, H.r0, D), H.T, D, rows(w.x16, H.r0, D), w.rs + H.r0);
+            });
+        for (const Half& H : halves)
+            launch(c, "gemm_ple_model_proj", [&] {
+                return launch_gemm_q8(H.s, m.pl_proj, rows(w.x16, H.r0, D), H.T, rows(w.ple, H.r0, LP), kEpiF32);
+            });
+        for (const Half& H : halves)
+            launch(c, "ple_norm", [&] {
+                return launch_ple_rmsnorm(H.s, rows(w.ple, H.r0, LP), H.T * m.layers, m.pl, m.pl_scale, w.rs + H.r0, m.layers,
+                                          m.pl_norm, m.eps, rows(w.ple, H.r0, LP));
+            });
+    }
     for (int l = 0; l < m.layers; l++) {
         const DevLayer& L = m.layer[size_t(l)];
-        for (const Half& H : halves)
-            launch(c, "gemm_qkv", [&] {
-                QkvEpilogue e;
-                e.q_norm = L.q_norm;
-                e.k_norm = L.k_norm;
-                e.positions = w.positions + H.r0;
-                e.rope = L.rope;
-                e.q = w.q + (size_t)H.r0 * L.qd;
-                e.k = w.k + (size_t)H.r0 * L.kvd;
-                e.v = nullptr;
-                e.vcol = w.vcol + H.r0;
-                e.vt = w.vt;
-                e.vt_cols = w.vt_cap;
-                e.scale = L.qkv_c;
-                e.eps = m.eps * L.qkv_c * L.qkv_c;
-                e.heads = m.heads;
-                e.kv_heads = L.kv_heads;
-                return launch_gemm_qkv(H.s, L.wqkv, w.h + (size_t)H.r0 * D, H.T, L.head_dim, e);
-            });
+        const size_t NQ = size_t(L.qd) + 2 * L.kvd;
+        if (L.qkv_fused) {
+            for (const Half& H : halves)
+                launch(c, "gemm_qkv", [&] {
+                    QkvEpilogue e;
+                    e.q_norm = L.q_norm;
+                    e.k_norm = L.k_norm;
+                    e.positions = w.positions + H.r0;
+                    e.rope = L.rope;
+                    e.q = rows(w.q, H.r0, L.qd);
+                    e.k = rows(w.k, H.r0, L.kvd);
+                    e.v = nullptr;
+                    e.vcol = w.vcol + H.r0;
+                    e.vt = w.vt;
+                    e.vt_cols = w.vt_cap;
+                    e.scale = L.qkv_c;
+                    e.eps = m.eps * L.qkv_c * L.qkv_c;
+                    e.heads = m.heads;
+                    e.kv_heads = L.kv_heads;
+                    return launch_gemm_qkv(H.s, L.wqkv, rows(w.h, H.r0, D), H.T, L.head_dim, e);
+                });
+        } else {
+            // the projection, then the norms and RoPE (fp16 kernel with V^T where the layout allows,
+            // else fp32 and a separate transpose), as encode() does
+            for (const Half& H : halves)
+                launch(c, "gemm_qkv", [&] {
+                    return L.qkv_gn ? launch_gemm_q8(H.s, L.wqkv, rows(w.h, H.r0, D), H.T, rows(w.qkv, H.r0, NQ / 2), kEpiF16,
+                                                     L.qkv_c)
+                                    : launch_gemm_q8(H.s, L.wqkv, rows(w.h, H.r0, D), H.T, rows(w.qkv, H.r0, NQ), kEpiF32);
+                });
+            for (const Half& H : halves)
+                launch(c, "qk_norm_rope", [&] {
+                    if (L.qkv_gn)
+                        return launch_qkv_norm_rope_vt(H.s, reinterpret_cast<const uint16_t*>(rows(w.qkv, H.r0, NQ / 2)), H.T,
+                                                       m.heads, L.kv_heads, L.head_dim, L.q_norm, L.k_norm,
+                                                       m.eps * L.qkv_c * L.qkv_c, w.positions + H.r0, L.rope,
+                                                       rows(w.q, H.r0, L.qd), rows(w.k, H.r0, L.kvd), rows(w.v, H.r0, L.kvd),
+                                                       w.vcol + H.r0, w.vt_cap, w.vt);
+                    return launch_qk_norm_rope(H.s, rows(w.qkv, H.r0, NQ), H.T, m.heads, L.kv_heads, L.head_dim, L.q_norm,
+                                               L.k_norm, m.eps, w.positions + H.r0, L.rope, rows(w.q, H.r0, L.qd),
+                                               rows(w.k, H.r0, L.kvd), rows(w.v, H.r0, L.kvd));
+                });
+            if (!L.qkv_gn)
+                for (const Half& H : halves)
+                    launch(c, "v_transpose", [&] {
+                        return launch_v_transpose(H.s, rows(w.v, H.r0, L.kvd), H.T, L.kvd, w.vcol + H.r0, w.vt_cap, w.vt);
+                    });
+        }
         const int hw = L.sliding ? m.window / 2 : 0;
         for (const Half& H : halves)
             launch(c, "attention", [&] {
@@ -996,33 +1043,59 @@ void encode_split(ge_ctx* c) {
             });
         for (const Half& H : halves)
             launch(c, "gemm_o", [&] {
-                return launch_gemm_q8(H.s, L.wo, w.attn + (size_t)H.r0 * L.qd, H.T, t16 + (size_t)H.r0 * D, kEpiF16, L.o_c);
+                return launch_gemm_q8(H.s, L.wo, rows(w.attn, H.r0, L.qd), H.T, rows(t16, H.r0, D), kEpiF16, L.o_c);
             });
         for (const Half& H : halves)
             launch(c, "residual_norm", [&] {
-                return launch_residual_norm(H.s, w.x + (size_t)H.r0 * D, t16 + (size_t)H.r0 * D, m.eps * L.o_c * L.o_c,
-                                            L.post_attn, 1.0f, L.ffn_norm, m.eps, H.T, D, w.h + (size_t)H.r0 * D);
+                return launch_residual_norm(H.s, rows(w.x, H.r0, D), rows(t16, H.r0, D), m.eps * L.o_c * L.o_c, L.post_attn,
+                                            1.0f, L.ffn_norm, m.eps, H.T, D, rows(w.h, H.r0, D));
             });
         for (const Half& H : halves)
             launch(c, "gemm_gate_up", [&] {
-                return launch_gemm_q8(H.s, L.wgu, w.h + (size_t)H.r0 * D, H.T, w.act + (size_t)H.r0 * m.ff, kEpiGeglu,
-                                      L.act_scale);
+                return launch_gemm_q8(H.s, L.wgu, rows(w.h, H.r0, D), H.T, rows(w.act, H.r0, m.ff), kEpiGeglu, L.act_scale);
             });
         for (const Half& H : halves)
             launch(c, "gemm_down", [&] {
-                return launch_gemm_q8(H.s, L.wd, w.act + (size_t)H.r0 * m.ff, H.T, t16 + (size_t)H.r0 * D, kEpiF16,
+                return launch_gemm_q8(H.s, L.wd, rows(w.act, H.r0, m.ff), H.T, rows(t16, H.r0, D), kEpiF16,
                                       L.down_scale * L.down_c);
             });
         const float* next = l + 1 < m.layers ? m.layer[size_t(l) + 1].attn_norm : m.out_norm;
+        if (m.pl > 0) {
+            const size_t LP = size_t(m.layers) * m.pl;
+            for (const Half& H : halves)
+                launch(c, "ple_residual_input", [&] {
+                    return launch_ple_residual_input(H.s, rows(w.x, H.r0, D), rows(t16, H.r0, D), m.eps * L.down_c * L.down_c,
+                                                     L.post_ffw, H.T, D, rows(w.x16, H.r0, D), w.rs + H.r0);
+                });
+            for (const Half& H : halves)
+                launch(c, "gemm_ple_gate", [&] {
+                    return launch_gemm_q8(H.s, L.inp_gate, rows(w.x16, H.r0, D), H.T, rows(w.ple_t, H.r0, m.pl), kEpiF32);
+                });
+            for (const Half& H : halves)
+                launch(c, "ple_gate", [&] {
+                    return launch_ple_gate(H.s, rows(w.ple_t, H.r0, m.pl), w.rs + H.r0, rows(w.ple, H.r0, LP), l, m.layers,
+                                           H.T, m.pl, rows(w.g16, H.r0, m.pl), w.rs2 + H.r0);
+                });
+            for (const Half& H : halves)
+                launch(c, "gemm_ple_proj", [&] {
+                    return launch_gemm_q8(H.s, L.proj, rows(w.g16, H.r0, m.pl), H.T, rows(w.t, H.r0, D), kEpiF32);
+                });
+            for (const Half& H : halves)
+                launch(c, "ple_residual_norm", [&] {
+                    return launch_ple_residual_norm(H.s, rows(w.x, H.r0, D), rows(w.t, H.r0, D), w.rs2 + H.r0, L.post_norm,
+                                                    L.out_scale, next, m.eps, H.T, D, rows(w.h, H.r0, D));
+                });
+            continue;
+        }
         for (const Half& H : halves)
             launch(c, "residual_norm", [&] {
-                return launch_residual_norm(H.s, w.x + (size_t)H.r0 * D, t16 + (size_t)H.r0 * D, m.eps * L.down_c * L.down_c,
-                                            L.post_ffw, L.out_scale, next, m.eps, H.T, D, w.h + (size_t)H.r0 * D);
+                return launch_residual_norm(H.s, rows(w.x, H.r0, D), rows(t16, H.r0, D), m.eps * L.down_c * L.down_c,
+                                            L.post_ffw, L.out_scale, next, m.eps, H.T, D, rows(w.h, H.r0, D));
             });
     }
     for (const Half& H : halves)
         launch(c, "gemm_output", [&] {
-            return launch_gemm_q8(H.s, m.output, w.h + (size_t)H.r0 * D, H.T, w.out + (size_t)H.r0 * m.out_dims, kEpiF32);
+            return launch_gemm_q8(H.s, m.output, rows(w.h, H.r0, D), H.T, rows(w.out, H.r0, m.out_dims), kEpiF32);
         });
     for (int p = 0; p < c->n_parts; p++)
         if (c->part_stream[p] != c->stream) {

@@ -60,8 +60,8 @@ struct DevModel {
     float* out_norm = nullptr;
     std::vector<DevLayer> layer;
     int max_qd = 0, max_kvd = 0, max_qkv = 0, max_kv_heads = 1;
-    bool all_fused = true;  // every layer: fused QKV epilogue and the LDS-copy attention
     bool any_v2 = false;
+    bool all_v2 = true;  // every layer: the LDS-copy attention (a large pack may then run in parts)
     bool items32_ok = true;  // every LDS-copy attention layer takes 32-query work items (<= 3 heads per KV head)
 };
 

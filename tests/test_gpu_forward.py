@@ -422,3 +422,22 @@ def test_reference_real_architecture_vs_oracle(real_shapes_gguf):
                 assert err <= tol.get((name, l), PER_LAYER_TOL), (name, l, i)
     finally:
         m.close()
+
+
+@pytest.mark.timeout(300)
+def test_reference_real_architecture_split_pack_bitwise(real_shapes_gguf):
+    """A pack of at least 4096 tokens runs as parts on several streams, through every layer type
+    of the real architecture (fused and fp32 QKV, head dims 256 and 512, the per-layer-input
+    branch): each text must have the bits it has alone (one stream)."""
+    m = ge.EmbeddingModel.load(real_shapes_gguf, batch_token_budget=16384)
+    try:
+        seqs = [ge.synth_tokens(s, 2, 262144, n).tolist() for s, n in ((51, 1500), (52, 1300), (53, 1200), (54, 700))]
+        packed = m.embed_tokens(seqs)
+        for i, sq in enumerate(seqs):
+            alone, _ = m.context.forward([sq])
+            assert np.array_equal(alone[0], packed[i]), i
+        with ora.OracleModel(real_shapes_gguf) as o:
+            want, _ = o.forward(seqs[3])
+        assert cosine(packed[3], want) >= COSINE_BAR
+    finally:
+        m.close()
