@@ -9,31 +9,47 @@ namespace ge {
 //
 // One wave per token row; each lane owns 4 consecutive elements of every 256-wide chunk.
 // x = dequant(table[id]) * scale, then h = rmsnorm(x) * w (reference Shaders/Elementwise.metal:8-35
-// and :38-75; Model/CPUReference.swift:190-204, :217).
+// and :38-75; Model/CPUReference.swift:190-204, :217). An id -(r + 1) is row r of `vectors`
+// ([rows][d] fp32), entered unscaled (Elementwise.metal:25-29); the host has checked r.
 template <int CH>
 __global__ __launch_bounds__(256) void embed_norm_kernel(const int8_t* __restrict__ tq, const uint16_t* __restrict__ ts,
                                                          const int32_t* __restrict__ tokens, int T, int d, float scale,
-                                                         const float* __restrict__ w, float eps, float* __restrict__ x,
-                                                         uint16_t* __restrict__ h) {
+                                                         const float* __restrict__ vectors, const float* __restrict__ w,
+                                                         float eps, float* __restrict__ x, uint16_t* __restrict__ h) {
     const int row = blockIdx.x * 4 + (threadIdx.x >> 6), lane = threadIdx.x & 63;
     if (row >= T) return;
     const int id = tokens[row];
-    const int8_t* q = tq + (size_t)id * d;
-    const uint16_t* sc = ts + (size_t)id * (d / 32);
     float v[CH][4];
     float ss = 0.0f;
+    if (id < 0) {
+        const float* src = vectors + (size_t)(-(id + 1)) * d;
 #pragma unroll
-    for (int c = 0; c < CH; c++) {
-        const int e = c * 256 + lane * 4;
-        if (e < d) {
-            const uint32_t packed = *reinterpret_cast<const uint32_t*>(q + e);
-            const float ds = h2f(sc[e / 32]);
+        for (int c = 0; c < CH; c++) {
+            const int e = c * 256 + lane * 4;
+            if (e < d) {
+                const float4 f = *reinterpret_cast<const float4*>(src + e);
+                v[c][0] = f.x, v[c][1] = f.y, v[c][2] = f.z, v[c][3] = f.w;
 #pragma unroll
-            for (int j = 0; j < 4; j++) {
-                v[c][j] = ds * float(int8_t((packed >> (8 * j)) & 0xff)) * scale;
-                ss += v[c][j] * v[c][j];
+                for (int j = 0; j < 4; j++) ss += v[c][j] * v[c][j];
+                *reinterpret_cast<float4*>(x + (size_t)row * d + e) = f;
             }
-            *reinterpret_cast<float4*>(x + (size_t)row * d + e) = make_float4(v[c][0], v[c][1], v[c][2], v[c][3]);
+        }
+    } else {
+        const int8_t* q = tq + (size_t)id * d;
+        const uint16_t* sc = ts + (size_t)id * (d / 32);
+#pragma unroll
+        for (int c = 0; c < CH; c++) {
+            const int e = c * 256 + lane * 4;
+            if (e < d) {
+                const uint32_t packed = *reinterpret_cast<const uint32_t*>(q + e);
+                const float ds = h2f(sc[e / 32]);
+#pragma unroll
+                for (int j = 0; j < 4; j++) {
+                    v[c][j] = ds * float(int8_t((packed >> (8 * j)) & 0xff)) * scale;
+                    ss += v[c][j] * v[c][j];
+                }
+                *reinterpret_cast<float4*>(x + (size_t)row * d + e) = make_float4(v[c][0], v[c][1], v[c][2], v[c][3]);
+            }
         }
     }
     ss = wave_sum(ss);
@@ -51,16 +67,16 @@ __global__ __launch_bounds__(256) void embed_norm_kernel(const int8_t* __restric
 }
 
 hipError_t launch_embed_norm(hipStream_t s, const Q8Dev& table, const int32_t* tokens, int T, float scale,
-                             const float* norm_w, float eps, float* x, uint16_t* h) {
+                             const float* vectors, const float* norm_w, float eps, float* x, uint16_t* h) {
     const int d = table.cols;
     if (T < 0 || d <= 0 || d % 32 != 0 || d > 1024) return hipErrorInvalidValue;
     if (T == 0) return hipSuccess;
     const int blocks = (T + 3) / 4, CH = (d + 255) / 256;
     switch (CH) {
-    case 1: launch_kernel(embed_norm_kernel<1>, blocks, 256, 0, s, table.q, table.s, tokens, T, d, scale, norm_w, eps, x, h); break;
-    case 2: launch_kernel(embed_norm_kernel<2>, blocks, 256, 0, s, table.q, table.s, tokens, T, d, scale, norm_w, eps, x, h); break;
-    case 3: launch_kernel(embed_norm_kernel<3>, blocks, 256, 0, s, table.q, table.s, tokens, T, d, scale, norm_w, eps, x, h); break;
-    default: launch_kernel(embed_norm_kernel<4>, blocks, 256, 0, s, table.q, table.s, tokens, T, d, scale, norm_w, eps, x, h); break;
+    case 1: launch_kernel(embed_norm_kernel<1>, blocks, 256, 0, s, table.q, table.s, tokens, T, d, scale, vectors, norm_w, eps, x, h); break;
+    case 2: launch_kernel(embed_norm_kernel<2>, blocks, 256, 0, s, table.q, table.s, tokens, T, d, scale, vectors, norm_w, eps, x, h); break;
+    case 3: launch_kernel(embed_norm_kernel<3>, blocks, 256, 0, s, table.q, table.s, tokens, T, d, scale, vectors, norm_w, eps, x, h); break;
+    default: launch_kernel(embed_norm_kernel<4>, blocks, 256, 0, s, table.q, table.s, tokens, T, d, scale, vectors, norm_w, eps, x, h); break;
     }
     return hipGetLastError();
 }

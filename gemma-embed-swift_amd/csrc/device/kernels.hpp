@@ -95,9 +95,10 @@ struct QkvEpilogue {
 bool gemm_qkv_supported(int hd, int H, int KV);
 hipError_t launch_gemm_qkv(hipStream_t s, const Q8Dev& w, const uint16_t* x, int M, int hd, const QkvEpilogue& e);
 
-// x = table[id] * scale (fp32 [T][d]), h = rmsnorm(x) * w (fp16 [T][d]).
+// x = table[id] * scale (fp32 [T][d]), or row -(id + 1) of vectors (fp32 [rows][d]) unscaled for a
+// negative id; h = rmsnorm(x) * w (fp16 [T][d]).
 hipError_t launch_embed_norm(hipStream_t s, const Q8Dev& table, const int32_t* tokens, int T, float scale,
-                             const float* norm_w, float eps, float* x, uint16_t* h);
+                             const float* vectors, const float* norm_w, float eps, float* x, uint16_t* h);
 
 // x = (x + rmsnorm(t) * w) * out_scale; if next_w: h = rmsnorm(x) * next_w (fp16).
 // t arrives as fp16 t16 = t * c for a power of two c, and t_eps = eps * c^2, so rmsnorm(t16)

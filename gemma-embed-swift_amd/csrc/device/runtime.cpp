@@ -681,14 +681,19 @@ VtLayout vt_layout(int n_tokens, const ge_seq* seqs, int n_seqs) {
 
 // Validates a packed batch and uploads it with its attention work list (PackedBatch and
 // AttentionWork.items, Metal/MetalForward.swift:8-58; execute :326-334).
-void stage(ge_ctx* c, const int32_t* tokens, const int32_t* positions, int n, const ge_seq* seqs, int n_seqs) {
+void stage(ge_ctx* c, const int32_t* tokens, const int32_t* positions, int n, const ge_seq* seqs, int n_seqs,
+           const float* vectors, int n_vectors) {
     if (!c->has_model) fail(GE_ERR_STATE, "no model has been uploaded");
     if (n <= 0 || !tokens || !positions) fail(GE_ERR_INVALID, "a batch needs at least one token");
     if (n_seqs <= 0 || !seqs) fail(GE_ERR_INVALID, "a batch needs at least one sequence");
     const DevModel& m = c->model;
+    if (!vectors) n_vectors = 0;
+    bool any_vector = false;
     for (int i = 0; i < n; i++) {
-        if (tokens[i] < 0 || tokens[i] >= m.vocab)
-            fail(GE_ERR_INVALID, "token %d at row %d is outside the vocabulary [0, %d)", tokens[i], i, m.vocab);
+        if (tokens[i] < -n_vectors || tokens[i] >= m.vocab)
+            fail(GE_ERR_INVALID, "token %d at row %d is neither in the vocabulary [0, %d) nor one of the %d vector rows",
+                 tokens[i], i, m.vocab, n_vectors);
+        any_vector |= tokens[i] < 0;
         if (positions[i] < 0 || positions[i] >= m.max_tokens)
             fail(GE_ERR_INVALID, "position %d at row %d is outside [0, %d)", positions[i], i, m.max_tokens);
     }
@@ -802,6 +807,7 @@ void stage(ge_ctx* c, const int32_t* tokens, const int32_t* positions, int n, co
     hip_check(hipEventRecord(c->staged_copy, c->stream), "hipEventRecord");
     c->staged_copy_recorded = true;
     c->staged_tokens = n;
+    c->staged_vectors = any_vector ? vectors : nullptr;
     c->staged_seqs = n_seqs;
     c->staged_work = int(work.size());
     c->staged_work2 = int(work2.size());
@@ -832,7 +838,7 @@ void encode(ge_ctx* c, StopPoint* sp) {
     hipStream_t s = c->stream;
     const int D = m.hidden;
     launch(c, "embed_norm", [&] {
-        return launch_embed_norm(s, m.tok_embd, w.tokens, T, m.emb_scale, m.layer[0].attn_norm, m.eps, w.x, w.h);
+        return launch_embed_norm(s, m.tok_embd, w.tokens, T, m.emb_scale, c->staged_vectors, m.layer[0].attn_norm, m.eps, w.x, w.h);
     });
     if (at(sp, "inp_scaled", -1) || at(sp, "attn_norm", 0)) return;
     if (m.pl > 0) {
@@ -962,11 +968,20 @@ void encode_split(ge_ctx* c) {
     hip_check(hipEventRecord(c->ev_fork, c->stream), "hipEventRecord");
     for (int p = 0; p < c->n_parts; p++)
         if (c->part_stream[p] != c->stream) hip_check(hipStreamWaitEvent(c->part_stream[p], c->ev_fork, 0), "hipStreamWaitEvent");
+    // The parts run unsynchronised, so one may be a layer ahead of another: each part owns the
+    // slice of a buffer that starts at row r0 times the buffer's allocated width, whatever width a
+    // layer uses (head dims differ between layers), and fp16 t16 lives in the part's slice of fp32 t.
+    // The attention kernels index absolute rows: they take the base at which row r0 lands at its
+    // part's slice (part_base), and rows past a sequence's end, which they read and mask, stay
+    // inside the buffer.
     uint16_t* t16 = reinterpret_cast<uint16_t*>(w.t);
     auto rows = [](auto* base, int r0, size_t width) { return base + size_t(r0) * width; };
+    auto part_base = [](auto* base, int r0, size_t width, size_t alloc_width) {
+        return base + size_t(r0) * (alloc_width - width);
+    };
     for (const Half& H : halves)
         launch(c, "embed_norm", [&] {
-            return launch_embed_norm(H.s, m.tok_embd, w.tokens + H.r0, H.T, m.emb_scale, m.layer[0].attn_norm, m.eps,
+            return launch_embed_norm(H.s, m.tok_embd, w.tokens + H.r0, H.T, m.emb_scale, c->staged_vectors, m.layer[0].attn_norm, m.eps,
                                      rows(w.x, H.r0, D), rows(w.h, H.r0, D));
         });
     if (m.pl > 0) {
@@ -987,7 +1002,6 @@ void encode_split(ge_ctx* c) {
     }
     for (int l = 0; l < m.layers; l++) {
         const DevLayer& L = m.layer[size_t(l)];
-        const size_t NQ = size_t(L.qd) + 2 * L.kvd;
         if (L.qkv_fused) {
             for (const Half& H : halves)
                 launch(c, "gemm_qkv", [&] {
@@ -996,8 +1010,8 @@ void encode_split(ge_ctx* c) {
                     e.k_norm = L.k_norm;
                     e.positions = w.positions + H.r0;
                     e.rope = L.rope;
-                    e.q = rows(w.q, H.r0, L.qd);
-                    e.k = rows(w.k, H.r0, L.kvd);
+                    e.q = rows(w.q, H.r0, m.max_qd);
+                    e.k = rows(w.k, H.r0, m.max_kvd);
                     e.v = nullptr;
                     e.vcol = w.vcol + H.r0;
                     e.vt = w.vt;
@@ -1013,41 +1027,42 @@ void encode_split(ge_ctx* c) {
             // else fp32 and a separate transpose), as encode() does
             for (const Half& H : halves)
                 launch(c, "gemm_qkv", [&] {
-                    return L.qkv_gn ? launch_gemm_q8(H.s, L.wqkv, rows(w.h, H.r0, D), H.T, rows(w.qkv, H.r0, NQ / 2), kEpiF16,
+                    return L.qkv_gn ? launch_gemm_q8(H.s, L.wqkv, rows(w.h, H.r0, D), H.T, rows(w.qkv, H.r0, m.max_qkv), kEpiF16,
                                                      L.qkv_c)
-                                    : launch_gemm_q8(H.s, L.wqkv, rows(w.h, H.r0, D), H.T, rows(w.qkv, H.r0, NQ), kEpiF32);
+                                    : launch_gemm_q8(H.s, L.wqkv, rows(w.h, H.r0, D), H.T, rows(w.qkv, H.r0, m.max_qkv), kEpiF32);
                 });
             for (const Half& H : halves)
                 launch(c, "qk_norm_rope", [&] {
                     if (L.qkv_gn)
-                        return launch_qkv_norm_rope_vt(H.s, reinterpret_cast<const uint16_t*>(rows(w.qkv, H.r0, NQ / 2)), H.T,
+                        return launch_qkv_norm_rope_vt(H.s, reinterpret_cast<const uint16_t*>(rows(w.qkv, H.r0, m.max_qkv)), H.T,
                                                        m.heads, L.kv_heads, L.head_dim, L.q_norm, L.k_norm,
                                                        m.eps * L.qkv_c * L.qkv_c, w.positions + H.r0, L.rope,
-                                                       rows(w.q, H.r0, L.qd), rows(w.k, H.r0, L.kvd), rows(w.v, H.r0, L.kvd),
+                                                       rows(w.q, H.r0, m.max_qd), rows(w.k, H.r0, m.max_kvd), rows(w.v, H.r0, m.max_kvd),
                                                        w.vcol + H.r0, w.vt_cap, w.vt);
-                    return launch_qk_norm_rope(H.s, rows(w.qkv, H.r0, NQ), H.T, m.heads, L.kv_heads, L.head_dim, L.q_norm,
-                                               L.k_norm, m.eps, w.positions + H.r0, L.rope, rows(w.q, H.r0, L.qd),
-                                               rows(w.k, H.r0, L.kvd), rows(w.v, H.r0, L.kvd));
+                    return launch_qk_norm_rope(H.s, rows(w.qkv, H.r0, m.max_qkv), H.T, m.heads, L.kv_heads, L.head_dim, L.q_norm,
+                                               L.k_norm, m.eps, w.positions + H.r0, L.rope, rows(w.q, H.r0, m.max_qd),
+                                               rows(w.k, H.r0, m.max_kvd), rows(w.v, H.r0, m.max_kvd));
                 });
             if (!L.qkv_gn)
                 for (const Half& H : halves)
                     launch(c, "v_transpose", [&] {
-                        return launch_v_transpose(H.s, rows(w.v, H.r0, L.kvd), H.T, L.kvd, w.vcol + H.r0, w.vt_cap, w.vt);
+                        return launch_v_transpose(H.s, rows(w.v, H.r0, m.max_kvd), H.T, L.kvd, w.vcol + H.r0, w.vt_cap, w.vt);
                     });
         }
         const int hw = L.sliding ? m.window / 2 : 0;
         for (const Half& H : halves)
             launch(c, "attention", [&] {
-                return launch_attention_v2(H.s, w.q, w.k, w.vt, w.vt_cap, w.attn, H.work, H.n_work, m.heads, L.kv_heads,
+                return launch_attention_v2(H.s, part_base(w.q, H.r0, L.qd, m.max_qd), part_base(w.k, H.r0, L.kvd, m.max_kvd),
+                                           w.vt, w.vt_cap, part_base(w.attn, H.r0, L.qd, m.max_qd), H.work, H.n_work, m.heads, L.kv_heads,
                                            L.head_dim, hw, 1.0f, c->attn_items);
             });
         for (const Half& H : halves)
             launch(c, "gemm_o", [&] {
-                return launch_gemm_q8(H.s, L.wo, rows(w.attn, H.r0, L.qd), H.T, rows(t16, H.r0, D), kEpiF16, L.o_c);
+                return launch_gemm_q8(H.s, L.wo, rows(w.attn, H.r0, m.max_qd), H.T, rows(t16, H.r0, 2 * size_t(D)), kEpiF16, L.o_c);
             });
         for (const Half& H : halves)
             launch(c, "residual_norm", [&] {
-                return launch_residual_norm(H.s, rows(w.x, H.r0, D), rows(t16, H.r0, D), m.eps * L.o_c * L.o_c, L.post_attn,
+                return launch_residual_norm(H.s, rows(w.x, H.r0, D), rows(t16, H.r0, 2 * size_t(D)), m.eps * L.o_c * L.o_c, L.post_attn,
                                             1.0f, L.ffn_norm, m.eps, H.T, D, rows(w.h, H.r0, D));
             });
         for (const Half& H : halves)
@@ -1056,7 +1071,7 @@ void encode_split(ge_ctx* c) {
             });
         for (const Half& H : halves)
             launch(c, "gemm_down", [&] {
-                return launch_gemm_q8(H.s, L.wd, rows(w.act, H.r0, m.ff), H.T, rows(t16, H.r0, D), kEpiF16,
+                return launch_gemm_q8(H.s, L.wd, rows(w.act, H.r0, m.ff), H.T, rows(t16, H.r0, 2 * size_t(D)), kEpiF16,
                                       L.down_scale * L.down_c);
             });
         const float* next = l + 1 < m.layers ? m.layer[size_t(l) + 1].attn_norm : m.out_norm;
@@ -1064,7 +1079,7 @@ void encode_split(ge_ctx* c) {
             const size_t LP = size_t(m.layers) * m.pl;
             for (const Half& H : halves)
                 launch(c, "ple_residual_input", [&] {
-                    return launch_ple_residual_input(H.s, rows(w.x, H.r0, D), rows(t16, H.r0, D), m.eps * L.down_c * L.down_c,
+                    return launch_ple_residual_input(H.s, rows(w.x, H.r0, D), rows(t16, H.r0, 2 * size_t(D)), m.eps * L.down_c * L.down_c,
                                                      L.post_ffw, H.T, D, rows(w.x16, H.r0, D), w.rs + H.r0);
                 });
             for (const Half& H : halves)
@@ -1089,7 +1104,7 @@ void encode_split(ge_ctx* c) {
         }
         for (const Half& H : halves)
             launch(c, "residual_norm", [&] {
-                return launch_residual_norm(H.s, rows(w.x, H.r0, D), rows(t16, H.r0, D), m.eps * L.down_c * L.down_c,
+                return launch_residual_norm(H.s, rows(w.x, H.r0, D), rows(t16, H.r0, 2 * size_t(D)), m.eps * L.down_c * L.down_c,
                                             L.post_ffw, L.out_scale, next, m.eps, H.T, D, rows(w.h, H.r0, D));
             });
     }
@@ -1150,12 +1165,35 @@ void run_graph(ge_ctx* c) {
     hip_check(hipGraphLaunch(g->exec, c->stream), "hipGraphLaunch");
 }
 
-void run_forward(ge_ctx* c, double* gpu_seconds) {
+// The rows ge_set_vectors uploaded, when they are as wide as the model's residual stream.
+const float* own_vectors(ge_ctx* c) { return c->vec_rows && c->vec_width == c->model.hidden ? c->vec_buf : nullptr; }
+int own_vector_rows(ge_ctx* c) { return own_vectors(c) ? c->vec_rows : 0; }
+
+// Copies `rows` vector rows (fp32 [rows][width]) into the context's buffer, growing it when needed.
+void set_vectors(ge_ctx* c, const float* rows, int n_rows, int width) {
+    if (n_rows < 0 || (n_rows > 0 && (!rows || width <= 0))) fail(GE_ERR_INVALID, "bad vector rows");
+    const size_t bytes = size_t(n_rows) * size_t(std::max(width, 0)) * 4;
+    hip_check(hipStreamSynchronize(c->stream), "hipStreamSynchronize");  // queued work may read the rows
+    if (bytes > c->vec_cap) {
+        if (c->staged_vectors && c->staged_vectors == c->vec_buf) c->staged_tokens = -1;  // the staged batch read the old rows
+        if (c->vec_buf) hip_check(hipFree(c->vec_buf), "hipFree");
+        c->vec_buf = nullptr;
+        c->vec_cap = 0;
+        c->vec_rows = 0;
+        hip_check(hipMalloc(reinterpret_cast<void**>(&c->vec_buf), bytes), "hipMalloc vector rows");
+        c->vec_cap = bytes;
+    }
+    if (bytes) hip_check(hipMemcpy(c->vec_buf, rows, bytes, hipMemcpyHostToDevice), "upload vector rows");
+    c->vec_rows = n_rows;
+    c->vec_width = width;
+}
+
+void run_forward(ge_ctx* c, double* gpu_seconds, bool record_start) {
     if (c->staged_tokens < 0) fail(GE_ERR_STATE, "no batch is staged");
-    hip_check(hipEventRecord(c->ev_start, c->stream), "hipEventRecord");
+    if (record_start) hip_check(hipEventRecord(c->ev_start, c->stream), "hipEventRecord");
     if (c->n_parts > 1 && !c->prof)
         encode_split(c);
-    else if (!c->prof && c->staged_tokens <= kGraphMaxTokens)
+    else if (!c->prof && c->staged_tokens <= kGraphMaxTokens && !c->staged_vectors)  // graphs hold no vector source
         run_graph(c);
     else
         encode(c, nullptr);
@@ -1326,6 +1364,7 @@ void ge_destroy(ge_ctx* c) {
     ge::free_workspace(c);
     ge::free_model(c);
     ge::free_vision(c);
+    if (c->vec_buf) (void)hipFree(c->vec_buf);
     for (auto& p : c->prof_pending) {
         (void)hipEventDestroy(p.a);
         (void)hipEventDestroy(p.b);
@@ -1366,7 +1405,7 @@ int ge_forward(ge_ctx* c, const int32_t* tokens, const int32_t* positions, int32
                float* pooled, double* gpu_seconds) {
     return guarded(c, [&] {
         if (!pooled) fail(GE_ERR_INVALID, "null output");
-        ge::stage(c, tokens, positions, n, seqs, n_seqs);
+        ge::stage(c, tokens, positions, n, seqs, n_seqs, ge::own_vectors(c), ge::own_vector_rows(c));
         ge::run_forward(c, gpu_seconds);
         ge::read_pooled(c, pooled);
     });
@@ -1375,13 +1414,17 @@ int ge_forward(ge_ctx* c, const int32_t* tokens, const int32_t* positions, int32
 int ge_forward_trace(ge_ctx* c, const int32_t* tokens, const int32_t* positions, int32_t n, const ge_seq* seqs,
                      int32_t n_seqs, const char* name, int32_t layer, float* out, size_t cap, size_t* needed) {
     return guarded(c, [&] {
-        ge::stage(c, tokens, positions, n, seqs, n_seqs);
+        ge::stage(c, tokens, positions, n, seqs, n_seqs, ge::own_vectors(c), ge::own_vector_rows(c));
         ge::trace(c, name, layer, out, cap, needed);
     });
 }
 
 int ge_batch_stage(ge_ctx* c, const int32_t* tokens, const int32_t* positions, int32_t n, const ge_seq* seqs, int32_t n_seqs) {
-    return guarded(c, [&] { ge::stage(c, tokens, positions, n, seqs, n_seqs); });
+    return guarded(c, [&] { ge::stage(c, tokens, positions, n, seqs, n_seqs, ge::own_vectors(c), ge::own_vector_rows(c)); });
+}
+
+int ge_set_vectors(ge_ctx* c, const float* rows, int32_t n_rows, int32_t width) {
+    return guarded(c, [&] { ge::set_vectors(c, rows, n_rows, width); });
 }
 
 int ge_batch_run(ge_ctx* c) {

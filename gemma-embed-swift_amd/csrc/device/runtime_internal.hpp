@@ -157,6 +157,13 @@ struct ge_ctx {
     std::vector<ge::ShortGraph> graphs;
     // the image tower, when one is uploaded (vision.cpp)
     ge::VisionState* vision = nullptr;
+    // Vector rows (ge_set_vectors): fp32 [vec_rows][vec_width] in HBM, referenced by token ids
+    // -(r + 1). staged_vectors: the rows the staged batch reads (these or the image tower's
+    // output), null when it has none.
+    float* vec_buf = nullptr;
+    size_t vec_cap = 0;
+    int vec_rows = 0, vec_width = 0;
+    const float* staged_vectors = nullptr;
 };
 
 namespace ge {
@@ -231,5 +238,13 @@ float fp16_range_scale(double bound);
 // Copies `rows` x `width` of a device buffer (fp32 or fp16, row stride `stride`) starting at
 // column `col0` into out as fp32, after the context's stream has drained.
 void copy_out(ge_ctx* c, const void* src, bool f16, int rows, int stride, int col0, int width, float* out);
+
+// Packed text batches (runtime.cpp): validate and upload (a negative id -(r + 1) names row r of
+// `vectors`, device fp32 [n_vectors][hidden]); enqueue the forward (record_start: time from here,
+// else from an ev_start the caller recorded); wait and copy the pooled vectors out.
+void stage(ge_ctx* c, const int32_t* tokens, const int32_t* positions, int n, const ge_seq* seqs, int n_seqs,
+           const float* vectors, int n_vectors);
+void run_forward(ge_ctx* c, double* gpu_seconds, bool record_start = true);
+void read_pooled(ge_ctx* c, float* out);
 
 }  // namespace ge

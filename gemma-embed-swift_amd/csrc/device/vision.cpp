@@ -519,6 +519,45 @@ void vision_trace(ge_ctx* c, const char* name, int layer, float* out, size_t cap
 
 }  // namespace
 
+// The image forward (MetalForward.run(images:), Metal/MetalForward.swift:213-219 with imageBatches
+// :285-294): the tower over every image, then the text tower over each image's
+// [bos, begin, v_1 .. v_n, end, eos] (Model/InputRow.swift:52-56), whose vector rows are the
+// tower's output rows in HBM (MetalForward.swift:23-32), on one stream with no host round trip.
+void image_forward(ge_ctx* c, const float* patches, int n_patches, const ge_image_grid* grids, int n_images,
+                   const int32_t* markers, float* pooled, double* gpu_seconds) {
+    if (!pooled || !markers) fail(GE_ERR_INVALID, "null argument");
+    if (!c->has_model) fail(GE_ERR_STATE, "no text model has been uploaded");
+    VisionState& v = vision_of(c);
+    if (v.proj != c->model.hidden)
+        fail(GE_ERR_INVALID, "the image tower's %d-wide vectors do not fit the text model's %d-wide rows", v.proj,
+             c->model.hidden);
+    vision_stage(c, patches, n_patches, grids, n_images);
+    std::vector<int32_t> ids, pos;
+    std::vector<ge_seq> seqs;
+    int row = 0;
+    for (int i = 0; i < n_images; i++) {
+        const int rows = (grids[i].grid_x / v.merge) * (grids[i].grid_y / v.merge);
+        if (rows + 4 > c->model.max_tokens)
+            fail(GE_ERR_INVALID, "image %d: %d vector rows and 4 markers exceed the %d-token context", i, rows,
+                 c->model.max_tokens);
+        seqs.push_back(ge_seq{uint32_t(ids.size()), uint32_t(rows + 4)});
+        ids.push_back(markers[0]);
+        ids.push_back(markers[1]);
+        for (int r = 0; r < rows; r++) ids.push_back(-(row + r) - 1);
+        ids.push_back(markers[2]);
+        ids.push_back(markers[3]);
+        row += rows;
+    }
+    for (size_t t = 0, s = 0; s < seqs.size(); s++)
+        for (uint32_t p = 0; p < seqs[s].length; p++, t++) pos.push_back(int32_t(p));
+    stage(c, ids.data(), pos.data(), int(ids.size()), seqs.data(), n_images, v.out, v.staged_tokens);
+    hip_check(hipEventRecord(c->ev_start, c->stream), "hipEventRecord");
+    vision_encode(c, nullptr);
+    run_forward(c, gpu_seconds, false);
+    read_pooled(c, pooled);
+    c->staged_tokens = -1;  // the batch reads the tower's buffers, which the next image batch may replace
+}
+
 void free_vision(ge_ctx* c) {
     if (!c->vision) return;
     VisionState& v = *c->vision;
@@ -570,6 +609,11 @@ int ge_vision_encode(ge_ctx* c, const float* patches, int32_t n_patches, const g
         }
         ge::vision_read(c, vectors);
     });
+}
+
+int ge_image_forward(ge_ctx* c, const float* patches, int32_t n_patches, const ge_image_grid* grids, int32_t n_images,
+                     const int32_t* markers, float* pooled, double* gpu_seconds) {
+    return ge::guarded(c, [&] { ge::image_forward(c, patches, n_patches, grids, n_images, markers, pooled, gpu_seconds); });
 }
 
 int ge_vision_trace(ge_ctx* c, const float* patches, int32_t n_patches, const ge_image_grid* grids, int32_t n_images,

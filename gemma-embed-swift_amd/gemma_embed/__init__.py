@@ -143,6 +143,9 @@ SIGNATURES = {
     "ge_upload_vision": (_I, [_P, _P, _P, C.c_size_t]),
     "ge_vision_load": (_I, [_P, C.c_char_p, C.c_char_p, C.c_size_t]),
     "ge_vision_encode": (_I, [_P, _PF, C.c_int32, C.POINTER(ge_image_grid), C.c_int32, _PF, C.POINTER(C.c_double)]),
+    "ge_image_forward": (_I, [_P, _PF, C.c_int32, C.POINTER(ge_image_grid), C.c_int32, _PI32, _PF,
+                              C.POINTER(C.c_double)]),
+    "ge_set_vectors": (_I, [_P, _PF, C.c_int32, C.c_int32]),
     "ge_vision_stage": (_I, [_P, _PF, C.c_int32, C.POINTER(ge_image_grid), C.c_int32]),
     "ge_vision_run": (_I, [_P]),
     "ge_vision_read": (_I, [_P, _PF]),
@@ -382,6 +385,25 @@ class Context:
         self._check(lib.ge_vision_encode(self.handle, _ptr(p, C.c_float), p.shape[0], _grid_array(grids), len(grids),
                                          _ptr(out, C.c_float), C.byref(secs)), "ge_vision_encode")
         return out, secs.value
+
+    def image_forward(self, patches: np.ndarray, grids: Sequence[Tuple[int, int]], markers: Sequence[int]):
+        """Image tower, then the text tower over [bos, begin, vectors, end, eos] per image ->
+        (pooled [images, out_dims] unnormalised, gpu_seconds of both towers)."""
+        p = np.ascontiguousarray(patches, dtype=np.float32)
+        mk = np.ascontiguousarray(markers, dtype=np.int32)
+        assert mk.size == 4
+        out = np.zeros((len(grids), self.out_dims), dtype=np.float32)
+        secs = C.c_double(0)
+        self._check(lib.ge_image_forward(self.handle, _ptr(p, C.c_float), p.shape[0], _grid_array(grids), len(grids),
+                                         _ptr(mk, C.c_int32), _ptr(out, C.c_float), C.byref(secs)), "ge_image_forward")
+        return out, secs.value
+
+    def set_vectors(self, rows: np.ndarray):
+        """Vector rows [n, hidden] fp32 for the negative ids of later batches (-(r + 1) is row r)."""
+        v = np.ascontiguousarray(rows, dtype=np.float32)
+        v2 = v.reshape(v.shape[0], -1) if v.size else v.reshape(0, 0)
+        self._check(lib.ge_set_vectors(self.handle, _ptr(v2, C.c_float) if v2.size else None, v2.shape[0],
+                                       v2.shape[1] if v2.ndim == 2 else 0), "ge_set_vectors")
 
     def vision_trace(self, patches: np.ndarray, grids: Sequence[Tuple[int, int]], name: str, layer: int = -1):
         p = np.ascontiguousarray(patches, dtype=np.float32)

@@ -94,10 +94,18 @@ typedef struct ge_seq {
 /* MetalForward.run / timeForward (Metal/MetalForward.swift:199-209): one packed batch, tokens
  * back to back, positions restarting at 0 per sequence (PackedBatch.append :17-21). Writes the
  * unnormalised mean-pooled vectors, n_seqs x out_dims fp32, into caller-owned `pooled_out`.
- * `gpu_seconds` (nullable) receives the GPU time of the forward. Synchronous. Token ids must be
- * in [0, vocab); the reference's negative ids (vector rows, :6-7) are multimodal and rejected. */
+ * `gpu_seconds` (nullable) receives the GPU time of the forward. Synchronous. Token ids are in
+ * [0, vocab), or -(r + 1) for row r of the vector rows ge_set_vectors uploaded (PackedBatch's
+ * convention, :6-7), entered into the residual stream unscaled (Shaders/Elementwise.metal:25-29). */
 int ge_forward(ge_ctx* ctx, const int32_t* tokens, const int32_t* positions, int32_t n_tokens, const ge_seq* seqs,
                int32_t n_seqs, float* pooled_out, double* gpu_seconds);
+
+/* The workspace's `vectors` buffer (Metal/MetalForward.swift:137,165), filled from the host: fp32
+ * [n_rows][width] copied into HBM, where the batches of ge_forward, ge_forward_trace and
+ * ge_batch_stage find the rows their negative ids name. Rows are used only while `width` equals
+ * the model's hidden size; n_rows 0 clears them. Kept until replaced; replacing them drops a
+ * staged batch that read the old ones. */
+int ge_set_vectors(ge_ctx* ctx, const float* rows, int32_t n_rows, int32_t width);
 
 /* Per-layer parity (CPUReference.forward's trace, Model/CPUReference.swift:204-276, and
  * MetalForward.attentionInputs :278-284): runs the forward up to the op that produces the named
@@ -216,6 +224,14 @@ int32_t ge_vision_tokens(ge_ctx* ctx);
  * (patch projection, no bias), pos_embd, pooled, pooled_normed, projected; per layer:
  * layer_inp_normed, Qcur, Kcur, Vcur (with bias, [patches][heads][hd]), kqv_out, attn_out (no
  * bias), ffn_inp, ffn_inp_normed, ffn_gelu, ffn_out (no bias), layer_out. */
+/* MetalForward.run(images:) (Metal/MetalForward.swift:213-219): the tower over the images, then
+ * the text tower over each image's [bos, begin, its vectors, end, eos] (markers[4] = {bos, begin,
+ * end, eos}: the ids of <bos>, <|image>, <image|>, <eos>; Model/InputRow.swift:16-56), reading the
+ * tower's output rows in HBM. Writes n_images x out_dims unnormalised pooled vectors into
+ * `pooled_out`; `gpu_seconds` (nullable) covers both towers. Needs an uploaded text model whose
+ * hidden size is the tower's projection width. Synchronous. */
+int ge_image_forward(ge_ctx* ctx, const float* patches, int32_t n_patches, const ge_image_grid* grids,
+                     int32_t n_images, const int32_t* markers, float* pooled_out, double* gpu_seconds);
 int ge_vision_trace(ge_ctx* ctx, const float* patches, int32_t n_patches, const ge_image_grid* grids, int32_t n_images,
                     const char* tensor_name, int32_t layer, float* out, size_t out_count, size_t* needed);
 

@@ -742,9 +742,11 @@ static void trace_emit(ora_trace_fn fn, void* user, const char* name, int layer,
     if (fn) fn(user, name, layer, p, n);
 }
 
-/* CPUReference.swift:183-283 for one sequence of token rows (vector rows are multimodal and out of
- * scope). Positions are 0..T-1 (:188). */
-int ora_forward(ora_model* m, const int32_t* tokens, int T, float* pooled, ora_trace_fn trace, void* user, int threads) {
+/* CPUReference.swift:183-283 for one sequence of token and vector rows. Positions are 0..T-1
+ * (:188). A token id -(r + 1) stands for row r of `vectors` ([n_vectors][hidden]), entered into the
+ * residual stream unscaled (:197-199; the packed-batch convention of Metal/MetalForward.swift:6-7). */
+int ora_forward_rows(ora_model* m, const int32_t* tokens, int T, const float* vectors, int n_vectors, float* pooled,
+                     ora_trace_fn trace, void* user, int threads) {
     if (T <= 0 || T > ORA_MAX_TOKENS) return -1;
     const int d = m->hidden;
     const float eps = m->eps;
@@ -781,8 +783,14 @@ int ora_forward(ora_model* m, const int32_t* tokens, int T, float* pooled, ora_t
     const uint8_t* emb = tensor_data(m, m->tok_embd);
     const int erb = row_bytes(m->tok_embd);
     for (int t = 0; t < T; t++) {
-        if (tokens[t] < 0 || tokens[t] >= m->vocab) { T = -1; break; }
         float* dst = x + (size_t)t * d;
+        if (tokens[t] < 0) {
+            const int r = -(tokens[t] + 1);
+            if (!vectors || r >= n_vectors) { T = -1; break; }
+            memcpy(dst, vectors + (size_t)r * d, (size_t)d * sizeof(float));
+            continue;
+        }
+        if (tokens[t] >= m->vocab) { T = -1; break; }
         ora_dequant_row(m->tok_embd->type, emb + (size_t)tokens[t] * erb, d, dst);
         for (int i = 0; i < d; i++) dst[i] *= m->emb_scale;
     }
@@ -874,6 +882,11 @@ done:
     free(pos); free(x); free(h); free(q); free(qn); free(k); free(kn); free(v); free(vn); free(attn);
     free(o); free(on); free(gate); free(up); free(per_layer); free(g);
     return rc;
+}
+
+/* A sequence of token rows only. */
+int ora_forward(ora_model* m, const int32_t* tokens, int T, float* pooled, ora_trace_fn trace, void* user, int threads) {
+    return ora_forward_rows(m, tokens, T, NULL, 0, pooled, trace, user, threads);
 }
 
 /* ================================================================ image tower (config 5)

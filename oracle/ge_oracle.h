@@ -43,6 +43,10 @@ int ora_vocab(const ora_model* m);
  * threads <= 0 uses every core. Returns 0 on success. */
 int ora_forward(ora_model* m, const int32_t* tokens, int T, float* pooled, ora_trace_fn trace, void* user,
                 int threads);
+/* The same over token and vector rows (CPUReference.swift:190-202): an id -(r + 1) selects row r of
+ * `vectors` ([n_vectors][hidden] fp32), entered unscaled. Returns nonzero for a row past n_vectors. */
+int ora_forward_rows(ora_model* m, const int32_t* tokens, int T, const float* vectors, int n_vectors, float* pooled,
+                     ora_trace_fn trace, void* user, int threads);
 
 /* Primitives, exposed for known-answer tests. */
 void ora_dequant_row(int type, const void* row, int cols, float* out);

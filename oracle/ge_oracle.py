@@ -24,6 +24,8 @@ _SIG = {
     "ora_layers": (C.c_int, [C.c_void_p]),
     "ora_vocab": (C.c_int, [C.c_void_p]),
     "ora_forward": (C.c_int, [C.c_void_p, C.POINTER(C.c_int32), C.c_int, _F, TRACE_FN, C.c_void_p, C.c_int]),
+    "ora_forward_rows": (C.c_int, [C.c_void_p, C.POINTER(C.c_int32), C.c_int, _F, C.c_int, _F, TRACE_FN, C.c_void_p,
+                                   C.c_int]),
     "ora_dequant_row": (None, [C.c_int, C.c_void_p, C.c_int, _F]),
     "ora_half_to_float": (C.c_float, [C.c_uint16]),
     "ora_float_to_half": (C.c_uint16, [C.c_float]),
@@ -93,9 +95,12 @@ class OracleModel:
     def __exit__(self, *a):
         self.close()
 
-    def forward(self, tokens, keep: Optional[Iterable[Tuple[str, int]]] = None, threads: int = 0):
-        """CPUReference.forward for one sequence -> (pooled, {(name, layer): array})."""
+    def forward(self, tokens, keep: Optional[Iterable[Tuple[str, int]]] = None, threads: int = 0,
+                vectors: Optional[np.ndarray] = None):
+        """CPUReference.forward for one sequence -> (pooled, {(name, layer): array}). With `vectors`
+        ([rows, hidden] fp32), a token id -(r + 1) is row r of it, entered unscaled."""
         t = np.ascontiguousarray(tokens, dtype=np.int32)
+        vec = None if vectors is None else np.ascontiguousarray(vectors, dtype=np.float32).reshape(-1, self.hidden)
         pooled = np.zeros(self.out_dims, dtype=np.float32)
         want = set(keep or [])
         traces: Dict[Tuple[str, int], np.ndarray] = {}
@@ -106,8 +111,9 @@ class OracleModel:
                 traces[key] = np.ctypeslib.as_array(data, shape=(count,)).copy()
 
         fn = TRACE_FN(cb)
-        rc = lib.ora_forward(self.h, t.ctypes.data_as(C.POINTER(C.c_int32)), t.size, _f(pooled),
-                             fn if want else TRACE_FN(), None, threads)
+        rc = lib.ora_forward_rows(self.h, t.ctypes.data_as(C.POINTER(C.c_int32)), t.size,
+                                  _f(vec) if vec is not None else None, 0 if vec is None else vec.shape[0], _f(pooled),
+                                  fn if want else TRACE_FN(), None, threads)
         if rc != 0:
             raise ValueError(f"ora_forward failed ({rc})")
         return pooled, traces

@@ -134,8 +134,9 @@ def attention(q, k, v, window: int) -> np.ndarray:
     return np.einsum("hij,jhd->ihd", p, vv)
 
 
-def forward(g: Gguf, tokens: np.ndarray, keep: Tuple = ()) -> Tuple[np.ndarray, Dict]:
-    """Mean-pooled, unnormalised output for one sequence, float64; keep = (name, layer) traces."""
+def forward(g: Gguf, tokens: np.ndarray, keep: Tuple = (), vectors=None) -> Tuple[np.ndarray, Dict]:
+    """Mean-pooled, unnormalised output for one sequence, float64; keep = (name, layer) traces.
+    A token id -(r + 1) is row r of `vectors`, entered unscaled (CPUReference.swift:197-199)."""
     a = "gemma-embedding2."
     m = g.meta
     L, d, H = m[a + "block_count"], m[a + "embedding_length"], m[a + "attention.head_count"]
@@ -158,10 +159,14 @@ def forward(g: Gguf, tokens: np.ndarray, keep: Tuple = ()) -> Tuple[np.ndarray, 
     emb = g.raw("token_embd.weight").reshape(-1, d // 32 * 34)
     rows = []
     for t in tokens:
+        if t < 0:
+            rows.append(None)
+            continue
         blk = emb[t].reshape(-1, 34)
         dd = blk[:, :2].copy().view(np.float16).astype(np.float64)
-        rows.append((dd * blk[:, 2:].view(np.int8)).reshape(-1))
-    x = np.stack(rows) * np.sqrt(np.float32(d)).astype(np.float64)
+        rows.append((dd * blk[:, 2:].view(np.int8)).reshape(-1) * np.sqrt(np.float32(d)).astype(np.float64))
+    x = np.stack([np.asarray(vectors, np.float64).reshape(-1, d)[-t - 1] if r is None else r
+                  for t, r in zip(tokens, rows)])
     tr("inp_scaled", -1, x)
     if ple:
         pl = m[a + "embedding_length_per_layer_input"]

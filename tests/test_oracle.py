@@ -256,6 +256,36 @@ def test_forward_per_layer_inputs_vs_float64(tiny_ple_gguf):
             assert not np.allclose(tr[("pe_in", 1)], tr[("l_out", 1)])
 
 
+def test_forward_vector_rows(tiny_gguf, tiny_ple_gguf):
+    """Vector rows (CPUReference.swift:190-202): an id -(r + 1) enters row r of the vectors unscaled.
+    A vector row equal to a token's scaled embedding row gives that token's bits exactly (a scaled
+    vector or a shifted row index does not), and random vector rows agree with float64."""
+    import gemma_embed as ge
+    for path in (tiny_gguf, tiny_ple_gguf):
+        g = npref.Gguf(path)
+        with ora.OracleModel(path) as m:
+            d = m.hidden
+            toks = ge.synth_tokens(31, 2, m.vocab, 12)
+            emb = g.tensor("token_embd.weight").astype(np.float32) * np.sqrt(np.float32(d))
+            vec = np.stack([emb[toks[5]], emb[toks[3]], emb[toks[9]]]).astype(np.float32)
+            mixed = toks.copy()
+            mixed[3], mixed[5], mixed[9] = -2, -1, -3
+            a, ta = m.forward(toks, keep=[("l_out", 1)])
+            b, tb = m.forward(mixed, keep=[("l_out", 1)], vectors=vec)
+            assert np.array_equal(a, b) and np.array_equal(ta[("l_out", 1)], tb[("l_out", 1)])
+            rnd = np.random.default_rng(5).standard_normal((4, d)).astype(np.float32) * 3
+            seq = np.array([2, 7, -1, -2, -3, -4, 9, 1], np.int32)
+            pooled, tr = m.forward(seq, keep=[("inp_scaled", -1), ("l_out", 1)], vectors=rnd)
+            want, wtr = npref.forward(g, seq, keep=(("inp_scaled", -1), ("l_out", 1)), vectors=rnd)
+            assert np.array_equal(tr[("inp_scaled", -1)].reshape(8, d)[2:6], rnd)
+            assert np.abs(pooled - want).max() < 2e-4 * np.abs(want).max()
+            assert np.abs(tr[("l_out", 1)] - wtr[("l_out", 1)]).max() < 2e-4 * np.abs(wtr[("l_out", 1)]).max()
+            with pytest.raises(ValueError):
+                m.forward(seq, vectors=rnd[:3])  # -4 names a fourth row
+            with pytest.raises(ValueError):
+                m.forward(seq)
+
+
 def test_forward_rejects_bad_tokens(tiny_gguf):
     with ora.OracleModel(tiny_gguf) as m:
         with pytest.raises(ValueError):
