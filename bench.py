@@ -147,6 +147,34 @@ def vision_variant(tmp: str, reps: int):
             "algorithmic_flops": gemm + attn, "kernels": kernels}
 
 
+def image_embed_variant(tmp: str, text_path: str, reps: int):
+    """The whole image embedding (MetalForward.run(images:)): config 5's 8 images through the tower,
+    then each image's [bos, <|image>, 256 vectors, <image|>, eos] (260 rows) through the 24-layer
+    config-2 text tower, whose width is the tower's projection width. GPU time of both towers per
+    batch (median), patches already in HBM when it starts (the patch upload precedes it)."""
+    import numpy as np
+    import gemma_embed as ge
+    v = VIT
+    grids = [(v["grid"], v["grid"])] * v["images"]
+    patches = ge.image_patches(52, grids, v["area"])
+    markers = [2, 255998, 255999, 1]
+    model = ge.EmbeddingModel.load(text_path)
+    try:
+        ctx = model.context
+        ctx.vision_load(os.path.join(tmp, "config5_vision.gguf"))
+        for _ in range(2):
+            ctx.image_forward(patches, grids, markers)
+        secs = sorted(ctx.image_forward(patches, grids, markers)[1] for _ in range(reps))
+        pooled, _ = ctx.image_forward(patches, grids, markers)
+        if pooled.shape != (v["images"], 768) or not np.all(np.isfinite(pooled)):
+            raise SystemExit("bad image-embedding output")
+    finally:
+        model.close()
+    ms = secs[len(secs) // 2] * 1e3
+    return {"workload": "config5 tower + config-2 text tower over 8 x 260 rows (vector rows from the tower in HBM)",
+            "images_per_s": round(v["images"] / (ms * 1e-3), 2), "ms_per_batch": round(ms, 3)}
+
+
 def reference_shapes_variant(tmp: str, reps: int):
     """The reference's own architecture at its real shapes (d 512, per-layer inputs; synthetic
     weights) on the shapes of its published benchmarks (an 8 x 1024-token pack in
@@ -426,6 +454,11 @@ def main():
     log(f"config 4 (4 x 8192): {long_ms:.2f} ms/step, {long_rate:,.0f} tok/s")
 
     vision = vision_variant(tmp, max(3, args.steps // 2))
+    image_embed = None
+    if not args.model:  # the synthetic config-2 text tower is 768 wide, the tower's projection width
+        image_embed = image_embed_variant(tmp, path, max(3, args.steps // 2))
+        log(f"image embedding (tower + text tower, 8 images): {image_embed['ms_per_batch']:.2f} ms/batch, "
+            f"{image_embed['images_per_s']:.1f} images/s")
     ref_shapes = reference_shapes_variant(tmp, max(3, args.steps // 4))
     log(f"reference shapes: 8 x 1024 in {ref_shapes['pack_8x1024_s'] * 1e3:.2f} ms "
         f"({ref_shapes['pack_8x1024_tokens_per_s']:,.0f} tok/s), 1 x 64 call {ref_shapes['call_1x64_ms']:.2f} ms")
@@ -465,6 +498,7 @@ def main():
                      "config4_4x8192": {"tokens_per_s": round(long_rate, 1), "ms_per_step": round(long_ms, 3),
                                         "tflops": round(long_flops / (long_ms * 1e-3) / 1e12, 1)},
                      "config5_vision_8_images": vision,
+                     "image_embedding_8_images": image_embed,
                      "reference_shapes_host_api": ref_shapes},
     }
     model.close()
