@@ -168,6 +168,12 @@ ATTN_CASES = [  # (lengths, H, KV, hd, half_window): the reference's packed-leng
     ([96, 40], 2, 1, 128, 8),
     ([257], 4, 4, 128, 0),
     ([130, 64], 4, 1, 128, 32),  # four query heads per KV head: the 32-query-wave kernel
+    # the reference's long mixes at both head dims and both GQA ratios, with and without a window
+    ([2048], 3, 1, 256, 0),
+    ([2048, 3, 1024, 7], 4, 2, 256, 256),
+    ([2048, 3, 1024, 7], 4, 1, 512, 0),
+    ([2048, 3, 1024, 7], 4, 2, 512, 256),
+    ([1024, 5], 4, 1, 512, 256),
 ]
 
 
