@@ -103,8 +103,9 @@ int ge_forward(ge_ctx* ctx, const int32_t* tokens, const int32_t* positions, int
 /* The workspace's `vectors` buffer (Metal/MetalForward.swift:137,165), filled from the host: fp32
  * [n_rows][width] copied into HBM, where the batches of ge_forward, ge_forward_trace and
  * ge_batch_stage find the rows their negative ids name. Rows are used only while `width` equals
- * the model's hidden size; n_rows 0 clears them. Kept until replaced; replacing them drops a
- * staged batch that read the old ones. */
+ * the model's hidden size; n_rows 0 clears them. Kept until replaced. A staged batch reads the
+ * rows present when it runs; a replacement that needs a larger buffer drops a staged batch that
+ * reads them (run it again after staging it again). */
 int ge_set_vectors(ge_ctx* ctx, const float* rows, int32_t n_rows, int32_t width);
 
 /* Per-layer parity (CPUReference.forward's trace, Model/CPUReference.swift:204-276, and
