@@ -28,6 +28,7 @@
 // Inputs are synthetic: Q8_0 rows with random int8 quants and fp16 scales, activations uniform
 // in [-0.5, 0.5). Each call of the GeGLU entry point also interleaves the two matrices and builds
 // their fragment-order copy; a profile reads the GEMM kernel's own rows.
+#include <algorithm>
 #include <chrono>
 #include <cstdint>
 #include <cstdio>
@@ -270,6 +271,60 @@ int probe_reference_shapes(int reps) {
     return 0;
 }
 
+// The whole image embedding: config 5's 8 images through the tower, then each image's 260 framed
+// rows through the 24-layer config-2 text tower (ge_image_forward), GPU time of both towers.
+int probe_image_embed(int reps) {
+    uint8_t pattern[24];
+    for (int i = 0; i < 24; i++) pattern[i] = (i % 6 == 5) ? 0 : 1;
+    ge_synth_spec spec{};
+    spec.layers = 24, spec.hidden = 768, spec.heads = 3, spec.feed_forward = 1152, spec.out_dims = 768;
+    spec.per_layer_input = 0, spec.vocab = 262144, spec.sliding_window = 512;
+    spec.head_dim_swa = 256, spec.head_dim_global = 256, spec.kv_heads_swa = 1, spec.kv_heads_global = 1;
+    spec.eps = 1e-6f, spec.rope_base = 1e6f, spec.rope_base_swa = 1e4f, spec.pattern = pattern, spec.seed = 4;
+    char err[512] = {0};
+    const char* path = "/tmp/ge_probe_config2.gguf";
+    if (ge_synth_write_gguf(path, &spec, err, sizeof err) != 0) {
+        std::fprintf(stderr, "ge_probe: synth: %s\n", err);
+        return 1;
+    }
+    ge_load_options lo{0, 8192, 1};
+    ge_model* m = nullptr;
+    if (ge_model_load(path, &lo, &m, err, sizeof err) != 0) {
+        std::fprintf(stderr, "ge_probe: load: %s\n", err);
+        return 1;
+    }
+    std::remove(path);
+    ge_ctx* c = ge_model_context(m);
+    ge_synth_vision_spec vs{};
+    vs.layers = 16, vs.hidden = 1152, vs.heads = 16, vs.feed_forward = 4304, vs.patch_size = 16;
+    vs.merge = 3, vs.proj_dims = 768, vs.positions = 48, vs.eps = 1e-6f, vs.ffn_down_type = 0, vs.seed = 5;
+    const char* vpath = "/tmp/ge_probe_config5_vision.gguf";
+    if (ge_synth_write_vision_gguf(vpath, &vs, err, sizeof err) != 0 || ge_vision_load(c, vpath, err, sizeof err) != 0) {
+        std::fprintf(stderr, "ge_probe: vision: %s\n", err);
+        return 1;
+    }
+    std::remove(vpath);
+    const int images = 8, grid = 48, area = 768;
+    std::vector<float> patches(size_t(images) * grid * grid * area), pooled(size_t(images) * 768);
+    ge_synth_uniform(52, -1.0f, 1.0f, int64_t(patches.size()), patches.data());
+    std::vector<ge_image_grid> grids(images, ge_image_grid{grid, grid});
+    const int32_t markers[4] = {2, 255998, 255999, 1};
+    std::vector<double> secs;
+    for (int r = 0; r < reps + 2; r++) {
+        double s = 0;
+        if (ge_image_forward(c, patches.data(), images * grid * grid, grids.data(), images, markers, pooled.data(), &s) != 0)
+            return fail(c, "image forward");
+        if (r >= 2) secs.push_back(s);
+    }
+    std::sort(secs.begin(), secs.end());
+    const double ms = secs[secs.size() / 2] * 1e3;
+    std::printf("image embedding (config 5 tower + config-2 text tower): %.3f ms per batch of %d images, %.1f images/s\n",
+                ms, images, images / (ms * 1e-3));
+    std::fflush(stdout);
+    ge_model_free(m);
+    return 0;
+}
+
 int probe_calibrate(ge_ctx* c) {
     const size_t n = size_t(1) << 28;
     void* src = ge_dev_alloc(c, 2 * n);
@@ -290,9 +345,10 @@ int main(int argc, char** argv) {
     const int reps = argc > 2 ? std::atoi(argv[2]) : 20;
     if (std::strcmp(what, "embed") == 0) return reps < 1 || reps > 10000 ? 2 : probe_embed(reps);
     if (std::strcmp(what, "reference_shapes") == 0) return reps < 1 || reps > 10000 ? 2 : probe_reference_shapes(reps);
+    if (std::strcmp(what, "image_embed") == 0) return reps < 1 || reps > 10000 ? 2 : probe_image_embed(reps);
     if (std::strcmp(what, "gate_up") != 0 && std::strcmp(what, "attention") != 0 && std::strcmp(what, "calibrate") != 0 &&
         std::strcmp(what, "vision") != 0) {
-        std::fprintf(stderr, "usage: ge_probe gate_up|attention|embed|vision|reference_shapes [reps] | ge_probe calibrate\n");
+        std::fprintf(stderr, "usage: ge_probe gate_up|attention|embed|vision|reference_shapes|image_embed [reps] | ge_probe calibrate\n");
         return 2;
     }
     if (reps < 1 || reps > 10000) {
