@@ -804,6 +804,253 @@ hipError_t launch_attention_v2(hipStream_t s, const uint16_t* q, const uint16_t*
     return attention_v2_dispatch_g<256>(s, q, k, vt, vt_cols, o, work, n_work, H, KV, half_window, scale, item_queries);
 }
 
+// ============================================================================ attention, split-precision scores
+//
+// For the layers whose QKV projection runs at split precision (head dim 512): q and k arrive as
+// fp16 pairs with hi + lo the fp32 value (hi = fp16(x), lo = fp16(x - hi)), and a score is
+// q_hi.k_hi + q_lo.k_hi + q_hi.k_lo on v_mfma_f32_16x16x32_f16 (the dropped q_lo.k_lo is below
+// 2^-22 of it). Scores of two RMS-normed 512-wide vectors at attention scale 1 reach several
+// hundred; with plain fp16 operands (2^-11 relative per element) they move by ~0.02, which
+// shifts the weights of two nearly tied keys by a few percent (reference: fp32 scores,
+// Shaders/Attention.metal:172-188, Model/CPUReference.swift:129-160).
+//
+// The fragment layouts, the key order of the S^T tiles, the masks and the lazily rescaled
+// log2-domain softmax are attention_v3_kernel's. One 16-query tile per wave, the G query heads
+// of one KV head as the workgroup's G waves: a wave's q_hi and q_lo fragments (16 x 512 each)
+// and its 16 x 512 output accumulators take 256 registers, so a SIMD runs one wave. LDS holds
+// K_hi and K_lo of a 32-key block in two stages (block it + 1 copies while block it is used)
+// and V^T of one block in one buffer, refilled after the P.V product while the next block's
+// scores are computed: 2 x 64 KB + 32 KB at head dim 512.
+namespace attns {
+constexpr int BKV = 32;  // keys per block
+}  // namespace attns
+
+template <int HD>
+constexpr int attention_split_lds_bytes() { return 2 * (2 * attns::BKV * HD * 2) + attns::BKV * HD * 2; }
+
+template <int HD, int G>
+__global__ __launch_bounds__(G * 64) void attention_split_kernel(const uint16_t* __restrict__ Qg,
+                                                                 const uint16_t* __restrict__ QLg,
+                                                                 const uint16_t* __restrict__ Kg,
+                                                                 const uint16_t* __restrict__ KLg,
+                                                                 const uint16_t* __restrict__ VTg,
+                                                                 uint16_t* __restrict__ Og,
+                                                                 const AttnWork* __restrict__ work, int H, int KV,
+                                                                 int vt_cols, int hw, float scale_log2) {
+    constexpr int BKV = attns::BKV, KS = HD / 32, DT = HD / 16;
+    constexpr int K_BYTES = BKV * HD * 2;  // one plane (K_hi or K_lo) of a block
+    constexpr int KCH = K_BYTES / 1024;    // its chunks (ks, m)
+    constexpr int KSTAGE = 2 * K_BYTES;    // K_hi, then K_lo
+    constexpr int KPW = 2 * KCH / G, VPW = DT / G;  // copies per wave per block: K planes, V^T
+    static_assert(KCH == 2 * KS && (2 * KCH) % G == 0 && DT % G == 0, "chunk counts");
+    static_assert(KPW + VPW < 64 && KS * 2 + KPW + VPW < 64, "outstanding copies fit the vmcnt counter");
+    extern __shared__ __attribute__((aligned(1024))) unsigned char ldss[];
+    unsigned char* const vbuf = ldss + 2 * KSTAGE;
+
+    // XCD-aware order, as in attention_v2_kernel.
+    const int nb = int(gridDim.x), full = nb / 8 * 8, bx = int(blockIdx.x);
+    const int widx = bx < full ? (bx % 8) * (full / 8) + bx / 8 : bx;
+    const int seq_start = __builtin_amdgcn_readfirstlane(int(work[widx].seq_start));
+    const int len = __builtin_amdgcn_readfirstlane(int(work[widx].seq_len));
+    const int q0 = __builtin_amdgcn_readfirstlane(int(work[widx].q0)) + int(blockIdx.z) * 16;
+    const int vt_start = __builtin_amdgcn_readfirstlane(int(work[widx].vt_start));
+    const int kvh = blockIdx.y;
+    const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(int(threadIdx.x >> 6));
+    const int h = kvh * G + wave;
+    const int l16 = lane & 15, g4 = lane >> 4;
+    const int qi = q0 + l16;
+    const int qStride = H * HD, kvStride = KV * HD;
+
+    int kstart = 0, kend = len;
+    if (hw > 0) {
+        kstart = max(q0 - hw, 0);
+        kend = min(q0 + 16 + hw, len);
+    }
+    kstart = kstart / BKV * BKV;
+    const int nblocks = (kend - kstart + BKV - 1) / BKV;
+
+    // Buffer resources over the sequence's rows (reads past them return zeros).
+    const uint32_t kbytes = uint32_t(((len - 1) * kvStride + HD) * 2);
+    const __amdgpu_buffer_rsrc_t kr = buffer_rsrc(Kg + (size_t)seq_start * kvStride + kvh * HD, kbytes);
+    const __amdgpu_buffer_rsrc_t klr = buffer_rsrc(KLg + (size_t)seq_start * kvStride + kvh * HD, kbytes);
+    const __amdgpu_buffer_rsrc_t vr = buffer_rsrc(VTg + (size_t)kvh * HD * vt_cols + vt_start,
+                                                  uint32_t(((HD - 1) * vt_cols + (vt_cols - vt_start)) * 2));
+    const uint32_t klane = uint32_t(((8 * (l16 >> 2) + (lane & 3)) * kvStride + 8 * g4) * 2);
+    const uint32_t vlane = uint32_t((l16 * vt_cols + 8 * g4) * 2);
+    // K chunk c of a block: plane c / KCH (hi, lo), (ks, m) = (c % KCH / 2, c % 2); wave w copies
+    // chunks w, w + G, ...; V^T chunk dt likewise.
+#define AS_KISSUE(kb, b)                                                                                   \
+    do {                                                                                                   \
+        _Pragma("unroll") for (int i = 0; i < KPW; i++) {                                                  \
+            const int c = wave + i * G, pl = c / KCH, cc = c % KCH;                                        \
+            lds_copy16(pl ? klr : kr, ldss + (b) * KSTAGE + pl * K_BYTES + cc * 1024,                      \
+                       klane + uint32_t(((kb) + 4 * (cc & 1)) * kvStride * 2 + (cc >> 1) * 64), 0);        \
+        }                                                                                                  \
+    } while (0)
+#define AS_VISSUE(kb)                                                                                      \
+    do {                                                                                                   \
+        _Pragma("unroll") for (int i = 0; i < VPW; i++) {                                                  \
+            const int c = wave + i * G;                                                                    \
+            lds_copy16(vr, vbuf + c * 1024, vlane + uint32_t(c * 16 * vt_cols * 2 + (kb) * 2), 0);        \
+        }                                                                                                  \
+    } while (0)
+
+    // This wave's query fragments, hi and lo (B operands of S^T = K Q^T): lane l: query qi (rows
+    // past the sequence re-read its last row; their outputs are never stored), head dims
+    // 32 ks + 8 (l / 16).
+    half8_t qh[KS], ql[KS];
+    {
+        const uint32_t qbytes = uint32_t(((len - 1) * qStride + HD) * 2);
+        const __amdgpu_buffer_rsrc_t qr = buffer_rsrc(Qg + (size_t)seq_start * qStride + h * HD, qbytes);
+        const __amdgpu_buffer_rsrc_t qlr = buffer_rsrc(QLg + (size_t)seq_start * qStride + h * HD, qbytes);
+        const uint32_t qo = uint32_t((min(qi, len - 1) * qStride + 8 * g4) * 2);
+#pragma unroll
+        for (int ks = 0; ks < KS; ks++) {
+            qh[ks] = __builtin_bit_cast(half8_t, __builtin_amdgcn_raw_buffer_load_b128(qr, qo + ks * 64, 0, 0));
+            ql[ks] = __builtin_bit_cast(half8_t, __builtin_amdgcn_raw_buffer_load_b128(qlr, qo + ks * 64, 0, 0));
+        }
+    }
+
+    float4_t o[DT];
+#pragma unroll
+    for (int i = 0; i < DT; i++) o[i] = float4_t{0.0f, 0.0f, 0.0f, 0.0f};
+    float m_run = -INFINITY, l_run = 0.0f;
+
+    if (nblocks > 0) {
+        AS_KISSUE(kstart, 0);
+        AS_VISSUE(kstart);
+    }
+    for (int it = 0; it < nblocks; it++) {
+        const int kb = kstart + it * BKV, b = it & 1;
+        const bool more = it + 1 < nblocks;
+        // K(it) has landed once only V(it)'s copies (issued after it) may be in flight; the
+        // barrier covers every wave's copies and frees the other K stage (read in block it - 1).
+        wait_vmcnt<VPW>();
+        wait_lgkmcnt0();
+        workgroup_barrier();
+        if (more) AS_KISSUE(kb + BKV, b ^ 1);
+        const unsigned char* const kf = ldss + b * KSTAGE + lane * 16;
+        // S^T tiles m = 0, 1: the hi.hi products in one chain, the two correction products in
+        // another; K fragments (hi and lo) read PF k-steps ahead
+        constexpr int PF = 2, RING = PF + 1;
+        float4_t s0 = {0.0f, 0.0f, 0.0f, 0.0f}, s1 = s0, c0 = s0, c1 = s0;
+        half8_t kh[RING][2], kl[RING][2];
+#pragma unroll
+        for (int f = 0; f < PF; f++)
+#pragma unroll
+            for (int m = 0; m < 2; m++) {
+                kh[f][m] = *reinterpret_cast<const half8_t*>(kf + (2 * f + m) * 1024);
+                kl[f][m] = *reinterpret_cast<const half8_t*>(kf + K_BYTES + (2 * f + m) * 1024);
+            }
+#pragma unroll
+        for (int ks = 0; ks < KS; ks++) {
+            if (ks + PF < KS)
+#pragma unroll
+                for (int m = 0; m < 2; m++) {
+                    kh[(ks + PF) % RING][m] = *reinterpret_cast<const half8_t*>(kf + (2 * (ks + PF) + m) * 1024);
+                    kl[(ks + PF) % RING][m] = *reinterpret_cast<const half8_t*>(kf + K_BYTES + (2 * (ks + PF) + m) * 1024);
+                }
+            __builtin_amdgcn_sched_barrier(0);
+            const int r = ks % RING;
+            s0 = __builtin_amdgcn_mfma_f32_16x16x32_f16(kh[r][0], qh[ks], s0, 0, 0, 0);
+            s1 = __builtin_amdgcn_mfma_f32_16x16x32_f16(kh[r][1], qh[ks], s1, 0, 0, 0);
+            c0 = __builtin_amdgcn_mfma_f32_16x16x32_f16(kh[r][0], ql[ks], c0, 0, 0, 0);
+            c1 = __builtin_amdgcn_mfma_f32_16x16x32_f16(kh[r][1], ql[ks], c1, 0, 0, 0);
+            c0 = __builtin_amdgcn_mfma_f32_16x16x32_f16(kl[r][0], qh[ks], c0, 0, 0, 0);
+            c1 = __builtin_amdgcn_mfma_f32_16x16x32_f16(kl[r][1], qh[ks], c1, 0, 0, 0);
+        }
+        s0 += c0;
+        s1 += c1;
+        // this lane's scores: keys kb + 8 g4 + e, e = 0..7
+        float sc[8] = {s0[0], s0[1], s0[2], s0[3], s1[0], s1[1], s1[2], s1[3]};
+        const bool inside = kb + BKV <= len && (hw == 0 || (kb >= q0 + 15 - hw && kb + BKV - 1 <= q0 + hw));
+        if (!inside) {
+            const int lim = hw > 0 ? hw : 1 << 30;
+#pragma unroll
+            for (int e = 0; e < 8; e++) {
+                const int key = kb + 8 * g4 + e;
+                const bool valid = (key < len) & (abs(qi - key) <= lim);
+                sc[e] = valid ? sc[e] : -INFINITY;
+            }
+        }
+        const float lmax =
+            fmaxf(fmaxf(fmaxf(sc[0], sc[1]), fmaxf(sc[2], sc[3])), fmaxf(fmaxf(sc[4], sc[5]), fmaxf(sc[6], sc[7])));
+        // lazy rescaling, as in attention_v3_kernel
+        if (__builtin_amdgcn_ballot_w64(lmax * scale_log2 > m_run + 8.0f)) {
+            const float bmax = max_over_key_groups(lmax) * scale_log2;
+            const float m_new = fmaxf(m_run, bmax);
+            const float alpha = m_new == -INFINITY ? 1.0f : __builtin_amdgcn_exp2f(m_run - m_new);
+            l_run *= alpha;
+#pragma unroll
+            for (int i = 0; i < DT; i++) o[i] *= alpha;
+            m_run = m_new;
+        }
+        const float m_ref = m_run == -INFINITY ? 0.0f : m_run;
+        float sum = 0.0f;
+        half8_t pb;
+#pragma unroll
+        for (int e = 0; e < 8; e++) {
+            const float p = __builtin_amdgcn_exp2f(__builtin_fmaf(sc[e], scale_log2, -m_ref));
+            sum += p;
+            pb[e] = _Float16(p);
+        }
+        l_run += sum;
+        // V(it) has landed once only K(it + 1)'s copies may be in flight.
+        if (more)
+            wait_vmcnt<KPW>();
+        else
+            wait_vmcnt<0>();
+        wait_lgkmcnt0();
+        workgroup_barrier();
+        const unsigned char* const vf = vbuf + lane * 16;
+        half8_t va[RING];
+#pragma unroll
+        for (int f = 0; f < PF; f++) va[f] = *reinterpret_cast<const half8_t*>(vf + f * 1024);
+#pragma unroll
+        for (int dt = 0; dt < DT; dt++) {
+            if (dt + PF < DT) va[(dt + PF) % RING] = *reinterpret_cast<const half8_t*>(vf + (dt + PF) * 1024);
+            __builtin_amdgcn_sched_barrier(0);
+            o[dt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(va[dt % RING], pb, o[dt], 0, 0, 0);
+        }
+        if (more) {
+            // every wave's V^T reads are done before the buffer is refilled
+            wait_lgkmcnt0();
+            workgroup_barrier();
+            AS_VISSUE(kb + BKV);
+        }
+    }
+#undef AS_KISSUE
+#undef AS_VISSUE
+    wait_vmcnt<0>();
+    l_run = sum_over_key_groups(l_run);
+    if (qi >= len) return;
+    const float inv = l_run > 0.0f ? 1.0f / l_run : 0.0f;
+    _Float16* op = reinterpret_cast<_Float16*>(Og) + (size_t)(seq_start + qi) * qStride + h * HD + 4 * g4;
+#pragma unroll
+    for (int dt = 0; dt < DT; dt++) {
+        half4_t v4;
+#pragma unroll
+        for (int r = 0; r < 4; r++) v4[r] = _Float16(o[dt][r] * inv);
+        *reinterpret_cast<half4_t*>(op + dt * 16) = v4;
+    }
+}
+
+bool attention_split_supported(int hd, int H, int KV) { return hd == 512 && KV > 0 && H == 4 * KV; }
+
+hipError_t launch_attention_split(hipStream_t s, const uint16_t* q, const uint16_t* q_lo, const uint16_t* k,
+                                  const uint16_t* k_lo, const uint16_t* vt, int vt_cols, uint16_t* o, const AttnWork* work,
+                                  int n_work, int H, int KV, int hd, int half_window, float scale, int item_queries) {
+    if (n_work < 0 || !attention_split_supported(hd, H, KV) || half_window < 0 || vt_cols <= 0 || vt_cols % 8 ||
+        (item_queries != 16 && item_queries != 32 && item_queries != 64) || !q || !q_lo || !k || !k_lo || !vt || !o || !work)
+        return hipErrorInvalidValue;
+    if (n_work == 0) return hipSuccess;
+    const float scale_log2 = scale * 1.4426950408889634f;
+    const dim3 grid(n_work, KV, item_queries / 16);
+    launch_kernel(attention_split_kernel<512, 4>, grid, dim3(4 * 64), uint32_t(attention_split_lds_bytes<512>()), s, q, q_lo, k,
+                  k_lo, vt, o, work, H, KV, vt_cols, half_window, scale_log2);
+    return hipGetLastError();
+}
+
 // The image tower's attention: one query head per KV head, no window, heads stored padded (HD
 // dims of which the first HO are real). As attention_v3_kernel (the same K/V^T ring in LDS, the
 // same MFMAs and softmax), but each wave owns QT tiles of 16 queries, so every K and V^T fragment
@@ -1095,6 +1342,9 @@ hipError_t configure_kernels() {
     if (e == hipSuccess)
         e = hipFuncSetAttribute(reinterpret_cast<const void*>(&attention_v3_kernel<512, 4, 2>),
                                 hipFuncAttributeMaxDynamicSharedMemorySize, attention_v3_lds_bytes<512>());
+    if (e == hipSuccess)
+        e = hipFuncSetAttribute(reinterpret_cast<const void*>(&attention_split_kernel<512, 4>),
+                                hipFuncAttributeMaxDynamicSharedMemorySize, attention_split_lds_bytes<512>());
     if (e == hipSuccess) e = attention_configure_all<256, 256>();
     if (e == hipSuccess) e = attention_configure_all<512, 256>();
     return e;

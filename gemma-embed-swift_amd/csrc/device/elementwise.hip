@@ -156,6 +156,64 @@ hipError_t launch_residual_norm(hipStream_t s, float* x, const uint16_t* t16, fl
     return hipGetLastError();
 }
 
+// ============================================================================ split-precision norm
+//
+// h3 = [hi | lo | hi] per row, with y = rmsnorm(x) * w in fp32 (the value the other norm kernels
+// round to fp16, with the same lane order of the sum of squares), hi = fp16(y) and
+// lo = fp16(y - hi). Against a weight stored as [W_hi | W_hi | W_lo] over 3 d columns the GEMM
+// sums hi W_hi + lo W_hi + hi W_lo, which is y W to about 2^-20 relative instead of the 2^-11 of
+// fp16 operands (the dropped lo W_lo term is below 2^-22).
+template <int CH>
+__global__ __launch_bounds__(256) void norm_split_kernel(const float* __restrict__ x, const float* __restrict__ w,
+                                                         float eps, int T, int d, uint16_t* __restrict__ h3) {
+    const int row = blockIdx.x * 4 + (threadIdx.x >> 6), lane = threadIdx.x & 63;
+    if (row >= T) return;
+    float xv[CH][4];
+    float ss = 0.0f;
+#pragma unroll
+    for (int c = 0; c < CH; c++) {
+        const int e = c * 256 + lane * 4;
+        if (e < d) {
+            const float4 a = *reinterpret_cast<const float4*>(x + (size_t)row * d + e);
+            xv[c][0] = a.x, xv[c][1] = a.y, xv[c][2] = a.z, xv[c][3] = a.w;
+#pragma unroll
+            for (int j = 0; j < 4; j++) ss += xv[c][j] * xv[c][j];
+        }
+    }
+    ss = wave_sum(ss);
+    const float inv = 1.0f / sqrtf(ss / float(d) + eps);
+    uint16_t* out = h3 + (size_t)row * 3 * d;
+#pragma unroll
+    for (int c = 0; c < CH; c++) {
+        const int e = c * 256 + lane * 4;
+        if (e < d) {
+            half4_t hi, lo;
+#pragma unroll
+            for (int j = 0; j < 4; j++) {
+                const float y = xv[c][j] * inv * w[e + j];
+                hi[j] = _Float16(y);
+                lo[j] = _Float16(y - float(hi[j]));
+            }
+            *reinterpret_cast<half4_t*>(out + e) = hi;
+            *reinterpret_cast<half4_t*>(out + d + e) = lo;
+            *reinterpret_cast<half4_t*>(out + 2 * d + e) = hi;
+        }
+    }
+}
+
+hipError_t launch_norm_split(hipStream_t s, const float* x, const float* w, float eps, int T, int d, uint16_t* h3) {
+    if (T < 0 || d <= 0 || d % 4 != 0 || d > 1024 || !x || !w || !h3) return hipErrorInvalidValue;
+    if (T == 0) return hipSuccess;
+    const int blocks = (T + 3) / 4, CH = (d + 255) / 256;
+    switch (CH) {
+    case 1: launch_kernel(norm_split_kernel<1>, blocks, 256, 0, s, x, w, eps, T, d, h3); break;
+    case 2: launch_kernel(norm_split_kernel<2>, blocks, 256, 0, s, x, w, eps, T, d, h3); break;
+    case 3: launch_kernel(norm_split_kernel<3>, blocks, 256, 0, s, x, w, eps, T, d, h3); break;
+    default: launch_kernel(norm_split_kernel<4>, blocks, 256, 0, s, x, w, eps, T, d, h3); break;
+    }
+    return hipGetLastError();
+}
+
 // ============================================================================ QK norm + RoPE
 //
 // One wave per (token, head slot) of the fused QKV projection. Lane l owns elements
@@ -168,7 +226,8 @@ __global__ __launch_bounds__(256) void qk_norm_rope_kernel(const float* __restri
                                                            const float* __restrict__ k_norm, float eps,
                                                            const int32_t* __restrict__ positions,
                                                            const float* __restrict__ table, uint16_t* __restrict__ q,
-                                                           uint16_t* __restrict__ k, uint16_t* __restrict__ v) {
+                                                           uint16_t* __restrict__ k, uint16_t* __restrict__ v,
+                                                           uint16_t* __restrict__ q_lo, uint16_t* __restrict__ k_lo) {
     constexpr int C = HD / 128, HALF = HD / 2;
     const int slots = H + 2 * KV;
     const int item = blockIdx.x * 4 + (threadIdx.x >> 6), lane = threadIdx.x & 63;
@@ -186,13 +245,16 @@ __global__ __launch_bounds__(256) void qk_norm_rope_kernel(const float* __restri
     ss = wave_sum(ss);
     const float inv = 1.0f / sqrtf(ss / float(HD) + eps);
     uint16_t* dst;
+    uint16_t* dlo = nullptr;  // the split pair's low halves (q_lo / k_lo set)
     const float* w = nullptr;
     bool rope = true;
     if (slot < H) {
         dst = q + ((size_t)t * H + slot) * HD;
+        if (q_lo) dlo = q_lo + ((size_t)t * H + slot) * HD;
         w = q_norm;
     } else if (slot < H + KV) {
         dst = k + ((size_t)t * KV + (slot - H)) * HD;
+        if (k_lo) dlo = k_lo + ((size_t)t * KV + (slot - H)) * HD;
         w = k_norm;
     } else {
         dst = v + ((size_t)t * KV + (slot - H - KV)) * HD;
@@ -215,20 +277,24 @@ __global__ __launch_bounds__(256) void qk_norm_rope_kernel(const float* __restri
         }
         dst[i] = f2h(a);
         dst[HALF + i] = f2h(b);
+        if (dlo) {
+            dlo[i] = f2h(a - h2f(dst[i]));
+            dlo[HALF + i] = f2h(b - h2f(dst[HALF + i]));
+        }
     }
 }
 
 hipError_t launch_qk_norm_rope(hipStream_t s, const float* qkv, int T, int H, int KV, int hd, const float* q_norm,
                                const float* k_norm, float eps, const int32_t* positions, const float* rope_table,
-                               uint16_t* q, uint16_t* k, uint16_t* v) {
-    if (T < 0 || H <= 0 || KV <= 0) return hipErrorInvalidValue;
+                               uint16_t* q, uint16_t* k, uint16_t* v, uint16_t* q_lo, uint16_t* k_lo) {
+    if (T < 0 || H <= 0 || KV <= 0 || (q_lo == nullptr) != (k_lo == nullptr)) return hipErrorInvalidValue;
     if (T == 0) return hipSuccess;
     const long items = (long)T * (H + 2 * KV);
     const int blocks = int((items + 3) / 4);
     switch (hd) {
-    case 128: launch_kernel(qk_norm_rope_kernel<128>, blocks, 256, 0, s, qkv, T, H, KV, q_norm, k_norm, eps, positions, rope_table, q, k, v); break;
-    case 256: launch_kernel(qk_norm_rope_kernel<256>, blocks, 256, 0, s, qkv, T, H, KV, q_norm, k_norm, eps, positions, rope_table, q, k, v); break;
-    case 512: launch_kernel(qk_norm_rope_kernel<512>, blocks, 256, 0, s, qkv, T, H, KV, q_norm, k_norm, eps, positions, rope_table, q, k, v); break;
+    case 128: launch_kernel(qk_norm_rope_kernel<128>, blocks, 256, 0, s, qkv, T, H, KV, q_norm, k_norm, eps, positions, rope_table, q, k, v, q_lo, k_lo); break;
+    case 256: launch_kernel(qk_norm_rope_kernel<256>, blocks, 256, 0, s, qkv, T, H, KV, q_norm, k_norm, eps, positions, rope_table, q, k, v, q_lo, k_lo); break;
+    case 512: launch_kernel(qk_norm_rope_kernel<512>, blocks, 256, 0, s, qkv, T, H, KV, q_norm, k_norm, eps, positions, rope_table, q, k, v, q_lo, k_lo); break;
     default: return hipErrorInvalidValue;
     }
     return hipGetLastError();

@@ -106,11 +106,16 @@ hipError_t launch_embed_norm(hipStream_t s, const Q8Dev& table, const int32_t* t
 hipError_t launch_residual_norm(hipStream_t s, float* x, const uint16_t* t16, float t_eps, const float* w,
                                 float out_scale, const float* next_w, float eps, int T, int d, uint16_t* h);
 
+// h3 fp16 [T][3 d] = [hi | lo | hi] of y = rmsnorm(x) * w (hi = fp16(y), lo = fp16(y - hi)): the
+// input of a split-precision GEMM against [W_hi | W_hi | W_lo]. d a multiple of 4, at most 1024.
+hipError_t launch_norm_split(hipStream_t s, const float* x, const float* w, float eps, int T, int d, uint16_t* h3);
+
 // qkv fp32 [T][(H + 2 KV) hd] -> q fp16 [T][H][hd], k, v fp16 [T][KV][hd]: weighted RMSNorm and
 // NeoX RoPE on q and k, unweighted RMSNorm on v.
+// With q_lo and k_lo set, q and k are also written as split pairs: q_lo = fp16(q - fp16(q)).
 hipError_t launch_qk_norm_rope(hipStream_t s, const float* qkv, int T, int H, int KV, int hd, const float* q_norm,
                                const float* k_norm, float eps, const int32_t* positions, const float* rope_table,
-                               uint16_t* q, uint16_t* k, uint16_t* v);
+                               uint16_t* q, uint16_t* k, uint16_t* v, uint16_t* q_lo = nullptr, uint16_t* k_lo = nullptr);
 
 // The same as launch_qk_norm_rope (head dims 128 and 256, H + 2 KV in {3, 4, 5, 6, 8, 10}) on the
 // QKV projection stored as fp16 qkv16 = qkv * c for a power of two c, with eps = eps_model * c^2;
@@ -136,6 +141,15 @@ bool attention_v2_supported(int hd, int H, int KV);
 hipError_t launch_attention_v2(hipStream_t s, const uint16_t* q, const uint16_t* k, const uint16_t* vt, int vt_cols,
                                uint16_t* o, const AttnWork* work, int n_work, int H, int KV, int hd, int half_window,
                                float scale, int item_queries = kAttnQueriesV2);
+
+// Attention with split-precision scores for the split-precision layers: q and k as fp16 pairs
+// (hi, lo) with hi + lo their fp32 values, same layouts as q and k; scores q_hi.k_hi + q_lo.k_hi +
+// q_hi.k_lo. Head dim 512 with 4 query heads per KV head; work items of item_queries (16, 32 or
+// 64) query rows with vt_start as for launch_attention_v2.
+bool attention_split_supported(int hd, int H, int KV);
+hipError_t launch_attention_split(hipStream_t s, const uint16_t* q, const uint16_t* q_lo, const uint16_t* k,
+                                  const uint16_t* k_lo, const uint16_t* vt, int vt_cols, uint16_t* o, const AttnWork* work,
+                                  int n_work, int H, int KV, int hd, int half_window, float scale, int item_queries);
 
 // The same attention over heads stored padded: q [T][H][hp], k [T][KV][hp] and vt [KV * hp][vt_cols]
 // hold hd real dims per head and zeros past them; out [T][H][hd]. Supported: hp 96 with hd 72

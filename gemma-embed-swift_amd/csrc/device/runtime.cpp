@@ -101,6 +101,14 @@ hipEvent_t take_event(ge_ctx* c) {
     return e;
 }
 
+// Waits for every stream of the context: its own and the part streams of split forwards.
+void drain(ge_ctx* c) {
+    hip_check(hipStreamSynchronize(c->stream), "hipStreamSynchronize");
+    for (int p = 0; p < kMaxParts; p++)
+        if (c->part_stream[p] && c->part_stream[p] != c->stream)
+            hip_check(hipStreamSynchronize(c->part_stream[p]), "hipStreamSynchronize");
+}
+
 void resolve_profile(ge_ctx* c) {
     for (auto& p : c->prof_pending) {
         hip_check(hipEventSynchronize(p.b), "hipEventSynchronize");
@@ -211,6 +219,9 @@ Q8Dev upload_q8(ge_ctx* c, const HostQ8& h, const char* what, bool gemm_weight) 
 
 float half_bits_to_float(uint16_t b) { return float(__builtin_bit_cast(_Float16, b)); }
 
+Q8Dev upload_dense_fragments(const std::vector<uint16_t>& dense, int rows, int cols, const char* what,
+                             std::vector<void*>& allocs);
+
 // A [cols, rows] weight of any accepted type as fp16 MFMA fragments (Q8Dev::fh order) with the
 // columns zero-padded to cols_pad: values are rounded to fp16 once (Q8_0: fp16 of q * d, as the
 // device dequantisation does; F16 as stored; F32 and BF16 rounded to nearest even).
@@ -253,23 +264,47 @@ Q8Dev upload_fragments(const ge_tensor_desc* t, int64_t cols, int64_t rows, int 
         for (int64_t i = 0; i < cols; i++)
             dense[size_t(r) * cols_pad + i] = __builtin_bit_cast(uint16_t, _Float16(row[size_t(i)]));
     }
-    // fragment order: 32-row block j, 16-wide k-step s: 512 halves, lane l's 8 halves are row
-    // 32 j + l % 32, columns 16 s + 8 (l / 32) + [0, 8)
-    const int KT = cols_pad / 16;
+    return upload_dense_fragments(dense, int(rows), cols_pad, t->name, allocs);
+}
+
+// A dense row-major fp16 matrix [rows][cols] (rows a multiple of 32, cols of 16) uploaded in
+// fragment order: 32-row block j, 16-wide k-step s: 512 halves, lane l's 8 halves are row
+// 32 j + l % 32, columns 16 s + 8 (l / 32) + [0, 8).
+Q8Dev upload_dense_fragments(const std::vector<uint16_t>& dense, int rows, int cols, const char* what,
+                             std::vector<void*>& allocs) {
+    const int KT = cols / 16;
     std::vector<uint16_t> fh(dense.size());
     for (int64_t j = 0; j < rows / 32; j++)
         for (int s = 0; s < KT; s++)
             for (int l = 0; l < 64; l++)
                 for (int e = 0; e < 8; e++)
-                    fh[((size_t(j) * KT + s) * 64 + l) * 8 + e] =
-                        dense[size_t(32 * j + l % 32) * cols_pad + 16 * s + 8 * (l / 32) + e];
+                    fh[((size_t(j) * KT + s) * 64 + l) * 8 + e] = dense[size_t(32 * j + l % 32) * cols + 16 * s + 8 * (l / 32) + e];
     Q8Dev m;
-    m.rows = int(rows);
-    m.cols = cols_pad;
-    m.fh = static_cast<uint16_t*>(dev_alloc(fh.size() * 2, t->name));
+    m.rows = rows;
+    m.cols = cols;
+    m.fh = static_cast<uint16_t*>(dev_alloc(fh.size() * 2, what));
     allocs.push_back(m.fh);
     hip_check(hipMemcpy(m.fh, fh.data(), fh.size() * 2, hipMemcpyHostToDevice), "hipMemcpy weights");
     return m;
+}
+
+// The split-precision copy of a Q8_0 matrix W [rows][cols]: fragments of [W_hi | W_hi | W_lo]
+// ([rows][3 cols]) with W_hi = fp16(q d), the value of the plain fragment copy, and
+// W_lo = fp16(q d - W_hi). q d has at most 18 significant bits, so W_hi + W_lo is q d up to the
+// fp16 subnormal step of W_lo (2^-25 absolute).
+Q8Dev upload_split_fragments(ge_ctx* c, const HostQ8& h, const char* what) {
+    const int K = h.cols, kb = K / 32;
+    std::vector<uint16_t> dense(size_t(h.rows) * 3 * K);
+    for (int r = 0; r < h.rows; r++)
+        for (int k = 0; k < K; k++) {
+            const float wv = host_h2f(h.s[size_t(r) * kb + k / 32]) * float(h.q[size_t(r) * K + k]);
+            const _Float16 hi = _Float16(wv);
+            const _Float16 lo = _Float16(wv - float(hi));
+            uint16_t* row = dense.data() + size_t(r) * 3 * K;
+            row[k] = row[K + k] = __builtin_bit_cast(uint16_t, hi);
+            row[2 * K + k] = __builtin_bit_cast(uint16_t, lo);
+        }
+    return upload_dense_fragments(dense, h.rows, 3 * K, what, c->weight_allocs);
 }
 
 const uint8_t* q8_tensor(const ge_model_desc* d, const std::string& name, int64_t cols, int64_t rows, const void* base,
@@ -408,7 +443,7 @@ void free_workspace(ge_ctx* c) {
     drop_graphs(c);
     Workspace& w = c->ws;
     void* ps[] = {w.x, w.qkv, w.t, w.out, w.h, w.q, w.k, w.v, w.attn, w.act, w.tokens, w.positions, w.seqs, w.work, w.pooled,
-                  w.vt, w.vcol, w.work2, w.ple, w.ple_t, w.rs, w.rs2, w.x16, w.g16};
+                  w.vt, w.vcol, w.work2, w.ple, w.ple_t, w.rs, w.rs2, w.x16, w.g16, w.h3, w.q_lo, w.k_lo};
     for (void* p : ps)
         if (p) (void)hipFree(p);
     c->ws = Workspace{};
@@ -424,6 +459,7 @@ void upload(ge_ctx* c, const ge_model_desc* d, const void* base, size_t len) {
     if (d->hidden % 64 || d->hidden > 1024) fail(GE_ERR_MODEL, "hidden size %d: the kernels need a multiple of 64 up to 1024", d->hidden);
     if (d->feed_forward % 32) fail(GE_ERR_MODEL, "feed_forward_length %d is not a multiple of 32", d->feed_forward);
     if (d->out_dims % 64) fail(GE_ERR_MODEL, "embedding_length_out %d is not a multiple of 64", d->out_dims);
+    drain(c);  // nothing queued may still read the old weights or workspace
     free_model(c);
     free_workspace(c);
     DevModel& m = c->model;
@@ -478,7 +514,10 @@ void upload(ge_ctx* c, const ge_model_desc* d, const void* base, size_t len) {
             repack_rows(q8_tensor(d, b + "attn_q.weight", D, L.qd, base, len), L.qd, D, &h, 0);
             repack_rows(q8_tensor(d, b + "attn_k.weight", D, L.kvd, base, len), L.kvd, D, &h, L.qd);
             repack_rows(q8_tensor(d, b + "attn_v.weight", D, L.kvd, base, len), L.kvd, D, &h, L.qd + L.kvd);
-            L.wqkv = upload_q8(c, h, "attn_qkv");
+            L.precise = hd >= kPreciseHeadDim && attention_split_supported(hd, m.heads, L.kv_heads);
+            // a precise layer's GEMMs read only the split copy
+            L.wqkv = upload_q8(c, h, "attn_qkv", !L.precise);
+            if (L.precise) L.wqkv3 = upload_split_fragments(c, h, "attn_qkv split");
             // |qkv_j| <= ||h|| ||W_j||, ||h|| <= sqrt(D) max|attn_norm|
             const double hn = std::sqrt(double(D)) * max_abs(d, b + "attn_norm.weight", D, base, len);
             L.qkv_c = fp16_range_scale(hn * max_row_norm(h));
@@ -533,6 +572,8 @@ void upload(ge_ctx* c, const ge_model_desc* d, const void* base, size_t len) {
         // layouts the separate kernel's V^T staging cannot hold (2 KV heads of 256); a trace of the
         // raw projection of such a layer runs the fp32 path.
         L.qkv_fused = gemm_qkv_supported(L.head_dim, m.heads, L.kv_heads);
+        if (L.precise) L.qkv_gn = L.qkv_fused = false;  // fp32 projection, separate norm kernel
+        m.any_precise = m.any_precise || L.precise;
         m.any_v2 = m.any_v2 || L.attn_v2;
         m.all_v2 = m.all_v2 && L.attn_v2;
         if (L.attn_v2 && m.heads / L.kv_heads > 3) m.items32_ok = false;
@@ -599,6 +640,11 @@ void ensure_workspace_impl(ge_ctx* c, int tokens, int seqs, int work, int work2,
         w.tokens = ws_alloc<int32_t>(rows, 1, "tokens");
         w.positions = ws_alloc<int32_t>(rows, 1, "positions");
         w.vcol = ws_alloc<int32_t>(rows, 1, "vt columns");
+        if (m.any_precise) {
+            w.h3 = ws_alloc<uint16_t>(rows, 3 * size_t(m.hidden), "split-precision input");
+            w.q_lo = ws_alloc<uint16_t>(rows, m.max_qd, "q low halves");
+            w.k_lo = ws_alloc<uint16_t>(rows, m.max_kvd, "k low halves");
+        }
         if (m.pl > 0) {
             w.ple = ws_alloc<float>(rows, size_t(m.layers) * m.pl, "per-layer inputs");
             w.ple_t = ws_alloc<float>(rows, size_t(std::max(m.pl, m.hidden)), "per-layer projection");
@@ -689,11 +735,13 @@ void stage(ge_ctx* c, const int32_t* tokens, const int32_t* positions, int n, co
     const DevModel& m = c->model;
     if (!vectors) n_vectors = 0;
     bool any_vector = false;
+    int vec_rows_read = 0;
     for (int i = 0; i < n; i++) {
         if (tokens[i] < -n_vectors || tokens[i] >= m.vocab)
             fail(GE_ERR_INVALID, "token %d at row %d is neither in the vocabulary [0, %d) nor one of the %d vector rows",
                  tokens[i], i, m.vocab, n_vectors);
         any_vector |= tokens[i] < 0;
+        if (tokens[i] < 0) vec_rows_read = std::max(vec_rows_read, -tokens[i]);
         if (positions[i] < 0 || positions[i] >= m.max_tokens)
             fail(GE_ERR_INVALID, "position %d at row %d is outside [0, %d)", positions[i], i, m.max_tokens);
     }
@@ -768,8 +816,7 @@ void stage(ge_ctx* c, const int32_t* tokens, const int32_t* positions, int n, co
         }
     }
     // The workspace may be reallocated below: nothing queued may still use it.
-    if (workspace_grows(c, n, n_seqs, int(work.size()), int(work2.size()), vl.cols))
-        hip_check(hipStreamSynchronize(c->stream), "hipStreamSynchronize");
+    if (workspace_grows(c, n, n_seqs, int(work.size()), int(work2.size()), vl.cols)) drain(c);
     ensure_workspace(c, n, n_seqs, int(work.size()), int(work2.size()), vl.cols);
     Workspace& w = c->ws;
     // The small arrays go through one pinned buffer: asynchronous copies, no wait for them here
@@ -808,6 +855,7 @@ void stage(ge_ctx* c, const int32_t* tokens, const int32_t* positions, int n, co
     c->staged_copy_recorded = true;
     c->staged_tokens = n;
     c->staged_vectors = any_vector ? vectors : nullptr;
+    c->staged_vec_rows = vec_rows_read;
     c->staged_seqs = n_seqs;
     c->staged_work = int(work.size());
     c->staged_work2 = int(work2.size());
@@ -875,6 +923,14 @@ void encode(ge_ctx* c, StopPoint* sp) {
                 e.stage = reinterpret_cast<uint16_t*>(w.qkv);  // [rows][max_qkv] fp32: room for fp16 [T][N]
                 return launch_gemm_qkv(s, L.wqkv, w.h, T, L.head_dim, e);
             });
+        } else if (L.precise) {
+            launch(c, "norm_split", [&] { return launch_norm_split(s, w.x, L.attn_norm, m.eps, T, D, w.h3); });
+            launch(c, "gemm_qkv", [&] { return launch_gemm_q8(s, L.wqkv3, w.h3, T, w.qkv, kEpiF32); });
+            if (at(sp, "Qcur", l) || at(sp, "Kcur", l) || at(sp, "Vcur", l)) return;
+            launch(c, "qk_norm_rope", [&] {
+                return launch_qk_norm_rope(s, w.qkv, T, m.heads, L.kv_heads, L.head_dim, L.q_norm, L.k_norm, m.eps,
+                                           w.positions, L.rope, w.q, w.k, w.v, w.q_lo, w.k_lo);
+            });
         } else {
             launch(c, "gemm_qkv", [&] {
                 return L.qkv_gn ? launch_gemm_q8(s, L.wqkv, w.h, T, w.qkv, kEpiF16, L.qkv_c)
@@ -898,6 +954,9 @@ void encode(ge_ctx* c, StopPoint* sp) {
         if (L.attn_v2) {
             if (!fused_vt) launch(c, "v_transpose", [&] { return launch_v_transpose(s, w.v, T, L.kvd, w.vcol, w.vt_cap, w.vt); });
             launch(c, "attention", [&] {
+                if (L.precise)
+                    return launch_attention_split(s, w.q, w.q_lo, w.k, w.k_lo, w.vt, w.vt_cap, w.attn, w.work2, c->staged_work2,
+                                                  m.heads, L.kv_heads, L.head_dim, hw, 1.0f, c->attn_items);
                 return launch_attention_v2(s, w.q, w.k, w.vt, w.vt_cap, w.attn, w.work2, c->staged_work2, m.heads, L.kv_heads,
                                            L.head_dim, hw, 1.0f, c->attn_items);
             });
@@ -1025,12 +1084,25 @@ void encode_split(ge_ctx* c) {
         } else {
             // the projection, then the norms and RoPE (fp16 kernel with V^T where the layout allows,
             // else fp32 and a separate transpose), as encode() does
-            for (const Half& H : halves)
-                launch(c, "gemm_qkv", [&] {
-                    return L.qkv_gn ? launch_gemm_q8(H.s, L.wqkv, rows(w.h, H.r0, D), H.T, rows(w.qkv, H.r0, m.max_qkv), kEpiF16,
-                                                     L.qkv_c)
-                                    : launch_gemm_q8(H.s, L.wqkv, rows(w.h, H.r0, D), H.T, rows(w.qkv, H.r0, m.max_qkv), kEpiF32);
-                });
+            if (L.precise) {
+                for (const Half& H : halves)
+                    launch(c, "norm_split", [&] {
+                        return launch_norm_split(H.s, rows(w.x, H.r0, D), L.attn_norm, m.eps, H.T, D, rows(w.h3, H.r0, 3 * size_t(D)));
+                    });
+                for (const Half& H : halves)
+                    launch(c, "gemm_qkv", [&] {
+                        return launch_gemm_q8(H.s, L.wqkv3, rows(w.h3, H.r0, 3 * size_t(D)), H.T, rows(w.qkv, H.r0, m.max_qkv),
+                                              kEpiF32);
+                    });
+            } else {
+                for (const Half& H : halves)
+                    launch(c, "gemm_qkv", [&] {
+                        return L.qkv_gn ? launch_gemm_q8(H.s, L.wqkv, rows(w.h, H.r0, D), H.T, rows(w.qkv, H.r0, m.max_qkv),
+                                                         kEpiF16, L.qkv_c)
+                                        : launch_gemm_q8(H.s, L.wqkv, rows(w.h, H.r0, D), H.T, rows(w.qkv, H.r0, m.max_qkv),
+                                                         kEpiF32);
+                    });
+            }
             for (const Half& H : halves)
                 launch(c, "qk_norm_rope", [&] {
                     if (L.qkv_gn)
@@ -1041,7 +1113,9 @@ void encode_split(ge_ctx* c) {
                                                        w.vcol + H.r0, w.vt_cap, w.vt);
                     return launch_qk_norm_rope(H.s, rows(w.qkv, H.r0, m.max_qkv), H.T, m.heads, L.kv_heads, L.head_dim, L.q_norm,
                                                L.k_norm, m.eps, w.positions + H.r0, L.rope, rows(w.q, H.r0, m.max_qd),
-                                               rows(w.k, H.r0, m.max_kvd), rows(w.v, H.r0, m.max_kvd));
+                                               rows(w.k, H.r0, m.max_kvd), rows(w.v, H.r0, m.max_kvd),
+                                               L.precise ? rows(w.q_lo, H.r0, m.max_qd) : nullptr,
+                                               L.precise ? rows(w.k_lo, H.r0, m.max_kvd) : nullptr);
                 });
             if (!L.qkv_gn)
                 for (const Half& H : halves)
@@ -1052,6 +1126,11 @@ void encode_split(ge_ctx* c) {
         const int hw = L.sliding ? m.window / 2 : 0;
         for (const Half& H : halves)
             launch(c, "attention", [&] {
+                if (L.precise)
+                    return launch_attention_split(H.s, part_base(w.q, H.r0, L.qd, m.max_qd), part_base(w.q_lo, H.r0, L.qd, m.max_qd),
+                                                  part_base(w.k, H.r0, L.kvd, m.max_kvd), part_base(w.k_lo, H.r0, L.kvd, m.max_kvd),
+                                                  w.vt, w.vt_cap, part_base(w.attn, H.r0, L.qd, m.max_qd), H.work, H.n_work, m.heads,
+                                                  L.kv_heads, L.head_dim, hw, 1.0f, c->attn_items);
                 return launch_attention_v2(H.s, part_base(w.q, H.r0, L.qd, m.max_qd), part_base(w.k, H.r0, L.kvd, m.max_kvd),
                                            w.vt, w.vt_cap, part_base(w.attn, H.r0, L.qd, m.max_qd), H.work, H.n_work, m.heads, L.kv_heads,
                                            L.head_dim, hw, 1.0f, c->attn_items);
@@ -1173,9 +1252,15 @@ int own_vector_rows(ge_ctx* c) { return own_vectors(c) ? c->vec_rows : 0; }
 void set_vectors(ge_ctx* c, const float* rows, int n_rows, int width) {
     if (n_rows < 0 || (n_rows > 0 && (!rows || width <= 0))) fail(GE_ERR_INVALID, "bad vector rows");
     const size_t bytes = size_t(n_rows) * size_t(std::max(width, 0)) * 4;
-    hip_check(hipStreamSynchronize(c->stream), "hipStreamSynchronize");  // queued work may read the rows
+    drain(c);  // queued work may read the rows
+    // A staged batch that reads these rows stays valid only while the new rows still cover the
+    // ones it names, at the residual stream's width, in the same buffer.
+    if (c->staged_vectors && c->staged_vectors == c->vec_buf &&
+        (bytes > c->vec_cap || n_rows < c->staged_vec_rows || width != c->model.hidden)) {
+        c->staged_tokens = -1;
+        c->staged_vectors = nullptr;
+    }
     if (bytes > c->vec_cap) {
-        if (c->staged_vectors && c->staged_vectors == c->vec_buf) c->staged_tokens = -1;  // the staged batch read the old rows
         if (c->vec_buf) hip_check(hipFree(c->vec_buf), "hipFree");
         c->vec_buf = nullptr;
         c->vec_cap = 0;
@@ -1360,7 +1445,12 @@ int ge_create(int device, ge_ctx** out) {
 void ge_destroy(ge_ctx* c) {
     if (!c) return;
     (void)hipSetDevice(c->device);
+    // Every stream that may still run kernels on the buffers below drains first: the context's
+    // stream, and the part streams, whose work the context's stream joins only when a forward
+    // ends normally (a forward that failed between the fork and the join leaves theirs unjoined).
     if (c->stream) (void)hipStreamSynchronize(c->stream);
+    for (int p = 0; p < ge::kMaxParts; p++)
+        if (c->part_stream[p] && c->part_stream[p] != c->stream) (void)hipStreamSynchronize(c->part_stream[p]);
     ge::free_workspace(c);
     ge::free_model(c);
     ge::free_vision(c);
@@ -1376,10 +1466,7 @@ void ge_destroy(ge_ctx* c) {
     if (c->staged_copy) (void)hipEventDestroy(c->staged_copy);
     if (c->pinned) (void)hipHostFree(c->pinned);
     for (int p = 0; p < ge::kMaxParts; p++) {
-        if (c->part_stream[p] && c->part_stream[p] != c->stream) {
-            (void)hipStreamSynchronize(c->part_stream[p]);
-            (void)hipStreamDestroy(c->part_stream[p]);
-        }
+        if (c->part_stream[p] && c->part_stream[p] != c->stream) (void)hipStreamDestroy(c->part_stream[p]);
         if (c->part_join[p]) (void)hipEventDestroy(c->part_join[p]);
     }
     if (c->stream) (void)hipStreamDestroy(c->stream);
@@ -1606,67 +1693,99 @@ int ge_op_gemm_q8_geglu(ge_ctx* c, const ge_q8_matrix* gate, const ge_q8_matrix*
 
 int32_t ge_attention_queries(void) { return ge::kAttnQueries; }
 
+}  // extern "C"
+
+namespace ge {
+
+// Kernels.attention on device memory (ge_op_attention, ge_op_attention_split): with q_lo and k_lo
+// set, the split-precision scores.
+void op_attention(ge_ctx* c, const void* q, const void* q_lo, const void* k, const void* k_lo, const void* v, void* out,
+                  const void* work, int n_work, int heads, int kv_heads, int head_dim, int half_window, float scale) {
+    if (n_work < 0 || (n_work > 0 && !work)) fail(GE_ERR_INVALID, "bad attention work list");
+    const bool split = q_lo || k_lo;
+    if (split && (!q_lo || !k_lo || !attention_split_supported(head_dim, heads, kv_heads)))
+        fail(GE_ERR_INVALID, "split-precision attention takes q_lo and k_lo, head dim 512 and 4 query heads per KV head");
+    if (n_work == 0) return;
+    // The ABI's work items (ge_attention_work) come in; the kernels take ge::AttnWork.
+    std::vector<ge_attention_work> items(static_cast<size_t>(n_work), ge_attention_work{});
+    hip_check(hipMemcpy(items.data(), work, items.size() * sizeof(ge_attention_work), hipMemcpyDeviceToHost), "read work");
+    std::vector<void*> temps;
+    struct Free {
+        std::vector<void*>* p;
+        ~Free() {
+            for (void* x : *p) (void)hipFree(x);
+        }
+    } guard{&temps};
+    auto temp = [&](size_t bytes) {
+        void* p = dev_alloc(bytes, "attention op");
+        temps.push_back(p);
+        return p;
+    };
+    if (split || attention_v2_supported(head_dim, heads, kv_heads)) {
+        // The sequences behind the work items, in order; V transposed into their layout.
+        std::vector<ge_seq> seqs;
+        int T = 0;
+        for (const auto& it : items) {
+            if (seqs.empty() || seqs.back().start != it.seq_start || seqs.back().length != it.seq_len)
+                if (it.q0 == 0) seqs.push_back(ge_seq{it.seq_start, it.seq_len});
+            T = std::max(T, int(it.seq_start + it.seq_len));
+        }
+        const VtLayout vl = vt_layout(T, seqs.data(), int(seqs.size()));
+        std::vector<AttnWork> w2;
+        for (size_t s = 0; s < seqs.size(); s++)
+            for (uint32_t q0 = 0; q0 < seqs[s].length; q0 += kAttnQueriesV2)
+                w2.push_back(AttnWork{seqs[s].start, seqs[s].length, q0, vl.start[s]});
+        const int kvd = kv_heads * head_dim;
+        auto* vt = static_cast<uint16_t*>(temp(size_t(kvd) * vl.cols * 2));
+        auto* vcol = static_cast<int32_t*>(temp(size_t(T) * 4));
+        auto* dw = static_cast<AttnWork*>(temp(w2.size() * sizeof(AttnWork)));
+        hip_check(hipMemsetAsync(vt, 0, size_t(kvd) * vl.cols * 2, c->stream), "hipMemset");
+        hip_check(hipMemcpyAsync(vcol, vl.vcol.data(), size_t(T) * 4, hipMemcpyHostToDevice, c->stream), "upload");
+        hip_check(hipMemcpyAsync(dw, w2.data(), w2.size() * sizeof(AttnWork), hipMemcpyHostToDevice, c->stream), "upload");
+        launch(c, "v_transpose", [&] {
+            return launch_v_transpose(c->stream, static_cast<const uint16_t*>(v), T, kvd, vcol, vl.cols, vt);
+        });
+        launch(c, "attention", [&] {
+            const auto* qh = static_cast<const uint16_t*>(q);
+            const auto* kh = static_cast<const uint16_t*>(k);
+            if (split)
+                return launch_attention_split(c->stream, qh, static_cast<const uint16_t*>(q_lo), kh,
+                                              static_cast<const uint16_t*>(k_lo), vt, vl.cols, static_cast<uint16_t*>(out), dw,
+                                              int(w2.size()), heads, kv_heads, head_dim, half_window, scale, kAttnQueriesV2);
+            return launch_attention_v2(c->stream, qh, kh, vt, vl.cols, static_cast<uint16_t*>(out), dw, int(w2.size()), heads,
+                                       kv_heads, head_dim, half_window, scale);
+        });
+    } else {
+        std::vector<AttnWork> w1;
+        for (const auto& it : items) w1.push_back(AttnWork{it.seq_start, it.seq_len, it.q0, 0});
+        auto* dw = static_cast<AttnWork*>(temp(w1.size() * sizeof(AttnWork)));
+        hip_check(hipMemcpyAsync(dw, w1.data(), w1.size() * sizeof(AttnWork), hipMemcpyHostToDevice, c->stream), "upload");
+        launch(c, "attention", [&] {
+            return launch_attention(c->stream, static_cast<const uint16_t*>(q), static_cast<const uint16_t*>(k),
+                                    static_cast<const uint16_t*>(v), static_cast<uint16_t*>(out), dw, n_work, heads, kv_heads,
+                                    head_dim, half_window, scale);
+        });
+    }
+    hip_check(hipStreamSynchronize(c->stream), "hipStreamSynchronize");
+}
+
+}  // namespace ge
+
+extern "C" {
+
 int ge_op_attention(ge_ctx* c, const void* q, const void* k, const void* v, void* out, const void* work, int32_t n_work,
                     int32_t heads, int32_t kv_heads, int32_t head_dim, int32_t half_window, float scale) {
     return guarded(c, [&] {
-        if (n_work < 0 || (n_work > 0 && !work)) fail(GE_ERR_INVALID, "bad attention work list");
-        if (n_work == 0) return;
-        // The ABI's work items (ge_attention_work) come in; the kernels take ge::AttnWork.
-        std::vector<ge_attention_work> items(static_cast<size_t>(n_work), ge_attention_work{});
-        ge::hip_check(hipMemcpy(items.data(), work, items.size() * sizeof(ge_attention_work), hipMemcpyDeviceToHost), "read work");
-        std::vector<void*> temps;
-        struct Free {
-            std::vector<void*>* p;
-            ~Free() {
-                for (void* x : *p) (void)hipFree(x);
-            }
-        } guard{&temps};
-        auto temp = [&](size_t bytes) {
-            void* p = ge::dev_alloc(bytes, "attention op");
-            temps.push_back(p);
-            return p;
-        };
-        if (ge::attention_v2_supported(head_dim, heads, kv_heads)) {
-            // The sequences behind the work items, in order; V transposed into their layout.
-            std::vector<ge_seq> seqs;
-            int T = 0;
-            for (const auto& it : items) {
-                if (seqs.empty() || seqs.back().start != it.seq_start || seqs.back().length != it.seq_len)
-                    if (it.q0 == 0) seqs.push_back(ge_seq{it.seq_start, it.seq_len});
-                T = std::max(T, int(it.seq_start + it.seq_len));
-            }
-            const ge::VtLayout vl = ge::vt_layout(T, seqs.data(), int(seqs.size()));
-            std::vector<ge::AttnWork> w2;
-            for (size_t s = 0; s < seqs.size(); s++)
-                for (uint32_t q0 = 0; q0 < seqs[s].length; q0 += ge::kAttnQueriesV2)
-                    w2.push_back(ge::AttnWork{seqs[s].start, seqs[s].length, q0, vl.start[s]});
-            const int kvd = kv_heads * head_dim;
-            auto* vt = static_cast<uint16_t*>(temp(size_t(kvd) * vl.cols * 2));
-            auto* vcol = static_cast<int32_t*>(temp(size_t(T) * 4));
-            auto* dw = static_cast<ge::AttnWork*>(temp(w2.size() * sizeof(ge::AttnWork)));
-            ge::hip_check(hipMemsetAsync(vt, 0, size_t(kvd) * vl.cols * 2, c->stream), "hipMemset");
-            ge::hip_check(hipMemcpyAsync(vcol, vl.vcol.data(), size_t(T) * 4, hipMemcpyHostToDevice, c->stream), "upload");
-            ge::hip_check(hipMemcpyAsync(dw, w2.data(), w2.size() * sizeof(ge::AttnWork), hipMemcpyHostToDevice, c->stream), "upload");
-            ge::launch(c, "v_transpose", [&] {
-                return ge::launch_v_transpose(c->stream, static_cast<const uint16_t*>(v), T, kvd, vcol, vl.cols, vt);
-            });
-            ge::launch(c, "attention", [&] {
-                return ge::launch_attention_v2(c->stream, static_cast<const uint16_t*>(q), static_cast<const uint16_t*>(k), vt,
-                                               vl.cols, static_cast<uint16_t*>(out), dw, int(w2.size()), heads, kv_heads,
-                                               head_dim, half_window, scale);
-            });
-        } else {
-            std::vector<ge::AttnWork> w1;
-            for (const auto& it : items) w1.push_back(ge::AttnWork{it.seq_start, it.seq_len, it.q0, 0});
-            auto* dw = static_cast<ge::AttnWork*>(temp(w1.size() * sizeof(ge::AttnWork)));
-            ge::hip_check(hipMemcpyAsync(dw, w1.data(), w1.size() * sizeof(ge::AttnWork), hipMemcpyHostToDevice, c->stream), "upload");
-            ge::launch(c, "attention", [&] {
-                return ge::launch_attention(c->stream, static_cast<const uint16_t*>(q), static_cast<const uint16_t*>(k),
-                                            static_cast<const uint16_t*>(v), static_cast<uint16_t*>(out), dw, n_work, heads,
-                                            kv_heads, head_dim, half_window, scale);
-            });
-        }
-        ge::hip_check(hipStreamSynchronize(c->stream), "hipStreamSynchronize");
+        ge::op_attention(c, q, nullptr, k, nullptr, v, out, work, n_work, heads, kv_heads, head_dim, half_window, scale);
+    });
+}
+
+int ge_op_attention_split(ge_ctx* c, const void* q, const void* q_lo, const void* k, const void* k_lo, const void* v,
+                          void* out, const void* work, int32_t n_work, int32_t heads, int32_t kv_heads, int32_t head_dim,
+                          int32_t half_window, float scale) {
+    return guarded(c, [&] {
+        if (!q_lo || !k_lo) ge::fail(GE_ERR_INVALID, "split-precision attention needs q_lo and k_lo");
+        ge::op_attention(c, q, q_lo, k, k_lo, v, out, work, n_work, heads, kv_heads, head_dim, half_window, scale);
     });
 }
 

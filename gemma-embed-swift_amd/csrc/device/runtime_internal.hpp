@@ -33,6 +33,10 @@ struct DevLayer {
     bool attn_v2 = false;  // attention with Q/K/V copied into LDS and V transposed
     bool qkv_gn = false;   // QKV projection stored as scaled fp16 and read by the fused norm kernel
     bool qkv_fused = false;  // QKV projection with the norms, RoPE and V^T in its epilogue
+    // Split-precision QKV projection (layers of head dim >= kPreciseHeadDim): the normed input as
+    // fp16 [hi | lo | hi] (launch_norm_split) against wqkv3 = [W_hi | W_hi | W_lo] over 3 hidden
+    // columns, fp32 out, so q and k reach their norms at about fp32 precision.
+    bool precise = false;
     // Projections stored in fp16 before an RMSNorm are multiplied by these powers of two, chosen
     // from load-time bounds so the values stay inside fp16's range; the norm then uses
     // eps * c^2, which makes it exact for the scaled values.
@@ -44,6 +48,7 @@ struct DevLayer {
     // 1 / act_scale. Both are powers of two, so the round trip is exact.
     float act_scale = 1, down_scale = 1;
     Q8Dev wqkv, wo, wgu, wd;  // wqkv rows: q | k | v; wgu rows: gate/up interleaved in 32-row groups
+    Q8Dev wqkv3;              // precise layers: fragments of [W_hi | W_hi | W_lo], [q | k | v rows][3 hidden]
     Q8Dev inp_gate, proj;     // per-layer-input branch (per_layer_input > 0)
     float* post_norm = nullptr;
     float *attn_norm = nullptr, *q_norm = nullptr, *k_norm = nullptr, *post_attn = nullptr, *ffn_norm = nullptr,
@@ -61,6 +66,7 @@ struct DevModel {
     std::vector<DevLayer> layer;
     int max_qd = 0, max_kvd = 0, max_qkv = 0, max_kv_heads = 1;
     bool any_v2 = false;
+    bool any_precise = false;
     bool all_v2 = true;  // every layer: the LDS-copy attention (a large pack may then run in parts)
     bool items32_ok = true;  // every LDS-copy attention layer takes 32-query work items (<= 3 heads per KV head)
 };
@@ -86,6 +92,10 @@ struct Workspace {
     // [T][max(pl, hidden)]
     float *ple = nullptr, *ple_t = nullptr, *rs = nullptr, *rs2 = nullptr;
     uint16_t *x16 = nullptr, *g16 = nullptr;
+    // split-precision QKV input [T][3 hidden] (any precise layer)
+    uint16_t* h3 = nullptr;
+    // their q and k as split pairs: the low halves beside w.q / w.k (same layouts)
+    uint16_t *q_lo = nullptr, *k_lo = nullptr;
 };
 
 struct ProfStat {
@@ -103,6 +113,13 @@ struct StopPoint {
     int layer = -1;
     bool hit = false;
 };
+
+// Layers whose heads are at least this wide take the split-precision QKV projection. Their
+// scores are dot products of two RMS-normed vectors of that width at attention scale 1, so they
+// reach several hundred, and fp16 rounding of the projection's operands (2^-11 relative per
+// element) moved them enough to put the attention output of the reference's global layers
+// (head dim 512) at 1.1e-2 max relative error against the fp32 oracle.
+constexpr int kPreciseHeadDim = 512;
 
 constexpr int kMaxParts = 4;  // streams a large batch is split over (measured 2, 3, 4: 5.93, 5.93, 5.85 ms at config 2)
 
@@ -164,6 +181,8 @@ struct ge_ctx {
     size_t vec_cap = 0;
     int vec_rows = 0, vec_width = 0;
     const float* staged_vectors = nullptr;
+    // One past the largest vector row the staged batch reads (0 when it reads none).
+    int staged_vec_rows = 0;
 };
 
 namespace ge {

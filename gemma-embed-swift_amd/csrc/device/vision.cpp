@@ -449,9 +449,11 @@ void vision_encode(ge_ctx* c, VitStop* sp) {
     launch(c, "vit_gemm_proj", [&] { return launch_gemm_q8(s, v.proj_w, v.pooled16, T, v.out, kEpiF32); });
 }
 
-void vision_read(ge_ctx* c, float* out) {
+void vision_read(ge_ctx* c, float* out, size_t cap) {
     VisionState& v = vision_of(c);
     if (v.staged_patches < 0) fail(GE_ERR_STATE, "no image batch is staged");
+    const size_t need = size_t(v.staged_tokens) * v.proj;
+    if (cap < need) fail(GE_ERR_INVALID, "vector buffer holds %zu floats, the staged images need %zu", cap, need);
     hip_check(hipStreamSynchronize(c->stream), "hipStreamSynchronize");
     hip_check(hipMemcpy(out, v.out, size_t(v.staged_tokens) * v.proj * 4, hipMemcpyDeviceToHost), "read vectors");
 }
@@ -531,6 +533,21 @@ void image_forward(ge_ctx* c, const float* patches, int n_patches, const ge_imag
     if (v.proj != c->model.hidden)
         fail(GE_ERR_INVALID, "the image tower's %d-wide vectors do not fit the text model's %d-wide rows", v.proj,
              c->model.hidden);
+    // The markers are vocabulary ids (InputRow.swift SpanMarkers); a negative id would name a
+    // vector row instead.
+    for (int i = 0; i < 4; i++)
+        if (markers[i] < 0 || markers[i] >= c->model.vocab)
+            fail(GE_ERR_INVALID, "marker %d (%d) is outside the vocabulary [0, %d)", i, markers[i], c->model.vocab);
+    // The text batch staged below reads the tower's buffers, which the next image batch may
+    // replace: it is dropped on every exit, a failed one included.
+    struct DropStaged {
+        ge_ctx* c;
+        ~DropStaged() {
+            c->staged_tokens = -1;
+            c->staged_vectors = nullptr;
+            c->staged_vec_rows = 0;
+        }
+    } drop{c};
     vision_stage(c, patches, n_patches, grids, n_images);
     std::vector<int32_t> ids, pos;
     std::vector<ge_seq> seqs;
@@ -555,7 +572,6 @@ void image_forward(ge_ctx* c, const float* patches, int n_patches, const ge_imag
     vision_encode(c, nullptr);
     run_forward(c, gpu_seconds, false);
     read_pooled(c, pooled);
-    c->staged_tokens = -1;  // the batch reads the tower's buffers, which the next image batch may replace
 }
 
 void free_vision(ge_ctx* c) {
@@ -583,9 +599,24 @@ int ge_vision_run(ge_ctx* c) {
     return ge::guarded(c, [&] { ge::vision_encode(c, nullptr); });
 }
 
-int ge_vision_read(ge_ctx* c, float* vectors) {
+int ge_vision_read(ge_ctx* c, float* vectors, size_t vectors_count) {
     if (!vectors) return GE_ERR_INVALID;
-    return ge::guarded(c, [&] { ge::vision_read(c, vectors); });
+    return ge::guarded(c, [&] { ge::vision_read(c, vectors, vectors_count); });
+}
+
+int ge_vision_get_info(ge_ctx* c, ge_vision_info* info) {
+    if (!info) return GE_ERR_INVALID;
+    return ge::guarded(c, [&] {
+        const ge::VisionState& v = ge::vision_of(c);
+        info->layers = v.layers;
+        info->hidden = v.hidden;
+        info->heads = v.heads;
+        info->patch_size = v.patch;
+        info->patch_area = v.area;
+        info->merge = v.merge;
+        info->proj_dims = v.proj;
+        info->positions = v.npos;
+    });
 }
 
 int32_t ge_vision_tokens(ge_ctx* c) {
@@ -594,7 +625,7 @@ int32_t ge_vision_tokens(ge_ctx* c) {
 }
 
 int ge_vision_encode(ge_ctx* c, const float* patches, int32_t n_patches, const ge_image_grid* grids, int32_t n_images,
-                     float* vectors, double* gpu_seconds) {
+                     float* vectors, size_t vectors_count, double* gpu_seconds) {
     if (!vectors) return GE_ERR_INVALID;
     return ge::guarded(c, [&] {
         ge::vision_stage(c, patches, n_patches, grids, n_images);
@@ -607,7 +638,7 @@ int ge_vision_encode(ge_ctx* c, const float* patches, int32_t n_patches, const g
             ge::hip_check(hipEventElapsedTime(&ms, c->ev_start, c->ev_stop), "hipEventElapsedTime");
             *gpu_seconds = ms * 1e-3;
         }
-        ge::vision_read(c, vectors);
+        ge::vision_read(c, vectors, vectors_count);
     });
 }
 

@@ -218,7 +218,7 @@ int probe_vision(ge_ctx* c, int reps) {
     ge_sync(c);
     const double ms = std::chrono::duration<double, std::milli>(std::chrono::steady_clock::now() - t0).count() / reps;
     std::vector<float> out(size_t(images) * 256 * 768);
-    if (ge_vision_read(c, out.data()) != 0) return fail(c, "vision read");
+    if (ge_vision_read(c, out.data(), out.size()) != 0) return fail(c, "vision read");
     std::printf("config 5 image tower: %.3f ms per batch of %d images, %.1f images/s\n", ms, images, images / (ms * 1e-3));
     std::fflush(stdout);
     return 0;

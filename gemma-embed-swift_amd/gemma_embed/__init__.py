@@ -77,6 +77,11 @@ class ge_synth_spec(C.Structure):
                 ("pattern", C.POINTER(C.c_uint8)), ("seed", C.c_uint64)]
 
 
+class ge_vision_info(C.Structure):
+    _fields_ = [(n, C.c_int32) for n in ("layers", "hidden", "heads", "patch_size", "patch_area", "merge",
+                                          "proj_dims", "positions")]
+
+
 class ge_synth_vision_spec(C.Structure):
     _fields_ = [("layers", C.c_int32), ("hidden", C.c_int32), ("heads", C.c_int32),
                 ("feed_forward", C.c_int32), ("patch_size", C.c_int32), ("merge", C.c_int32),
@@ -126,6 +131,8 @@ SIGNATURES = {
     "ge_attention_queries": (C.c_int32, []),
     "ge_op_attention": (_I, [_P, _P, _P, _P, _P, _P, C.c_int32, C.c_int32, C.c_int32, C.c_int32, C.c_int32,
                              C.c_float]),
+    "ge_op_attention_split": (_I, [_P, _P, _P, _P, _P, _P, _P, _P, C.c_int32, C.c_int32, C.c_int32, C.c_int32,
+                                   C.c_int32, C.c_float]),
     "ge_model_load": (_I, [C.c_char_p, C.POINTER(ge_load_options), C.POINTER(_P), C.c_char_p, C.c_size_t]),
     "ge_model_free": (None, [_P]),
     "ge_model_last_error": (C.c_char_p, [_P]),
@@ -142,13 +149,15 @@ SIGNATURES = {
     "ge_synth_write_vision_gguf": (_I, [C.c_char_p, C.POINTER(ge_synth_vision_spec), C.c_char_p, C.c_size_t]),
     "ge_upload_vision": (_I, [_P, _P, _P, C.c_size_t]),
     "ge_vision_load": (_I, [_P, C.c_char_p, C.c_char_p, C.c_size_t]),
-    "ge_vision_encode": (_I, [_P, _PF, C.c_int32, C.POINTER(ge_image_grid), C.c_int32, _PF, C.POINTER(C.c_double)]),
+    "ge_vision_encode": (_I, [_P, _PF, C.c_int32, C.POINTER(ge_image_grid), C.c_int32, _PF, C.c_size_t,
+                              C.POINTER(C.c_double)]),
+    "ge_vision_get_info": (_I, [_P, C.POINTER(ge_vision_info)]),
     "ge_image_forward": (_I, [_P, _PF, C.c_int32, C.POINTER(ge_image_grid), C.c_int32, _PI32, _PF,
                               C.POINTER(C.c_double)]),
     "ge_set_vectors": (_I, [_P, _PF, C.c_int32, C.c_int32]),
     "ge_vision_stage": (_I, [_P, _PF, C.c_int32, C.POINTER(ge_image_grid), C.c_int32]),
     "ge_vision_run": (_I, [_P]),
-    "ge_vision_read": (_I, [_P, _PF]),
+    "ge_vision_read": (_I, [_P, _PF, C.c_size_t]),
     "ge_vision_tokens": (C.c_int32, [_P]),
     "ge_vision_trace": (_I, [_P, _PF, C.c_int32, C.POINTER(ge_image_grid), C.c_int32, C.c_char_p, C.c_int32, _PF,
                              C.c_size_t, C.POINTER(C.c_size_t)]),
@@ -376,22 +385,41 @@ class Context:
         if rc != GE_OK:
             raise GemmaEmbedError(rc, err.value.decode())
 
-    def vision_encode(self, patches: np.ndarray, grids: Sequence[Tuple[int, int]], proj_dims: int, merge: int = 3):
-        """Patches [P, area] of images with the given grids -> (vectors [tokens, proj_dims], gpu_seconds)."""
+    def vision_info(self) -> "ge_vision_info":
+        """The uploaded tower's shapes (patch area, merge size, projection width, ...)."""
+        info = ge_vision_info()
+        self._check(lib.ge_vision_get_info(self.handle, C.byref(info)), "ge_vision_get_info")
+        return info
+
+    def _patches(self, patches: np.ndarray) -> Tuple[np.ndarray, "ge_vision_info"]:
+        info = self.vision_info()
         p = np.ascontiguousarray(patches, dtype=np.float32)
-        tokens = sum((gx // merge) * (gy // merge) for gx, gy in grids)
-        out = np.zeros((tokens, proj_dims), dtype=np.float32)
+        if p.ndim != 2 or p.shape[1] != info.patch_area:
+            raise GemmaEmbedError(GE_ERR_INVALID, f"patches of shape {p.shape}: the tower takes rows of "
+                                                  f"{info.patch_area} floats")
+        return p, info
+
+    def vision_encode(self, patches: np.ndarray, grids: Sequence[Tuple[int, int]], proj_dims: Optional[int] = None,
+                      merge: Optional[int] = None):
+        """Patches [P, area] of images with the given grids -> (vectors [tokens, proj_dims], gpu_seconds).
+        The output is sized from the loaded tower; proj_dims and merge, when given, must match it."""
+        p, info = self._patches(patches)
+        if (proj_dims is not None and proj_dims != info.proj_dims) or (merge is not None and merge != info.merge):
+            raise GemmaEmbedError(GE_ERR_INVALID, f"the tower has merge {info.merge} and {info.proj_dims}-wide vectors")
+        tokens = sum((gx // info.merge) * (gy // info.merge) for gx, gy in grids)
+        out = np.zeros((tokens, info.proj_dims), dtype=np.float32)
         secs = C.c_double(0)
         self._check(lib.ge_vision_encode(self.handle, _ptr(p, C.c_float), p.shape[0], _grid_array(grids), len(grids),
-                                         _ptr(out, C.c_float), C.byref(secs)), "ge_vision_encode")
+                                         _ptr(out, C.c_float), out.size, C.byref(secs)), "ge_vision_encode")
         return out, secs.value
 
     def image_forward(self, patches: np.ndarray, grids: Sequence[Tuple[int, int]], markers: Sequence[int]):
         """Image tower, then the text tower over [bos, begin, vectors, end, eos] per image ->
         (pooled [images, out_dims] unnormalised, gpu_seconds of both towers)."""
-        p = np.ascontiguousarray(patches, dtype=np.float32)
+        p, _ = self._patches(patches)
         mk = np.ascontiguousarray(markers, dtype=np.int32)
-        assert mk.size == 4
+        if mk.size != 4:
+            raise GemmaEmbedError(GE_ERR_INVALID, "four marker ids: bos, image begin, image end, eos")
         out = np.zeros((len(grids), self.out_dims), dtype=np.float32)
         secs = C.c_double(0)
         self._check(lib.ge_image_forward(self.handle, _ptr(p, C.c_float), p.shape[0], _grid_array(grids), len(grids),
@@ -406,7 +434,7 @@ class Context:
                                        v2.shape[1] if v2.ndim == 2 else 0), "ge_set_vectors")
 
     def vision_trace(self, patches: np.ndarray, grids: Sequence[Tuple[int, int]], name: str, layer: int = -1):
-        p = np.ascontiguousarray(patches, dtype=np.float32)
+        p, _ = self._patches(patches)
         ga = _grid_array(grids)
         need = C.c_size_t(0)
         self._check(lib.ge_vision_trace(self.handle, _ptr(p, C.c_float), p.shape[0], ga, len(grids), name.encode(),
@@ -417,17 +445,20 @@ class Context:
         return out
 
     def vision_stage(self, patches: np.ndarray, grids: Sequence[Tuple[int, int]]):
-        p = np.ascontiguousarray(patches, dtype=np.float32)
+        p, _ = self._patches(patches)
         self._check(lib.ge_vision_stage(self.handle, _ptr(p, C.c_float), p.shape[0], _grid_array(grids), len(grids)),
                     "ge_vision_stage")
 
     def vision_run(self):
         self._check(lib.ge_vision_run(self.handle), "ge_vision_run")
 
-    def vision_read(self, proj_dims: int) -> np.ndarray:
+    def vision_read(self, proj_dims: Optional[int] = None) -> np.ndarray:
+        info = self.vision_info()
+        if proj_dims is not None and proj_dims != info.proj_dims:
+            raise GemmaEmbedError(GE_ERR_INVALID, f"the tower's vectors are {info.proj_dims} wide")
         n = lib.ge_vision_tokens(self.handle)
-        out = np.zeros((max(n, 0), proj_dims), dtype=np.float32)
-        self._check(lib.ge_vision_read(self.handle, _ptr(out, C.c_float)), "ge_vision_read")
+        out = np.zeros((max(n, 0), info.proj_dims), dtype=np.float32)
+        self._check(lib.ge_vision_read(self.handle, _ptr(out, C.c_float), out.size), "ge_vision_read")
         return out
 
     def batch_stage(self, sequences: Sequence[Sequence[int]]):
@@ -516,6 +547,14 @@ class Context:
         self._check(lib.ge_op_attention(self.handle, C.c_void_p(q), C.c_void_p(k), C.c_void_p(v), C.c_void_p(out),
                                         C.c_void_p(work), n_work, heads, kv_heads, head_dim, half_window, scale),
                     "ge_op_attention")
+
+    def attention_split(self, q: int, q_lo: int, k: int, k_lo: int, v: int, out: int, work: int, n_work: int,
+                        heads: int, kv_heads: int, head_dim: int, half_window: int, scale: float = 1.0):
+        """Split-precision scores: q and k as fp16 (hi, lo) pairs in device memory."""
+        self._check(lib.ge_op_attention_split(self.handle, C.c_void_p(q), C.c_void_p(q_lo), C.c_void_p(k),
+                                              C.c_void_p(k_lo), C.c_void_p(v), C.c_void_p(out), C.c_void_p(work),
+                                              n_work, heads, kv_heads, head_dim, half_window, scale),
+                    "ge_op_attention_split")
 
 
 def attention_work(sequences_ranges, queries: Optional[int] = None) -> np.ndarray:

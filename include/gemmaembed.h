@@ -183,6 +183,14 @@ int ge_op_attention(ge_ctx* ctx, const void* q, const void* k, const void* v, vo
                     int32_t n_work, int32_t heads, int32_t kv_heads, int32_t head_dim, int32_t half_window,
                     float scale);
 
+/* Kernels.attention at split precision (the forward's head-dim-512 layers; reference fp32 scores,
+ * Shaders/Attention.metal:172-188): q and k as fp16 pairs, q_lo = fp16(q - q_hi) beside q_hi in
+ * the same layout, scores q_hi.k_hi + q_lo.k_hi + q_hi.k_lo. head_dim 512 with heads = 4 kv_heads;
+ * otherwise as ge_op_attention. */
+int ge_op_attention_split(ge_ctx* ctx, const void* q, const void* q_lo, const void* k, const void* k_lo, const void* v,
+                          void* out, const void* work, int32_t n_work, int32_t heads, int32_t kv_heads, int32_t head_dim,
+                          int32_t half_window, float scale);
+
 /* ---- image tower, on the same context as the text encoder.
  * Replaces Metal/VisionTower.swift (VisionTower.upload :113-140, encode :143-185) for a
  * pre-LayerNorm ViT: per layer x += attn_out(attn(LN1(x))) + b, x += down(gelu_tanh(up(LN2(x)))),
@@ -209,15 +217,25 @@ typedef struct ge_image_grid {
     int32_t grid_x, grid_y;
 } ge_image_grid;
 
-/* VisionTower.upload + encode + read back: patches fp32 [n_patches][3 p^2] -> vectors fp32
- * [tokens][proj_dims] (caller-owned; tokens = sum of the images' pooled tokens). Synchronous. */
+/* The uploaded tower's shapes (VisionConfig, Model/VisionConfig.swift:44-81): patch_area =
+ * 3 patch_size^2 floats per patch row, merge x merge patches pool into one output token of
+ * proj_dims floats. GE_ERR_STATE without a tower. */
+typedef struct ge_vision_info {
+    int32_t layers, hidden, heads, patch_size, patch_area, merge, proj_dims, positions;
+} ge_vision_info;
+int ge_vision_get_info(ge_ctx* ctx, ge_vision_info* info);
+
+/* VisionTower.upload + encode + read back: patches fp32 [n_patches][patch_area] -> vectors fp32
+ * [tokens][proj_dims] (caller-owned, capacity vectors_count floats; tokens = sum of the images'
+ * pooled tokens; GE_ERR_INVALID when it does not fit). Synchronous. */
 int ge_vision_encode(ge_ctx* ctx, const float* patches, int32_t n_patches, const ge_image_grid* grids, int32_t n_images,
-                     float* vectors, double* gpu_seconds);
+                     float* vectors, size_t vectors_count, double* gpu_seconds);
 /* Device-resident image batches (as ge_batch_*): stage uploads the patches and descriptors, run
- * enqueues the tower without waiting, read waits and copies the vectors out. */
+ * enqueues the tower without waiting, read waits and copies the vectors out (capacity
+ * vectors_count floats). */
 int ge_vision_stage(ge_ctx* ctx, const float* patches, int32_t n_patches, const ge_image_grid* grids, int32_t n_images);
 int ge_vision_run(ge_ctx* ctx);
-int ge_vision_read(ge_ctx* ctx, float* vectors);
+int ge_vision_read(ge_ctx* ctx, float* vectors, size_t vectors_count);
 /* Pooled tokens of the staged image batch, or -1 when none is staged. */
 int32_t ge_vision_tokens(ge_ctx* ctx);
 /* Per-layer parity (CPUVisionReference.forward's trace, Model/CPUVisionReference.swift:89-165):
@@ -227,7 +245,8 @@ int32_t ge_vision_tokens(ge_ctx* ctx);
  * bias), ffn_inp, ffn_inp_normed, ffn_gelu, ffn_out (no bias), layer_out. */
 /* MetalForward.run(images:) (Metal/MetalForward.swift:213-219): the tower over the images, then
  * the text tower over each image's [bos, begin, its vectors, end, eos] (markers[4] = {bos, begin,
- * end, eos}: the ids of <bos>, <|image>, <image|>, <eos>; Model/InputRow.swift:16-56), reading the
+ * end, eos}: the vocabulary ids of <bos>, <|image>, <image|>, <eos>, each in [0, vocab);
+ * Model/InputRow.swift:16-56), reading the
  * tower's output rows in HBM. Writes n_images x out_dims unnormalised pooled vectors into
  * `pooled_out`; `gpu_seconds` (nullable) covers both towers. Needs an uploaded text model whose
  * hidden size is the tower's projection width. Synchronous. */

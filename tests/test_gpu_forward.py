@@ -405,13 +405,10 @@ def test_reference_real_architecture_vs_oracle(real_shapes_gguf):
             for i, part in enumerate(_split(got, lengths)):
                 assert max_rel(part, want[i][1][("l_out", l)].reshape(part.shape)) <= PER_LAYER_TOL, (l, i)
         # the raw projection of a sliding layer (its fp32 trace path) and the attention of a sliding
-        # and a global layer (head dim 512 through the LDS-copy kernel). The global layer's scores
-        # are dot products of two normed 512-wide fp16 vectors at scale 1 (magnitudes up to ~500),
-        # so the fp16 rounding of q and k moves them by ~0.02 and a near-tie between keys by a few
-        # percent: its attention output is held to 2e-2 (measured 1.1e-2, the same with the
-        # previous kernel); the layer outputs above meet 1e-2.
-        keep2 = [("Qcur", 0), ("Vcur_normed", 0), ("kqv_out", 4), ("kqv_out", 5)]
-        tol = {("kqv_out", 5): 2e-2}
+        # and a global layer. The global layer (head dim 512) scores dot products of two normed
+        # 512-wide vectors at scale 1 (magnitudes of several hundred): its QKV projection and scores
+        # run at split precision, without which its attention output reached 1.1e-2.
+        keep2 = [("Qcur", 0), ("Vcur_normed", 0), ("Qcur", 5), ("kqv_out", 4), ("kqv_out", 5)]
         with ora.OracleModel(real_shapes_gguf) as o:
             want2 = [o.forward(sq, keep=keep2)[1] for sq in seqs]
         for name, l in keep2:
@@ -419,7 +416,7 @@ def test_reference_real_architecture_vs_oracle(real_shapes_gguf):
             for i, part in enumerate(_split(got, lengths)):
                 err = max_rel(part, want2[i][(name, l)].reshape(part.shape))
                 print(f"real shapes: {name} layer {l} text {i}: max_rel {err:.2e}", flush=True)
-                assert err <= tol.get((name, l), PER_LAYER_TOL), (name, l, i)
+                assert err <= PER_LAYER_TOL, (name, l, i)
     finally:
         m.close()
 

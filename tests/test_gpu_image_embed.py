@@ -167,3 +167,74 @@ def test_image_forward_needs_matching_widths(c2_model, tmp_path):
     with pytest.raises(ge.GemmaEmbedError) as e:
         ctx.image_forward(np.zeros((4, 768), np.float32), [(2, 2)], MARKERS)
     assert e.value.code == ge.GE_ERR_INVALID
+
+
+def test_image_forward_rejects_bad_markers_and_patch_rows(image_model):
+    """Markers are vocabulary ids (InputRow.swift SpanMarkers): a negative one would name a vector
+    row. Patch rows must be the tower's 3 p^2 floats wide."""
+    m, _ = image_model
+    ctx = m.context
+    patches = ge.image_patches(73, GRIDS[:1], 3 * 16 * 16)
+    for bad in ([-1, 500, 501, 1], [2, 500, 501, 512]):
+        with pytest.raises(ge.GemmaEmbedError) as e:
+            ctx.image_forward(patches, GRIDS[:1], bad)
+        assert e.value.code == ge.GE_ERR_INVALID
+    with pytest.raises(ge.GemmaEmbedError) as e:
+        ctx.image_forward(patches[:, :700], GRIDS[:1], MARKERS)
+    assert e.value.code == ge.GE_ERR_INVALID
+    # a call that fails once staging has begun (a grid that is not a multiple of the merge size)
+    # leaves no batch staged: nothing stale can run
+    ctx.batch_stage([[2, 3, 1]])
+    with pytest.raises(ge.GemmaEmbedError) as e:
+        ctx.image_forward(ge.image_patches(75, [(3, 3)], 768), [(3, 3)], MARKERS)
+    assert e.value.code == ge.GE_ERR_INVALID
+    with pytest.raises(ge.GemmaEmbedError) as e:
+        ctx.batch_run()
+    assert e.value.code == ge.GE_ERR_STATE
+    ok, _ = ctx.image_forward(patches, GRIDS[:1], MARKERS)
+    assert np.all(np.isfinite(ok))
+
+
+def test_vision_outputs_are_sized_by_capacity(image_model):
+    """ge_vision_encode / ge_vision_read take the capacity of the caller's buffer and refuse a
+    smaller one instead of writing past it."""
+    import ctypes as C
+    m, _ = image_model
+    ctx = m.context
+    info = ctx.vision_info()
+    assert (info.patch_area, info.merge, info.proj_dims) == (768, 2, 128)
+    patches = np.ascontiguousarray(ge.image_patches(74, GRIDS[:1], info.patch_area), np.float32)
+    tokens = (GRIDS[0][0] // 2) * (GRIDS[0][1] // 2)
+    out = np.zeros(tokens * 128, np.float32)
+    grid = (ge.ge_image_grid * 1)(ge.ge_image_grid(*GRIDS[0]))
+    rc = ge.lib.ge_vision_encode(ctx.handle, patches.ctypes.data_as(C.POINTER(C.c_float)), patches.shape[0], grid, 1,
+                                 out.ctypes.data_as(C.POINTER(C.c_float)), out.size - 1, None)
+    assert rc == ge.GE_ERR_INVALID
+    rc = ge.lib.ge_vision_encode(ctx.handle, patches.ctypes.data_as(C.POINTER(C.c_float)), patches.shape[0], grid, 1,
+                                 out.ctypes.data_as(C.POINTER(C.c_float)), out.size, None)
+    assert rc == ge.GE_OK
+    assert ge.lib.ge_vision_read(ctx.handle, out.ctypes.data_as(C.POINTER(C.c_float)), out.size - 128) == ge.GE_ERR_INVALID
+    with pytest.raises(ge.GemmaEmbedError):
+        ctx.vision_encode(patches, GRIDS[:1], 768)  # not the tower's projection width
+
+
+def test_replaced_vector_rows_drop_a_staged_batch_that_reads_past_them(c2_model):
+    """A staged batch names vector rows; replacing the rows with fewer (or of another width) drops
+    it rather than letting it read stale rows."""
+    ctx = c2_model.context
+    ctx.set_vectors(np.ones((6, 768), np.float32))
+    ctx.batch_stage([[2, -6, 1]])
+    ctx.set_vectors(np.ones((6, 768), np.float32))  # still covers row 5: the batch stays
+    ctx.batch_run()
+    ctx.batch_read()
+    ctx.set_vectors(np.ones((3, 768), np.float32))  # row 5 is gone
+    with pytest.raises(ge.GemmaEmbedError) as e:
+        ctx.batch_run()
+    assert e.value.code == ge.GE_ERR_STATE
+    ctx.set_vectors(np.ones((6, 768), np.float32))
+    ctx.batch_stage([[2, -2, 1]])
+    ctx.set_vectors(np.ones((6, 512), np.float32))  # another width
+    with pytest.raises(ge.GemmaEmbedError) as e:
+        ctx.batch_run()
+    assert e.value.code == ge.GE_ERR_STATE
+    ctx.set_vectors(np.zeros((0, 768), np.float32))

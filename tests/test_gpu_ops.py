@@ -207,3 +207,74 @@ def test_attention_vs_oracle(ctx, lengths, H, KV, hd, hw):
         want = ora.attention(q[st:st + n].astype(np.float32), k[st:st + n].astype(np.float32),
                              v[st:st + n].astype(np.float32), n, H, KV, hd, 1.0, 2 * hw)
         assert max_rel(out[st:st + n], want) < 5e-3, (st, n)
+
+
+def split_f16(a):
+    """fp16 (hi, lo) with hi + lo = a to about 2^-22 relative (hi = fp16(a), lo = fp16(a - hi))."""
+    a = np.asarray(a, np.float32)
+    hi = a.astype(np.float16)
+    lo = (a - hi.astype(np.float32)).astype(np.float16)
+    return hi, lo
+
+
+def rms_normed(x, w):
+    """RMSNorm over the last axis times w (the reference's QK norm, CPUReference.swift:77-90)."""
+    return (x / np.sqrt((x * x).mean(-1, keepdims=True) + 1e-6) * w).astype(np.float32)
+
+
+SPLIT_CASES = [  # (lengths, H, KV, half_window, correlation of the rows with one shared direction)
+    ([1024, 300], 4, 1, 0, 0.0),
+    ([2048, 7, 129], 4, 1, 0, 0.95),
+    ([700, 1], 8, 2, 256, 0.5),
+]
+
+
+@pytest.mark.parametrize("lengths,H,KV,hw,corr", SPLIT_CASES)
+def test_attention_split_normed_hd512_vs_oracle(ctx, lengths, H, KV, hw, corr):
+    """RMS-normed, weighted q and k of width 512 at attention scale 1 (the reference's global
+    layers, Model/Architecture.md:8-9, CPUReference.swift:225-233): scores of several hundred.
+    The oracle gets the fp32 q and k; the GPU gets them as split fp16 pairs. fp16 operands alone
+    put such cases at 6-8e-3 of max |want| (a near-tie between keys moves with a 0.02 score shift);
+    the split scores leave the fp16 rounding of V and P (~4e-4)."""
+    print(f"split attention lengths={lengths} H={H} KV={KV} hw={hw} corr={corr}", flush=True)
+    hd, T, slack = 512, sum(lengths), 64
+    rng = np.random.default_rng(1000 + T)
+    base = rng.standard_normal(hd)
+    mix = lambda shape: corr * base + np.sqrt(1 - corr * corr) * rng.standard_normal(shape)
+    wq, wk = 1 + 0.1 * rng.standard_normal(hd), 1 + 0.1 * rng.standard_normal(hd)
+    q, k = rms_normed(mix((T, H, hd)), wq), rms_normed(mix((T, KV, hd)), wk)
+    v = f16_round(rms_normed(rng.standard_normal((T, KV, hd)), 1.0))
+    qh, ql = split_f16(q)
+    kh, kl = split_f16(k)
+    ranges, s = [], 0
+    for n in lengths:
+        ranges.append((s, n))
+        s += n
+    work = ge.attention_work(ranges)
+    pad = lambda a: np.concatenate([a, np.zeros((slack,) + a.shape[1:], a.dtype)])
+    bufs = [ctx.alloc(pad(a).nbytes) for a in (qh, ql, kh, kl, v, qh)] + [ctx.alloc(work.nbytes)]
+    try:
+        for b, a in zip(bufs, (qh, ql, kh, kl, v)):
+            ctx.upload(b, pad(a))
+        ctx.upload(bufs[6], work)
+        ctx.attention_split(bufs[0], bufs[1], bufs[2], bufs[3], bufs[4], bufs[5], bufs[6], len(work), H, KV, hd, hw, 1.0)
+        out = ctx.download(bufs[5], (T, H, hd), np.float16).astype(np.float32)
+    finally:
+        for b in bufs:
+            ctx.free(b)
+    for st, n in ranges:
+        want = ora.attention(q[st:st + n], k[st:st + n], v[st:st + n].astype(np.float32), n, H, KV, hd, 1.0, 2 * hw)
+        err = max_rel(out[st:st + n], want)
+        print(f"  sequence [{st}, +{n}): max_rel {err:.2e}", flush=True)
+        assert err < 2e-3, (st, n)
+
+
+def test_attention_split_rejects_unsupported(ctx):
+    d = ctx.alloc(1024)
+    try:
+        with pytest.raises(ge.GemmaEmbedError):
+            ctx.attention_split(d, d, d, d, d, d, d, 1, 3, 1, 512, 0, 1.0)  # 3 query heads per KV head
+        with pytest.raises(ge.GemmaEmbedError):
+            ctx.attention_split(d, d, d, d, d, d, d, 1, 4, 1, 256, 0, 1.0)  # head dim 256
+    finally:
+        ctx.free(d)
