@@ -20,7 +20,11 @@ Also reported on the same JSON line:
                 the host API, beside the reference's published M3 Max times (context only: a
                 different chip and real weights);
   cpu_baseline  the CPU oracle (a C restatement of the reference's CPUReference.swift) on a
-                bounded sample of the same workload, on this host's cores.
+                bounded sample of the same workload, on this host's cores;
+  parity        the timed pack's pooled vectors against the oracle's on the texts cpu_baseline
+                ran: min cosine and max abs difference of the L2-normalised vectors;
+  config3 / config1 variants  BASELINE configs 3 (256 ragged texts, Matryoshka 256) and 1 (one
+                Q8_0 GEMM) on the GPU and, on a sample, on the CPU oracle.
 """
 from __future__ import annotations
 
@@ -299,30 +303,190 @@ def library_gemm_comparison(reps: int = 30):
     return rows
 
 
-def cpu_baseline(model_path: str, batch, budget_s: float = 12.0):
-    """The oracle forward on this host's cores over whole texts of the workload until about
-    budget_s seconds of CPU work, scaled to tokens/s."""
-    sys.path.insert(0, os.path.join(ROOT, "oracle"))
-    import ge_oracle as ora
-
+def cpu_threads() -> int:
     threads = len(os.sched_getaffinity(0))
     env_threads = os.environ.get("OMP_NUM_THREADS")
     if env_threads and env_threads.isdigit():
         threads = min(threads, int(env_threads))
-    done_tokens, t_total, n = 0, 0.0, 0
+    return threads
+
+
+def cpu_model() -> str:
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
+def oracle_sample(model_path: str, texts, budget_s: float, label: str):
+    """The oracle forward on this host's cores over whole texts until about budget_s seconds of CPU
+    work: (pooled vectors of the texts done, tokens, seconds, threads)."""
+    sys.path.insert(0, os.path.join(ROOT, "oracle"))
+    import ge_oracle as ora
+
+    threads = cpu_threads()
+    vectors, done_tokens, t_total = [], 0, 0.0
     with ora.OracleModel(model_path) as m:
-        for seq in batch:
+        for seq in texts:
             t0 = time.perf_counter()
-            m.forward(seq, threads=threads)
+            pooled, _ = m.forward(seq, threads=threads)
             t_total += time.perf_counter() - t0
+            vectors.append(pooled)
             done_tokens += len(seq)
-            n += 1
-            log(f"cpu oracle: {n} texts, {t_total:.1f} s")
+            log(f"cpu oracle ({label}): {len(vectors)} texts, {t_total:.1f} s")
             if t_total >= budget_s:
                 break
+    return vectors, done_tokens, t_total, threads
+
+
+def cpu_baseline(model_path: str, batch, budget_s: float = 12.0):
+    """The oracle forward on this host's cores over whole texts of the workload until about
+    budget_s seconds of CPU work, scaled to tokens/s; also returns the oracle's pooled vectors."""
+    vectors, done_tokens, t_total, threads = oracle_sample(model_path, batch, budget_s, "config 2")
+    n = len(vectors)
     return {"value": done_tokens / t_total, "unit": "tokens/s", "cores": threads, "kind": "port",
+            "cpu_model": cpu_model(),
             "sample": f"{n} of the {len(batch)} config-2 texts ({done_tokens} tokens), oracle forward "
-                      f"(ge_oracle.c, OpenMP {threads} threads), {t_total:.2f} s"}
+                      f"(ge_oracle.c, OpenMP {threads} threads), {t_total:.2f} s"}, vectors
+
+
+def parity(gpu_vectors, oracle_vectors, dims=None):
+    """Cosine and the largest difference of the L2-normalised vectors (Matryoshka-truncated to
+    `dims` first when given), GPU against oracle, over the texts both computed (the reference's
+    bars: cosine > 0.99999 and max abs difference < 1e-4, MetalForwardTests.swift:213-214)."""
+    import numpy as np
+    cos, mabs = 1.0, 0.0
+    for g, o in zip(gpu_vectors, oracle_vectors):
+        g, o = np.asarray(g, np.float64), np.asarray(o, np.float64)
+        if dims:
+            g, o = g[:dims], o[:dims]
+        g, o = g / np.linalg.norm(g), o / np.linalg.norm(o)
+        cos = min(cos, float(g @ o))
+        mabs = max(mabs, float(np.abs(g - o).max()))
+    return {"texts": min(len(gpu_vectors), len(oracle_vectors)), "min_cosine": round(cos, 9),
+            "max_abs_normalised": float(f"{mabs:.3e}"), "bar_cosine": 0.99999, "bar_max_abs": 1e-4}
+
+
+def config3_texts():
+    """256 texts of lengths uniform in [8, 256] (SplitMix64 seed 31), ids uniform in
+    [2, 262144) (seed 32)."""
+    import gemma_embed as ge
+    lengths = [int(n) for n in ge.synth_tokens(31, 8, 257, 256)]
+    ids = ge.synth_tokens(32, 2, 262144, sum(lengths))
+    texts, off = [], 0
+    for n in lengths:
+        texts.append([int(t) for t in ids[off:off + n]])
+        off += n
+    return texts
+
+
+def config3_variant(model_path: str, reps: int, with_cpu: bool):
+    """BASELINE config 3 through the host API at the reference's default options with Matryoshka 256:
+    the 256 ragged texts are planned by token count (budget 8192), run, truncated to 256 dims and
+    L2-normalised. Reports the host API's rate (ids in host memory -> normalised vectors, PCIe
+    included), the GPU time of the device forwards of the same planned batches (each batch staged
+    and run; its GPU seconds from events on the library's stream), and the oracle on a sample of
+    the same texts on this host's cores, with the parity of those texts' vectors."""
+    import numpy as np
+    import gemma_embed as ge
+    texts = config3_texts()
+    tokens = sum(len(t) for t in texts)
+    model = ge.EmbeddingModel.load(model_path)
+    try:
+        opts = ge.EmbedOptions(dimensions=256)
+        out = model.embed(texts, opts)
+        t0 = time.perf_counter()
+        for _ in range(reps):
+            out = model.embed(texts, opts)
+        api_s = (time.perf_counter() - t0) / reps
+        vecs = np.stack([e.vector for e in out])
+        if vecs.shape != (256, 256) or not np.all(np.isfinite(vecs)):
+            raise SystemExit("bad config-3 output")
+        ranges = ge.plan_batches([len(t) for t in texts], [8192])
+        ctx = model.context
+        gpu_s = []
+        for _ in range(reps):
+            total = 0.0
+            for r in ranges:
+                total += ctx.forward(texts[r.start:r.stop])[1]
+            gpu_s.append(total)
+        gpu_s = sorted(gpu_s)[len(gpu_s) // 2]
+    finally:
+        model.close()
+    res = {"workload": "config3: 256 texts, lengths U[8, 256], planned by token count (budget 8192), "
+                       "Matryoshka 256 + L2", "tokens": tokens, "planned_batches": len(ranges),
+           "host_api_pcie_inclusive_tokens_per_s": round(tokens / api_s, 1),
+           "gpu_forward_tokens_per_s": round(tokens / gpu_s, 1), "gpu_forward_ms": round(gpu_s * 1e3, 3)}
+    if with_cpu:
+        oracle_vecs, done, secs, threads = oracle_sample(model_path, texts, 6.0, "config 3")
+        res["cpu_oracle"] = {"tokens_per_s": round(done / secs, 1), "cores": threads, "kind": "port",
+                             "sample": f"{len(oracle_vecs)} of the 256 texts ({done} tokens), {secs:.2f} s"}
+        res["parity"] = parity(vecs, oracle_vecs, dims=256)
+    return res
+
+
+def config1_variant(model_path: str, with_cpu: bool):
+    """one Q8_0 GEMM, X fp32 [128 x 768] ~ N(0, 1), W Q8_0 [1152 x 768]
+    (blk.0.ffn_gate.weight of the synthetic config-2 model), Y fp32 [128 x 1152]: the oracle's
+    sgemm on the dequantised weight (the reference caches the dequantised matrix,
+    CPUReference.swift:31-38), median of 5 on this host's cores, and the GPU kernel
+    (ge_op_gemm_q8 on fp16 X), median launch time."""
+    import numpy as np
+    import gemma_embed as ge
+    with ge.GgufFile(model_path) as g:
+        name, shape, typ, off = next(t for t in g.tensors() if t[0] == "blk.0.ffn_gate.weight")
+        assert shape == [768, 1152] and typ == "Q8_0"
+        raw = np.fromfile(model_path, dtype=np.uint8, count=1152 * 24 * 34, offset=g.data_offset + off)
+    x = np.random.default_rng(1).standard_normal((128, 768)).astype(np.float32)
+    flops = 2 * 128 * 1152 * 768
+    res = {"workload": "config1: Y[128 x 1152] = X[128 x 768] W^T, W Q8_0", "flops": flops}
+    ctx = ge.Context.create(0)
+    try:
+        w = ctx.q8_create(raw, 1152, 768)
+        x16 = x.astype(np.float16)
+        dx, dy = ctx.alloc(x16.nbytes), ctx.alloc(128 * 1152 * 4)
+        try:
+            ctx.upload(dx, x16)
+            for _ in range(3):
+                ctx.gemm_q8(w, dx, 128, dy, False)
+            times = []
+            for _ in range(20):
+                ctx.profile_reset()
+                ctx.profile_enable("gemm")
+                ctx.gemm_q8(w, dx, 128, dy, False)
+                times.append(ctx.profile_stats()["gemm"][1])
+                ctx.profile_disable()
+            y = ctx.download(dy, (128, 1152), np.float32)
+        finally:
+            ctx.free(dx)
+            ctx.free(dy)
+            ctx.q8_destroy(w)
+    finally:
+        ctx.close()
+    gpu_ms = sorted(times)[len(times) // 2]
+    res["gpu_ms"] = round(gpu_ms, 5)
+    res["gpu_gflops"] = round(flops / (gpu_ms * 1e-3) / 1e9, 1)
+    if with_cpu:
+        sys.path.insert(0, os.path.join(ROOT, "oracle"))
+        import ge_oracle as ora
+        blocks = raw.reshape(-1, 34)  # Q8_0: fp16 scale, 32 int8 quants (Model/Weights.swift:33-41)
+        wf = (blocks[:, :2].copy().view(np.float16).astype(np.float32) *
+              blocks[:, 2:].view(np.int8).astype(np.float32)).reshape(1152, 768)
+        threads = cpu_threads()
+        cpu_times, want = [], None
+        for _ in range(5):
+            t0 = time.perf_counter()
+            want = ora.matmul(x, wf, threads=threads)
+            cpu_times.append(time.perf_counter() - t0)
+        cpu_s = sorted(cpu_times)[2]
+        res["cpu_oracle"] = {"ms": round(cpu_s * 1e3, 4), "gflops": round(flops / cpu_s / 1e9, 2), "cores": threads,
+                             "kind": "port", "runs": 5, "statistic": "median"}
+        res["max_rel_vs_oracle"] = float(f"{np.abs(y - want).max() / np.abs(want).max():.3e}")
+    return res
 
 
 def main():
@@ -502,8 +666,19 @@ def main():
                      "reference_shapes_host_api": ref_shapes},
     }
     model.close()
+    config3 = config3_variant(path, 3, not args.no_cpu)
+    log(f"config 3 (256 ragged texts): GPU forwards {config3['gpu_forward_tokens_per_s']:,.0f} tok/s, host API "
+        f"{config3['host_api_pcie_inclusive_tokens_per_s']:,.0f} tok/s")
+    config1 = config1_variant(path, not args.no_cpu)
+    log(f"config 1 (one Q8_0 GEMM 128 x 1152 x 768): GPU {config1['gpu_ms'] * 1e3:.1f} us")
+    result["variants"]["config3_ragged_256"] = config3
+    result["variants"]["config1_gemm"] = config1
     if not args.no_cpu:
-        result["cpu_baseline"] = cpu_baseline(path, batch)
+        result["cpu_baseline"], oracle_vectors = cpu_baseline(path, batch)
+        # the timed pack's own vectors (pooled, in text order) against the oracle's on the same texts
+        result["parity"] = parity(pooled, oracle_vectors)
+        log(f"parity over {result['parity']['texts']} texts: min cosine {result['parity']['min_cosine']}, "
+            f"max abs {result['parity']['max_abs_normalised']}")
     print(json.dumps(result))
 
 

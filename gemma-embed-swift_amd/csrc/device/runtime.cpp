@@ -61,10 +61,6 @@ float host_h2f(uint16_t h) {
 
 }  // namespace ge
 
-struct ge_q8_matrix {
-    ge::Q8Dev m;
-};
-
 namespace ge {
 
 LaunchEvents& launch_events() {
@@ -1360,6 +1356,7 @@ void trace(ge_ctx* c, const char* name, int layer, float* out, size_t cap, size_
     } else if (n == "ffn_geglu") {
         need_layer();
         buf = w.act; f16 = true; stride = width = m.ff;
+        unscale = 1.0f / L->act_scale;  // stored times the power of two act_scale
     } else if (n == "ffn_out") {
         need_layer();
         buf = w.t; stride = width = m.hidden;

@@ -136,6 +136,11 @@ void free_vision(ge_ctx* c);
 
 }  // namespace ge
 
+// A Q8_0 matrix of the per-op entry points (ge_op_q8_create).
+struct ge_q8_matrix {
+    ge::Q8Dev m;
+};
+
 struct ge_ctx {
     int device = 0;
     hipStream_t stream = nullptr;
@@ -261,6 +266,10 @@ void copy_out(ge_ctx* c, const void* src, bool f16, int rows, int stride, int co
 // Packed text batches (runtime.cpp): validate and upload (a negative id -(r + 1) names row r of
 // `vectors`, device fp32 [n_vectors][hidden]); enqueue the forward (record_start: time from here,
 // else from an ev_start the caller recorded); wait and copy the pooled vectors out.
+// RopeTable (Model/RopeTable.swift:16-31) for (hd, base) over `positions` positions, cached on the
+// context with the model's weights (freed with them).
+const float* rope_table(ge_ctx* c, int hd, float base, int positions);
+
 void stage(ge_ctx* c, const int32_t* tokens, const int32_t* positions, int n, const ge_seq* seqs, int n_seqs,
            const float* vectors, int n_vectors);
 void run_forward(ge_ctx* c, double* gpu_seconds, bool record_start = true);

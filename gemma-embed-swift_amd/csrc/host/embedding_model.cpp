@@ -98,6 +98,32 @@ int run_batch(ge_model* m, const std::vector<std::vector<int32_t>>& seqs, std::v
 }  // namespace
 }  // namespace ge
 
+namespace ge {
+
+// ModelInfo (Model/ModelConfig.swift:6-32) from a parsed configuration.
+void fill_info(const ModelConfig& cfg, const GGUFFile& file, const std::string& device_name, ge_model_info* info) {
+    std::memset(info, 0, sizeof(*info));
+    std::snprintf(info->architecture, sizeof(info->architecture), "%s", cfg.architecture.c_str());
+    std::snprintf(info->name, sizeof(info->name), "%s", cfg.name.c_str());
+    std::snprintf(info->quantization, sizeof(info->quantization), "%s", cfg.quantization.c_str());
+    std::snprintf(info->device_name, sizeof(info->device_name), "%s", device_name.c_str());
+    info->layers = cfg.layers;
+    info->hidden = cfg.hidden;
+    info->out_dims = cfg.out_dims;
+    info->feed_forward = cfg.feed_forward;
+    info->per_layer_input = cfg.per_layer_input;
+    info->heads = cfg.heads;
+    info->vocab = cfg.vocab;
+    info->sliding_window = cfg.sliding_window;
+    info->max_tokens = cfg.max_tokens;
+    info->eps = cfg.eps;
+    info->file_size = int64_t(file.size());
+    info->bos_id = cfg.bos_id;
+    info->eos_id = cfg.eos_id;
+}
+
+}  // namespace ge
+
 extern "C" {
 
 int ge_model_load(const char* path, const ge_load_options* options, ge_model** out, char* err, size_t errlen) {
@@ -143,25 +169,64 @@ ge_ctx* ge_model_context(ge_model* m) { return m ? m->ctx : nullptr; }
 
 int ge_model_get_info(const ge_model* m, ge_model_info* info) {
     if (!m || !info) return GE_ERR_INVALID;
-    std::memset(info, 0, sizeof(*info));
-    std::snprintf(info->architecture, sizeof(info->architecture), "%s", m->cfg.architecture.c_str());
-    std::snprintf(info->name, sizeof(info->name), "%s", m->cfg.name.c_str());
-    std::snprintf(info->quantization, sizeof(info->quantization), "%s", m->cfg.quantization.c_str());
-    std::snprintf(info->device_name, sizeof(info->device_name), "%s", m->device_name.c_str());
-    info->layers = m->cfg.layers;
-    info->hidden = m->cfg.hidden;
-    info->out_dims = m->cfg.out_dims;
-    info->feed_forward = m->cfg.feed_forward;
-    info->per_layer_input = m->cfg.per_layer_input;
-    info->heads = m->cfg.heads;
-    info->vocab = m->cfg.vocab;
-    info->sliding_window = m->cfg.sliding_window;
-    info->max_tokens = m->cfg.max_tokens;
-    info->eps = m->cfg.eps;
-    info->file_size = int64_t(m->file->size());
-    info->bos_id = m->cfg.bos_id;
-    info->eos_id = m->cfg.eos_id;
+    ge::fill_info(m->cfg, *m->file, m->device_name, info);
     return GE_OK;
+}
+
+// ---- the GGUF reader on its own, host only (GGUFFile, GGUF/GGUFFile.swift:21-67; ModelConfig.init)
+
+struct ge_gguf {
+    std::unique_ptr<ge::GGUFFile> file;
+};
+
+int ge_gguf_open(const char* path, ge_gguf** out, char* err, size_t errlen) {
+    if (!path || !out) return GE_ERR_INVALID;
+    *out = nullptr;
+    try {
+        std::unique_ptr<ge_gguf> g(new ge_gguf);
+        g->file.reset(new ge::GGUFFile(path));
+        *out = g.release();
+        return GE_OK;
+    } catch (const ge::Error& e) {
+        if (err && errlen) std::snprintf(err, errlen, "%s", e.what());
+        return e.code;
+    }
+}
+
+void ge_gguf_close(ge_gguf* g) { delete g; }
+
+int ge_gguf_counts(const ge_gguf* g, uint32_t* version, int64_t* kv_count, int64_t* tensor_count, uint64_t* data_offset,
+                   uint64_t* file_size) {
+    if (!g) return GE_ERR_INVALID;
+    if (version) *version = g->file->version();
+    if (kv_count) *kv_count = int64_t(g->file->meta_count());
+    if (tensor_count) *tensor_count = int64_t(g->file->tensors().size());
+    if (data_offset) *data_offset = g->file->data_offset();
+    if (file_size) *file_size = g->file->size();
+    return GE_OK;
+}
+
+int ge_gguf_tensor(const ge_gguf* g, int64_t i, ge_tensor_desc* out) {
+    if (!g || !out || i < 0 || i >= int64_t(g->file->tensors().size())) return GE_ERR_INVALID;
+    const ge::TensorInfo& t = g->file->tensors()[size_t(i)];
+    if (t.shape.size() > 4) return GE_ERR_GGUF;
+    out->name = t.name.c_str();
+    out->offset = t.offset;
+    out->type = t.type;
+    out->ndim = int32_t(t.shape.size());
+    for (int k = 0; k < 4; k++) out->shape[k] = k < out->ndim ? t.shape[size_t(k)] : 1;
+    return GE_OK;
+}
+
+int ge_gguf_text_config(const ge_gguf* g, ge_model_info* info, char* err, size_t errlen) {
+    if (!g || !info) return GE_ERR_INVALID;
+    try {
+        ge::fill_info(ge::read_config(*g->file), *g->file, "", info);
+        return GE_OK;
+    } catch (const ge::Error& e) {
+        if (err && errlen) std::snprintf(err, errlen, "%s", e.what());
+        return e.code;
+    }
 }
 
 int ge_plan_batches(const int32_t* costs, int32_t n, const int32_t* budgets, int32_t nb, int32_t batch_size,

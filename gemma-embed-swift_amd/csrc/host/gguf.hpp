@@ -74,6 +74,8 @@ public:
     const uint8_t* data(const TensorInfo& t) const { return base_ + file_offset(t); }
     const std::vector<TensorInfo>& tensors() const { return tensors_; }
     uint32_t version() const { return version_; }
+    size_t meta_count() const { return meta_.size(); }
+    uint64_t data_offset() const { return data_offset_; }
 
 private:
     uint8_t* base_ = nullptr;

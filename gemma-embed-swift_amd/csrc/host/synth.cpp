@@ -72,6 +72,9 @@ struct TensorSpec {
     // value rule: Q8_0 block scales from |N(0, scale)|; F32 offset + scale N(0, 1); F16 and BF16
     // scale N(0, 1)
     double scale = -1, offset_f = 1;
+    // F32: this many entries replaced by +-U(outlier / 6, outlier)
+    int outliers = 0;
+    double outlier = 0;
     size_t bytes() const {
         int64_t n = 1;
         for (auto d : shape) n *= d;
@@ -128,7 +131,14 @@ void write_tensor_data(Writer& w, const TensorSpec& t, uint64_t seed) {
         }
     } else if (t.type == GE_TYPE_F32) {
         const double sc = t.scale >= 0 ? t.scale : 0.1;
-        for (int64_t i = 0; i < n; i++) w.put<float>(float(t.offset_f + sc * rng.gaussian()));
+        std::vector<float> v(static_cast<size_t>(n));
+        for (int64_t i = 0; i < n; i++) v[size_t(i)] = float(t.offset_f + sc * rng.gaussian());
+        for (int k = 0; k < t.outliers && n > 0; k++) {
+            const int64_t at = int64_t(rng.uniform_int(0, n));
+            const double mag = t.outlier * (1.0 / 6.0 + (5.0 / 6.0) * rng.unit());
+            v[size_t(at)] = float(rng.unit() < 0.5 ? -mag : mag);
+        }
+        for (float x : v) w.put<float>(x);
     } else if (t.type == GE_TYPE_BF16) {
         const double sc = t.scale > 0 ? t.scale : 0.02;
         for (int64_t i = 0; i < n; i++) w.put<uint16_t>(float_to_bf16(float(sc * rng.gaussian())));
@@ -157,7 +167,9 @@ void synth_write(const std::string& path, const ge_synth_spec& s) {
     str("general.name", "synthetic-gemma-embedding2");
     u32("general.alignment", 32);
     u32(a + "block_count", uint64_t(s.layers));
-    u32(a + "context_length", 8192);
+    if (s.context_length < 0 || s.norm_outliers < 0 || s.norm_outlier < 0)
+        throw Error(GE_ERR_INVALID, "synthetic spec has a negative context length or outlier setting");
+    u32(a + "context_length", uint64_t(s.context_length > 0 ? s.context_length : 8192));
     u32(a + "embedding_length", uint64_t(s.hidden));
     u32(a + "embedding_length_out", uint64_t(s.out_dims));
     if (s.per_layer_input > 0) u32(a + "embedding_length_per_layer_input", uint64_t(s.per_layer_input));
@@ -199,8 +211,14 @@ void synth_write(const std::string& path, const ge_synth_spec& s) {
     const int64_t d = s.hidden, ff = s.feed_forward, pl = s.per_layer_input;
     std::vector<TensorSpec> ts;
     auto add = [&](const std::string& n, std::vector<int64_t> shape, int type) { ts.push_back({n, shape, type, 0}); };
+    // a residual-stream norm weight, with the spec's outliers
+    auto add_norm = [&](const std::string& n, int64_t width) {
+        add(n, {width}, GE_TYPE_F32);
+        ts.back().outliers = s.norm_outliers;
+        ts.back().outlier = s.norm_outlier;
+    };
     add("output.weight", {d, s.out_dims}, GE_TYPE_Q8_0);
-    add("output_norm.weight", {d}, GE_TYPE_F32);
+    add_norm("output_norm.weight", d);
     if (pl > 0) {
         add("per_layer_model_proj.weight", {d, pl * s.layers}, GE_TYPE_BF16);
         add("per_layer_proj_norm.weight", {pl}, GE_TYPE_F32);
@@ -214,23 +232,23 @@ void synth_write(const std::string& path, const ge_synth_spec& s) {
         const std::string b = "blk." + std::to_string(i) + ".";
         add(b + "attn_k.weight", {d, kvd}, GE_TYPE_Q8_0);
         add(b + "attn_k_norm.weight", {hd}, GE_TYPE_F32);
-        add(b + "attn_norm.weight", {d}, GE_TYPE_F32);
+        add_norm(b + "attn_norm.weight", d);
         add(b + "attn_output.weight", {qd, d}, GE_TYPE_Q8_0);
         add(b + "attn_q.weight", {d, qd}, GE_TYPE_Q8_0);
         add(b + "attn_q_norm.weight", {hd}, GE_TYPE_F32);
         add(b + "attn_v.weight", {d, kvd}, GE_TYPE_Q8_0);
         add(b + "ffn_down.weight", {ff, d}, GE_TYPE_Q8_0);
         add(b + "ffn_gate.weight", {d, ff}, GE_TYPE_Q8_0);
-        add(b + "ffn_norm.weight", {d}, GE_TYPE_F32);
+        add_norm(b + "ffn_norm.weight", d);
         add(b + "ffn_up.weight", {d, ff}, GE_TYPE_Q8_0);
         if (pl > 0) {
             add(b + "inp_gate.weight", {d, pl}, GE_TYPE_Q8_0);
             add(b + "layer_output_scale.weight", {1}, GE_TYPE_F32);
         }
-        add(b + "post_attention_norm.weight", {d}, GE_TYPE_F32);
-        add(b + "post_ffw_norm.weight", {d}, GE_TYPE_F32);
+        add_norm(b + "post_attention_norm.weight", d);
+        add_norm(b + "post_ffw_norm.weight", d);
         if (pl > 0) {
-            add(b + "post_norm.weight", {d}, GE_TYPE_F32);
+            add_norm(b + "post_norm.weight", d);
             add(b + "proj.weight", {pl, d}, GE_TYPE_Q8_0);
         }
     }

@@ -59,6 +59,11 @@ class ge_embed_options(C.Structure):
                 ("batch_size", C.c_int32)]
 
 
+class ge_tensor_desc(C.Structure):
+    _fields_ = [("name", C.c_char_p), ("offset", C.c_uint64), ("type", C.c_int32), ("ndim", C.c_int32),
+                ("shape", C.c_int64 * 4)]
+
+
 class ge_model_info(C.Structure):
     _fields_ = [("architecture", C.c_char * 64), ("name", C.c_char * 128),
                 ("layers", C.c_int32), ("hidden", C.c_int32), ("out_dims", C.c_int32),
@@ -74,7 +79,8 @@ class ge_synth_spec(C.Structure):
                 ("vocab", C.c_int32), ("sliding_window", C.c_int32), ("head_dim_swa", C.c_int32),
                 ("head_dim_global", C.c_int32), ("kv_heads_swa", C.c_int32), ("kv_heads_global", C.c_int32),
                 ("eps", C.c_float), ("rope_base", C.c_float), ("rope_base_swa", C.c_float),
-                ("pattern", C.POINTER(C.c_uint8)), ("seed", C.c_uint64)]
+                ("pattern", C.POINTER(C.c_uint8)), ("seed", C.c_uint64), ("context_length", C.c_int32),
+                ("norm_outliers", C.c_int32), ("norm_outlier", C.c_float)]
 
 
 class ge_vision_info(C.Structure):
@@ -131,9 +137,21 @@ SIGNATURES = {
     "ge_attention_queries": (C.c_int32, []),
     "ge_op_attention": (_I, [_P, _P, _P, _P, _P, _P, C.c_int32, C.c_int32, C.c_int32, C.c_int32, C.c_int32,
                              C.c_float]),
+    "ge_op_rmsnorm": (_I, [_P, _P, _P, _P, C.c_int32, C.c_int32, C.c_float, C.c_float]),
+    "ge_op_rmsnorm_residual": (_I, [_P, _P, _P, _P, C.c_float, _P, _P, C.c_int32, C.c_int32, C.c_float]),
+    "ge_op_qk_norm_rope": (_I, [_P, _P, C.c_int32, C.c_int32, C.c_int32, C.c_int32, _P, _P, C.c_float, _P, C.c_float,
+                                _P, _P, _P]),
+    "ge_op_embed": (_I, [_P, _P, _P, C.c_int32, C.c_float, _P, C.c_int32, _P, C.c_float, _P, _P]),
+    "ge_op_mean_pool": (_I, [_P, _P, C.c_int32, C.c_int32, _P, C.c_int32, _P]),
     "ge_op_attention_split": (_I, [_P, _P, _P, _P, _P, _P, _P, _P, C.c_int32, C.c_int32, C.c_int32, C.c_int32,
                                    C.c_int32, C.c_float]),
     "ge_model_load": (_I, [C.c_char_p, C.POINTER(ge_load_options), C.POINTER(_P), C.c_char_p, C.c_size_t]),
+    "ge_gguf_open": (_I, [C.c_char_p, C.POINTER(_P), C.c_char_p, C.c_size_t]),
+    "ge_gguf_close": (None, [_P]),
+    "ge_gguf_counts": (_I, [_P, C.POINTER(C.c_uint32), C.POINTER(C.c_int64), C.POINTER(C.c_int64),
+                            C.POINTER(C.c_uint64), C.POINTER(C.c_uint64)]),
+    "ge_gguf_tensor": (_I, [_P, C.c_int64, C.POINTER(ge_tensor_desc)]),
+    "ge_gguf_text_config": (_I, [_P, C.POINTER(ge_model_info), C.c_char_p, C.c_size_t]),
     "ge_model_free": (None, [_P]),
     "ge_model_last_error": (C.c_char_p, [_P]),
     "ge_model_get_info": (_I, [_P, C.POINTER(ge_model_info)]),
@@ -239,6 +257,9 @@ TINY = dict(layers=2, hidden=128, heads=2, feed_forward=256, out_dims=128, per_l
             eps=1e-6, rope_base=1e6, rope_base_swa=1e4, pattern=[1, 0], seed=7)
 # The same with the per-layer-input branch (64-wide per-layer inputs).
 TINY_PLE = dict(TINY, per_layer_input=64, heads=2, kv_heads_swa=1, kv_heads_global=1, seed=9)
+# Config 2's shapes over 6 layers (one global) with norm weights carrying outliers of 50 to 300,
+# as trained models' residual-stream norms do: stresses the fp16 range scales chosen at load.
+OUTLIER_NORMS = dict(CONFIG2, layers=6, pattern=[1, 1, 1, 1, 1, 0], norm_outliers=4, norm_outlier=300.0, seed=21)
 # The reference's real architecture (Model/Architecture.md:7-9, Fixtures/model.json): d 512, 4 query
 # heads, sliding layers of 2 KV heads of 256 (window 1024, RoPE 1e4), global layers 5, 11, 17, 23 of
 # 1 KV head of 512 (RoPE 1e6), GeGLU 2048, per-layer inputs of 512, output 768; synthetic weights.
@@ -258,6 +279,9 @@ def synth_write_gguf(path: str, **spec) -> str:
     s.eps, s.rope_base, s.rope_base_swa = spec["eps"], spec["rope_base"], spec["rope_base_swa"]
     s.pattern = _ptr(pattern, C.c_uint8)
     s.seed = int(spec["seed"])
+    s.context_length = int(spec.get("context_length", 0))
+    s.norm_outliers = int(spec.get("norm_outliers", 0))
+    s.norm_outlier = float(spec.get("norm_outlier", 0.0))
     err = C.create_string_buffer(512)
     rc = lib.ge_synth_write_gguf(path.encode(), C.byref(s), err, 512)
     if rc != GE_OK:
@@ -548,6 +572,35 @@ class Context:
                                         C.c_void_p(work), n_work, heads, kv_heads, head_dim, half_window, scale),
                     "ge_op_attention")
 
+    # ---- the forward's row kernels on device memory (pointers from alloc)
+    def rmsnorm(self, x: int, out: int, w: Optional[int], rows: int, width: int, eps: float, pre_scale: float = 1.0):
+        self._check(lib.ge_op_rmsnorm(self.handle, C.c_void_p(x), C.c_void_p(out), C.c_void_p(w) if w else None, rows,
+                                      width, eps, pre_scale), "ge_op_rmsnorm")
+
+    def rmsnorm_residual(self, x: int, t16: int, w: int, scale: float, next_w: Optional[int], h16: Optional[int],
+                         rows: int, width: int, eps: float):
+        self._check(lib.ge_op_rmsnorm_residual(self.handle, C.c_void_p(x), C.c_void_p(t16), C.c_void_p(w), scale,
+                                               C.c_void_p(next_w) if next_w else None,
+                                               C.c_void_p(h16) if h16 else None, rows, width, eps),
+                    "ge_op_rmsnorm_residual")
+
+    def qk_norm_rope(self, qkv: int, tokens: int, heads: int, kv_heads: int, head_dim: int, q_norm: int, k_norm: int,
+                     eps: float, positions: int, rope_base: float, q: int, k: int, v: int):
+        self._check(lib.ge_op_qk_norm_rope(self.handle, C.c_void_p(qkv), tokens, heads, kv_heads, head_dim,
+                                           C.c_void_p(q_norm), C.c_void_p(k_norm), eps, C.c_void_p(positions), rope_base,
+                                           C.c_void_p(q), C.c_void_p(k), C.c_void_p(v)), "ge_op_qk_norm_rope")
+
+    def embed(self, table, tokens: int, n_tokens: int, scale: float, vectors: Optional[int], n_vectors: int,
+              norm_w: Optional[int], eps: float, x: int, h16: Optional[int]):
+        self._check(lib.ge_op_embed(self.handle, table, C.c_void_p(tokens), n_tokens, scale,
+                                    C.c_void_p(vectors) if vectors else None, n_vectors,
+                                    C.c_void_p(norm_w) if norm_w else None, eps, C.c_void_p(x),
+                                    C.c_void_p(h16) if h16 else None), "ge_op_embed")
+
+    def mean_pool(self, x: int, rows: int, width: int, seqs: int, n_seqs: int, pooled: int):
+        self._check(lib.ge_op_mean_pool(self.handle, C.c_void_p(x), rows, width, C.c_void_p(seqs), n_seqs,
+                                        C.c_void_p(pooled)), "ge_op_mean_pool")
+
     def attention_split(self, q: int, q_lo: int, k: int, k_lo: int, v: int, out: int, work: int, n_work: int,
                         heads: int, kv_heads: int, head_dim: int, half_window: int, scale: float = 1.0):
         """Split-precision scores: q and k as fp16 (hi, lo) pairs in device memory."""
@@ -565,6 +618,58 @@ def attention_work(sequences_ranges, queries: Optional[int] = None) -> np.ndarra
         for q0 in range(0, length, q):
             items.append((start, length, q0))
     return np.asarray(items, dtype=np.uint32).reshape(-1, 3)
+
+
+# ---------------------------------------------------------------------------- GGUF reader (host only)
+
+class GgufFile:
+    """The library's GGUF reader on its own (GGUFFile(url:), GGUF/GGUFFile.swift:21-67): counts, the
+    tensor directory in file order, and the text configuration ModelConfig.init derives. No GPU."""
+
+    TYPE_NAMES = {GE_TYPE_F32: "F32", GE_TYPE_F16: "F16", GE_TYPE_Q8_0: "Q8_0", GE_TYPE_BF16: "BF16"}
+
+    def __init__(self, path: str):
+        h = _P()
+        err = C.create_string_buffer(512)
+        rc = lib.ge_gguf_open(path.encode(), C.byref(h), err, 512)
+        if rc != GE_OK:
+            raise GemmaEmbedError(rc, err.value.decode())
+        self.handle = h
+        v, kv, nt, do, fs = C.c_uint32(), C.c_int64(), C.c_int64(), C.c_uint64(), C.c_uint64()
+        lib.ge_gguf_counts(h, C.byref(v), C.byref(kv), C.byref(nt), C.byref(do), C.byref(fs))
+        self.version, self.kv_count, self.tensor_count = v.value, kv.value, nt.value
+        self.data_offset, self.file_size = do.value, fs.value
+
+    def tensors(self) -> List[Tuple[str, List[int], str, int]]:
+        """(name, ne shape, type name, offset in the data section) in file order."""
+        out = []
+        d = ge_tensor_desc()
+        for i in range(self.tensor_count):
+            rc = lib.ge_gguf_tensor(self.handle, i, C.byref(d))
+            if rc != GE_OK:
+                raise GemmaEmbedError(rc, f"tensor {i}")
+            out.append((d.name.decode(), [int(d.shape[k]) for k in range(d.ndim)],
+                        self.TYPE_NAMES.get(d.type, str(d.type)), int(d.offset)))
+        return out
+
+    def text_config(self) -> "ge_model_info":
+        info = ge_model_info()
+        err = C.create_string_buffer(512)
+        rc = lib.ge_gguf_text_config(self.handle, C.byref(info), err, 512)
+        if rc != GE_OK:
+            raise GemmaEmbedError(rc, err.value.decode())
+        return info
+
+    def close(self):
+        if self.handle:
+            lib.ge_gguf_close(self.handle)
+            self.handle = None
+
+    def __enter__(self):
+        return self
+
+    def __exit__(self, *a):
+        self.close()
 
 
 # ---------------------------------------------------------------------------- host API mirror

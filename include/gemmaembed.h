@@ -164,6 +164,42 @@ int ge_op_gemm_q8(ge_ctx* ctx, const ge_q8_matrix* w, const void* x, int32_t m, 
 int ge_op_gemm_q8_geglu(ge_ctx* ctx, const ge_q8_matrix* gate, const ge_q8_matrix* up, const void* x, int32_t m,
                         void* act);
 
+/* The forward's row kernels on device memory (fp32 unless stated; widths a multiple of 4 up to
+ * 1024). Integer inputs the kernels gather with (ids, positions, sequence ranges) are checked on
+ * the host first.
+ *
+ * Kernels.rmsNorm (Metal/MetalForward.swift:502-511; Shaders/Elementwise.metal:38-75):
+ * out[r] = rmsnorm(x[r] * pre_scale) * w over `rows` rows of `width`; w nullable (no weight); out
+ * may be x. */
+int ge_op_rmsnorm(ge_ctx* ctx, const void* x, void* out, const void* w, int32_t rows, int32_t width, float eps,
+                  float pre_scale);
+/* Kernels.rmsNormResidual and rmsNormResidualNorm (Metal/MetalForward.swift:615-643;
+ * Shaders/Elementwise.metal:260-354): x = (x + rmsnorm(t) * w) * scale in place, with the sublayer
+ * output t in fp16 (as the forward stores it); with next_w set, also h16 = rmsnorm(x) * next_w in
+ * fp16. */
+int ge_op_rmsnorm_residual(ge_ctx* ctx, void* x, const void* t16, const void* w, float scale, const void* next_w,
+                           void* h16, int32_t rows, int32_t width, float eps);
+/* Kernels.rmsNormRope (Metal/MetalForward.swift:655-667; Shaders/Elementwise.metal:97-141) with the V
+ * norm (:394), as the forward runs them on the QKV projection: qkv [tokens][(heads + 2 kv_heads)
+ * head_dim] -> q fp16 [tokens][heads][head_dim] (weighted RMSNorm, NeoX RoPE), k fp16 likewise with
+ * k_norm, v fp16 (unweighted RMSNorm). positions: device int32 [tokens] in [0, 8192); the RoPE
+ * table of (head_dim, rope_base) is computed in fp64 (Model/RopeTable.swift:16-31). head_dim 128,
+ * 256 or 512. */
+int ge_op_qk_norm_rope(ge_ctx* ctx, const void* qkv, int32_t tokens, int32_t heads, int32_t kv_heads, int32_t head_dim,
+                       const void* q_norm, const void* k_norm, float eps, const void* positions, float rope_base, void* q,
+                       void* k, void* v);
+/* Kernels.embed (Metal/MetalForward.swift:490-500; Shaders/Elementwise.metal:8-35), fused with the
+ * first RMSNorm as the forward runs it: x[t] = dequant(table[id]) * scale for id >= 0, row
+ * -(id + 1) of `vectors` (device fp32 [n_vectors][cols]) unscaled for id < 0; h16 (nullable) =
+ * rmsnorm(x) * norm_w in fp16. tokens: device int32 [n_tokens] in [-n_vectors, table rows). */
+int ge_op_embed(ge_ctx* ctx, const ge_q8_matrix* table, const void* tokens, int32_t n_tokens, float scale,
+                const void* vectors, int32_t n_vectors, const void* norm_w, float eps, void* x, void* h16);
+/* Kernels.meanPool (Metal/MetalForward.swift:751-758; Shaders/Elementwise.metal:243-256):
+ * pooled[s] = mean of rows [start, start + length) of x [rows][width]; seqs: device ge_seq [n_seqs]
+ * inside the rows (an empty sequence pools to 0). */
+int ge_op_mean_pool(ge_ctx* ctx, const void* x, int32_t rows, int32_t width, const void* seqs, int32_t n_seqs,
+                    void* pooled);
+
 /* AttentionWork (Shaders/Common.metal:75-79): a block of query rows of one sequence. */
 typedef struct ge_attention_work {
     uint32_t seq_start;
@@ -299,6 +335,21 @@ int ge_model_get_info(const ge_model* model, ge_model_info* info);
 /* The model's device context, for ge_forward_trace / ge_profile_* on a loaded model. */
 ge_ctx* ge_model_context(ge_model* model);
 
+/* The GGUF reader alone, on the host (GGUFFile(url:), GGUF/GGUFFile.swift:21-67): what the
+ * reference's GGUFReaderTests check against Fixtures/model.json. ge_gguf_counts: GGUF version,
+ * metadata key count, tensor count, data section offset and file size (each nullable).
+ * ge_gguf_tensor: tensor i in file order, offset from the data section's start; the name stays
+ * valid until ge_gguf_close. ge_gguf_text_config: ModelConfig.init and the weight directory's
+ * checks (Model/ModelConfig.swift:54-112, Model/Weights.swift:92-132) as a ModelInfo with an
+ * empty device name. */
+typedef struct ge_gguf ge_gguf;
+int ge_gguf_open(const char* path, ge_gguf** out, char* err, size_t errlen);
+void ge_gguf_close(ge_gguf* g);
+int ge_gguf_counts(const ge_gguf* g, uint32_t* version, int64_t* kv_count, int64_t* tensor_count, uint64_t* data_offset,
+                   uint64_t* file_size);
+int ge_gguf_tensor(const ge_gguf* g, int64_t i, ge_tensor_desc* out);
+int ge_gguf_text_config(const ge_gguf* g, ge_model_info* info, char* err, size_t errlen);
+
 /* EmbeddingModel.embed(_:options:progress:) (EmbeddingModel.swift:145-175) over pre-tokenized
  * texts: `tokens` holds n_texts sequences back to back, `lengths[i]` ids each (BOS/EOS included,
  * as the tokenizer returns them). Truncates to max_tokens keeping EOS (:189-196), batches
@@ -327,13 +378,20 @@ int ge_finish(const float* vector, int32_t width, int32_t dimensions, int32_t no
 /* Synthetic GGUF writer for seeded test and bench models (no reference counterpart: the
  * reference's models are downloaded). Rules: q ~ U{-127..127} per Q8_0 block with fp16 scale
  * |N(0, 0.02)| * max|q| / 127; fp32 norm weights 1 + 0.1 N(0,1); SplitMix64 streams seeded per
- * tensor from (seed, tensor name). per_layer_input = 0 writes no per-layer-input tensors. */
+ * tensor from (seed, tensor name). per_layer_input = 0 writes no per-layer-input tensors.
+ * context_length 0 writes 8192. norm_outliers > 0 replaces that many entries (at random positions)
+ * of every residual-stream norm weight (attn_norm, post_attention_norm, ffn_norm, post_ffw_norm,
+ * post_norm, output_norm) with +-U(norm_outlier / 6, norm_outlier): trained models' norm weights
+ * carry such outliers, which stress the fp16 range scales chosen at load. */
 typedef struct ge_synth_spec {
     int32_t layers, hidden, heads, feed_forward, out_dims, per_layer_input, vocab, sliding_window;
     int32_t head_dim_swa, head_dim_global, kv_heads_swa, kv_heads_global;
     float eps, rope_base, rope_base_swa;
     const uint8_t* pattern; /* [layers], 1 = sliding */
     uint64_t seed;
+    int32_t context_length;
+    int32_t norm_outliers;
+    float norm_outlier;
 } ge_synth_spec;
 int ge_synth_write_gguf(const char* path, const ge_synth_spec* spec, char* err, size_t errlen);
 

@@ -73,16 +73,30 @@ def config2_batch():
     return [t.tolist() for t in toks]
 
 
+def normalised(v):
+    v = np.asarray(v, np.float64)
+    return v / np.linalg.norm(v)
+
+
+@pytest.mark.timeout(600)
 def test_config2_pooled_vs_oracle(c2_model, c2_oracle, config2_batch):
+    """All 32 texts of BASELINE config 2 in one pack against the oracle: cosine and the largest
+    difference of the normalised vectors (the reference's own GPU-vs-CPU bar is 1e-4,
+    MetalForwardTests.swift:213-214)."""
     print("config2 forward 32 x 512 (one pack of 16384)", flush=True)
     pooled, secs = c2_model.context.forward(config2_batch)
     print(f"gpu forward {secs * 1e3:.2f} ms", flush=True)
     assert pooled.shape == (32, 768)
-    for i in (0, 13, 31):
+    worst_cos, worst_abs = 1.0, 0.0
+    for i in range(32):
         want, _ = c2_oracle.forward(config2_batch[i])
         c = cosine(pooled[i], want)
-        print(f"seq {i} cosine {c:.9f} max_rel {max_rel(pooled[i], want):.3e}", flush=True)
-        assert c >= COSINE_BAR
+        d = float(np.abs(normalised(pooled[i]) - normalised(want)).max())
+        worst_cos, worst_abs = min(worst_cos, c), max(worst_abs, d)
+        print(f"seq {i} cosine {c:.9f} max_abs(normalised) {d:.2e}", flush=True)
+        assert c >= COSINE_BAR, i
+    print(f"config2: min cosine {worst_cos:.9f}, max abs difference of normalised vectors {worst_abs:.2e}", flush=True)
+    assert worst_abs < 1e-4
 
 
 def test_config2_per_layer_vs_oracle(c2_model, c2_oracle, config2_batch):
@@ -97,8 +111,6 @@ def test_config2_per_layer_vs_oracle(c2_model, c2_oracle, config2_batch):
         got = c2_model.context.trace(batch, name, layer)
         rows = got[idx * 512:(idx + 1) * 512]
         want = tr[(name, layer)].reshape(512, -1)
-        if name == "ffn_geglu":  # stored scaled by a power of two; compare the shape-invariant ratio
-            rows = rows * (np.abs(want).max() / max(np.abs(rows).max(), 1e-30))
         r = max_rel(rows, want)
         worst = max(worst, r) if name == "l_out" else worst
         print(f"{name}-{layer}: max_rel {r:.3e}", flush=True)
@@ -123,8 +135,6 @@ def test_every_trace_tensor_vs_oracle(c2_model, c2_oracle, config2_batch, length
     for name, layer in names:
         got = c2_model.context.trace(batch, name, layer)[lo:lo + n]
         want = tr[(name, layer)].reshape(n, -1)
-        if name == "ffn_geglu":  # stored scaled by a power of two; compare the shape-invariant ratio
-            got = got * (np.abs(want).max() / max(np.abs(got).max(), 1e-30))
         r = max_rel(got, want)
         print(f"{name}-{layer}: max_rel {r:.3e}", flush=True)
         assert r <= PER_LAYER_TOL, (name, layer)
@@ -152,6 +162,80 @@ def test_split_batch_matches_single_stream(c2_model, config2_batch):
     finally:
         ctx.profile_disable()
     assert np.array_equal(split, single)
+
+
+@pytest.mark.timeout(300)
+def test_split_forward_repeats_bitwise(c2_model, config2_batch):
+    """The pack split into parts on several streams, whose layers run unsynchronised on shared
+    buffer slices, run 50 times (and three times queued back to back): every run equals the
+    single-stream result bit for bit (the reference's concurrent-vs-serial check,
+    MetalImageForwardTests.swift:189-224)."""
+    ctx = c2_model.context
+    ctx.profile_enable("")
+    try:
+        single, _ = ctx.forward(config2_batch)
+    finally:
+        ctx.profile_disable()
+    ctx.batch_stage(config2_batch)
+    for i in range(50):
+        ctx.batch_run()
+        got = ctx.batch_read()
+        assert np.array_equal(got, single), f"run {i} differs from the single-stream forward"
+    for _ in range(3):
+        ctx.batch_run()
+    assert np.array_equal(ctx.batch_read(), single)
+    print("50 split forwards equal the single-stream forward", flush=True)
+
+
+@pytest.fixture(scope="module")
+def outlier_gguf(model_dir):
+    import os
+    return ge.synth_write_gguf(os.path.join(model_dir, "outlier_norms.gguf"), **ge.OUTLIER_NORMS)
+
+
+@pytest.mark.timeout(300)
+def test_outlier_norm_weights_vs_oracle(outlier_gguf):
+    """Residual-stream norm weights with entries of 50 to 300 (ge.OUTLIER_NORMS), against the oracle:
+    pooled vectors at cosine >= 0.99999, and every traced intermediate within 1e-2 or, where the
+    fp16-operand arithmetic itself moves it further, within twice what a float64 emulation of the
+    kernels' fp16 rounding points gives (tests/fp16_emulation.py; recorded per text, layer and
+    tensor in tests/golden/outlier_fp16_emulation.json). The FFN intermediates stay near 1e-3, so
+    the fp16 range scales chosen at load hold with such weights. The attention outputs of the
+    global layer do not: its queries' best keys nearly tie (a 0.1% quantile gap of 0.005 between
+    the two largest scores), and the 2^-11 roundings of the dequantised weights alone, through the
+    five layers before it, move them by up to 13% (emulated: 0.204 with every rounding)."""
+    import json
+    import os
+    import npref
+    g = npref.Gguf(outlier_gguf)
+    assert np.abs(g.tensor("blk.0.ffn_norm.weight")).max() >= 50  # the outliers are there
+    emulated = json.load(open(os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden",
+                                           "outlier_fp16_emulation.json")))
+    assert emulated["spec"]["seed"] == ge.OUTLIER_NORMS["seed"]
+    m = ge.EmbeddingModel.load(outlier_gguf)
+    try:
+        seqs = [ge.synth_tokens(t["seed"], 2, 262144, t["length"]).tolist() for t in emulated["texts"]]
+        lengths = [len(x) for x in seqs]
+        pooled = m.embed_tokens(seqs)
+        names = [(n, l) for l in range(6) for n in ("l_out", "kqv_out", "ffn_geglu", "ffn_out")]
+        with ora.OracleModel(outlier_gguf) as o:
+            want = [o.forward(sq, keep=names) for sq in seqs]
+        for i in range(len(seqs)):
+            c = cosine(pooled[i], want[i][0])
+            print(f"outlier norms: text {i} ({lengths[i]} tokens) cosine {c:.8f}", flush=True)
+            assert c >= COSINE_BAR, i
+        for name, layer in names:
+            got = m.context.trace(seqs, name, layer)
+            off = 0
+            for i, n in enumerate(lengths):
+                err = max_rel(got[off:off + n], want[i][1][(name, layer)].reshape(n, -1))
+                off += n
+                emu = emulated["texts"][i]["max_rel"][f"{name}/{layer}"]
+                print(f"outlier norms: {name} layer {layer} text {i}: max_rel {err:.2e} (fp16 emulation {emu:.2e})",
+                      flush=True)
+                assert err <= max(PER_LAYER_TOL, 2 * emu), (name, layer, i)
+    finally:
+        m.close()
 
 
 def test_attention_item_size_does_not_change_results(c2_model, config2_batch):

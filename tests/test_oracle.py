@@ -11,6 +11,7 @@ import numpy as np
 import pytest
 
 import ge_oracle as ora
+import gemma_embed as ge
 import npref
 
 RNG = np.random.default_rng(1234)
@@ -299,3 +300,24 @@ def test_open_rejects_non_gguf(tmp_path):
     p.write_bytes(b"\x41" * 4096)  # GGUFReaderTests.swift:68-75
     with pytest.raises(ValueError, match="invalid GGUF"):
         ora.OracleModel(str(p))
+
+
+def test_fp16_emulation_is_the_float64_forward_without_rounding(tmp_path):
+    """tests/fp16_emulation.py with rounding off is tests/npref.py's float64 forward (so its rounded
+    run differs from the reference's arithmetic only by the fp16 roundings it injects), and its
+    rounding is fp16's round-to-nearest-even on values in the normal range."""
+    import fp16_emulation as emu
+    path = ge.synth_write_gguf(str(tmp_path / "tiny.gguf"), **ge.TINY)
+    g = npref.Gguf(path)
+    toks = [int(t) for t in ge.synth_tokens(5, 2, 512, 37)]
+    keep = [("l_out", 0), ("l_out", 1), ("kqv_out", 1), ("ffn_geglu", 0)]
+    pooled, tr = emu.forward(g, toks, False, keep)
+    want_pooled, want = npref.forward(g, np.asarray(toks), keep=tuple(keep))
+    assert np.allclose(pooled, want_pooled, rtol=1e-12, atol=1e-12)
+    for k in keep:
+        assert np.allclose(tr[k].reshape(-1), want[k], rtol=1e-10, atol=1e-12), k
+    x = np.random.default_rng(3).standard_normal(10000) * 100
+    x[0] = 2.0 ** 14 * 1.5  # the largest entry maps to 2^14 exactly: no rescaling error
+    assert np.array_equal(emu.f16(x), x.astype(np.float16).astype(np.float64))
+    _, rounded = emu.forward(g, toks, True, keep)
+    assert 0 < np.abs(rounded[("l_out", 1)] - tr[("l_out", 1)]).max() / np.abs(tr[("l_out", 1)]).max() < 1e-2
