@@ -687,20 +687,11 @@ void ensure_workspace_impl(ge_ctx* c, int tokens, int seqs, int work, int work2,
     }
 }
 
-// Batches of at least this many tokens are split into two halves on two streams.
-constexpr int kSplitMinTokens = 4096;
 // Below this many 64-query workgroups (one per CU), use 32-query items. Measured at config 2's
 // sliding layers: a 8192-token pack (128 items) 36.5 -> 31.0 us per attention launch; a 16384-token
 // pack (256 items) 41.0 -> 57.0 us, so it keeps 64-query items.
 constexpr int kAttnSmallItems = 256;
 
-// Transposed-V layout of a packed batch: each sequence's keys start at a column that is a
-// multiple of 8 (16-byte aligned copies); vt_cols leaves a key block of slack past the end.
-struct VtLayout {
-    std::vector<uint32_t> start;  // per sequence
-    std::vector<int32_t> vcol;    // per token
-    int cols = 0;
-};
 
 VtLayout vt_layout(int n_tokens, const ge_seq* seqs, int n_seqs) {
     VtLayout v;
@@ -721,35 +712,33 @@ VtLayout vt_layout(int n_tokens, const ge_seq* seqs, int n_seqs) {
 
 // ---------------------------------------------------------------- batch staging
 
-// Validates a packed batch and uploads it with its attention work list (PackedBatch and
-// AttentionWork.items, Metal/MetalForward.swift:8-58; execute :326-334).
-void stage(ge_ctx* c, const int32_t* tokens, const int32_t* positions, int n, const ge_seq* seqs, int n_seqs,
-           const float* vectors, int n_vectors) {
+// Validates a packed batch and builds its attention work lists, V^T layout and split into parts
+// (PackedBatch and AttentionWork.items, Metal/MetalForward.swift:8-58; execute :326-334). Host only.
+BatchPlan plan_batch(ge_ctx* c, const int32_t* tokens, const int32_t* positions, int n, const ge_seq* seqs, int n_seqs,
+                     const float* vectors, int n_vectors) {
     if (!c->has_model) fail(GE_ERR_STATE, "no model has been uploaded");
     if (n <= 0 || !tokens || !positions) fail(GE_ERR_INVALID, "a batch needs at least one token");
     if (n_seqs <= 0 || !seqs) fail(GE_ERR_INVALID, "a batch needs at least one sequence");
     const DevModel& m = c->model;
     if (!vectors) n_vectors = 0;
-    bool any_vector = false;
-    int vec_rows_read = 0;
+    BatchPlan b;
     for (int i = 0; i < n; i++) {
         if (tokens[i] < -n_vectors || tokens[i] >= m.vocab)
             fail(GE_ERR_INVALID, "token %d at row %d is neither in the vocabulary [0, %d) nor one of the %d vector rows",
                  tokens[i], i, m.vocab, n_vectors);
-        any_vector |= tokens[i] < 0;
-        if (tokens[i] < 0) vec_rows_read = std::max(vec_rows_read, -tokens[i]);
+        b.any_vector |= tokens[i] < 0;
+        if (tokens[i] < 0) b.vec_rows_read = std::max(b.vec_rows_read, -tokens[i]);
         if (positions[i] < 0 || positions[i] >= m.max_tokens)
             fail(GE_ERR_INVALID, "position %d at row %d is outside [0, %d)", positions[i], i, m.max_tokens);
     }
-    std::vector<AttnWork> work;
-    std::vector<SeqRange> sr((size_t)n_seqs);
+    b.sr.resize(size_t(n_seqs));
     for (int s = 0; s < n_seqs; s++) {
         const uint64_t end = uint64_t(seqs[s].start) + seqs[s].length;
         if (end > uint64_t(n)) fail(GE_ERR_INVALID, "sequence %d [%u, +%u) runs past the %d tokens", s, seqs[s].start, seqs[s].length, n);
         if (seqs[s].length > uint32_t(m.max_tokens)) fail(GE_ERR_INVALID, "sequence %d has %u tokens, more than %d", s, seqs[s].length, m.max_tokens);
-        sr[s] = SeqRange{seqs[s].start, seqs[s].length};
+        b.sr[size_t(s)] = SeqRange{seqs[s].start, seqs[s].length};
         for (uint32_t q0 = 0; q0 < seqs[s].length; q0 += kAttnQueries)
-            work.push_back(AttnWork{seqs[s].start, seqs[s].length, q0, 0});
+            b.work.push_back(AttnWork{seqs[s].start, seqs[s].length, q0, 0});
     }
     // Sequences may not share tokens: each token's key and value belong to one sequence.
     {
@@ -760,26 +749,21 @@ void stage(ge_ctx* c, const int32_t* tokens, const int32_t* positions, int n, co
         for (size_t i = 1; i < iv.size(); i++)
             if (iv[i].first < iv[i - 1].second) fail(GE_ERR_INVALID, "sequences overlap at token %u", iv[i].first);
     }
-    std::vector<AttnWork> work2;
-    VtLayout vl;
-    int items = kAttnQueriesV2;
     if (m.any_v2) {
-        vl = vt_layout(n, seqs, n_seqs);
+        b.vl = vt_layout(n, seqs, n_seqs);
         // A batch whose 64-query items would give fewer than kAttnSmallItems workgroups (a pack of
         // 8192 tokens: 128) takes 32-query items: twice the workgroups, the same results (a query's
         // wave sees the same key blocks; blocks outside its window add exact zeros).
         int64_t items64 = 0;
         for (int s = 0; s < n_seqs; s++) items64 += (seqs[s].length + kAttnQueriesV2 - 1) / kAttnQueriesV2;
-        if (m.items32_ok && items64 * m.max_kv_heads < kAttnSmallItems) items = 32;
+        if (m.items32_ok && items64 * m.max_kv_heads < kAttnSmallItems) b.items = 32;
         for (int s = 0; s < n_seqs; s++)
-            for (uint32_t q0 = 0; q0 < seqs[s].length; q0 += uint32_t(items))
-                work2.push_back(AttnWork{seqs[s].start, seqs[s].length, q0, vl.start[size_t(s)]});
+            for (uint32_t q0 = 0; q0 < seqs[s].length; q0 += uint32_t(b.items))
+                b.work2.push_back(AttnWork{seqs[s].start, seqs[s].length, q0, b.vl.start[size_t(s)]});
     }
     // Split a large batch of several sequences into parts of whole sequences, cut at the
     // sequence starts nearest to p n / P, whose layers run on their own streams: one part's
     // memory-bound kernels and its kernels' start and end phases overlap the others' work.
-    int n_parts = 1;
-    int part_row[kMaxParts + 1] = {0}, part_work[kMaxParts + 1] = {0};
     if (m.all_v2 && n >= kSplitMinTokens && n_seqs >= 2) {
         const int want = kMaxParts;
         std::vector<int> starts;
@@ -796,24 +780,47 @@ void stage(ge_ctx* c, const int32_t* tokens, const int32_t* positions, int n, co
             if (best > 0 && best < n) cuts.push_back(best);
         }
         if (!cuts.empty()) {
-            n_parts = int(cuts.size()) + 1;
-            for (int p = 1; p < n_parts; p++) part_row[p] = cuts[size_t(p) - 1];
-            part_row[n_parts] = n;
+            b.n_parts = int(cuts.size()) + 1;
+            for (int p = 1; p < b.n_parts; p++) b.part_row[p] = cuts[size_t(p) - 1];
+            b.part_row[b.n_parts] = n;
             auto part_of = [&](const AttnWork& a) {
                 int p = 0;
-                while (p + 1 < n_parts && int(a.seq_start) >= part_row[p + 1]) p++;
+                while (p + 1 < b.n_parts && int(a.seq_start) >= b.part_row[p + 1]) p++;
                 return p;
             };
-            std::stable_sort(work2.begin(), work2.end(), [&](const AttnWork& a, const AttnWork& b) { return part_of(a) < part_of(b); });
-            for (const AttnWork& a : work2) part_work[part_of(a) + 1]++;
-            for (int p = 0; p < n_parts; p++) part_work[p + 1] += part_work[p];
-            for (int p = 0; p < n_parts; p++)
-                if (part_work[p + 1] == part_work[p]) n_parts = 1;  // a part without work: do not split
+            std::stable_sort(b.work2.begin(), b.work2.end(), [&](const AttnWork& x, const AttnWork& y) { return part_of(x) < part_of(y); });
+            for (const AttnWork& a : b.work2) b.part_work[part_of(a) + 1]++;
+            for (int p = 0; p < b.n_parts; p++) b.part_work[p + 1] += b.part_work[p];
+            for (int p = 0; p < b.n_parts; p++)
+                if (b.part_work[p + 1] == b.part_work[p]) b.n_parts = 1;  // a part without work: do not split
         }
     }
+    return b;
+}
+
+// Records a planned batch as the context's staged batch (its arrays already on their way to the
+// workspace the forward reads).
+void set_staged(ge_ctx* c, const BatchPlan& b, int n, int n_seqs, const float* vectors) {
+    c->staged_tokens = n;
+    c->staged_vectors = b.any_vector ? vectors : nullptr;
+    c->staged_vec_rows = b.vec_rows_read;
+    c->staged_seqs = n_seqs;
+    c->staged_work = int(b.work.size());
+    c->staged_work2 = int(b.work2.size());
+    c->staged_vt_cols = b.vl.cols;
+    c->attn_items = b.items;
+    c->n_parts = b.n_parts;
+    std::copy(b.part_row, b.part_row + kMaxParts + 1, c->part_row);
+    std::copy(b.part_work, b.part_work + kMaxParts + 1, c->part_work);
+}
+
+// Validates and uploads a packed batch into the context's workspace, grown as needed.
+void stage(ge_ctx* c, const int32_t* tokens, const int32_t* positions, int n, const ge_seq* seqs, int n_seqs,
+           const float* vectors, int n_vectors) {
+    const BatchPlan b = plan_batch(c, tokens, positions, n, seqs, n_seqs, vectors, n_vectors);
     // The workspace may be reallocated below: nothing queued may still use it.
-    if (workspace_grows(c, n, n_seqs, int(work.size()), int(work2.size()), vl.cols)) drain(c);
-    ensure_workspace(c, n, n_seqs, int(work.size()), int(work2.size()), vl.cols);
+    if (workspace_grows(c, n, n_seqs, int(b.work.size()), int(b.work2.size()), b.vl.cols)) drain(c);
+    ensure_workspace(c, n, n_seqs, int(b.work.size()), int(b.work2.size()), b.vl.cols);
     Workspace& w = c->ws;
     // The small arrays go through one pinned buffer: asynchronous copies, no wait for them here
     // (the forward's kernels follow them on the same stream).
@@ -824,10 +831,10 @@ void stage(ge_ctx* c, const int32_t* tokens, const int32_t* positions, int n, co
     };
     const Piece pieces[] = {{w.tokens, tokens, size_t(n) * 4},
                             {w.positions, positions, size_t(n) * 4},
-                            {w.seqs, sr.data(), sr.size() * sizeof(SeqRange)},
-                            {w.work, work.data(), work.size() * sizeof(AttnWork)},
-                            {w.work2, work2.data(), work2.size() * sizeof(AttnWork)},
-                            {w.vcol, vl.vcol.data(), work2.empty() ? 0 : size_t(n) * 4}};
+                            {w.seqs, b.sr.data(), b.sr.size() * sizeof(SeqRange)},
+                            {w.work, b.work.data(), b.work.size() * sizeof(AttnWork)},
+                            {w.work2, b.work2.data(), b.work2.size() * sizeof(AttnWork)},
+                            {w.vcol, b.vl.vcol.data(), b.work2.empty() ? 0 : size_t(n) * 4}};
     size_t total = 0;
     for (const Piece& pc : pieces) total += (pc.bytes + 255) / 256 * 256;
     if (c->staged_copy_recorded) hip_check(hipEventSynchronize(c->staged_copy), "hipEventSynchronize");
@@ -849,17 +856,7 @@ void stage(ge_ctx* c, const int32_t* tokens, const int32_t* positions, int n, co
     }
     hip_check(hipEventRecord(c->staged_copy, c->stream), "hipEventRecord");
     c->staged_copy_recorded = true;
-    c->staged_tokens = n;
-    c->staged_vectors = any_vector ? vectors : nullptr;
-    c->staged_vec_rows = vec_rows_read;
-    c->staged_seqs = n_seqs;
-    c->staged_work = int(work.size());
-    c->staged_work2 = int(work2.size());
-    c->staged_vt_cols = vl.cols;
-    c->attn_items = items;
-    c->n_parts = n_parts;
-    std::copy(part_row, part_row + kMaxParts + 1, c->part_row);
-    std::copy(part_work, part_work + kMaxParts + 1, c->part_work);
+    set_staged(c, b, n, n_seqs, vectors);
 }
 
 // ---------------------------------------------------------------- forward

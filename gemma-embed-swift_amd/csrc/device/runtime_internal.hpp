@@ -266,6 +266,43 @@ void copy_out(ge_ctx* c, const void* src, bool f16, int rows, int stride, int co
 // Packed text batches (runtime.cpp): validate and upload (a negative id -(r + 1) names row r of
 // `vectors`, device fp32 [n_vectors][hidden]); enqueue the forward (record_start: time from here,
 // else from an ev_start the caller recorded); wait and copy the pooled vectors out.
+// Transposed-V layout of a packed batch: each sequence's keys start at a column that is a
+// multiple of 8 (16-byte aligned copies); cols leaves a key block of slack past the end.
+struct VtLayout {
+    std::vector<uint32_t> start;  // per sequence
+    std::vector<int32_t> vcol;    // per token
+    int cols = 0;
+};
+
+// A validated packed batch, planned on the host: sequence ranges, attention work lists (32-query
+// items; LDS-copy attention items of `items` queries with V^T columns), the V^T layout and the
+// split into parts.
+struct BatchPlan {
+    std::vector<SeqRange> sr;
+    std::vector<AttnWork> work, work2;
+    VtLayout vl;
+    int items = kAttnQueriesV2;
+    int n_parts = 1;
+    int part_row[kMaxParts + 1] = {0}, part_work[kMaxParts + 1] = {0};
+    bool any_vector = false;
+    int vec_rows_read = 0;
+};
+BatchPlan plan_batch(ge_ctx* c, const int32_t* tokens, const int32_t* positions, int n, const ge_seq* seqs, int n_seqs,
+                     const float* vectors, int n_vectors);
+void set_staged(ge_ctx* c, const BatchPlan& b, int n, int n_seqs, const float* vectors);
+// The rows ge_set_vectors uploaded, when they are as wide as the model's residual stream.
+const float* own_vectors(ge_ctx* c);
+int own_vector_rows(ge_ctx* c);
+// MetalForward.encode (Metal/MetalForward.swift:364-423) of the staged batch on the context's
+// stream, one launch after another (sp: stop after the op producing a traced tensor; null = all).
+struct StopPoint;
+void encode(ge_ctx* c, StopPoint* sp);
+// Waits for every stream of the context.
+void drain(ge_ctx* c);
+// Packs of at least this many tokens (of two or more sequences) run as parts on several streams.
+constexpr int kSplitMinTokens = 4096;
+
+
 // RopeTable (Model/RopeTable.swift:16-31) for (hd, base) over `positions` positions, cached on the
 // context with the model's weights (freed with them).
 const float* rope_table(ge_ctx* c, int hd, float base, int positions);
