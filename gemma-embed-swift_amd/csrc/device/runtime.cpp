@@ -1420,6 +1420,7 @@ int ge_create(int device, ge_ctx** out) {
         if (std::strncmp(prop.gcnArchName, "gfx950", 6) != 0)
             fail(GE_ERR_NO_DEVICE, "device %d is %s; this library is built for gfx950 (MI355X)", device, prop.gcnArchName);
         ge::hip_check(ge::configure_kernels(), "configure kernels");
+        ge::noalloc_init(c.get());
     });
     if (rc != GE_OK) {
         ge::g_create_error = c->err;

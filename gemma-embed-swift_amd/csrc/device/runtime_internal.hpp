@@ -188,6 +188,8 @@ struct ge_ctx {
     const float* staged_vectors = nullptr;
     // One past the largest vector row the staged batch reads (0 when it reads none).
     int staged_vec_rows = 0;
+    // This device's copy of the no-allocation forward's scratch array (noalloc.cpp).
+    void* scratch = nullptr;
 };
 
 namespace ge {
@@ -301,7 +303,9 @@ void encode(ge_ctx* c, StopPoint* sp);
 void drain(ge_ctx* c);
 // Packs of at least this many tokens (of two or more sequences) run as parts on several streams.
 constexpr int kSplitMinTokens = 4096;
-
+// Takes the device address of the no-allocation forward's scratch array on the context's device
+// (noalloc.cpp); called once per context at creation.
+void noalloc_init(ge_ctx* c);
 
 // RopeTable (Model/RopeTable.swift:16-31) for (hd, base) over `positions` positions, cached on the
 // context with the model's weights (freed with them).

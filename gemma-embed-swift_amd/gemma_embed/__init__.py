@@ -137,6 +137,8 @@ SIGNATURES = {
     "ge_attention_queries": (C.c_int32, []),
     "ge_op_attention": (_I, [_P, _P, _P, _P, _P, _P, C.c_int32, C.c_int32, C.c_int32, C.c_int32, C.c_int32,
                              C.c_float]),
+    "ge_forward_noalloc": (_I, [_P, _PI32, _PI32, C.c_int32, C.POINTER(ge_seq), C.c_int32, _PF,
+                                C.POINTER(C.c_double)]),
     "ge_op_rmsnorm": (_I, [_P, _P, _P, _P, C.c_int32, C.c_int32, C.c_float, C.c_float]),
     "ge_op_rmsnorm_residual": (_I, [_P, _P, _P, _P, C.c_float, _P, _P, C.c_int32, C.c_int32, C.c_float]),
     "ge_op_qk_norm_rope": (_I, [_P, _P, C.c_int32, C.c_int32, C.c_int32, C.c_int32, _P, _P, C.c_float, _P, C.c_float,
@@ -379,6 +381,16 @@ class Context:
     @property
     def device_name(self) -> str:
         return lib.ge_device_name(self.handle).decode()
+
+    def forward_noalloc(self, sequences: Sequence[Sequence[int]]):
+        """ge_forward_noalloc: as forward(), with no device allocation (the library's scratch array)."""
+        toks, pos, seqs = pack(sequences)
+        out = np.zeros((len(seqs), self.out_dims), dtype=np.float32)
+        secs = C.c_double(0)
+        self._check(lib.ge_forward_noalloc(self.handle, _ptr(toks, C.c_int32), _ptr(pos, C.c_int32), len(toks),
+                                           _seq_array(seqs), len(seqs), _ptr(out, C.c_float), C.byref(secs)),
+                    "ge_forward_noalloc")
+        return out, secs.value
 
     def forward(self, sequences: Sequence[Sequence[int]]):
         """One packed batch -> (pooled [n_seqs, out_dims], gpu_seconds)."""

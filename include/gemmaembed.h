@@ -100,6 +100,19 @@ typedef struct ge_seq {
 int ge_forward(ge_ctx* ctx, const int32_t* tokens, const int32_t* positions, int32_t n_tokens, const ge_seq* seqs,
                int32_t n_seqs, float* pooled_out, double* gpu_seconds);
 
+/* ge_forward with no device allocation: no counterpart in the reference; for callers that cannot
+ * allocate device memory (code under HIP graph capture, tight serving loops, harnesses that forbid
+ * hipMalloc). Same arguments, results bitwise those of ge_forward. The forward's workspace
+ * (activations, staged ids and work lists, V^T, pooled output) lives in a 64 MiB device array of
+ * the library, one per GPU, held until the process ends; its address is taken at ge_create. A pack
+ * whose workspace does not fit (above about 2700 tokens for config 2's model, 380 for the
+ * reference's architecture with its per-layer inputs) or of 4096 tokens or
+ * more is refused with GE_ERR_INVALID, as is a call while profiling is enabled. Calls on one GPU
+ * share the array: calls that overlap (two contexts of one GPU used from two threads) race. The
+ * context's own staged batch and workspace are left as they were. */
+int ge_forward_noalloc(ge_ctx* ctx, const int32_t* tokens, const int32_t* positions, int32_t n_tokens,
+                       const ge_seq* seqs, int32_t n_seqs, float* pooled_out, double* gpu_seconds);
+
 /* The workspace's `vectors` buffer (Metal/MetalForward.swift:137,165), filled from the host: fp32
  * [n_rows][width] copied into HBM, where the batches of ge_forward, ge_forward_trace and
  * ge_batch_stage find the rows their negative ids name. Rows are used only while `width` equals
