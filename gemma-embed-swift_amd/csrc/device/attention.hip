@@ -106,6 +106,9 @@ __global__ __launch_bounds__(256) void attention_kernel(const uint16_t* __restri
     const bool computes = wave < G;
     const int h = kvh * G + wave;
     const int len = int(wi.seq_len), q0 = int(wi.q0);
+    // A work item of an empty sequence has nothing to attend; leaving before any access also keeps
+    // the (len - 1) in the buffer ranges and row clamps below from wrapping around.
+    if (len <= 0) return;
     const int qStride = H * HD, kvStride = KV * HD;
     const int d0 = slice * DS;
     const int qi = q0 + (lane & 31);
@@ -308,6 +311,9 @@ __global__ __launch_bounds__(2 * G * 64) void attention_v2_kernel(const uint16_t
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int h = kvh * G + wave % G;
     const int len = int(wi.seq_len), q0 = int(wi.q0) + (wave / G) * 32;
+    // A work item of an empty sequence has nothing to attend; leaving before any access also keeps
+    // the (len - 1) in the buffer ranges and row clamps below from wrapping around.
+    if (len <= 0) return;
     const int qi = q0 + (lane & 31), half = lane >> 5;
     const int qStride = H * HD, kvStride = KV * HD;
 
@@ -563,6 +569,9 @@ __global__ __launch_bounds__(QW * G * 64) void attention_v3_kernel(const uint16_
     const int widx = bx < full ? (bx % 8) * (full / 8) + bx / 8 : bx;
     const int seq_start = __builtin_amdgcn_readfirstlane(int(work[widx].seq_start));
     const int len = __builtin_amdgcn_readfirstlane(int(work[widx].seq_len));
+    // A work item of an empty sequence has nothing to attend; leaving before any access also keeps
+    // the (len - 1) in the buffer ranges and row clamps below from wrapping around.
+    if (len <= 0) return;
     // grid z splits a work item into parts of QB queries (head dim 512: 32-query workgroups over
     // 64-query items)
     const int wq0 = __builtin_amdgcn_readfirstlane(int(work[widx].q0)) + int(blockIdx.z) * QB;
@@ -852,6 +861,9 @@ __global__ __launch_bounds__(G * 64) void attention_split_kernel(const uint16_t*
     const int widx = bx < full ? (bx % 8) * (full / 8) + bx / 8 : bx;
     const int seq_start = __builtin_amdgcn_readfirstlane(int(work[widx].seq_start));
     const int len = __builtin_amdgcn_readfirstlane(int(work[widx].seq_len));
+    // A work item of an empty sequence has nothing to attend; leaving before any access also keeps
+    // the (len - 1) in the buffer ranges and row clamps below from wrapping around.
+    if (len <= 0) return;
     const int q0 = __builtin_amdgcn_readfirstlane(int(work[widx].q0)) + int(blockIdx.z) * 16;
     const int vt_start = __builtin_amdgcn_readfirstlane(int(work[widx].vt_start));
     const int kvh = blockIdx.y;
@@ -1076,6 +1088,9 @@ __global__ __launch_bounds__(QW * 64) void attention_mq_kernel(const uint16_t* _
     const int widx = bx < full ? (bx % 8) * (full / 8) + bx / 8 : bx;
     const int seq_start = __builtin_amdgcn_readfirstlane(int(work[widx].seq_start));
     const int len = __builtin_amdgcn_readfirstlane(int(work[widx].seq_len));
+    // A work item of an empty sequence has nothing to attend; leaving before any access also keeps
+    // the (len - 1) in the buffer ranges and row clamps below from wrapping around.
+    if (len <= 0) return;
     const int wq0 = __builtin_amdgcn_readfirstlane(int(work[widx].q0));
     const int vt_start = __builtin_amdgcn_readfirstlane(int(work[widx].vt_start));
     const int h = blockIdx.y;

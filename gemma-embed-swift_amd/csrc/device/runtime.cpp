@@ -814,6 +814,18 @@ void set_staged(ge_ctx* c, const BatchPlan& b, int n, int n_seqs, const float* v
     std::copy(b.part_work, b.part_work + kMaxParts + 1, c->part_work);
 }
 
+// GE_SYNC_STAGING=1 uploads staged batches with synchronous hipMemcpy instead of asynchronous
+// copies from pinned host memory. Under rocprofv3 --pmc the asynchronous copies did not reach the
+// workspace (a staged config-2 pack read back as zeros: every pooled vector 0), so counter runs of
+// whole forwards set it; nothing else needs it.
+bool sync_staging() {
+    static const bool on = [] {
+        const char* e = std::getenv("GE_SYNC_STAGING");
+        return e && e[0] == '1';
+    }();
+    return on;
+}
+
 // Validates and uploads a packed batch into the context's workspace, grown as needed.
 void stage(ge_ctx* c, const int32_t* tokens, const int32_t* positions, int n, const ge_seq* seqs, int n_seqs,
            const float* vectors, int n_vectors) {
@@ -835,6 +847,14 @@ void stage(ge_ctx* c, const int32_t* tokens, const int32_t* positions, int n, co
                             {w.work, b.work.data(), b.work.size() * sizeof(AttnWork)},
                             {w.work2, b.work2.data(), b.work2.size() * sizeof(AttnWork)},
                             {w.vcol, b.vl.vcol.data(), b.work2.empty() ? 0 : size_t(n) * 4}};
+    if (sync_staging()) {
+        // Synchronous copies from the caller's arrays (profiling aid, see sync_staging).
+        drain(c);
+        for (const Piece& pc : pieces)
+            if (pc.bytes) hip_check(hipMemcpy(pc.dst, pc.src, pc.bytes, hipMemcpyHostToDevice), "upload batch");
+        set_staged(c, b, n, n_seqs, vectors);
+        return;
+    }
     size_t total = 0;
     for (const Piece& pc : pieces) total += (pc.bytes + 255) / 256 * 256;
     if (c->staged_copy_recorded) hip_check(hipEventSynchronize(c->staged_copy), "hipEventSynchronize");

@@ -22,6 +22,15 @@
 //                             heads, KV 2 x 256 sliding / 1 x 512 global, GeGLU 2048, per-layer
 //                             inputs 512, 24 layers; synthetic weights): a resident 8 x 1024-token
 //                             pack and a 1 x 64-token pack (ge_batch_run), the time per forward
+//   ge_probe forward [reps] [parts]
+//                             the whole config-2 forward (synthetic 24-layer model, a resident pack of
+//                             32 x 512 tokens): every kernel class of the text path at its config-2
+//                             shape. By default on one stream with every launch timed by HIP events
+//                             (ge_profile_enable), so each kernel runs at M = 16384 and the probe
+//                             prints a per-kernel table; with "parts" the pack runs as the timed
+//                             forward does (four parts on four streams, no events)
+//   ge_probe reference_forward [reps]
+//                             the same for the reference's real architecture (8 x 1024 tokens)
 //   ge_probe calibrate        fp16 -> fp32 conversion of 2^28 values (reads 512 MiB, writes 1 GiB):
 //                             the known-size kernel that scales the HBM byte counters
 //
@@ -30,6 +39,7 @@
 // their fragment-order copy; a profile reads the GEMM kernel's own rows.
 #include <algorithm>
 #include <chrono>
+#include <cmath>
 #include <cstdint>
 #include <cstdio>
 #include <cstdlib>
@@ -325,6 +335,78 @@ int probe_image_embed(int reps) {
     return 0;
 }
 
+// A synthetic model written to a temporary GGUF and loaded (config 2, or the reference's real
+// shapes), the file removed once loaded.
+ge_model* load_synthetic(bool real_shapes) {
+    static uint8_t pattern[24];
+    for (int l = 0; l < 24; l++) pattern[l] = (l % 6 == 5) ? 0 : 1;
+    ge_synth_spec spec{};
+    spec.layers = 24, spec.heads = real_shapes ? 4 : 3, spec.out_dims = 768, spec.vocab = 262144;
+    spec.hidden = real_shapes ? 512 : 768, spec.feed_forward = real_shapes ? 2048 : 1152;
+    spec.per_layer_input = real_shapes ? 512 : 0, spec.sliding_window = real_shapes ? 1024 : 512;
+    spec.head_dim_swa = 256, spec.head_dim_global = real_shapes ? 512 : 256;
+    spec.kv_heads_swa = real_shapes ? 2 : 1, spec.kv_heads_global = 1;
+    spec.eps = 1e-6f, spec.rope_base = 1e6f, spec.rope_base_swa = 1e4f, spec.pattern = pattern;
+    spec.seed = real_shapes ? 12 : 4;
+    char err[512] = {0};
+    const char* path = real_shapes ? "/tmp/ge_probe_reference_shapes.gguf" : "/tmp/ge_probe_config2.gguf";
+    if (ge_synth_write_gguf(path, &spec, err, sizeof err) != 0) {
+        std::fprintf(stderr, "ge_probe: synth: %s\n", err);
+        return nullptr;
+    }
+    ge_load_options lo{0, 16384, 1};
+    ge_model* m = nullptr;
+    if (ge_model_load(path, &lo, &m, err, sizeof err) != 0) std::fprintf(stderr, "ge_probe: load: %s\n", err);
+    std::remove(path);
+    return m;
+}
+
+// The whole forward over a resident pack (config 2: 32 x 512; real shapes: 8 x 1024), per-kernel
+// HIP-event times unless `parts`.
+int probe_forward(int reps, bool real_shapes, bool parts) {
+    ge_model* m = load_synthetic(real_shapes);
+    if (!m) return 1;
+    ge_ctx* c = ge_model_context(m);
+    const int texts = real_shapes ? 8 : 32, len = real_shapes ? 1024 : 512;
+    std::vector<int32_t> ids(size_t(texts) * len), pos(ids.size());
+    std::vector<ge_seq> seqs(static_cast<size_t>(texts));
+    ge_synth_tokens(3, 2, 262144, int32_t(ids.size()), ids.data());
+    for (int t = 0; t < texts; t++) {
+        seqs[size_t(t)] = ge_seq{uint32_t(t * len), uint32_t(len)};
+        for (int i = 0; i < len; i++) pos[size_t(t) * len + i] = i;
+    }
+    if (ge_batch_stage(c, ids.data(), pos.data(), int32_t(ids.size()), seqs.data(), texts) != 0) return fail(c, "stage");
+    for (int r = 0; r < 2; r++) ge_batch_run(c);
+    ge_sync(c);
+    if (!parts) ge_profile_enable(c, "");
+    ge_profile_reset(c);
+    const auto t0 = std::chrono::steady_clock::now();
+    for (int r = 0; r < reps; r++)
+        if (ge_batch_run(c) != 0) return fail(c, "run");
+    std::vector<float> out(size_t(texts) * 768);
+    if (ge_batch_read(c, out.data()) != 0) return fail(c, "read");
+    const double ms = std::chrono::duration<double, std::milli>(std::chrono::steady_clock::now() - t0).count() / reps;
+    double check = 0;
+    for (float v : out) check += std::fabs(double(v));
+    std::printf("%s forward, %d x %d tokens (%s): %.3f ms per forward; sum |pooled| %.6e\n",
+                real_shapes ? "reference shapes" : "config 2", texts, len,
+                parts ? "parts on four streams" : "one stream, every launch timed", ms, check);
+    if (!parts) {
+        std::printf("%-24s %9s %10s %12s\n", "kernel", "launches", "avg us", "ms/forward");
+        for (int i = 0;; i++) {
+            const char* name = nullptr;
+            int64_t n = 0;
+            double total = 0;
+            if (ge_profile_get(c, i, &name, &n, &total) != 0) break;
+            std::printf("%-24s %9lld %10.2f %12.4f\n", name, (long long)(n / reps), total / double(n) * 1e3, total / reps);
+        }
+        ge_profile_disable(c);
+    }
+    std::fflush(stdout);
+    ge_model_free(m);
+    return 0;
+}
+
 int probe_calibrate(ge_ctx* c) {
     const size_t n = size_t(1) << 28;
     void* src = ge_dev_alloc(c, 2 * n);
@@ -346,9 +428,12 @@ int main(int argc, char** argv) {
     if (std::strcmp(what, "embed") == 0) return reps < 1 || reps > 10000 ? 2 : probe_embed(reps);
     if (std::strcmp(what, "reference_shapes") == 0) return reps < 1 || reps > 10000 ? 2 : probe_reference_shapes(reps);
     if (std::strcmp(what, "image_embed") == 0) return reps < 1 || reps > 10000 ? 2 : probe_image_embed(reps);
+    if (std::strcmp(what, "forward") == 0 || std::strcmp(what, "reference_forward") == 0)
+        return reps < 1 || reps > 10000 ? 2
+                                        : probe_forward(reps, what[0] == 'r', argc > 3 && std::strcmp(argv[3], "parts") == 0);
     if (std::strcmp(what, "gate_up") != 0 && std::strcmp(what, "attention") != 0 && std::strcmp(what, "calibrate") != 0 &&
         std::strcmp(what, "vision") != 0) {
-        std::fprintf(stderr, "usage: ge_probe gate_up|attention|embed|vision|reference_shapes|image_embed [reps] | ge_probe calibrate\n");
+        std::fprintf(stderr, "usage: ge_probe gate_up|attention|embed|vision|reference_shapes|image_embed|forward|reference_forward [reps] | ge_probe calibrate\n");
         return 2;
     }
     if (reps < 1 || reps > 10000) {
