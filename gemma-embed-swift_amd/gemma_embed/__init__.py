@@ -16,7 +16,8 @@ from typing import Callable, Iterable, List, Optional, Sequence, Tuple
 import numpy as np
 
 _HERE = os.path.dirname(os.path.abspath(__file__))
-LIB_PATH = os.path.join(os.path.dirname(_HERE), "libgemmaembed.so")
+# GE_LIBRARY names another build of the same library (the sanitizer build the CPU tests load).
+LIB_PATH = os.environ.get("GE_LIBRARY") or os.path.join(os.path.dirname(_HERE), "libgemmaembed.so")
 
 GE_OK = 0
 ERRORS = {
