@@ -21,46 +21,61 @@ __global__ __launch_bounds__(256) void embed_norm_kernel(const int8_t* __restric
     const int id = tokens[row];
     float v[CH][4];
     float ss = 0.0f;
+    // Every chunk's loads are issued before any is used (a lane past d reads chunk d - 4 and
+    // discards it), so the row's loads are in flight together instead of one after another.
     if (id < 0) {
         const float* src = vectors + (size_t)(-(id + 1)) * d;
+        float4 f[CH];
+#pragma unroll
+        for (int c = 0; c < CH; c++) f[c] = *reinterpret_cast<const float4*>(src + min(c * 256 + lane * 4, d - 4));
 #pragma unroll
         for (int c = 0; c < CH; c++) {
             const int e = c * 256 + lane * 4;
             if (e < d) {
-                const float4 f = *reinterpret_cast<const float4*>(src + e);
-                v[c][0] = f.x, v[c][1] = f.y, v[c][2] = f.z, v[c][3] = f.w;
+                v[c][0] = f[c].x, v[c][1] = f[c].y, v[c][2] = f[c].z, v[c][3] = f[c].w;
 #pragma unroll
                 for (int j = 0; j < 4; j++) ss += v[c][j] * v[c][j];
-                *reinterpret_cast<float4*>(x + (size_t)row * d + e) = f;
+                *reinterpret_cast<float4*>(x + (size_t)row * d + e) = f[c];
             }
         }
     } else {
         const int8_t* q = tq + (size_t)id * d;
         const uint16_t* sc = ts + (size_t)id * (d / 32);
+        uint32_t packed[CH];
+        uint16_t sbits[CH];
+#pragma unroll
+        for (int c = 0; c < CH; c++) {
+            const int ec = min(c * 256 + lane * 4, d - 4);
+            packed[c] = *reinterpret_cast<const uint32_t*>(q + ec);
+            sbits[c] = sc[ec / 32];
+        }
 #pragma unroll
         for (int c = 0; c < CH; c++) {
             const int e = c * 256 + lane * 4;
             if (e < d) {
-                const uint32_t packed = *reinterpret_cast<const uint32_t*>(q + e);
-                const float ds = h2f(sc[e / 32]);
+                const float ds = h2f(sbits[c]);
 #pragma unroll
                 for (int j = 0; j < 4; j++) {
-                    v[c][j] = ds * float(int8_t((packed >> (8 * j)) & 0xff)) * scale;
+                    v[c][j] = ds * float(int8_t((packed[c] >> (8 * j)) & 0xff)) * scale;
                     ss += v[c][j] * v[c][j];
                 }
                 *reinterpret_cast<float4*>(x + (size_t)row * d + e) = make_float4(v[c][0], v[c][1], v[c][2], v[c][3]);
             }
         }
     }
+    float4 wa[CH];
+#pragma unroll
+    for (int c = 0; c < CH; c++) wa[c] = *reinterpret_cast<const float4*>(w + min(c * 256 + lane * 4, d - 4));
     ss = wave_sum(ss);
     const float inv = 1.0f / sqrtf(ss / float(d) + eps);
 #pragma unroll
     for (int c = 0; c < CH; c++) {
         const int e = c * 256 + lane * 4;
         if (e < d) {
+            const float wv[4] = {wa[c].x, wa[c].y, wa[c].z, wa[c].w};
             half4_t o;
 #pragma unroll
-            for (int j = 0; j < 4; j++) o[j] = _Float16(v[c][j] * inv * w[e + j]);
+            for (int j = 0; j < 4; j++) o[j] = _Float16(v[c][j] * inv * wv[j]);
             *reinterpret_cast<half4_t*>(h + (size_t)row * d + e) = o;
         }
     }
@@ -97,14 +112,25 @@ __global__ __launch_bounds__(256) void residual_norm_kernel(float* __restrict__ 
     // stored values with t_eps is the RMSNorm of t.
     float tv[CH][4], xv[CH][4];
     float ss = 0.0f;
+    // Both inputs' chunks are loaded before any is used (a lane past d reads chunk d - 4 and
+    // discards it): the row's loads are in flight together.
+    half4_t ta[CH];
+    float4 xa4[CH], wa[CH], nwa[CH];
+#pragma unroll
+    for (int c = 0; c < CH; c++) {
+        const int ec = min(c * 256 + lane * 4, d - 4);
+        ta[c] = *reinterpret_cast<const half4_t*>(t16 + (size_t)row * d + ec);
+        xa4[c] = *reinterpret_cast<const float4*>(x + (size_t)row * d + ec);
+        wa[c] = *reinterpret_cast<const float4*>(w + ec);
+        if (next_w) nwa[c] = *reinterpret_cast<const float4*>(next_w + ec);
+    }
 #pragma unroll
     for (int c = 0; c < CH; c++) {
         const int e = c * 256 + lane * 4;
         if (e < d) {
-            const half4_t a = *reinterpret_cast<const half4_t*>(t16 + (size_t)row * d + e);
 #pragma unroll
             for (int j = 0; j < 4; j++) {
-                tv[c][j] = float(a[j]);
+                tv[c][j] = float(ta[c][j]);
                 ss += tv[c][j] * tv[c][j];
             }
         }
@@ -116,15 +142,14 @@ __global__ __launch_bounds__(256) void residual_norm_kernel(float* __restrict__ 
     for (int c = 0; c < CH; c++) {
         const int e = c * 256 + lane * 4;
         if (e < d) {
-            float4* xp = reinterpret_cast<float4*>(x + (size_t)row * d + e);
-            const float4 a = *xp;
-            const float xa[4] = {a.x, a.y, a.z, a.w};
+            const float xa[4] = {xa4[c].x, xa4[c].y, xa4[c].z, xa4[c].w};
+            const float wv[4] = {wa[c].x, wa[c].y, wa[c].z, wa[c].w};
 #pragma unroll
             for (int j = 0; j < 4; j++) {
-                xv[c][j] = (xa[j] + tv[c][j] * inv * w[e + j]) * out_scale;
+                xv[c][j] = (xa[j] + tv[c][j] * inv * wv[j]) * out_scale;
                 ss2 += xv[c][j] * xv[c][j];
             }
-            *xp = make_float4(xv[c][0], xv[c][1], xv[c][2], xv[c][3]);
+            *reinterpret_cast<float4*>(x + (size_t)row * d + e) = make_float4(xv[c][0], xv[c][1], xv[c][2], xv[c][3]);
         }
     }
     if (!next_w) return;
@@ -134,9 +159,10 @@ __global__ __launch_bounds__(256) void residual_norm_kernel(float* __restrict__ 
     for (int c = 0; c < CH; c++) {
         const int e = c * 256 + lane * 4;
         if (e < d) {
+            const float nw[4] = {nwa[c].x, nwa[c].y, nwa[c].z, nwa[c].w};
             half4_t o;
 #pragma unroll
-            for (int j = 0; j < 4; j++) o[j] = _Float16(xv[c][j] * inv2 * next_w[e + j]);
+            for (int j = 0; j < 4; j++) o[j] = _Float16(xv[c][j] * inv2 * nw[j]);
             *reinterpret_cast<half4_t*>(h + (size_t)row * d + e) = o;
         }
     }
@@ -170,12 +196,18 @@ __global__ __launch_bounds__(256) void norm_split_kernel(const float* __restrict
     if (row >= T) return;
     float xv[CH][4];
     float ss = 0.0f;
+    float4 xa4[CH], wa[CH];  // all chunks in flight together (a lane past d reads chunk d - 4, unused)
+#pragma unroll
+    for (int c = 0; c < CH; c++) {
+        const int ec = min(c * 256 + lane * 4, d - 4);
+        xa4[c] = *reinterpret_cast<const float4*>(x + (size_t)row * d + ec);
+        wa[c] = *reinterpret_cast<const float4*>(w + ec);
+    }
 #pragma unroll
     for (int c = 0; c < CH; c++) {
         const int e = c * 256 + lane * 4;
         if (e < d) {
-            const float4 a = *reinterpret_cast<const float4*>(x + (size_t)row * d + e);
-            xv[c][0] = a.x, xv[c][1] = a.y, xv[c][2] = a.z, xv[c][3] = a.w;
+            xv[c][0] = xa4[c].x, xv[c][1] = xa4[c].y, xv[c][2] = xa4[c].z, xv[c][3] = xa4[c].w;
 #pragma unroll
             for (int j = 0; j < 4; j++) ss += xv[c][j] * xv[c][j];
         }
@@ -190,7 +222,7 @@ __global__ __launch_bounds__(256) void norm_split_kernel(const float* __restrict
             half4_t hi, lo;
 #pragma unroll
             for (int j = 0; j < 4; j++) {
-                const float y = xv[c][j] * inv * w[e + j];
+                const float y = xv[c][j] * inv * wa[c][j];
                 hi[j] = _Float16(y);
                 lo[j] = _Float16(y - float(hi[j]));
             }
@@ -450,42 +482,63 @@ hipError_t launch_qkv_norm_rope_vt(hipStream_t s, const uint16_t* qkv, int T, in
 // ============================================================================ mean pool
 //
 // pooled[s] = mean over the sequence's rows (reference Shaders/Elementwise.metal:243-256;
-// Model/CPUReference.swift:277-282). Workgroup (64-column chunk, sequence): 4 row slices of 64
-// threads each sum every fourth row, four loads in flight per thread, then the four partial sums
-// combine in a fixed order, so the result does not depend on scheduling.
-__global__ __launch_bounds__(256) void mean_pool_kernel(const float* __restrict__ x, const SeqRange* __restrict__ seqs,
-                                                        int width, float* __restrict__ pooled) {
-    __shared__ float part[4][64];
+// Model/CPUReference.swift:277-282). Workgroup (256-column chunk, sequence) of 16 waves: wave w
+// sums rows w, w + 16, ... in order, each lane 4 columns (16-byte loads, four rows in flight);
+// the 16 partial sums then combine in a fixed tree order, so the result does not depend on
+// scheduling or on the sequence's place in the pack.
+__global__ __launch_bounds__(1024) void mean_pool_kernel(const float* __restrict__ x, const SeqRange* __restrict__ seqs,
+                                                         int width, float* __restrict__ pooled) {
+    __shared__ float4 part[16][64];
     const SeqRange sq = seqs[blockIdx.y];
-    const int c = blockIdx.x * 64 + (threadIdx.x & 63), slice = threadIdx.x >> 6;
-    float acc = 0.0f;
+    const int lane = threadIdx.x & 63, slice = threadIdx.x >> 6;
+    const int c = blockIdx.x * 256 + lane * 4;
+    float4 acc = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
     if (c < width) {
         const float* p = x + (size_t)sq.start * width + c;
         const int n = int(sq.length);
         int r = slice;
-        for (; r + 12 < n; r += 16) {
-            const float a = p[(size_t)r * width], b = p[(size_t)(r + 4) * width];
-            const float e = p[(size_t)(r + 8) * width], f = p[(size_t)(r + 12) * width];
-            acc += a;
-            acc += b;
-            acc += e;
-            acc += f;
+        for (; r + 48 < n; r += 64) {
+            const float4 a = *reinterpret_cast<const float4*>(p + (size_t)r * width);
+            const float4 b = *reinterpret_cast<const float4*>(p + (size_t)(r + 16) * width);
+            const float4 e = *reinterpret_cast<const float4*>(p + (size_t)(r + 32) * width);
+            const float4 f = *reinterpret_cast<const float4*>(p + (size_t)(r + 48) * width);
+            acc.x += a.x, acc.y += a.y, acc.z += a.z, acc.w += a.w;
+            acc.x += b.x, acc.y += b.y, acc.z += b.z, acc.w += b.w;
+            acc.x += e.x, acc.y += e.y, acc.z += e.z, acc.w += e.w;
+            acc.x += f.x, acc.y += f.y, acc.z += f.z, acc.w += f.w;
         }
-        for (; r < n; r += 4) acc += p[(size_t)r * width];
+        for (; r < n; r += 16) {
+            const float4 a = *reinterpret_cast<const float4*>(p + (size_t)r * width);
+            acc.x += a.x, acc.y += a.y, acc.z += a.z, acc.w += a.w;
+        }
     }
-    part[slice][threadIdx.x & 63] = acc;
+    part[slice][lane] = acc;
     __syncthreads();
     if (slice == 0 && c < width) {
-        const int i = threadIdx.x;
-        const float sum = (part[0][i] + part[1][i]) + (part[2][i] + part[3][i]);
-        pooled[(size_t)blockIdx.y * width + c] = sq.length ? sum / float(sq.length) : 0.0f;
+        float4 t[8];
+#pragma unroll
+        for (int i = 0; i < 8; i++) {
+            const float4 u = part[2 * i][lane], v = part[2 * i + 1][lane];
+            t[i] = make_float4(u.x + v.x, u.y + v.y, u.z + v.z, u.w + v.w);
+        }
+#pragma unroll
+        for (int i = 0; i < 4; i++) t[i] = make_float4(t[2 * i].x + t[2 * i + 1].x, t[2 * i].y + t[2 * i + 1].y,
+                                                     t[2 * i].z + t[2 * i + 1].z, t[2 * i].w + t[2 * i + 1].w);
+#pragma unroll
+        for (int i = 0; i < 2; i++) t[i] = make_float4(t[2 * i].x + t[2 * i + 1].x, t[2 * i].y + t[2 * i + 1].y,
+                                                     t[2 * i].z + t[2 * i + 1].z, t[2 * i].w + t[2 * i + 1].w);
+        const float4 sum = make_float4(t[0].x + t[1].x, t[0].y + t[1].y, t[0].z + t[1].z, t[0].w + t[1].w);
+        const float4 m = sq.length ? make_float4(sum.x / float(sq.length), sum.y / float(sq.length), sum.z / float(sq.length),
+                                                 sum.w / float(sq.length))
+                                   : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+        *reinterpret_cast<float4*>(pooled + (size_t)blockIdx.y * width + c) = m;
     }
 }
 
 hipError_t launch_mean_pool(hipStream_t s, const float* x, const SeqRange* seqs, int n_seqs, int width, float* pooled) {
-    if (n_seqs < 0 || width <= 0) return hipErrorInvalidValue;
+    if (n_seqs < 0 || width <= 0 || width % 4) return hipErrorInvalidValue;
     if (n_seqs == 0) return hipSuccess;
-    launch_kernel(mean_pool_kernel, dim3((width + 63) / 64, n_seqs), 256, 0, s, x, seqs, width, pooled);
+    launch_kernel(mean_pool_kernel, dim3((width + 255) / 256, n_seqs), 1024, 0, s, x, seqs, width, pooled);
     return hipGetLastError();
 }
 

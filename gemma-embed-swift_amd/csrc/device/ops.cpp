@@ -139,6 +139,7 @@ int ge_op_mean_pool(ge_ctx* c, const void* x, int32_t rows, int32_t width, const
     return guarded(c, [&] {
         if (!x || !seqs || !pooled || rows < 0 || width <= 0 || n_seqs < 0)
             fail(GE_ERR_INVALID, "mean_pool: x, sequences and output with non-negative sizes");
+        if (width % 4) fail(GE_ERR_INVALID, "mean_pool: width %d is not a multiple of 4", width);
         if (n_seqs == 0) return;
         const std::vector<ge_seq> sq = ge::read_back<ge_seq>(seqs, size_t(n_seqs));
         for (int s = 0; s < n_seqs; s++)

@@ -209,7 +209,8 @@ int ge_op_embed(ge_ctx* ctx, const ge_q8_matrix* table, const void* tokens, int3
                 const void* vectors, int32_t n_vectors, const void* norm_w, float eps, void* x, void* h16);
 /* Kernels.meanPool (Metal/MetalForward.swift:751-758; Shaders/Elementwise.metal:243-256):
  * pooled[s] = mean of rows [start, start + length) of x [rows][width]; seqs: device ge_seq [n_seqs]
- * inside the rows (an empty sequence pools to 0). */
+ * inside the rows (an empty sequence pools to 0). width a multiple of 4; x and pooled 16-byte
+ * aligned. */
 int ge_op_mean_pool(ge_ctx* ctx, const void* x, int32_t rows, int32_t width, const void* seqs, int32_t n_seqs,
                     void* pooled);
 
