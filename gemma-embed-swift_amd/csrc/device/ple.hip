@@ -35,11 +35,19 @@ __global__ __launch_bounds__(256) void ple_rmsnorm_kernel(const float* __restric
     const float sc = mul * rscale[row / per_scale];
     float v[CH][4];
     float ss = 0.0f;
+    // every chunk's loads before any use (a lane past the width reads the last chunk, unused)
+    float4 ia[CH], wa[CH];
+#pragma unroll
+    for (int c = 0; c < CH; c++) {
+        const int ec = min(c * 256 + lane * 4, width - 4);
+        ia[c] = *reinterpret_cast<const float4*>(in + (size_t)row * width + ec);
+        wa[c] = *reinterpret_cast<const float4*>(w + ec);
+    }
 #pragma unroll
     for (int c = 0; c < CH; c++) {
         const int e = c * 256 + lane * 4;
         if (e < width) {
-            const float4 a = *reinterpret_cast<const float4*>(in + (size_t)row * width + e);
+            const float4 a = ia[c];
             v[c][0] = a.x * sc;
             v[c][1] = a.y * sc;
             v[c][2] = a.z * sc;
@@ -54,7 +62,7 @@ __global__ __launch_bounds__(256) void ple_rmsnorm_kernel(const float* __restric
         const int e = c * 256 + lane * 4;
         if (e < width)
             *reinterpret_cast<float4*>(out + (size_t)row * width + e) =
-                make_float4(v[c][0] * inv * w[e], v[c][1] * inv * w[e + 1], v[c][2] * inv * w[e + 2], v[c][3] * inv * w[e + 3]);
+                make_float4(v[c][0] * inv * wa[c].x, v[c][1] * inv * wa[c].y, v[c][2] * inv * wa[c].z, v[c][3] * inv * wa[c].w);
     }
 }
 
@@ -66,11 +74,14 @@ __global__ __launch_bounds__(256) void ple_input_kernel(const float* __restrict_
     if (row >= T) return;
     float v[CH][4];
     float ss = 0.0f;
+    float4 xa[CH];  // every chunk in flight before any use (a lane past d reads the last chunk, unused)
+#pragma unroll
+    for (int c = 0; c < CH; c++) xa[c] = *reinterpret_cast<const float4*>(x + (size_t)row * d + min(c * 256 + lane * 4, d - 4));
 #pragma unroll
     for (int c = 0; c < CH; c++) {
         const int e = c * 256 + lane * 4;
         if (e < d) {
-            const float4 a = *reinterpret_cast<const float4*>(x + (size_t)row * d + e);
+            const float4 a = xa[c];
             v[c][0] = a.x;
             v[c][1] = a.y;
             v[c][2] = a.z;
@@ -104,14 +115,23 @@ __global__ __launch_bounds__(256) void ple_residual_input_kernel(float* __restri
     if (row >= T) return;
     float tv[CH][4], xv[CH][4];
     float ss = 0.0f;
+    // every chunk's loads before any use (a lane past d reads the last chunk, unused)
+    half4_t ta[CH];
+    float4 xa4[CH], wa[CH];
+#pragma unroll
+    for (int c = 0; c < CH; c++) {
+        const int ec = min(c * 256 + lane * 4, d - 4);
+        ta[c] = *reinterpret_cast<const half4_t*>(t16 + (size_t)row * d + ec);
+        xa4[c] = *reinterpret_cast<const float4*>(x + (size_t)row * d + ec);
+        wa[c] = *reinterpret_cast<const float4*>(w + ec);
+    }
 #pragma unroll
     for (int c = 0; c < CH; c++) {
         const int e = c * 256 + lane * 4;
         if (e < d) {
-            const half4_t a = *reinterpret_cast<const half4_t*>(t16 + (size_t)row * d + e);
 #pragma unroll
             for (int j = 0; j < 4; j++) {
-                tv[c][j] = float(a[j]);
+                tv[c][j] = float(ta[c][j]);
                 ss += tv[c][j] * tv[c][j];
             }
         }
@@ -122,15 +142,14 @@ __global__ __launch_bounds__(256) void ple_residual_input_kernel(float* __restri
     for (int c = 0; c < CH; c++) {
         const int e = c * 256 + lane * 4;
         if (e < d) {
-            float4* xp = reinterpret_cast<float4*>(x + (size_t)row * d + e);
-            const float4 a = *xp;
-            const float xa[4] = {a.x, a.y, a.z, a.w};
+            const float xa[4] = {xa4[c].x, xa4[c].y, xa4[c].z, xa4[c].w};
+            const float wv[4] = {wa[c].x, wa[c].y, wa[c].z, wa[c].w};
 #pragma unroll
             for (int j = 0; j < 4; j++) {
-                xv[c][j] = xa[j] + tv[c][j] * inv * w[e + j];
+                xv[c][j] = xa[j] + tv[c][j] * inv * wv[j];
                 ss2 += xv[c][j] * xv[c][j];
             }
-            *xp = make_float4(xv[c][0], xv[c][1], xv[c][2], xv[c][3]);
+            *reinterpret_cast<float4*>(x + (size_t)row * d + e) = make_float4(xv[c][0], xv[c][1], xv[c][2], xv[c][3]);
         }
     }
     const float sc = ple_row_scale(wave_sum(ss2)), is = 1.0f / sc;
@@ -158,12 +177,19 @@ __global__ __launch_bounds__(256) void ple_gate_kernel(const float* __restrict__
     const float* pr = ple + ((size_t)row * layers + layer) * pl;
     float v[CH][4];
     float ss = 0.0f;
+    float4 ga[CH], pa[CH];  // every chunk in flight before any use (a lane past pl reads the last chunk, unused)
+#pragma unroll
+    for (int c = 0; c < CH; c++) {
+        const int ec = min(c * 256 + lane * 4, pl - 4);
+        ga[c] = *reinterpret_cast<const float4*>(graw + (size_t)row * pl + ec);
+        pa[c] = *reinterpret_cast<const float4*>(pr + ec);
+    }
 #pragma unroll
     for (int c = 0; c < CH; c++) {
         const int e = c * 256 + lane * 4;
         if (e < pl) {
-            const float4 a = *reinterpret_cast<const float4*>(graw + (size_t)row * pl + e);
-            const float4 p = *reinterpret_cast<const float4*>(pr + e);
+            const float4 a = ga[c];
+            const float4 p = pa[c];
             v[c][0] = gelu_tanh(a.x * s) * p.x;
             v[c][1] = gelu_tanh(a.y * s) * p.y;
             v[c][2] = gelu_tanh(a.z * s) * p.z;
@@ -199,11 +225,21 @@ __global__ __launch_bounds__(256) void ple_residual_norm_kernel(float* __restric
     const float s2 = rscale2[row];
     float p[CH][4], xv[CH][4];
     float ss = 0.0f;
+    // every chunk's loads before any use (a lane past d reads the last chunk, unused)
+    float4 pa[CH], xa4[CH], wa[CH], nwa[CH];
+#pragma unroll
+    for (int c = 0; c < CH; c++) {
+        const int ec = min(c * 256 + lane * 4, d - 4);
+        pa[c] = *reinterpret_cast<const float4*>(praw + (size_t)row * d + ec);
+        xa4[c] = *reinterpret_cast<const float4*>(x + (size_t)row * d + ec);
+        wa[c] = *reinterpret_cast<const float4*>(w + ec);
+        if (next_w) nwa[c] = *reinterpret_cast<const float4*>(next_w + ec);
+    }
 #pragma unroll
     for (int c = 0; c < CH; c++) {
         const int e = c * 256 + lane * 4;
         if (e < d) {
-            const float4 a = *reinterpret_cast<const float4*>(praw + (size_t)row * d + e);
+            const float4 a = pa[c];
             p[c][0] = a.x * s2;
             p[c][1] = a.y * s2;
             p[c][2] = a.z * s2;
@@ -218,15 +254,14 @@ __global__ __launch_bounds__(256) void ple_residual_norm_kernel(float* __restric
     for (int c = 0; c < CH; c++) {
         const int e = c * 256 + lane * 4;
         if (e < d) {
-            float4* xp = reinterpret_cast<float4*>(x + (size_t)row * d + e);
-            const float4 a = *xp;
-            const float xa[4] = {a.x, a.y, a.z, a.w};
+            const float xa[4] = {xa4[c].x, xa4[c].y, xa4[c].z, xa4[c].w};
+            const float wv[4] = {wa[c].x, wa[c].y, wa[c].z, wa[c].w};
 #pragma unroll
             for (int j = 0; j < 4; j++) {
-                xv[c][j] = (xa[j] + p[c][j] * inv * w[e + j]) * out_scale;
+                xv[c][j] = (xa[j] + p[c][j] * inv * wv[j]) * out_scale;
                 ss2 += xv[c][j] * xv[c][j];
             }
-            *xp = make_float4(xv[c][0], xv[c][1], xv[c][2], xv[c][3]);
+            *reinterpret_cast<float4*>(x + (size_t)row * d + e) = make_float4(xv[c][0], xv[c][1], xv[c][2], xv[c][3]);
         }
     }
     if (!next_w) return;
@@ -237,7 +272,7 @@ __global__ __launch_bounds__(256) void ple_residual_norm_kernel(float* __restric
         if (e < d) {
             half4_t o;
 #pragma unroll
-            for (int j = 0; j < 4; j++) o[j] = _Float16(xv[c][j] * inv2 * next_w[e + j]);
+            for (int j = 0; j < 4; j++) o[j] = _Float16(xv[c][j] * inv2 * nwa[c][j]);
             *reinterpret_cast<half4_t*>(h + (size_t)row * d + e) = o;
         }
     }
