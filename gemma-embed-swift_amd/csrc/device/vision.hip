@@ -38,17 +38,24 @@ __device__ __forceinline__ void vit_ln_stats(const float (&v)[CH][4], int d, int
     rstd = 1.0f / sqrtf(wave_sum(ss) / float(d) + eps);
 }
 
-// h = fp16((v - mean) * rstd * w + b) for the row's elements.
+// The lane's chunks of a row vector (a lane past d reads the last chunk, unused): loaded before
+// anything needs them, so a row's loads are in flight together rather than one after another.
+template <int CH>
+__device__ __forceinline__ void vit_load_chunks(const float* __restrict__ p, int d, int lane, float4 (&out)[CH]) {
+#pragma unroll
+    for (int c = 0; c < CH; c++) out[c] = *reinterpret_cast<const float4*>(p + min(c * 256 + lane * 4, d - 4));
+}
+
+// h = fp16((v - mean) * rstd * w + b) for the row's elements (w and b: the lane's chunks).
 template <int CH>
 __device__ __forceinline__ void vit_ln_store(const float (&v)[CH][4], int d, int lane, float mean, float rstd,
-                                             const float* __restrict__ w, const float* __restrict__ b,
+                                             const float4 (&w)[CH], const float4 (&b)[CH],
                                              uint16_t* __restrict__ hrow) {
 #pragma unroll
     for (int c = 0; c < CH; c++) {
         const int e = c * 256 + lane * 4;
         if (e < d) {
-            const float4 wv = *reinterpret_cast<const float4*>(w + e);
-            const float4 bv = *reinterpret_cast<const float4*>(b + e);
+            const float4 wv = w[c], bv = b[c];
             const float wa[4] = {wv.x, wv.y, wv.z, wv.w}, ba[4] = {bv.x, bv.y, bv.z, bv.w};
             half4_t o;
 #pragma unroll
@@ -73,14 +80,18 @@ __global__ __launch_bounds__(256) void vit_embed_kernel(const float* __restrict_
     const float* pxr = pos + (size_t)px[row] * d;
     const float* pyr = pos + (size_t)(npos + py[row]) * d;
     float v[CH][4];
+    float4 ta[CH], ba[CH], xa[CH], ya[CH], wa[CH], lb[CH];
+    vit_load_chunks<CH>(t + (size_t)row * d, d, lane, ta);
+    vit_load_chunks<CH>(bias, d, lane, ba);
+    vit_load_chunks<CH>(pxr, d, lane, xa);
+    vit_load_chunks<CH>(pyr, d, lane, ya);
+    vit_load_chunks<CH>(w, d, lane, wa);
+    vit_load_chunks<CH>(b, d, lane, lb);
 #pragma unroll
     for (int c = 0; c < CH; c++) {
         const int e = c * 256 + lane * 4;
         if (e < d) {
-            const float4 tv = *reinterpret_cast<const float4*>(t + (size_t)row * d + e);
-            const float4 bv = *reinterpret_cast<const float4*>(bias + e);
-            const float4 xv = *reinterpret_cast<const float4*>(pxr + e);
-            const float4 yv = *reinterpret_cast<const float4*>(pyr + e);
+            const float4 tv = ta[c], bv = ba[c], xv = xa[c], yv = ya[c];
             v[c][0] = ((tv.x + bv.x) + xv.x) + yv.x;
             v[c][1] = ((tv.y + bv.y) + xv.y) + yv.y;
             v[c][2] = ((tv.z + bv.z) + xv.z) + yv.z;
@@ -90,7 +101,7 @@ __global__ __launch_bounds__(256) void vit_embed_kernel(const float* __restrict_
     }
     float mean, rstd;
     vit_ln_stats<CH>(v, d, lane, eps, mean, rstd);
-    vit_ln_store<CH>(v, d, lane, mean, rstd, w, b, h + (size_t)row * d);
+    vit_ln_store<CH>(v, d, lane, mean, rstd, wa, lb, h + (size_t)row * d);
 }
 
 // x = x + (t + bias); with w: h = LayerNorm(x) * w + b (fp16), the next block's pre-norm.
@@ -102,14 +113,20 @@ __global__ __launch_bounds__(256) void vit_residual_ln_kernel(float* __restrict_
     const int row = blockIdx.x * 4 + (threadIdx.x >> 6), lane = threadIdx.x & 63;
     if (row >= T) return;
     float v[CH][4];
+    float4 xa[CH], ta[CH], ba[CH], wa[CH], lb[CH];
+    vit_load_chunks<CH>(x + (size_t)row * d, d, lane, xa);
+    vit_load_chunks<CH>(t + (size_t)row * d, d, lane, ta);
+    vit_load_chunks<CH>(bias, d, lane, ba);
+    if (w) {
+        vit_load_chunks<CH>(w, d, lane, wa);
+        vit_load_chunks<CH>(b, d, lane, lb);
+    }
 #pragma unroll
     for (int c = 0; c < CH; c++) {
         const int e = c * 256 + lane * 4;
         if (e < d) {
             float4* xp = reinterpret_cast<float4*>(x + (size_t)row * d + e);
-            const float4 xv = *xp;
-            const float4 tv = *reinterpret_cast<const float4*>(t + (size_t)row * d + e);
-            const float4 bv = *reinterpret_cast<const float4*>(bias + e);
+            const float4 xv = xa[c], tv = ta[c], bv = ba[c];
             v[c][0] = xv.x + (tv.x + bv.x);
             v[c][1] = xv.y + (tv.y + bv.y);
             v[c][2] = xv.z + (tv.z + bv.z);
@@ -120,7 +137,7 @@ __global__ __launch_bounds__(256) void vit_residual_ln_kernel(float* __restrict_
     if (!w) return;
     float mean, rstd;
     vit_ln_stats<CH>(v, d, lane, eps, mean, rstd);
-    vit_ln_store<CH>(v, d, lane, mean, rstd, w, b, h + (size_t)row * d);
+    vit_ln_store<CH>(v, d, lane, mean, rstd, wa, lb, h + (size_t)row * d);
 }
 
 // One wave per output token: the merge x merge patches of its window (row0 + dy * gx + dx), each
@@ -140,15 +157,21 @@ __global__ __launch_bounds__(256) void vit_pool_kernel(const float* __restrict__
     for (int c = 0; c < CH; c++)
 #pragma unroll
         for (int j = 0; j < 4; j++) acc[c][j] = 0.0f;
+    float4 pwa[CH], pba[CH], nwa[CH];
+    vit_load_chunks<CH>(pw, d, lane, pwa);
+    vit_load_chunks<CH>(pb, d, lane, pba);
+    vit_load_chunks<CH>(nw, d, lane, nwa);
     for (int dy = 0; dy < merge; dy++)
         for (int dx = 0; dx < merge; dx++) {
             const float* xr = x + (size_t)(r0 + dy * stride + dx) * d;
             float v[CH][4];
+            float4 xa[CH];
+            vit_load_chunks<CH>(xr, d, lane, xa);
 #pragma unroll
             for (int c = 0; c < CH; c++) {
                 const int e = c * 256 + lane * 4;
                 if (e < d) {
-                    const float4 xv = *reinterpret_cast<const float4*>(xr + e);
+                    const float4 xv = xa[c];
                     v[c][0] = xv.x;
                     v[c][1] = xv.y;
                     v[c][2] = xv.z;
@@ -161,8 +184,7 @@ __global__ __launch_bounds__(256) void vit_pool_kernel(const float* __restrict__
             for (int c = 0; c < CH; c++) {
                 const int e = c * 256 + lane * 4;
                 if (e < d) {
-                    const float4 wv = *reinterpret_cast<const float4*>(pw + e);
-                    const float4 bv = *reinterpret_cast<const float4*>(pb + e);
+                    const float4 wv = pwa[c], bv = pba[c];
                     const float wa[4] = {wv.x, wv.y, wv.z, wv.w}, ba[4] = {bv.x, bv.y, bv.z, bv.w};
 #pragma unroll
                     for (int j = 0; j < 4; j++) acc[c][j] += (v[c][j] - mean) * rstd * wa[j] + ba[j];
@@ -188,7 +210,7 @@ __global__ __launch_bounds__(256) void vit_pool_kernel(const float* __restrict__
     for (int c = 0; c < CH; c++) {
         const int e = c * 256 + lane * 4;
         if (e < d) {
-            const float4 wv = *reinterpret_cast<const float4*>(nw + e);
+            const float4 wv = nwa[c];
             const float wa[4] = {wv.x, wv.y, wv.z, wv.w};
             half4_t o;
 #pragma unroll
