@@ -190,9 +190,10 @@ def at(ptr, nbytes):
 # ---------------------------------------------------------------- kernels
 
 def row_kernel(a, kernel, T, spans):
-    """The one-wave-per-row kernels (embed_norm_kernel elementwise.hip:15, residual_norm_kernel :90,
-    norm_split_kernel :167, the ple_*_kernel family ple.hip:30-192): row < T, element
-    e = c * 256 + 4 lane + j < width. spans: (pointer, bytes per row of the access)."""
+    """The one-wave-per-row kernels (embed_norm_kernel elementwise.hip:15, residual_norm_kernel :105,
+    norm_split_kernel :193, the ple_*_kernel family ple.hip:30-218): row < T; loads of chunk
+    min(e, width - 4) and stores of element e = c * 256 + 4 lane + j < width. spans: (pointer, bytes
+    per row of the access)."""
     for ptr, row_bytes in spans:
         if ptr is not None:
             a.span(kernel, ptr, 0, T * row_bytes)
@@ -211,7 +212,7 @@ def norm_split(a, T, D, x, h3):
 
 
 def qk_norm_rope(a, T, H, KV, HD, qkv, positions, q, k, v, q_lo=None, k_lo=None, pos=None, table_rows=8192):
-    """qk_norm_rope_kernel (elementwise.hip:224): item = (t, slot) < T (H + 2 KV); reads
+    """qk_norm_rope_kernel (elementwise.hip:256): item = (t, slot) < T (H + 2 KV); reads
     qkv[t][slot][0, HD), the RoPE row positions[t]; writes q / k / v (and the low halves)."""
     S = H + 2 * KV
     a.span("qk_norm_rope", qkv, 0, T * S * HD * F32)
@@ -233,7 +234,7 @@ def vt_rows(a, kernel, vt, rows, vt_cols, vcol_used):
 
 
 def qkv_norm_rope_vt(a, T, H, KV, HD, qkv16, positions, q, k, v, vcol, vt_cols, vt, vc):
-    """qkv_norm_rope_vt_kernel (elementwise.hip:314): token t = 64 blockIdx + 4 wave + i < T; V^T rows
+    """qkv_norm_rope_vt_kernel (elementwise.hip:346): token t = 64 blockIdx + 4 wave + i < T; V^T rows
     r < KV HD at column vcol[t] for t < T."""
     S = H + 2 * KV
     a.span("qkv_norm_rope_vt", qkv16, 0, T * S * HD * F16)
@@ -334,7 +335,8 @@ def attention_legacy(a, work, H, KV, HD, hw, q, k, v, o, rows_alloc_k):
 
 
 def mean_pool(a, seqs, width, x, seq_ptr, pooled):
-    """mean_pool_kernel (elementwise.hip:456): rows start .. start + len - 1 of each sequence."""
+    """mean_pool_kernel (elementwise.hip:489): rows start .. start + len - 1 of each sequence, 16-byte
+    loads of columns c .. c + 3 < width."""
     a.span("mean_pool", seq_ptr, 0, len(seqs) * SEQ_BYTES)
     a.span("mean_pool", pooled, 0, len(seqs) * width * F32)
     for st, n in seqs:
@@ -443,7 +445,7 @@ def replay(m, b, positions=None):
                                                         (rs, F32)])
                 ple_t = rows("ple_t", r0, m["pl"], F32)
                 gemm(a, "gemm_ple_gate", T, m["pl"], D, x16, ple_t, "f32")
-                # ple_gate_kernel (ple.hip:152) reads ple[(row L + layer) pl .. + pl) of its part's rows
+                # ple_gate_kernel (ple.hip:171) reads ple[(row L + layer) pl .. + pl) of its part's rows
                 row_kernel(a, "ple_gate", T, [(ple_t, m["pl"] * F32), (rs, F32), (rows("g16", r0, m["pl"], F16), m["pl"] * F16),
                                               (rows("rs2", r0, 1, F32), F32)])
                 if T:
