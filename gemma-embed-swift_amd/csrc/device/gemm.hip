@@ -283,20 +283,27 @@ __global__ __launch_bounds__(C::NT) void gemm_kernel(const uint16_t* __restrict_
 // order of the k-steps are those of the tiled kernel, so every output has the same bits there
 // and here, whichever the batch size selects. TR: the transposed accumulation of the QKV kernel,
 // stored as its fp16 staging (acc * out_scale, row-major [M][N]) for the separate row pass.
-// SK: k-steps in flight per wave (a short batch's GEMM is bound by the latency of its weight reads:
-// few waves, each streaming 32 or 64 weight rows): the largest of 24, 16, 8 (12, 8, 4 for the
-// GeGLU pairs) that divides K / 16. It sets only how far the loads run ahead, not the order of
-// the MFMAs, so it does not change a bit of the result.
+// SK: k-steps in flight per wave (a short batch's GEMM is bound by how fast its few waves stream
+// the weights): the largest of 24, 16, 8 (16, 12, 4 for the GeGLU pairs) that divides K / 16. It
+// sets only how far the loads run ahead, not the order of the MFMAs, so it does not change a bit
+// of the result. One wave per workgroup, so that the waves land on as many CUs (and their L1
+// and L2 request paths) as there are waves: with four per workgroup, a real-architecture
+// 1 x 64-token forward took 2.48 ms, with one 1.89 ms, and 1.47 ms once the loads also ran as
+// one continuous pipeline (every slot refilled right after its MFMA, no branch around a load).
+constexpr int kSkinnyWaves = 1;
 template <int EPI, bool TR, int NJ, int SK>
-__global__ __launch_bounds__(256) void gemm_skinny_kernel(const uint16_t* __restrict__ X,
+__global__ __launch_bounds__(64 * kSkinnyWaves) void gemm_skinny_kernel(const uint16_t* __restrict__ X,
                                                           const uint16_t* __restrict__ Fh, void* __restrict__ Y,
                                                           int M, int N, int K, float out_scale, GemmEpiArgs ea) {
     const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(int(threadIdx.x >> 6));
     const int groups = N / (32 * NJ), items = (M + 31) / 32 * groups;
-    const int item = blockIdx.x * 4 + wave;
+    const int item = blockIdx.x * kSkinnyWaves + wave;
     if (item >= items) return;
     const int rt = item / groups, cg = item % groups;
     const int KT = K / 16;
+    // The launcher picks SK dividing K / 16 > 0; known here, the first chunk's loads stay in
+    // the entry block, in slot order, instead of sinking below a loop guard.
+    __builtin_assume(KT >= SK);
     asm volatile("" ::"s"(Y), "s"(out_scale));
     const __amdgpu_buffer_rsrc_t xr = buffer_rsrc(X, uint32_t(M) * uint32_t(K) * 2u);
     const __amdgpu_buffer_rsrc_t fr = buffer_rsrc(Fh, uint32_t(N) * uint32_t(K) * 2u);
@@ -307,31 +314,40 @@ __global__ __launch_bounds__(256) void gemm_skinny_kernel(const uint16_t* __rest
 #pragma unroll
     for (int j = 0; j < NJ; j++) boff[j] = uint32_t(((cg * NJ + j) * KT * 512 + lane * 8) * 2);
     half8_t a[SK], b[SK][NJ];
+    // k-step t (wave-uniform) through the scalar offset: no per-load address arithmetic
 #define SK_LOAD(u, t)                                                                                   \
     do {                                                                                                \
-        a[u] = __builtin_bit_cast(half8_t, __builtin_amdgcn_raw_buffer_load_b128(xr, aoff + (t) * 32, 0, 0)); \
+        a[u] = __builtin_bit_cast(half8_t, __builtin_amdgcn_raw_buffer_load_b128(xr, aoff, (t) * 32, 0)); \
         _Pragma("unroll") for (int j = 0; j < NJ; j++) b[u][j] =                                        \
-            __builtin_bit_cast(half8_t, __builtin_amdgcn_raw_buffer_load_b128(fr, boff[j] + (t) * 1024, 0, 0)); \
+            __builtin_bit_cast(half8_t, __builtin_amdgcn_raw_buffer_load_b128(fr, boff[j], (t) * 1024, 0)); \
     } while (0)
     float16_t acc[1][NJ];
 #pragma unroll
     for (int j = 0; j < NJ; j++)
 #pragma unroll
         for (int r = 0; r < 16; r++) acc[0][j][r] = 0.0f;
+    // Loads issue in slot order, in the prologue and in the loop (the scheduling barriers), so
+    // slot u is always the oldest load in flight when its MFMA comes: the wait before it can
+    // leave the other slots' loads in flight.
 #pragma unroll
-    for (int u = 0; u < SK; u++) SK_LOAD(u, u);
+    for (int u = 0; u < SK; u++) {
+        SK_LOAD(u, u);
+        __builtin_amdgcn_sched_barrier(0);
+    }
+#pragma unroll 1
     for (int t0 = 0; t0 < KT; t0 += SK) {
 #pragma unroll
         for (int u = 0; u < SK; u++) {
-            const half8_t av = a[u];
-            half8_t bv[NJ];
-#pragma unroll
-            for (int j = 0; j < NJ; j++) bv[j] = b[u][j];
-            if (t0 + SK < KT) SK_LOAD(u, t0 + SK + u);
 #pragma unroll
             for (int j = 0; j < NJ; j++)
-                acc[0][j] = TR ? __builtin_amdgcn_mfma_f32_32x32x16_f16(bv[j], av, acc[0][j], 0, 0, 0)
-                               : __builtin_amdgcn_mfma_f32_32x32x16_f16(av, bv[j], acc[0][j], 0, 0, 0);
+                acc[0][j] = TR ? __builtin_amdgcn_mfma_f32_32x32x16_f16(b[u][j], a[u], acc[0][j], 0, 0, 0)
+                               : __builtin_amdgcn_mfma_f32_32x32x16_f16(a[u], b[u][j], acc[0][j], 0, 0, 0);
+            // The refill of slot u after its MFMAs (the old values dead, so the new ones take the
+            // same registers) and unconditional, the last chunk re-reading k-step KT - 1 (never
+            // used): a load under a branch, or into a register still holding the previous value,
+            // makes the compiler wait for every load in flight.
+            SK_LOAD(u, min(t0 + SK + u, KT - 1));
+            __builtin_amdgcn_sched_barrier(0);
         }
     }
 #undef SK_LOAD
@@ -662,9 +678,9 @@ template <int EPI, bool TR, int NJ>
 hipError_t gemm_skinny_launch(hipStream_t s, const Q8Dev& w, const uint16_t* x, int M, void* y, float out_scale,
                               const GemmEpiArgs& ea = GemmEpiArgs{}) {
     const int items = (M + 31) / 32 * (w.rows / (32 * NJ));
-    const dim3 grid((items + 3) / 4), block(256);
+    const dim3 grid((items + kSkinnyWaves - 1) / kSkinnyWaves), block(64 * kSkinnyWaves);
     const int KT = w.cols / 16;
-    constexpr int S0 = NJ == 1 ? 24 : 12, S1 = NJ == 1 ? 16 : 8, S2 = NJ == 1 ? 8 : 4;
+    constexpr int S0 = NJ == 1 ? 24 : 16, S1 = NJ == 1 ? 16 : 12, S2 = NJ == 1 ? 8 : 4;
     if (KT % S0 == 0)
         launch_kernel(gemm_skinny_kernel<EPI, TR, NJ, S0>, grid, block, 0, s, x, w.fh, y, M, w.rows, w.cols, out_scale, ea);
     else if (KT % S1 == 0)

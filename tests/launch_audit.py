@@ -257,9 +257,9 @@ EPI_BYTES = {"f32": lambda N: N * F32, "f16": lambda N: N * F16, "geglu": lambda
 
 
 def gemm(a, kernel, M, N, K, x, y, epi):
-    """launch_gemm_q8 (gemm.hip:682): gemm_kernel (:259) or gemm_skinny_kernel (:291). The activation
+    """launch_gemm_q8 (gemm.hip:698): gemm_kernel (:259) or gemm_skinny_kernel (:295). The activation
     resource covers X[M][K] (buffer_rsrc(X, M K 2)); stores are guarded by row < M, col < N
-    (gemm_store_tile, :80), the GeGLU pairs writing column gcol / 2 of N / 2."""
+    (gemm_store_tile, :81), the GeGLU pairs writing column gcol / 2 of N / 2."""
     if M == 0:
         return
     a.rsrc(kernel, x, 0, M * K * F16)
@@ -267,8 +267,8 @@ def gemm(a, kernel, M, N, K, x, y, epi):
 
 
 def gemm_qkv(a, M, N, K, hd, H, KV, x, e, pos, vc):
-    """launch_gemm_qkv (gemm.hip:718): short batches take the skinny GEMM into the fp16 staging
-    [M][N] and qkv_rowpass_kernel (:537), else gemm_qkv_kernel (:425); both read positions[t] and
+    """launch_gemm_qkv (gemm.hip:734): short batches take the skinny GEMM into the fp16 staging
+    [M][N] and qkv_rowpass_kernel (:553), else gemm_qkv_kernel (:441); both read positions[t] and
     vcol[t] for t < M, store q / k / v rows t < M and V^T rows (slot - H - KV) HD + d at vcol[t]."""
     if M == 0:
         return
