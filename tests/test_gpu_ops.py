@@ -112,6 +112,61 @@ def test_gemm_short_batches_match_tiled_rows(ctx, c2, name, y_f16):
         assert np.array_equal(full[lo:lo + n], part), (lo, n)
 
 
+def q8_raw(rows, cols, rng):
+    """Q8_0 rows as the GGUF stores them: per 32 values an fp16 scale, then 32 int8."""
+    nb = rows * cols // 32
+    blocks = np.zeros((nb, 34), np.uint8)
+    d = (np.abs(rng.standard_normal(nb)) * 0.02 / 127 + 1e-4).astype(np.float16)
+    blocks[:, :2] = d.view(np.uint8).reshape(nb, 2)
+    blocks[:, 2:] = rng.integers(-127, 128, size=(nb, 32), dtype=np.int8).view(np.uint8)
+    return blocks.reshape(-1)
+
+
+def q8_dequant(raw, rows, cols):
+    b = raw.reshape(-1, 34)
+    d = b[:, :2].copy().view(np.float16).astype(np.float32)
+    q = b[:, 2:].view(np.int8).astype(np.float32)
+    return (q * d).reshape(rows, cols)
+
+
+@pytest.mark.parametrize("cols", [640, 1024, 1152])
+def test_gemm_short_batch_every_pipeline_depth(ctx, cols):
+    """K / 16 = 40, 64 and 72 reach each depth of the skinny kernel's load pipeline (8, 16 and 24
+    k-steps in flight for the plain GEMM; 4, 16 and 12 for the GeGLU pairs). Short batches match
+    the same rows of a 300-row batch on the tiled kernel bit for bit, and the oracle within the
+    fp16 rounding of the dequantised weights."""
+    rng = np.random.default_rng(cols)
+    rows = 256
+    raw = q8_raw(rows, cols, rng)
+    x16 = f16_round(rng.standard_normal((300, cols)))
+    full = run_gemm(ctx, raw, rows, cols, x16)
+    want = ora.matmul(x16[:64].astype(np.float32), q8_dequant(raw, rows, cols))
+    assert max_rel(full[:64], want) < 3e-3
+    for lo, n in ((0, 1), (40, 64), (250, 33)):
+        assert np.array_equal(full[lo:lo + n], run_gemm(ctx, raw, rows, cols, x16[lo:lo + n].copy())), (lo, n)
+    g = ctx.q8_create(q8_raw(rows, cols, rng), rows, cols)
+    u = ctx.q8_create(q8_raw(rows, cols, rng), rows, cols)
+
+    def geglu(x):
+        dx, da = ctx.alloc(x.nbytes), ctx.alloc(x.shape[0] * rows * 2)
+        try:
+            ctx.upload(dx, x)
+            ctx.gemm_q8_geglu(g, u, dx, x.shape[0], da)
+            return ctx.download(da, (x.shape[0], rows), np.float16)
+        finally:
+            ctx.free(dx)
+            ctx.free(da)
+    try:
+        xs = f16_round(rng.standard_normal((300, cols)) * 0.05)
+        gfull = geglu(xs)
+        assert np.all(np.isfinite(gfull.astype(np.float32)))
+        for lo, n in ((0, 3), (40, 64), (250, 50)):
+            assert np.array_equal(gfull[lo:lo + n], geglu(xs[lo:lo + n].copy())), (lo, n)
+    finally:
+        ctx.q8_destroy(g)
+        ctx.q8_destroy(u)
+
+
 def test_gemm_geglu_short_batch_matches_tiled_rows(ctx, c2):
     M = 300
     x16 = f16_round(RNG.standard_normal((M, 768)) * 0.05)
