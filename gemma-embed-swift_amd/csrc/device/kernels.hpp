@@ -61,8 +61,11 @@ struct GemmEpiArgs {
 // interleaved in 32-row gate/up groups and writes fp16 act[M][N / 2] = gelu_tanh(gate) * up *
 // out_scale. out_scale is a power of two wherever the forward uses it, so it is exact.
 // Batches of at most kSkinnyMaxRows rows (and K a multiple of 128) run on the skinny kernel,
-// one wave per 32-row block; the results are bitwise those of the tiled kernel.
-constexpr int kSkinnyMaxRows = 64;
+// one wave per 32-row by 32-column block; the results are bitwise those of the tiled kernel.
+// Up to 512 rows the skinny kernel is the faster of the two at every projection of the
+// config-2 and real-architecture models (at 128 rows 4-6 against 8-18 us; 512 rows is about
+// the crossover), since the tiled kernel's few workgroups sit on a few CUs.
+constexpr int kSkinnyMaxRows = 512;
 // kEpiGeluBias and kEpiHeads take their operands from ea (y is then unused by kEpiHeads).
 hipError_t launch_gemm_q8(hipStream_t s, const Q8Dev& w, const uint16_t* x, int M, void* y, GemmEpilogue epi,
                           float out_scale = 1.0f, const GemmEpiArgs* ea = nullptr);

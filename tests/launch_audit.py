@@ -23,7 +23,7 @@ ATTN_QUERIES_V2 = 64     # kAttnQueriesV2, kernels.hpp:139
 SMALL_ITEMS = 256        # kAttnSmallItems, runtime.cpp
 SPLIT_MIN_TOKENS = 4096  # kSplitMinTokens, runtime_internal.hpp
 MAX_PARTS = 4            # kMaxParts, runtime_internal.hpp
-SKINNY_MAX_ROWS = 64     # kSkinnyMaxRows, kernels.hpp
+SKINNY_MAX_ROWS = 512    # kSkinnyMaxRows, kernels.hpp
 WORK_BYTES, SEQ_BYTES = 16, 8  # sizeof(AttnWork), sizeof(SeqRange)
 
 

@@ -118,12 +118,14 @@ def test_config2_per_layer_vs_oracle(c2_model, c2_oracle, config2_batch):
     print(f"worst l_out max_rel {worst:.3e}", flush=True)
 
 
-@pytest.mark.parametrize("lengths", [(100, 37, 64), (20, 25, 10)], ids=["tiled", "short"])
+@pytest.mark.parametrize("lengths", [(400, 37, 100), (100, 37, 64), (20, 25, 10)], ids=["tiled", "mid", "short"])
 def test_every_trace_tensor_vs_oracle(c2_model, c2_oracle, config2_batch, lengths):
     """Every named intermediate the C-ABI traces (llama.cpp names), at a sliding (0) and a global (5)
     layer, against the oracle on the middle text of a pack: the embedding, the norms, the raw and
     the normed/rotated projections, attention, the GeGLU product, the FFN output, the layer output
-    and the final norm and projection. A pack of at most 64 tokens runs the short-batch kernels."""
+    and the final norm and projection. A pack of at most 512 tokens runs its GEMMs on the skinny
+    kernel (the mid pack: 201 rows, a partial last row block), one of at most 64 also replays as a
+    graph (short)."""
     batch = [config2_batch[2 + 4 * i][:n] for i, n in enumerate(lengths)]
     idx, lo = 1, lengths[0]
     per_layer = ["attn_norm", "Qcur", "Kcur", "Vcur", "Qcur_pos", "Kcur_pos", "Vcur_normed", "kqv_out",
@@ -262,21 +264,22 @@ def test_packing_invariance_and_determinism(c2_model, config2_batch):
 
 
 def test_short_texts_alone_match_larger_packs(c2_model, config2_batch):
-    """A short pack (at most 64 tokens) runs its GEMMs on the skinny kernel and the QKV epilogue as
-    a separate row pass; inside a larger pack the same text runs on the tiled kernels. The vector
-    must have the same bits either way (MetalForwardTests.swift:95-120: counts around the tile
-    boundaries, alone and between a 19- and a 97-token text)."""
+    """A pack of at most 512 tokens runs its GEMMs on the skinny kernel and the QKV epilogue as a
+    separate row pass (and, up to 64 tokens, replays as a graph); inside a pack of more than 512
+    tokens the same text runs on the tiled kernels. The vector must have the same bits either
+    way (MetalForwardTests.swift:95-120: counts around the tile boundaries, alone and between a
+    19- and a 500-token text)."""
     body = config2_batch[7]
     ctx = c2_model.context
-    for count in (1, 2, 13, 15, 16, 17, 31, 32, 33, 63, 64, 65):
+    for count in (1, 2, 13, 15, 16, 17, 31, 32, 33, 63, 64, 65, 127, 128, 129, 255, 256, 257, 480, 511, 512):
         subject = body[:count]
-        packed, _ = ctx.forward([config2_batch[3][:19], subject, config2_batch[4][:97]])
+        packed, _ = ctx.forward([config2_batch[3][:19], subject, config2_batch[4][:500]])
         alone, _ = ctx.forward([subject])
         assert np.array_equal(alone[0], packed[1]), count
-    for lengths in ([5, 8], [8, 8], [8, 9], [30, 34]):
+    for lengths in ([5, 8], [8, 8], [8, 9], [30, 34], [100, 200, 150]):
         small = [config2_batch[9 + i][:n] for i, n in enumerate(lengths)]
         got, _ = ctx.forward(small)
-        want, _ = ctx.forward(small + [config2_batch[20][:97]])
+        want, _ = ctx.forward(small + [config2_batch[20][:500]])
         for i in range(len(lengths)):
             assert np.array_equal(got[i], want[i]), (lengths, i)
 

@@ -55,10 +55,12 @@ def run_gemm(ctx, raw_q8, rows, cols, x16, y_f16=False):
     return y.astype(np.float32)
 
 
-GEMM_SHAPES = [  # (tensor, M): every config-2 projection plus ragged row counts
+GEMM_SHAPES = [  # (tensor, M): every config-2 projection plus ragged row counts, on the skinny
+    # kernel (M <= 512) and on the tiled one
     ("blk.0.attn_q.weight", 200), ("blk.0.attn_k.weight", 129), ("blk.0.attn_v.weight", 1),
     ("blk.0.attn_output.weight", 300), ("blk.0.ffn_gate.weight", 128), ("blk.0.ffn_up.weight", 513),
-    ("blk.0.ffn_down.weight", 257), ("output.weight", 64),
+    ("blk.0.ffn_down.weight", 257), ("output.weight", 64), ("blk.0.attn_q.weight", 700),
+    ("blk.0.attn_output.weight", 600), ("blk.0.ffn_down.weight", 1100),
 ]
 
 
@@ -86,7 +88,7 @@ def test_gemm_config1(ctx, c2):
 
 def test_gemm_f16_output_and_row_independence(ctx, c2):
     name = "blk.3.attn_output.weight"
-    x16 = f16_round(RNG.standard_normal((300, 768)))
+    x16 = f16_round(RNG.standard_normal((600, 768)))
     raw = np.asarray(c2.raw(name))
     y = run_gemm(ctx, raw, 768, 768, x16, y_f16=True)
     want = ora.matmul(x16.astype(np.float32), c2.tensor(name).astype(np.float32))
@@ -100,14 +102,14 @@ def test_gemm_f16_output_and_row_independence(ctx, c2):
 @pytest.mark.parametrize("name,y_f16", [("blk.1.attn_q.weight", False), ("blk.1.ffn_down.weight", True),
                                          ("output.weight", False)])
 def test_gemm_short_batches_match_tiled_rows(ctx, c2, name, y_f16):
-    """Up to 64 rows run on the skinny kernel; the same rows inside a 300-row batch run on the
+    """Up to 512 rows run on the skinny kernel; the same rows inside a 600-row batch run on the
     tiled kernel. Same MFMA, operand order and k order: the same bits."""
     shape, _, _ = c2.tensors[name]
     cols, rows = shape
     raw = np.asarray(c2.raw(name))
-    x16 = f16_round(RNG.standard_normal((300, cols)))
+    x16 = f16_round(RNG.standard_normal((600, cols)))
     full = run_gemm(ctx, raw, rows, cols, x16, y_f16)
-    for lo, n in ((0, 1), (5, 7), (100, 32), (200, 33), (236, 64)):
+    for lo, n in ((0, 1), (5, 7), (100, 32), (200, 33), (236, 64), (88, 300), (50, 512)):
         part = run_gemm(ctx, raw, rows, cols, x16[lo:lo + n].copy(), y_f16)
         assert np.array_equal(full[lo:lo + n], part), (lo, n)
 
@@ -132,17 +134,17 @@ def q8_dequant(raw, rows, cols):
 @pytest.mark.parametrize("cols", [640, 1024, 1152])
 def test_gemm_short_batch_every_pipeline_depth(ctx, cols):
     """K / 16 = 40, 64 and 72 reach each depth of the skinny kernel's load pipeline (8, 16 and 24
-    k-steps in flight for the plain GEMM; 4, 16 and 12 for the GeGLU pairs). Short batches match
-    the same rows of a 300-row batch on the tiled kernel bit for bit, and the oracle within the
-    fp16 rounding of the dequantised weights."""
+    k-steps in flight for the plain GEMM; 4, 16 and 12 for the GeGLU pairs). Batches of up to 512
+    rows match the same rows of a 600-row batch on the tiled kernel bit for bit, and the oracle
+    within the fp16 rounding of the dequantised weights."""
     rng = np.random.default_rng(cols)
     rows = 256
     raw = q8_raw(rows, cols, rng)
-    x16 = f16_round(rng.standard_normal((300, cols)))
+    x16 = f16_round(rng.standard_normal((600, cols)))
     full = run_gemm(ctx, raw, rows, cols, x16)
     want = ora.matmul(x16[:64].astype(np.float32), q8_dequant(raw, rows, cols))
     assert max_rel(full[:64], want) < 3e-3
-    for lo, n in ((0, 1), (40, 64), (250, 33)):
+    for lo, n in ((0, 1), (40, 64), (250, 33), (80, 512)):
         assert np.array_equal(full[lo:lo + n], run_gemm(ctx, raw, rows, cols, x16[lo:lo + n].copy())), (lo, n)
     g = ctx.q8_create(q8_raw(rows, cols, rng), rows, cols)
     u = ctx.q8_create(q8_raw(rows, cols, rng), rows, cols)
@@ -157,10 +159,10 @@ def test_gemm_short_batch_every_pipeline_depth(ctx, cols):
             ctx.free(dx)
             ctx.free(da)
     try:
-        xs = f16_round(rng.standard_normal((300, cols)) * 0.05)
+        xs = f16_round(rng.standard_normal((600, cols)) * 0.05)
         gfull = geglu(xs)
         assert np.all(np.isfinite(gfull.astype(np.float32)))
-        for lo, n in ((0, 3), (40, 64), (250, 50)):
+        for lo, n in ((0, 3), (40, 64), (250, 50), (70, 512)):
             assert np.array_equal(gfull[lo:lo + n], geglu(xs[lo:lo + n].copy())), (lo, n)
     finally:
         ctx.q8_destroy(g)
@@ -168,7 +170,7 @@ def test_gemm_short_batch_every_pipeline_depth(ctx, cols):
 
 
 def test_gemm_geglu_short_batch_matches_tiled_rows(ctx, c2):
-    M = 300
+    M = 600
     x16 = f16_round(RNG.standard_normal((M, 768)) * 0.05)
     g = ctx.q8_create(np.asarray(c2.raw("blk.4.ffn_gate.weight")), 1152, 768)
     u = ctx.q8_create(np.asarray(c2.raw("blk.4.ffn_up.weight")), 1152, 768)
@@ -184,7 +186,7 @@ def test_gemm_geglu_short_batch_matches_tiled_rows(ctx, c2):
             ctx.free(da)
     try:
         full = geglu(x16)
-        for lo, n in ((0, 3), (40, 64), (250, 50)):
+        for lo, n in ((0, 3), (40, 64), (250, 50), (60, 512)):
             assert np.array_equal(full[lo:lo + n], geglu(x16[lo:lo + n].copy())), (lo, n)
     finally:
         ctx.q8_destroy(g)
