@@ -181,10 +181,11 @@ def image_embed_variant(tmp: str, text_path: str, reps: int):
 
 def reference_shapes_variant(tmp: str, reps: int):
     """The reference's own architecture at its real shapes (d 512, per-layer inputs; synthetic
-    weights) on the shapes of its published benchmarks (an 8 x 1024-token pack in
-    0.4078 s median, a 1 x 64-token call in 6.18 ms, on an Apple M3 Max with the real model),
-    through the host API: token ids in host memory -> normalised vectors, the reference's own
-    boundary (COMPARISON.md:57-60)."""
+    weights) on the shapes of its published benchmarks (Apple M3 Max with the real
+    model, first run's medians: an 8 x 1024-token pack in 0.4078 s, 32 x 64 in 0.0604 s, 8 x 256
+    in 0.0686 s, a 1 x 64-token call in 6.18 ms, 12 queries of 171 tokens in all as 12 separate
+    calls in 52.2 ms), through the host API: token ids in host memory -> normalised vectors, the
+    reference's own boundary (COMPARISON.md:57-60)."""
     import numpy as np
     import gemma_embed as ge
     path = os.path.join(tmp, "real_shapes.gguf")
@@ -192,19 +193,27 @@ def reference_shapes_variant(tmp: str, reps: int):
     model = ge.EmbeddingModel.load(path)
     try:
         opts = ge.EmbedOptions()
-        pack = [r.tolist() for r in ge.synth_tokens(81, 2, 262144, 8 * 1024).reshape(8, 1024)]
+
+        def pack_of(seed, n, length):
+            return [r.tolist() for r in ge.synth_tokens(seed, 2, 262144, n * length).reshape(n, length)]
+
+        def timed(fn, n):
+            fn()
+            fn()
+            t0 = time.perf_counter()
+            for _ in range(n):
+                r = fn()
+            return (time.perf_counter() - t0) / n, r
+
+        pack = pack_of(81, 8, 1024)
         one = [ge.synth_tokens(82, 2, 262144, 64).tolist()]
-        for _ in range(2):
-            model.embed(pack, opts)
-            model.embed(one, opts)
-        t0 = time.perf_counter()
-        for _ in range(reps):
-            out = model.embed(pack, opts)
-        pack_s = (time.perf_counter() - t0) / reps
-        t0 = time.perf_counter()
-        for _ in range(reps * 4):
-            model.embed(one, opts)
-        one_s = (time.perf_counter() - t0) / (reps * 4)
+        p32x64, p8x256 = pack_of(83, 32, 64), pack_of(84, 8, 256)
+        queries = [ge.synth_tokens(85 + i, 2, 262144, 15 if i < 3 else 14).tolist() for i in range(12)]  # 171 tokens
+        pack_s, out = timed(lambda: model.embed(pack, opts), reps)
+        one_s, _ = timed(lambda: model.embed(one, opts), reps * 4)
+        s32x64, _ = timed(lambda: model.embed(p32x64, opts), reps)
+        s8x256, _ = timed(lambda: model.embed(p8x256, opts), reps)
+        queries_s, _ = timed(lambda: [model.embed([q], opts) for q in queries], reps)
         if not all(np.all(np.isfinite(e.vector)) for e in out):
             raise SystemExit("non-finite output (reference shapes)")
     finally:
@@ -213,7 +222,10 @@ def reference_shapes_variant(tmp: str, reps: int):
                      "GeGLU 2048, per-layer inputs 512, 24 layers; synthetic Q8_0 weights",
             "pack_8x1024_s": round(pack_s, 5), "pack_8x1024_tokens_per_s": round(8 * 1024 / pack_s, 1),
             "reference_m3max_pack_8x1024_s": 0.4078,
-            "call_1x64_ms": round(one_s * 1e3, 3), "reference_m3max_call_1x64_ms": 6.18}
+            "pack_32x64_s": round(s32x64, 5), "reference_m3max_pack_32x64_s": 0.0604,
+            "pack_8x256_s": round(s8x256, 5), "reference_m3max_pack_8x256_s": 0.0686,
+            "call_1x64_ms": round(one_s * 1e3, 3), "reference_m3max_call_1x64_ms": 6.18,
+            "queries_12_separate_calls_ms": round(queries_s * 1e3, 3), "reference_m3max_queries_12_ms": 52.2}
 
 
 def measured_traffic(label: str):
@@ -625,7 +637,9 @@ def main():
             f"{image_embed['images_per_s']:.1f} images/s")
     ref_shapes = reference_shapes_variant(tmp, max(3, args.steps // 4))
     log(f"reference shapes: 8 x 1024 in {ref_shapes['pack_8x1024_s'] * 1e3:.2f} ms "
-        f"({ref_shapes['pack_8x1024_tokens_per_s']:,.0f} tok/s), 1 x 64 call {ref_shapes['call_1x64_ms']:.2f} ms")
+        f"({ref_shapes['pack_8x1024_tokens_per_s']:,.0f} tok/s), 32 x 64 in {ref_shapes['pack_32x64_s'] * 1e3:.2f} ms, "
+        f"8 x 256 in {ref_shapes['pack_8x256_s'] * 1e3:.2f} ms, 1 x 64 call {ref_shapes['call_1x64_ms']:.2f} ms, "
+        f"12 queries as separate calls {ref_shapes['queries_12_separate_calls_ms']:.2f} ms")
     log(f"config 5 (8 images): {vision['ms_per_batch']:.2f} ms/batch, {vision['images_per_s']:.1f} images/s, "
         f"{vision['tflops']} TFLOP/s")
 
