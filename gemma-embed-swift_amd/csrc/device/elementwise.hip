@@ -482,43 +482,42 @@ hipError_t launch_qkv_norm_rope_vt(hipStream_t s, const uint16_t* qkv, int T, in
 // ============================================================================ mean pool
 //
 // pooled[s] = mean over the sequence's rows (reference Shaders/Elementwise.metal:243-256;
-// Model/CPUReference.swift:277-282). Workgroup (256-column chunk, sequence) of 16 waves: wave w
-// sums rows w, w + 16, ... in order, each lane 4 columns (16-byte loads, four rows in flight);
-// the 16 partial sums then combine in a fixed tree order, so the result does not depend on
-// scheduling or on the sequence's place in the pack.
-__global__ __launch_bounds__(1024) void mean_pool_kernel(const float* __restrict__ x, const SeqRange* __restrict__ seqs,
-                                                         int width, float* __restrict__ pooled) {
-    __shared__ float4 part[16][64];
+// Model/CPUReference.swift:277-282). Workgroup (64-column chunk, sequence) of 4 waves: 16 lanes
+// hold a row's 64 columns (4 each, 16-byte loads), 16 row slots; slot j sums rows j, j + 16, ...
+// in order, eight rows in flight; the 16 partial sums then combine in a fixed tree order, so the
+// result does not depend on scheduling or on the sequence's place in the pack. 64-column chunks
+// give a sequence's pool width / 64 workgroups, spread over that many CUs: with 256-column
+// chunks of 16 waves, four 8192-token sequences ran on 12 CUs at 1 TB/s.
+__global__ __launch_bounds__(256) void mean_pool_kernel(const float* __restrict__ x, const SeqRange* __restrict__ seqs,
+                                                        int width, float* __restrict__ pooled) {
+    __shared__ float4 part[16][16];
     const SeqRange sq = seqs[blockIdx.y];
-    const int lane = threadIdx.x & 63, slice = threadIdx.x >> 6;
-    const int c = blockIdx.x * 256 + lane * 4;
+    const int l16 = threadIdx.x & 15, slot = threadIdx.x >> 4;
+    const int c = blockIdx.x * 64 + l16 * 4;
     float4 acc = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
     if (c < width) {
         const float* p = x + (size_t)sq.start * width + c;
         const int n = int(sq.length);
-        int r = slice;
-        for (; r + 48 < n; r += 64) {
-            const float4 a = *reinterpret_cast<const float4*>(p + (size_t)r * width);
-            const float4 b = *reinterpret_cast<const float4*>(p + (size_t)(r + 16) * width);
-            const float4 e = *reinterpret_cast<const float4*>(p + (size_t)(r + 32) * width);
-            const float4 f = *reinterpret_cast<const float4*>(p + (size_t)(r + 48) * width);
-            acc.x += a.x, acc.y += a.y, acc.z += a.z, acc.w += a.w;
-            acc.x += b.x, acc.y += b.y, acc.z += b.z, acc.w += b.w;
-            acc.x += e.x, acc.y += e.y, acc.z += e.z, acc.w += e.w;
-            acc.x += f.x, acc.y += f.y, acc.z += f.z, acc.w += f.w;
+        int r = slot;
+        for (; r + 112 < n; r += 128) {
+            float4 v[8];
+#pragma unroll
+            for (int u = 0; u < 8; u++) v[u] = *reinterpret_cast<const float4*>(p + (size_t)(r + 16 * u) * width);
+#pragma unroll
+            for (int u = 0; u < 8; u++) acc.x += v[u].x, acc.y += v[u].y, acc.z += v[u].z, acc.w += v[u].w;
         }
         for (; r < n; r += 16) {
             const float4 a = *reinterpret_cast<const float4*>(p + (size_t)r * width);
             acc.x += a.x, acc.y += a.y, acc.z += a.z, acc.w += a.w;
         }
     }
-    part[slice][lane] = acc;
+    part[slot][l16] = acc;
     __syncthreads();
-    if (slice == 0 && c < width) {
+    if (slot == 0 && c < width) {
         float4 t[8];
 #pragma unroll
         for (int i = 0; i < 8; i++) {
-            const float4 u = part[2 * i][lane], v = part[2 * i + 1][lane];
+            const float4 u = part[2 * i][l16], v = part[2 * i + 1][l16];
             t[i] = make_float4(u.x + v.x, u.y + v.y, u.z + v.z, u.w + v.w);
         }
 #pragma unroll
@@ -538,7 +537,7 @@ __global__ __launch_bounds__(1024) void mean_pool_kernel(const float* __restrict
 hipError_t launch_mean_pool(hipStream_t s, const float* x, const SeqRange* seqs, int n_seqs, int width, float* pooled) {
     if (n_seqs < 0 || width <= 0 || width % 4) return hipErrorInvalidValue;
     if (n_seqs == 0) return hipSuccess;
-    launch_kernel(mean_pool_kernel, dim3((width + 255) / 256, n_seqs), 1024, 0, s, x, seqs, width, pooled);
+    launch_kernel(mean_pool_kernel, dim3((width + 63) / 64, n_seqs), 256, 0, s, x, seqs, width, pooled);
     return hipGetLastError();
 }
 

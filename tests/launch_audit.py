@@ -335,7 +335,7 @@ def attention_legacy(a, work, H, KV, HD, hw, q, k, v, o, rows_alloc_k):
 
 
 def mean_pool(a, seqs, width, x, seq_ptr, pooled):
-    """mean_pool_kernel (elementwise.hip:489): rows start .. start + len - 1 of each sequence, 16-byte
+    """mean_pool_kernel (elementwise.hip:491): rows start .. start + len - 1 of each sequence, 16-byte
     loads of columns c .. c + 3 < width."""
     a.span("mean_pool", seq_ptr, 0, len(seqs) * SEQ_BYTES)
     a.span("mean_pool", pooled, 0, len(seqs) * width * F32)
