@@ -548,15 +548,19 @@ constexpr int BKV = 32;   // keys per block
 template <int HD>
 constexpr int attention_v3_lds_bytes() { return attn3::NS * 2 * attn3::BKV * HD * 2; }
 
-template <int HD, int G, int QW>
-__global__ __launch_bounds__(QW * G * 64) void attention_v3_kernel(const uint16_t* __restrict__ Qg,
+// ONE: one query head per workgroup (grid y over the H query heads, QW waves) instead of the G
+// heads of a KV head (grid y over the KV heads, QW G waves). For the smallest batches: each
+// workgroup's key-block loop then carries a G-th of the work, on G times as many CUs. A head's
+// waves run the same operations either way, so the outputs are the same bits.
+template <int HD, int G, int QW, bool ONE = false>
+__global__ __launch_bounds__(QW * (ONE ? 1 : G) * 64) void attention_v3_kernel(const uint16_t* __restrict__ Qg,
                                                                   const uint16_t* __restrict__ Kg,
                                                                   const uint16_t* __restrict__ VTg,
                                                                   uint16_t* __restrict__ Og,
                                                                   const AttnWork* __restrict__ work, int H, int KV,
                                                                   int vt_cols, int hw, float scale_log2) {
     using namespace attn3;
-    constexpr int QB = 16 * QW, NW = QW * G, KS = HD / 32, DT = HD / 16;
+    constexpr int QB = 16 * QW, NW = QW * (ONE ? 1 : G), KS = HD / 32, DT = HD / 16;
     constexpr int K_BYTES = BKV * HD * 2, STAGE = 2 * K_BYTES;
     constexpr int KCH = K_BYTES / 1024, CH = 2 * KCH;  // K chunks (ks, m), then V^T chunks dt
     static_assert(KCH == 2 * KS && KCH == DT, "chunk counts");
@@ -576,10 +580,10 @@ __global__ __launch_bounds__(QW * G * 64) void attention_v3_kernel(const uint16_
     // 64-query items)
     const int wq0 = __builtin_amdgcn_readfirstlane(int(work[widx].q0)) + int(blockIdx.z) * QB;
     const int vt_start = __builtin_amdgcn_readfirstlane(int(work[widx].vt_start));
-    const int kvh = blockIdx.y;
+    const int kvh = ONE ? int(blockIdx.y) / G : int(blockIdx.y);
     const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(int(threadIdx.x >> 6));
-    const int h = kvh * G + wave % G;
-    const int q0 = wq0 + (wave / G) * 16;
+    const int h = ONE ? int(blockIdx.y) : kvh * G + wave % G;
+    const int q0 = wq0 + (ONE ? wave : wave / G) * 16;
     const int l16 = lane & 15, g4 = lane >> 4;  // query column, lane group
     const int qi = q0 + l16;
     const int qStride = H * HD, kvStride = KV * HD;
@@ -744,17 +748,32 @@ __global__ __launch_bounds__(QW * G * 64) void attention_v3_kernel(const uint16_
     }
 }
 
+// Batches of fewer workgroups than this (one per work item and KV head: a text of up to about 250
+// tokens) run one query head per workgroup. One 64-token text's attention: 9.2 -> 7.1 us per
+// layer (config-2 model); at 16 work items and more it gained nothing (one 512-token text) or
+// lost (eight: 26.7 -> 34.5 us).
+constexpr int kAttnOneHeadWork = 16;
+
 template <int HD, int G>
 static hipError_t attention_v3_dispatch(hipStream_t s, const uint16_t* q, const uint16_t* k, const uint16_t* vt,
                                         int vt_cols, uint16_t* o, const AttnWork* work, int n_work, int H, int KV, int hw,
                                         float scale, int item_queries) {
     const float scale_log2 = scale * 1.4426950408889634f;
-    if (item_queries == 32)
-        launch_kernel(attention_v3_kernel<HD, G, 2>, dim3(n_work, KV), dim3(2 * G * 64), uint32_t(attention_v3_lds_bytes<HD>()),
-                      s, q, k, vt, o, work, H, KV, vt_cols, hw, scale_log2);
-    else
-        launch_kernel(attention_v3_kernel<HD, G, 4>, dim3(n_work, KV), dim3(4 * G * 64), uint32_t(attention_v3_lds_bytes<HD>()),
-                      s, q, k, vt, o, work, H, KV, vt_cols, hw, scale_log2);
+    const uint32_t lds = uint32_t(attention_v3_lds_bytes<HD>());
+    if (G > 1 && n_work * KV < kAttnOneHeadWork) {
+        if (item_queries == 32)
+            launch_kernel(attention_v3_kernel<HD, G, 2, true>, dim3(n_work, H), dim3(2 * 64), lds, s, q, k, vt, o, work, H, KV,
+                          vt_cols, hw, scale_log2);
+        else
+            launch_kernel(attention_v3_kernel<HD, G, 4, true>, dim3(n_work, H), dim3(4 * 64), lds, s, q, k, vt, o, work, H, KV,
+                          vt_cols, hw, scale_log2);
+    } else if (item_queries == 32) {
+        launch_kernel(attention_v3_kernel<HD, G, 2>, dim3(n_work, KV), dim3(2 * G * 64), lds, s, q, k, vt, o, work, H, KV, vt_cols,
+                      hw, scale_log2);
+    } else {
+        launch_kernel(attention_v3_kernel<HD, G, 4>, dim3(n_work, KV), dim3(4 * G * 64), lds, s, q, k, vt, o, work, H, KV, vt_cols,
+                      hw, scale_log2);
+    }
     return hipGetLastError();
 }
 
@@ -1333,9 +1352,16 @@ template <int HD, int G>
 static hipError_t attention_v3_configure() {
     hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&attention_v3_kernel<HD, G, 4>),
                                        hipFuncAttributeMaxDynamicSharedMemorySize, attention_v3_lds_bytes<HD>());
-    if (e != hipSuccess) return e;
-    return hipFuncSetAttribute(reinterpret_cast<const void*>(&attention_v3_kernel<HD, G, 2>),
-                               hipFuncAttributeMaxDynamicSharedMemorySize, attention_v3_lds_bytes<HD>());
+    if (e == hipSuccess)
+        e = hipFuncSetAttribute(reinterpret_cast<const void*>(&attention_v3_kernel<HD, G, 2>),
+                                hipFuncAttributeMaxDynamicSharedMemorySize, attention_v3_lds_bytes<HD>());
+    if (e == hipSuccess)
+        e = hipFuncSetAttribute(reinterpret_cast<const void*>(&attention_v3_kernel<HD, G, 4, true>),
+                                hipFuncAttributeMaxDynamicSharedMemorySize, attention_v3_lds_bytes<HD>());
+    if (e == hipSuccess)
+        e = hipFuncSetAttribute(reinterpret_cast<const void*>(&attention_v3_kernel<HD, G, 2, true>),
+                                hipFuncAttributeMaxDynamicSharedMemorySize, attention_v3_lds_bytes<HD>());
+    return e;
 }
 
 hipError_t configure_kernels() {
