@@ -30,7 +30,7 @@ WORK_BYTES, SEQ_BYTES = 16, 8  # sizeof(AttnWork), sizeof(SeqRange)
 # ---------------------------------------------------------------- model
 
 def v2_supported(hd, H, KV):
-    """attention_v2_supported (csrc/device/attention.hip:789)."""
+    """attention_v2_supported (csrc/device/attention.hip:808)."""
     if hd == 512:
         return KV > 0 and H == 4 * KV
     if not (hd in (128, 256) and KV > 0 and H % KV == 0 and 1 <= H // KV <= 4):
@@ -246,7 +246,7 @@ def qkv_norm_rope_vt(a, T, H, KV, HD, qkv16, positions, q, k, v, vcol, vt_cols, 
 
 
 def v_transpose(a, T, width, v, vcol, vt_cols, vt, vc):
-    """v_transpose_kernel (attention.hip:1275): reads v[t][c0 + cc .. + 8) for t < T, c0 + cc < width;
+    """v_transpose_kernel (attention.hip:1294): reads v[t][c0 + cc .. + 8) for t < T, c0 + cc < width;
     writes vt[c0 + d][vcol[t]]."""
     a.span("v_transpose", v, 0, T * width * F16)
     a.span("v_transpose", vcol, 0, T * I32)
@@ -286,8 +286,8 @@ def gemm_qkv(a, M, N, K, hd, H, KV, x, e, pos, vc):
 
 def attention_items(a, kernel, work, H, KV, HD, q, k, vt, vt_cols, o, item_queries, q_lo=None, k_lo=None,
                     leave_empty=True):
-    """attention_v2_kernel (attention.hip:291), attention_v3_kernel (:552) and attention_split_kernel
-    (:841): per work item (seq_start, len, q0, vt_start) with len > 0 and head h, resources
+    """attention_v2_kernel (attention.hip:291), attention_v3_kernel (:556, one workgroup per KV head or per query head) and
+    attention_split_kernel (:860): per work item (seq_start, len, q0, vt_start) with len > 0 and head h, resources
         Q at (seq_start qStride + h HD) of ((len - 1) qStride + HD) halves, K likewise over kvStride,
         V^T at (kvh HD vt_cols + vt_start) of ((HD - 1) vt_cols + vt_cols - vt_start) halves,
     and output stores at row seq_start + qi for qi < min(q0 + item_queries, len). The kernels leave
