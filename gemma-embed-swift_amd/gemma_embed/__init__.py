@@ -9,6 +9,7 @@ carrying the C status code (Errors.swift:6-24). Compute always runs in the nativ
 from __future__ import annotations
 
 import ctypes as C
+import itertools
 import os
 from dataclasses import dataclass
 from typing import Callable, Iterable, List, Optional, Sequence, Tuple
@@ -203,6 +204,12 @@ def _i32(a) -> np.ndarray:
     return np.ascontiguousarray(a, dtype=np.int32)
 
 
+def _flat_i32(sequences) -> np.ndarray:
+    """The sequences' ids back to back as int32 (out-of-range ids raise OverflowError)."""
+    n = sum(len(s) for s in sequences)
+    return np.fromiter(itertools.chain.from_iterable(sequences), dtype=np.int32, count=n)
+
+
 def _ptr(a: np.ndarray, ctype):
     return a.ctypes.data_as(C.POINTER(ctype))
 
@@ -338,12 +345,13 @@ def _grid_array(grids) -> C.Array:
 
 def pack(sequences: Sequence[Sequence[int]]):
     """PackedBatch.append (Metal/MetalForward.swift:17-21): ids back to back, positions from 0."""
-    toks, pos, seqs = [], [], []
-    for s in sequences:
-        seqs.append((len(toks), len(s)))
-        toks.extend(int(t) for t in s)
-        pos.extend(range(len(s)))
-    return _i32(toks), _i32(pos), seqs
+    lengths = [len(s) for s in sequences]
+    seqs, start = [], 0
+    for n in lengths:
+        seqs.append((start, n))
+        start += n
+    pos = np.concatenate([np.arange(n, dtype=np.int32) for n in lengths]) if lengths else np.zeros(0, np.int32)
+    return _flat_i32(sequences), pos, seqs
 
 
 def _seq_array(seqs) -> C.Array:
@@ -753,7 +761,7 @@ class EmbeddingModel:
         """embed(_:options:progress:) (EmbeddingModel.swift:145-175) over token id lists. A
         progress callback returning True cancels before the next batch."""
         lengths = _i32([len(t) for t in texts])
-        flat = _i32([int(x) for t in texts for x in t])
+        flat = _flat_i32(texts)
         n = len(texts)
         out = np.zeros((max(n, 1), options.dimensions), dtype=np.float32)
         counts = np.zeros(max(n, 1), dtype=np.int32)
@@ -776,7 +784,7 @@ class EmbeddingModel:
     def embed_tokens(self, sequences: Sequence[Sequence[int]]) -> np.ndarray:
         """embedTokens (EmbeddingModel.swift:285-289): unnormalised pooled vectors, one batch."""
         lengths = _i32([len(t) for t in sequences])
-        flat = _i32([int(x) for t in sequences for x in t])
+        flat = _flat_i32(sequences)
         out = np.zeros((len(sequences), self.info.out_dims), dtype=np.float32)
         rc = lib.ge_model_embed_tokens(self._h, _ptr(flat, C.c_int32), _ptr(lengths, C.c_int32), len(sequences),
                                        _ptr(out, C.c_float))
