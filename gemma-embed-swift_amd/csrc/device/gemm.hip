@@ -378,10 +378,10 @@ __global__ __launch_bounds__(64 * kSkinnyWaves) void gemm_skinny_kernel(const ui
 // Metal/MetalForward.swift:375-395, Shaders/Elementwise.metal). A 128 x 256 tile holds 256 / HD
 // whole heads of 128 tokens. The accumulators (transposed, so a lane holds 4 consecutive columns of
 // one token) are staged in LDS as fp16 qkv * scale, the rounding the unfused path stores; then
-// each wave takes whole token rows: a lane holds 4 columns of one head, the head's sum of
-// squares is a butterfly over its HD / 4 lanes, and the NeoX partner of column j (j + HD / 2) sits
-// HD / 8 lanes away. Normalised V rows go back into LDS for the transposed write, one V^T row
-// (128 tokens) per wave instruction pair.
+// the waves take (token, head) units of HD / 16 lanes: a lane holds 8 dims of the head and their
+// 8 NeoX partners (qkv_unit below), so the rotation stays in the lane and the head's sum of
+// squares is a butterfly over the unit's lanes. Normalised V rows go back into LDS for the
+// transposed write, one V^T row (128 tokens) per wave instruction pair.
 // One (token, head) unit of the QKV epilogue. The unit's hd/16 lanes each hold dims [k8, k8 + 8)
 // (x0) and their NeoX partners [hd/2 + k8, hd/2 + k8 + 8) (x1) of the projection (fp16, scaled by
 // c), and the RoPE table entries of pairs k8 .. k8 + 7 (cs: cos, sin interleaved). Returns the
