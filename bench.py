@@ -50,14 +50,18 @@ def log(msg: str):
 
 
 def gemm_flops(m: int):
-    """Algorithmic FLOPs (2 M N K, M = real tokens) of one launch of each GEMM class; the four
-    layer GEMMs launch once per layer, the output projection once per forward."""
+    """Algorithmic FLOPs (2 M N K, M = real tokens) of one launch of each GEMM class; they launch
+    once per layer."""
     qkv = 2 * m * (H + 2 * KV) * HD * D
     o = 2 * m * D * H * HD
     gu = 2 * m * 2 * FF * D
     down = 2 * m * D * FF
-    out = 2 * m * OUT * D
-    return {"gemm_qkv": qkv, "gemm_o": o, "gemm_gate_up": gu, "gemm_down": down, "gemm_output": out}
+    return {"gemm_qkv": qkv, "gemm_o": o, "gemm_gate_up": gu, "gemm_down": down}
+
+
+def projection_flops(seqs: int):
+    """The output projection runs once per sequence, on its pooled final-norm row (fp32)."""
+    return 2 * seqs * OUT * D
 
 
 def gemm_bytes(m: int):
@@ -65,7 +69,7 @@ def gemm_bytes(m: int):
     (fp32, or fp16 for the GeGLU product)."""
     b = {}
     for name, n, k, out_bytes in (("gemm_qkv", (H + 2 * KV) * HD, D, 4), ("gemm_o", D, H * HD, 4),
-                                  ("gemm_gate_up", 2 * FF, D, 2), ("gemm_down", D, FF, 4), ("gemm_output", OUT, D, 4)):
+                                  ("gemm_gate_up", 2 * FF, D, 2), ("gemm_down", D, FF, 4)):
         n_out = n // 2 if name == "gemm_gate_up" else n
         b[name] = 2 * m * k + 2 * n * k + out_bytes * m * n_out
     return b
@@ -566,8 +570,7 @@ def main():
     log(f"resident pack: {ms_per_step:.3f} ms/step, {value:,.0f} tokens/s")
 
     flops = gemm_flops(n_tokens)
-    step_gemm_flops = LAYERS * (flops["gemm_qkv"] + flops["gemm_o"] + flops["gemm_gate_up"] + flops["gemm_down"]) \
-        + flops["gemm_output"]
+    step_gemm_flops = LAYERS * (flops["gemm_qkv"] + flops["gemm_o"] + flops["gemm_gate_up"] + flops["gemm_down"])
     dom = "gemm_gate_up"
     launches, total_ms = stats.get(dom, (0, 0.0))
     avg_ms = total_ms / max(launches, 1)
@@ -626,7 +629,7 @@ def main():
     if not np.all(np.isfinite(ctx.batch_read())):
         raise SystemExit("non-finite pooled output (config 4)")
     long_flops = LAYERS * sum(gemm_flops(long_texts * long_len)[k] for k in ("gemm_qkv", "gemm_o", "gemm_gate_up", "gemm_down")) \
-        + gemm_flops(long_texts * long_len)["gemm_output"] + attention_flops([long_len] * long_texts)
+        + projection_flops(long_texts) + attention_flops([long_len] * long_texts)
     log(f"config 4 (4 x 8192): {long_ms:.2f} ms/step, {long_rate:,.0f} tok/s")
 
     vision = vision_variant(tmp, max(3, args.steps // 2))
@@ -643,7 +646,7 @@ def main():
     log(f"config 5 (8 images): {vision['ms_per_batch']:.2f} ms/batch, {vision['images_per_s']:.1f} images/s, "
         f"{vision['tflops']} TFLOP/s")
 
-    total_flops = step_gemm_flops + attention_flops([TOKENS] * TEXTS)
+    total_flops = step_gemm_flops + attention_flops([TOKENS] * TEXTS) + projection_flops(TEXTS)
     traffic, traffic_kernel = measured_traffic(dom)
     result = {
         "metric": METRIC,

@@ -101,11 +101,11 @@ hipError_t launch_embed_norm(hipStream_t s, const Q8Dev& table, const int32_t* t
 // x = (x + rmsnorm(t) * w) * out_scale, then optionally h = rmsnorm(x) * next_w in fp16: the
 // post-attention / post-FFN norm, the residual add and the next block's pre-norm in one pass
 // (reference Shaders/Elementwise.metal:260-354; Model/CPUReference.swift:240-245, :254-257, :269).
-template <int CH>
+template <int CH, bool F32OUT>
 __global__ __launch_bounds__(256) void residual_norm_kernel(float* __restrict__ x, const uint16_t* __restrict__ t16,
                                                             float t_eps, const float* __restrict__ w, float out_scale,
                                                             const float* __restrict__ next_w, float eps, int T, int d,
-                                                            uint16_t* __restrict__ h) {
+                                                            uint16_t* __restrict__ h, float* __restrict__ h32) {
     const int row = blockIdx.x * 4 + (threadIdx.x >> 6), lane = threadIdx.x & 63;
     if (row >= T) return;
     // t arrives as fp16 t * c (c a power of two) with t_eps = eps * c^2: the RMSNorm of the
@@ -160,25 +160,35 @@ __global__ __launch_bounds__(256) void residual_norm_kernel(float* __restrict__ 
         const int e = c * 256 + lane * 4;
         if (e < d) {
             const float nw[4] = {nwa[c].x, nwa[c].y, nwa[c].z, nwa[c].w};
-            half4_t o;
+            if constexpr (F32OUT) {
+                *reinterpret_cast<float4*>(h32 + (size_t)row * d + e) =
+                    make_float4(xv[c][0] * inv2 * nw[0], xv[c][1] * inv2 * nw[1], xv[c][2] * inv2 * nw[2], xv[c][3] * inv2 * nw[3]);
+            } else {
+                half4_t o;
 #pragma unroll
-            for (int j = 0; j < 4; j++) o[j] = _Float16(xv[c][j] * inv2 * nw[j]);
-            *reinterpret_cast<half4_t*>(h + (size_t)row * d + e) = o;
+                for (int j = 0; j < 4; j++) o[j] = _Float16(xv[c][j] * inv2 * nw[j]);
+                *reinterpret_cast<half4_t*>(h + (size_t)row * d + e) = o;
+            }
         }
     }
 }
 
 hipError_t launch_residual_norm(hipStream_t s, float* x, const uint16_t* t16, float t_eps, const float* w,
-                                float out_scale, const float* next_w, float eps, int T, int d, uint16_t* h) {
-    if (T < 0 || d <= 0 || d % 4 != 0 || d > 1024 || (next_w && !h) || !t16) return hipErrorInvalidValue;
+                                float out_scale, const float* next_w, float eps, int T, int d, uint16_t* h, float* h32) {
+    if (T < 0 || d <= 0 || d % 4 != 0 || d > 1024 || (next_w && !h && !h32) || !t16) return hipErrorInvalidValue;
     if (T == 0) return hipSuccess;
     const int blocks = (T + 3) / 4, CH = (d + 255) / 256;
+    // the fp32 output is a separate instantiation, so the fp16 one compiles as on its own
+#define RN_LAUNCH(C)                                                                                              \
+    (h32 ? launch_kernel(residual_norm_kernel<C, true>, blocks, 256, 0, s, x, t16, t_eps, w, out_scale, next_w, eps, T, d, h, h32) \
+         : launch_kernel(residual_norm_kernel<C, false>, blocks, 256, 0, s, x, t16, t_eps, w, out_scale, next_w, eps, T, d, h, h32))
     switch (CH) {
-    case 1: launch_kernel(residual_norm_kernel<1>, blocks, 256, 0, s, x, t16, t_eps, w, out_scale, next_w, eps, T, d, h); break;
-    case 2: launch_kernel(residual_norm_kernel<2>, blocks, 256, 0, s, x, t16, t_eps, w, out_scale, next_w, eps, T, d, h); break;
-    case 3: launch_kernel(residual_norm_kernel<3>, blocks, 256, 0, s, x, t16, t_eps, w, out_scale, next_w, eps, T, d, h); break;
-    default: launch_kernel(residual_norm_kernel<4>, blocks, 256, 0, s, x, t16, t_eps, w, out_scale, next_w, eps, T, d, h); break;
+    case 1: RN_LAUNCH(1); break;
+    case 2: RN_LAUNCH(2); break;
+    case 3: RN_LAUNCH(3); break;
+    default: RN_LAUNCH(4); break;
     }
+#undef RN_LAUNCH
     return hipGetLastError();
 }
 
@@ -538,6 +548,78 @@ hipError_t launch_mean_pool(hipStream_t s, const float* x, const SeqRange* seqs,
     if (n_seqs < 0 || width <= 0 || width % 4) return hipErrorInvalidValue;
     if (n_seqs == 0) return hipSuccess;
     launch_kernel(mean_pool_kernel, dim3((width + 63) / 64, n_seqs), 256, 0, s, x, seqs, width, pooled);
+    return hipGetLastError();
+}
+
+// ============================================================================ output projection
+//
+// The output projection applied to pooled rows: pooling is a mean and the projection is linear,
+// so projecting the sequence's mean normed row equals the reference's mean of projected tokens
+// (Model/CPUReference.swift:274-282) up to fp32 rounding, on one row per sequence instead of one
+// per token, and in fp32 throughout: the Q8_0 weights as d * q (exact in fp32) and the normed rows
+// as the final norm computed them, where the token-wise GEMM rounds both to fp16.
+// One wave per output column n: lane l holds columns c * 256 + 4 l .. + 3 of the weight row
+// (dequantised once), then walks the workgroup's rows; each row's dot product is summed per lane
+// over its chunks in order, then over the lanes by a fixed butterfly, so a row's output depends
+// on that row alone.
+constexpr int kProjRows = 64;   // rows (sequences) per workgroup row of the grid
+constexpr int kProjUnroll = 8;  // rows whose loads are in flight together
+
+template <int CH>
+__global__ __launch_bounds__(256) void pooled_projection_kernel(const float* __restrict__ in, int n_rows, int width,
+                                                                const int8_t* __restrict__ q,
+                                                                const uint16_t* __restrict__ sc, int n_out,
+                                                                float* __restrict__ out) {
+    const int n = blockIdx.x * 4 + (threadIdx.x >> 6), lane = threadIdx.x & 63;
+    if (n >= n_out) return;
+    const int r0 = blockIdx.y * kProjRows, r1 = min(r0 + kProjRows, n_rows);
+    float wv[CH][4];
+#pragma unroll
+    for (int c = 0; c < CH; c++) {
+        const int ec = min(c * 256 + lane * 4, width - 4);
+        const char4 q4 = *reinterpret_cast<const char4*>(q + (size_t)n * width + ec);
+        const float dsc = h2f(sc[(size_t)n * (width / 32) + ec / 32]);
+        wv[c][0] = dsc * float(q4.x), wv[c][1] = dsc * float(q4.y), wv[c][2] = dsc * float(q4.z), wv[c][3] = dsc * float(q4.w);
+    }
+    // kProjUnroll rows at a time, all their loads issued before any product (rows past r1 re-read
+    // row r1 - 1, unused), so the loop waits for one batch of loads rather than for each row's
+    for (int r = r0; r < r1; r += kProjUnroll) {
+        float4 xa[kProjUnroll][CH];
+#pragma unroll
+        for (int u = 0; u < kProjUnroll; u++)
+#pragma unroll
+            for (int c = 0; c < CH; c++)
+                xa[u][c] = *reinterpret_cast<const float4*>(in + (size_t)min(r + u, r1 - 1) * width +
+                                                            min(c * 256 + lane * 4, width - 4));
+#pragma unroll
+        for (int u = 0; u < kProjUnroll; u++) {
+            float acc = 0.0f;
+#pragma unroll
+            for (int c = 0; c < CH; c++)
+                if (c * 256 + lane * 4 < width) {
+                    acc = __builtin_fmaf(xa[u][c].x, wv[c][0], acc);
+                    acc = __builtin_fmaf(xa[u][c].y, wv[c][1], acc);
+                    acc = __builtin_fmaf(xa[u][c].z, wv[c][2], acc);
+                    acc = __builtin_fmaf(xa[u][c].w, wv[c][3], acc);
+                }
+            acc = wave_sum(acc);
+            if (lane == 0 && r + u < r1) out[(size_t)(r + u) * n_out + n] = acc;
+        }
+    }
+}
+
+hipError_t launch_pooled_projection(hipStream_t s, const float* in, int n_rows, int width, const Q8Dev& w, float* out) {
+    if (n_rows < 0 || width <= 0 || width % 32 || width > 1024 || w.cols != width || w.rows <= 0 || !w.q || !w.s ||
+        !in || !out)
+        return hipErrorInvalidValue;
+    if (n_rows == 0) return hipSuccess;
+    const dim3 grid((w.rows + 3) / 4, (n_rows + kProjRows - 1) / kProjRows);
+    switch ((width + 255) / 256) {
+    case 1: launch_kernel(pooled_projection_kernel<1>, grid, 256, 0, s, in, n_rows, width, w.q, w.s, w.rows, out); break;
+    case 2: launch_kernel(pooled_projection_kernel<2>, grid, 256, 0, s, in, n_rows, width, w.q, w.s, w.rows, out); break;
+    case 3: launch_kernel(pooled_projection_kernel<3>, grid, 256, 0, s, in, n_rows, width, w.q, w.s, w.rows, out); break;
+    default: launch_kernel(pooled_projection_kernel<4>, grid, 256, 0, s, in, n_rows, width, w.q, w.s, w.rows, out); break;
+    }
     return hipGetLastError();
 }
 

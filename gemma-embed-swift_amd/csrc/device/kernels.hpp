@@ -103,11 +103,13 @@ hipError_t launch_gemm_qkv(hipStream_t s, const Q8Dev& w, const uint16_t* x, int
 hipError_t launch_embed_norm(hipStream_t s, const Q8Dev& table, const int32_t* tokens, int T, float scale,
                              const float* vectors, const float* norm_w, float eps, float* x, uint16_t* h);
 
-// x = (x + rmsnorm(t) * w) * out_scale; if next_w: h = rmsnorm(x) * next_w (fp16).
+// x = (x + rmsnorm(t) * w) * out_scale; if next_w: h = rmsnorm(x) * next_w (fp16), or into h32 in
+// fp32 when h32 is given (the final norm, whose rows are pooled before the output projection).
 // t arrives as fp16 t16 = t * c for a power of two c, and t_eps = eps * c^2, so rmsnorm(t16)
 // with t_eps is rmsnorm(t) exactly. d a multiple of 4, at most 1024.
 hipError_t launch_residual_norm(hipStream_t s, float* x, const uint16_t* t16, float t_eps, const float* w,
-                                float out_scale, const float* next_w, float eps, int T, int d, uint16_t* h);
+                                float out_scale, const float* next_w, float eps, int T, int d, uint16_t* h,
+                                float* h32 = nullptr);
 
 // h3 fp16 [T][3 d] = [hi | lo | hi] of y = rmsnorm(x) * w (hi = fp16(y), lo = fp16(y - hi)): the
 // input of a split-precision GEMM against [W_hi | W_hi | W_lo]. d a multiple of 4, at most 1024.
@@ -170,6 +172,10 @@ hipError_t launch_v_transpose(hipStream_t s, const uint16_t* v, int T, int width
 // pooled[s] = mean of the sequence's rows of x [*][width].
 hipError_t launch_mean_pool(hipStream_t s, const float* x, const SeqRange* seqs, int n_seqs, int width, float* pooled);
 
+// out[r][n] = sum over k of in[r][k] * W[n][k], W = d * q from w's Q8_0 planes, all in fp32 (the
+// output projection of pooled rows; w.cols = width, a multiple of 32 up to 1024).
+hipError_t launch_pooled_projection(hipStream_t s, const float* in, int n_rows, int width, const Q8Dev& w, float* out);
+
 // ---- per-layer-input branch (ple.hip); widths a multiple of 4, at most 1024.
 // out[r] = rmsnorm(in[r] * mul * rscale[r / per_scale]) * w for rows of `width` (in may be out).
 hipError_t launch_ple_rmsnorm(hipStream_t s, const float* in, int rows, int width, float mul, const float* rscale,
@@ -183,9 +189,11 @@ hipError_t launch_ple_residual_input(hipStream_t s, float* x, const uint16_t* t1
 // rscale2[r] = s2_r, chosen as in launch_ple_input.
 hipError_t launch_ple_gate(hipStream_t s, const float* graw, const float* rscale, const float* ple, int layer, int layers,
                            int T, int pl, uint16_t* g16, float* rscale2);
-// x = (x + rmsnorm(praw[r] * rscale2[r]) * w) * out_scale; if next_w: h = rmsnorm(x) * next_w (fp16).
+// x = (x + rmsnorm(praw[r] * rscale2[r]) * w) * out_scale; if next_w: h = rmsnorm(x) * next_w (fp16),
+// or into h32 in fp32 when h32 is given.
 hipError_t launch_ple_residual_norm(hipStream_t s, float* x, const float* praw, const float* rscale2, const float* w,
-                                    float out_scale, const float* next_w, float eps, int T, int d, uint16_t* h);
+                                    float out_scale, const float* next_w, float eps, int T, int d, uint16_t* h,
+                                    float* h32 = nullptr);
 
 // ---- image tower row kernels (vision.hip); widths a multiple of 4, at most kVitMaxWidth.
 constexpr int kVitMaxWidth = 2048;

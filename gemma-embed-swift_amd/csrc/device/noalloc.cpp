@@ -59,6 +59,7 @@ Workspace carve(const DevModel& m, const BatchPlan& b, int n, int n_seqs, Carver
     w.t = cv.take<float>(R * m.hidden);
     w.act = cv.take<uint16_t>(R * m.ff);
     w.out = cv.take<float>(R * m.out_dims);
+    w.hn = cv.take<float>(R * m.hidden);
     w.tokens = cv.take<int32_t>(R);
     w.positions = cv.take<int32_t>(R);
     w.vcol = cv.take<int32_t>(R);
@@ -78,6 +79,7 @@ Workspace carve(const DevModel& m, const BatchPlan& b, int n, int n_seqs, Carver
     w.seq_cap = n_seqs;
     w.seqs = cv.take<SeqRange>(size_t(n_seqs));
     w.pooled = cv.take<float>(size_t(n_seqs) * m.out_dims);
+    w.pooled_n = cv.take<float>(size_t(n_seqs) * m.hidden);
     w.work_cap = std::max(int(b.work.size()), 1);
     w.work = cv.take<AttnWork>(size_t(w.work_cap));
     if (m.any_v2) {

@@ -214,12 +214,12 @@ __global__ __launch_bounds__(256) void ple_gate_kernel(const float* __restrict__
 
 // p = praw[r] * rscale2[r]; x = (x + rmsnorm(p) * w) * out_scale; with next_w also
 // h = rmsnorm(x) * next_w (fp16), the next layer's pre-norm.
-template <int CH>
+template <int CH, bool F32OUT>
 __global__ __launch_bounds__(256) void ple_residual_norm_kernel(float* __restrict__ x, const float* __restrict__ praw,
                                                                 const float* __restrict__ rscale2,
                                                                 const float* __restrict__ w, float out_scale,
                                                                 const float* __restrict__ next_w, float eps, int T, int d,
-                                                                uint16_t* __restrict__ h) {
+                                                                uint16_t* __restrict__ h, float* __restrict__ h32) {
     const int row = blockIdx.x * 4 + (threadIdx.x >> 6), lane = threadIdx.x & 63;
     if (row >= T) return;
     const float s2 = rscale2[row];
@@ -270,13 +270,24 @@ __global__ __launch_bounds__(256) void ple_residual_norm_kernel(float* __restric
     for (int c = 0; c < CH; c++) {
         const int e = c * 256 + lane * 4;
         if (e < d) {
-            half4_t o;
+            if constexpr (F32OUT) {
+                *reinterpret_cast<float4*>(h32 + (size_t)row * d + e) =
+                    make_float4(xv[c][0] * inv2 * nwa[c][0], xv[c][1] * inv2 * nwa[c][1], xv[c][2] * inv2 * nwa[c][2],
+                                xv[c][3] * inv2 * nwa[c][3]);
+            } else {
+                half4_t o;
 #pragma unroll
-            for (int j = 0; j < 4; j++) o[j] = _Float16(xv[c][j] * inv2 * nwa[c][j]);
-            *reinterpret_cast<half4_t*>(h + (size_t)row * d + e) = o;
+                for (int j = 0; j < 4; j++) o[j] = _Float16(xv[c][j] * inv2 * nwa[c][j]);
+                *reinterpret_cast<half4_t*>(h + (size_t)row * d + e) = o;
+            }
         }
     }
 }
+
+template <int CH>
+constexpr auto ple_residual_norm_f16 = ple_residual_norm_kernel<CH, false>;
+template <int CH>
+constexpr auto ple_residual_norm_f32 = ple_residual_norm_kernel<CH, true>;
 
 #define PLE_DISPATCH(KERNEL, WIDTH, ROWS, ...)                                                          \
     do {                                                                                                \
@@ -324,10 +335,14 @@ hipError_t launch_ple_gate(hipStream_t s, const float* graw, const float* rscale
 }
 
 hipError_t launch_ple_residual_norm(hipStream_t s, float* x, const float* praw, const float* rscale2, const float* w,
-                                    float out_scale, const float* next_w, float eps, int T, int d, uint16_t* h) {
-    if (T < 0 || !ple_width_ok(d) || !x || !praw || !rscale2 || !w || (next_w && !h)) return hipErrorInvalidValue;
+                                    float out_scale, const float* next_w, float eps, int T, int d, uint16_t* h, float* h32) {
+    if (T < 0 || !ple_width_ok(d) || !x || !praw || !rscale2 || !w || (next_w && !h && !h32)) return hipErrorInvalidValue;
     if (T == 0) return hipSuccess;
-    PLE_DISPATCH(ple_residual_norm_kernel, d, T, s, x, praw, rscale2, w, out_scale, next_w, eps, T, d, h);
+    // the fp32 output is a separate instantiation, so the fp16 one compiles as on its own
+    if (h32)
+        PLE_DISPATCH(ple_residual_norm_f32, d, T, s, x, praw, rscale2, w, out_scale, next_w, eps, T, d, h, h32);
+    else
+        PLE_DISPATCH(ple_residual_norm_f16, d, T, s, x, praw, rscale2, w, out_scale, next_w, eps, T, d, h, h32);
     return hipGetLastError();
 }
 

@@ -439,7 +439,8 @@ void free_workspace(ge_ctx* c) {
     drop_graphs(c);
     Workspace& w = c->ws;
     void* ps[] = {w.x, w.qkv, w.t, w.out, w.h, w.q, w.k, w.v, w.attn, w.act, w.tokens, w.positions, w.seqs, w.work, w.pooled,
-                  w.vt, w.vcol, w.work2, w.ple, w.ple_t, w.rs, w.rs2, w.x16, w.g16, w.h3, w.q_lo, w.k_lo};
+                  w.vt, w.vcol, w.work2, w.ple, w.ple_t, w.rs, w.rs2, w.x16, w.g16, w.h3, w.q_lo, w.k_lo, w.hn,
+                  w.pooled_n};
     for (void* p : ps)
         if (p) (void)hipFree(p);
     c->ws = Workspace{};
@@ -633,6 +634,7 @@ void ensure_workspace_impl(ge_ctx* c, int tokens, int seqs, int work, int work2,
         w.t = ws_alloc<float>(rows, m.hidden, "t");
         w.act = ws_alloc<uint16_t>(rows, m.ff, "act");
         w.out = ws_alloc<float>(rows, m.out_dims, "out");
+        w.hn = ws_alloc<float>(rows, m.hidden, "final norm");
         w.tokens = ws_alloc<int32_t>(rows, 1, "tokens");
         w.positions = ws_alloc<int32_t>(rows, 1, "positions");
         w.vcol = ws_alloc<int32_t>(rows, 1, "vt columns");
@@ -652,6 +654,7 @@ void ensure_workspace_impl(ge_ctx* c, int tokens, int seqs, int work, int work2,
         w.seqs = nullptr;
         w.work = nullptr;
         w.pooled = nullptr;
+        w.pooled_n = nullptr;
         w.seq_cap = 0;
         w.work_cap = 0;
         w.vt = nullptr;
@@ -662,9 +665,13 @@ void ensure_workspace_impl(ge_ctx* c, int tokens, int seqs, int work, int work2,
     if (seqs > w.seq_cap || !w.seqs) {
         if (w.seqs) (void)hipFree(w.seqs);
         if (w.pooled) (void)hipFree(w.pooled);
+        if (w.pooled_n) (void)hipFree(w.pooled_n);
+        w.seqs = nullptr;
+        w.pooled = w.pooled_n = nullptr;
         w.seq_cap = std::max(seqs, 1);
         w.seqs = ws_alloc<SeqRange>(w.seq_cap, 1, "sequences");
         w.pooled = ws_alloc<float>(w.seq_cap, m.out_dims, "pooled");
+        w.pooled_n = ws_alloc<float>(w.seq_cap, m.hidden, "pooled rows");
     }
     if (work > w.work_cap || !w.work) {
         if (w.work) (void)hipFree(w.work);
@@ -890,6 +897,19 @@ bool at(StopPoint* sp, const char* name, int layer) {
     return false;
 }
 
+// The output (CPUReference.swift:272-282): the mean of each sequence's final-norm rows (fp32),
+// then the output projection of those means. The reference projects every token and averages
+// the projections; the mean and the projection are both linear, so the order does not change
+// the result beyond fp32 rounding, and here the projection runs once per sequence, in fp32.
+void encode_tail(ge_ctx* c, hipStream_t s) {
+    const DevModel& m = c->model;
+    Workspace& w = c->ws;
+    launch(c, "mean_pool", [&] { return launch_mean_pool(s, w.hn, w.seqs, c->staged_seqs, m.hidden, w.pooled_n); });
+    launch(c, "output_projection", [&] {
+        return launch_pooled_projection(s, w.pooled_n, c->staged_seqs, m.hidden, m.output, w.pooled);
+    });
+}
+
 // MetalForward.encode (Metal/MetalForward.swift:364-423) for the text path without the
 // per-layer-input branch: 7 launches per layer. Returns early after the op producing the stop point.
 void encode(ge_ctx* c, StopPoint* sp) {
@@ -990,6 +1010,7 @@ void encode(ge_ctx* c, StopPoint* sp) {
         launch(c, "gemm_down", [&] { return launch_gemm_q8(s, L.wd, w.act, T, t16, kEpiF16, L.down_scale * L.down_c); });
         if (at(sp, "ffn_out", l)) return;
         const float* next = l + 1 < m.layers ? m.layer[size_t(l) + 1].attn_norm : m.out_norm;
+        float* const h32 = l + 1 < m.layers ? nullptr : w.hn;  // the final norm stays fp32
         if (m.pl > 0) {
             // CPUReference.swift:259-269: x += rmsnorm(proj(gelu(inp_gate(x)) * ple_l), post_norm), then
             // the layer output scale; the unnormalised inputs of both projections go row-scaled
@@ -1002,21 +1023,25 @@ void encode(ge_ctx* c, StopPoint* sp) {
             // the projection (fp32 [T][hidden]) goes to t, free once the FFN residual has read it
             launch(c, "gemm_ple_proj", [&] { return launch_gemm_q8(s, L.proj, w.g16, T, w.t, kEpiF32); });
             launch(c, "ple_residual_norm", [&] {
-                return launch_ple_residual_norm(s, w.x, w.t, w.rs2, L.post_norm, L.out_scale, next, m.eps, T, D, w.h);
+                return launch_ple_residual_norm(s, w.x, w.t, w.rs2, L.post_norm, L.out_scale, next, m.eps, T, D, w.h, h32);
             });
             if (at(sp, "l_out", l) || at(sp, "attn_norm", l + 1)) return;
             continue;
         }
         launch(c, "residual_norm", [&] {
             return launch_residual_norm(s, w.x, t16, m.eps * L.down_c * L.down_c, L.post_ffw, L.out_scale, next, m.eps, T, D,
-                                        w.h);
+                                        w.h, h32);
         });
         if (at(sp, "pe_in", l) || at(sp, "l_out", l) || at(sp, "attn_norm", l + 1)) return;
     }
     if (at(sp, "result_norm", -1)) return;
-    launch(c, "gemm_output", [&] { return launch_gemm_q8(s, m.output, w.h, T, w.out, kEpiF32); });
-    if (at(sp, "result_embd", -1)) return;
-    launch(c, "mean_pool", [&] { return launch_mean_pool(s, w.out, w.seqs, c->staged_seqs, m.out_dims, w.pooled); });
+    if (sp && !sp->hit && sp->name == "result_embd") {
+        // the reference's per-token projection, traced only: every row through the same projection
+        launch(c, "output_projection", [&] { return launch_pooled_projection(s, w.hn, T, D, m.output, w.out); });
+        at(sp, "result_embd", -1);
+        return;
+    }
+    encode_tail(c, s);
 }
 
 // The forward of a split batch (see stage()): every layer's kernels run for each part's rows
@@ -1167,6 +1192,7 @@ void encode_split(ge_ctx* c) {
                                       L.down_scale * L.down_c);
             });
         const float* next = l + 1 < m.layers ? m.layer[size_t(l) + 1].attn_norm : m.out_norm;
+        const bool last = l + 1 == m.layers;  // the final norm stays fp32
         if (m.pl > 0) {
             const size_t LP = size_t(m.layers) * m.pl;
             for (const Half& H : halves)
@@ -1190,26 +1216,24 @@ void encode_split(ge_ctx* c) {
             for (const Half& H : halves)
                 launch(c, "ple_residual_norm", [&] {
                     return launch_ple_residual_norm(H.s, rows(w.x, H.r0, D), rows(w.t, H.r0, D), w.rs2 + H.r0, L.post_norm,
-                                                    L.out_scale, next, m.eps, H.T, D, rows(w.h, H.r0, D));
+                                                    L.out_scale, next, m.eps, H.T, D, rows(w.h, H.r0, D),
+                                                    last ? rows(w.hn, H.r0, D) : nullptr);
                 });
             continue;
         }
         for (const Half& H : halves)
             launch(c, "residual_norm", [&] {
                 return launch_residual_norm(H.s, rows(w.x, H.r0, D), rows(t16, H.r0, 2 * size_t(D)), m.eps * L.down_c * L.down_c,
-                                            L.post_ffw, L.out_scale, next, m.eps, H.T, D, rows(w.h, H.r0, D));
+                                            L.post_ffw, L.out_scale, next, m.eps, H.T, D, rows(w.h, H.r0, D),
+                                            last ? rows(w.hn, H.r0, D) : nullptr);
             });
     }
-    for (const Half& H : halves)
-        launch(c, "gemm_output", [&] {
-            return launch_gemm_q8(H.s, m.output, rows(w.h, H.r0, D), H.T, rows(w.out, H.r0, m.out_dims), kEpiF32);
-        });
     for (int p = 0; p < c->n_parts; p++)
         if (c->part_stream[p] != c->stream) {
             hip_check(hipEventRecord(c->part_join[p], c->part_stream[p]), "hipEventRecord");
             hip_check(hipStreamWaitEvent(c->stream, c->part_join[p], 0), "hipStreamWaitEvent");
         }
-    launch(c, "mean_pool", [&] { return launch_mean_pool(c->stream, w.out, w.seqs, c->staged_seqs, m.out_dims, w.pooled); });
+    encode_tail(c, c->stream);
 }
 
 // Packs of at most this many tokens replay their forward as a HIP graph from the second run of
@@ -1351,9 +1375,11 @@ void trace(ge_ctx* c, const char* name, int layer, float* out, size_t cap, size_
     if (n == "inp_scaled" || n == "attn_out" || n == "pe_in" || n == "l_out") {
         if (n != "inp_scaled") need_layer();
         buf = w.x; stride = width = m.hidden;
-    } else if (n == "attn_norm" || n == "ffn_norm" || n == "result_norm") {
-        if (n != "result_norm") need_layer();
+    } else if (n == "attn_norm" || n == "ffn_norm") {
+        need_layer();
         buf = w.h; f16 = true; stride = width = m.hidden;
+    } else if (n == "result_norm") {
+        buf = w.hn; stride = width = m.hidden;
     } else if (n == "Qcur" || n == "Kcur" || n == "Vcur") {
         need_layer();
         buf = w.qkv; stride = L->qd + 2 * L->kvd;

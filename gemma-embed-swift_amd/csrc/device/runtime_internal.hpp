@@ -94,6 +94,9 @@ struct Workspace {
     uint16_t *x16 = nullptr, *g16 = nullptr;
     // split-precision QKV input [T][3 hidden] (any precise layer)
     uint16_t* h3 = nullptr;
+    // the final norm's rows in fp32 [T][hidden] and their per-sequence means [seq_cap][hidden],
+    // the input of the output projection
+    float *hn = nullptr, *pooled_n = nullptr;
     // their q and k as split pairs: the low halves beside w.q / w.k (same layouts)
     uint16_t *q_lo = nullptr, *k_lo = nullptr;
 };

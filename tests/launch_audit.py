@@ -2,9 +2,9 @@
 
 For every kernel the forward launches, this module restates the index arithmetic by which the
 kernel's threads address global memory, the workspace the runtime allocates for a batch
-(ensure_workspace_impl, csrc/device/runtime.cpp:616), the batch plan it stages (plan_batch :717,
-vt_layout :696, stage :830) and the launch sequence with its pointer arguments (encode :895 for one
-stream, encode_split :1026 for a batch split over streams). Every access range of every launch is
+(ensure_workspace_impl, csrc/device/runtime.cpp:617), the batch plan it stages (plan_batch :724,
+vt_layout :703, stage :837) and the launch sequence with its pointer arguments (encode :915 for one
+stream, encode_split :1051 for a batch split over streams, both ending in encode_tail :904). Every access range of every launch is
 checked against the allocation its pointer falls in.
 
 - Plain loads and stores: the range of element indices the kernel's guards let through.
@@ -40,7 +40,7 @@ def v2_supported(hd, H, KV):
 
 
 def model_of(spec):
-    """The device model's shape and per-layer path flags, as upload() (runtime.cpp:449) derives them
+    """The device model's shape and per-layer path flags, as upload() (runtime.cpp:450) derives them
     from a synthetic model spec (gemma_embed.synth_write_gguf's keyword arguments)."""
     H, D = spec["heads"], spec["hidden"]
     m = dict(layers=spec["layers"], hidden=D, heads=H, ff=spec["feed_forward"], out_dims=spec["out_dims"],
@@ -76,9 +76,9 @@ def model_of(spec):
 # ---------------------------------------------------------------- batch plan and workspace
 
 def plan(m, lengths, gaps=None):
-    """plan_batch (runtime.cpp:717) for sequences of the given lengths packed back to back (with
+    """plan_batch (runtime.cpp:724) for sequences of the given lengths packed back to back (with
     `gaps[i]` unused rows before sequence i): sequence ranges, both attention work lists as arrays
-    of (seq_start, seq_len, q0, vt_start), the V^T layout (vt_layout :696) and the split into parts."""
+    of (seq_start, seq_len, q0, vt_start), the V^T layout (vt_layout :703) and the split into parts."""
     starts, r = [], 0
     for i, n in enumerate(lengths):
         r += gaps[i] if gaps else 0
@@ -130,13 +130,13 @@ def plan(m, lengths, gaps=None):
 
 
 def workspace(m, b):
-    """Allocation sizes of ensure_workspace_impl (runtime.cpp:616) for a staged batch (a fresh
+    """Allocation sizes of ensure_workspace_impl (runtime.cpp:617) for a staged batch (a fresh
     context: every capacity is the batch's own)."""
     R = (b["n"] + 63) // 64 * 64 + ROW_SLACK
     D = m["hidden"]
     ws = dict(x=R * D * F32, h=R * D * F16, qkv=R * m["max_qkv"] * F32, q=R * m["max_qd"] * F16,
               k=R * m["max_kvd"] * F16, v=R * m["max_kvd"] * F16, attn=R * m["max_qd"] * F16, t=R * D * F32,
-              act=R * m["ff"] * F16, out=R * m["out_dims"] * F32, tokens=R * I32, positions=R * I32,
+              act=R * m["ff"] * F16, out=R * m["out_dims"] * F32, hn=R * D * F32, tokens=R * I32, positions=R * I32,
               vcol=R * I32)
     if m["any_precise"]:
         ws.update(h3=R * 3 * D * F16, q_lo=R * m["max_qd"] * F16, k_lo=R * m["max_kvd"] * F16)
@@ -144,7 +144,7 @@ def workspace(m, b):
         ws.update(ple=R * m["layers"] * m["pl"] * F32, ple_t=R * max(m["pl"], D) * F32, rs=R * F32, rs2=R * F32,
                   x16=R * D * F16, g16=R * m["pl"] * F16)
     seq_cap = max(len(b["seqs"]), 1)
-    ws.update(seqs=seq_cap * SEQ_BYTES, pooled=seq_cap * m["out_dims"] * F32,
+    ws.update(seqs=seq_cap * SEQ_BYTES, pooled=seq_cap * m["out_dims"] * F32, pooled_n=seq_cap * D * F32,
               work=max(len(b["work"]), 1) * WORK_BYTES)
     if m["any_v2"]:
         ws["work2"] = max(len(b["work2"]), 1) * WORK_BYTES
@@ -191,7 +191,7 @@ def at(ptr, nbytes):
 
 def row_kernel(a, kernel, T, spans):
     """The one-wave-per-row kernels (embed_norm_kernel elementwise.hip:15, residual_norm_kernel :105,
-    norm_split_kernel :193, the ple_*_kernel family ple.hip:30-218): row < T; loads of chunk
+    norm_split_kernel :198, the ple_*_kernel family ple.hip:30-218): row < T; loads of chunk
     min(e, width - 4) and stores of element e = c * 256 + 4 lane + j < width. spans: (pointer, bytes
     per row of the access)."""
     for ptr, row_bytes in spans:
@@ -212,7 +212,7 @@ def norm_split(a, T, D, x, h3):
 
 
 def qk_norm_rope(a, T, H, KV, HD, qkv, positions, q, k, v, q_lo=None, k_lo=None, pos=None, table_rows=8192):
-    """qk_norm_rope_kernel (elementwise.hip:256): item = (t, slot) < T (H + 2 KV); reads
+    """qk_norm_rope_kernel (elementwise.hip:261): item = (t, slot) < T (H + 2 KV); reads
     qkv[t][slot][0, HD), the RoPE row positions[t]; writes q / k / v (and the low halves)."""
     S = H + 2 * KV
     a.span("qk_norm_rope", qkv, 0, T * S * HD * F32)
@@ -234,7 +234,7 @@ def vt_rows(a, kernel, vt, rows, vt_cols, vcol_used):
 
 
 def qkv_norm_rope_vt(a, T, H, KV, HD, qkv16, positions, q, k, v, vcol, vt_cols, vt, vc):
-    """qkv_norm_rope_vt_kernel (elementwise.hip:346): token t = 64 blockIdx + 4 wave + i < T; V^T rows
+    """qkv_norm_rope_vt_kernel (elementwise.hip:351): token t = 64 blockIdx + 4 wave + i < T; V^T rows
     r < KV HD at column vcol[t] for t < T."""
     S = H + 2 * KV
     a.span("qkv_norm_rope_vt", qkv16, 0, T * S * HD * F16)
@@ -334,8 +334,15 @@ def attention_legacy(a, work, H, KV, HD, hw, q, k, v, o, rows_alloc_k):
         a.span("attention", p, (s + kstart) * kS * F16, last_key * kS * F16)
 
 
+def pooled_projection(a, n_rows, width, n_out, x, out):
+    """pooled_projection_kernel (elementwise.hip:569): rows r < n_rows of x [*][width] (16-byte loads
+    of columns clamped to width - 4), out[r][n] for n < n_out. The weight planes are the model's."""
+    a.span("pooled_projection", x, 0, n_rows * width * F32)
+    a.span("pooled_projection", out, 0, n_rows * n_out * F32)
+
+
 def mean_pool(a, seqs, width, x, seq_ptr, pooled):
-    """mean_pool_kernel (elementwise.hip:491): rows start .. start + len - 1 of each sequence, 16-byte
+    """mean_pool_kernel (elementwise.hip:501): rows start .. start + len - 1 of each sequence, 16-byte
     loads of columns c .. c + 3 < width."""
     a.span("mean_pool", seq_ptr, 0, len(seqs) * SEQ_BYTES)
     a.span("mean_pool", pooled, 0, len(seqs) * width * F32)
@@ -347,7 +354,7 @@ def mean_pool(a, seqs, width, x, seq_ptr, pooled):
 # ---------------------------------------------------------------- the forward
 
 def stage_copies(a, b):
-    """The staged arrays stage() (runtime.cpp:830) copies into the workspace."""
+    """The staged arrays stage() (runtime.cpp:837) copies into the workspace."""
     n = b["n"]
     a.span("stage", ("tokens", 0), 0, n * I32)
     a.span("stage", ("positions", 0), 0, n * I32)
@@ -393,6 +400,7 @@ def replay(m, b, positions=None):
             row_kernel(a, "ple_norm", T * m["layers"], [(rows("ple", r0, LP, F32), m["pl"] * F32)])
             a.span("ple_norm", rows("rs", r0, 1, F32), 0, T * F32)
         for li, L in enumerate(m["layer"]):
+            last = li + 1 == m["layers"]
             hd, KV, qd, kvd = L["hd"], L["kv"], L["qd"], L["kvd"]
             N = qd + 2 * kvd
             hw = m["window"] // 2 if L["sliding"] else 0
@@ -452,12 +460,15 @@ def replay(m, b, positions=None):
                     a.span("ple_gate", rows("ple", r0, LP, F32), li * m["pl"] * F32,
                            ((T - 1) * m["layers"] + li + 1) * m["pl"] * F32)
                 gemm(a, "gemm_ple_proj", T, D, m["pl"], rows("g16", r0, m["pl"], F16), rows("t", r0, D, F32), "f32")
+                # the last layer's norm writes fp32 rows into hn (the final norm), the others fp16 h
+                hout = (rows("hn", r0, D, F32), D * F32) if last else (rows("h", r0, D, F16), D * F16)
                 row_kernel(a, "ple_residual_norm", T, [(rows("x", r0, D, F32), D * F32), (rows("t", r0, D, F32), D * F32),
-                                                       (rows("rs2", r0, 1, F32), F32), (rows("h", r0, D, F16), D * F16)])
+                                                       (rows("rs2", r0, 1, F32), F32), hout])
             else:
-                residual_norm(a, T, D, rows("x", r0, D, F32), t16, rows("h", r0, D, F16))
-        gemm(a, "gemm_output", T, m["out_dims"], D, rows("h", r0, D, F16), rows("out", r0, m["out_dims"], F32), "f32")
-    mean_pool(a, b["seqs"], m["out_dims"], ("out", 0), ("seqs", 0), ("pooled", 0))
+                row_kernel(a, "residual_norm", T, [(rows("x", r0, D, F32), D * F32), (t16, D * F16),
+                                                   (rows("hn", r0, D, F32), D * F32) if last else (rows("h", r0, D, F16), D * F16)])
+    mean_pool(a, b["seqs"], D, ("hn", 0), ("seqs", 0), ("pooled_n", 0))
+    pooled_projection(a, len(b["seqs"]), D, m["out_dims"], ("pooled_n", 0), ("pooled", 0))
     return a
 
 
@@ -469,7 +480,7 @@ def check_parts_disjoint(m, b):
         return errs
     widths = dict(x=m["hidden"] * F32, h=m["hidden"] * F16, q=m["max_qd"] * F16, k=m["max_kvd"] * F16,
                   attn=m["max_qd"] * F16, t=m["hidden"] * F32, act=m["ff"] * F16, out=m["out_dims"] * F32,
-                  qkv=m["max_qkv"] * F32)
+                  qkv=m["max_qkv"] * F32, hn=m["hidden"] * F32)
     for name, wb in widths.items():
         spans = [(b["part_row"][p] * wb, b["part_row"][p + 1] * wb) for p in range(b["n_parts"])]
         for i in range(1, len(spans)):
