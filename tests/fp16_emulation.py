@@ -7,6 +7,8 @@ The GPU path rounds to fp16, each time to the nearest representable value (relat
   - the projections that feed a norm (QKV, attention output, FFN down), stored as fp16 times a
     power of two;
   - q, k and v after their norms and RoPE; the softmax weights P before the P.V product.
+The final norm's rows stay fp32: their mean per sequence goes through the output projection in
+fp32 on the exact Q8_0 weights (projecting the mean equals the mean of the projections).
 Sums are fp32 on the GPU and float64 here. Powers of two do not change a relative rounding, so
 each rounded tensor is scaled into fp16's normal range here before rounding, as the kernels' range
 scales do. Comparing this with the float64 forward (no rounding) shows how far the design itself
@@ -94,5 +96,5 @@ def forward(g, tokens, rounded: bool, keep=()):
         out[("ffn_out", l)] = down
         x = x + rmsnorm(down, g.tensor(b + "post_ffw_norm.weight"), eps)
         out[("l_out", l)] = x
-    y = r(rmsnorm(x, g.tensor("output_norm.weight"), eps)) @ W("output.weight").T
-    return y.mean(axis=0), {k: v for k, v in out.items() if k in keep}
+    pooled = rmsnorm(x, g.tensor("output_norm.weight"), eps).mean(axis=0) @ g.tensor("output.weight").T
+    return pooled, {k: v for k, v in out.items() if k in keep}
