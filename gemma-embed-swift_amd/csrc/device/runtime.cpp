@@ -482,7 +482,7 @@ void upload(ge_ctx* c, const ge_model_desc* d, const void* base, size_t len) {
     {
         HostQ8 h = host_q8(m.out_dims, D);
         repack_rows(q8_tensor(d, "output.weight", D, m.out_dims, base, len), m.out_dims, D, &h, 0);
-        m.output = upload_q8(c, h, "output");
+        m.output = upload_q8(c, h, "output", false);  // projected from its Q8_0 planes (pooled_projection_kernel)
     }
     m.out_norm = upload_f32(c, d, "output_norm.weight", D, base, len);
     if (m.pl > 0) {
