@@ -105,7 +105,7 @@ int ge_forward(ge_ctx* ctx, const int32_t* tokens, const int32_t* positions, int
  * hipMalloc). Same arguments, results bitwise those of ge_forward. The forward's workspace
  * (activations, staged ids and work lists, V^T, pooled output) lives in a 64 MiB device array of
  * the library, one per GPU, held until the process ends; its address is taken at ge_create. A pack
- * whose workspace does not fit (above about 2700 tokens for config 2's model, 380 for the
+ * whose workspace does not fit (above about 2300 tokens for config 2's model, 380 for the
  * reference's architecture with its per-layer inputs) or of 4096 tokens or
  * more is refused with GE_ERR_INVALID, as is a call while profiling is enabled. Calls on one GPU
  * share the array: calls that overlap (two contexts of one GPU used from two threads) race. The
