@@ -251,6 +251,24 @@ def test_attention_item_size_does_not_change_results(c2_model, config2_batch):
     assert np.array_equal(full[20:24], quarter)
 
 
+def test_pooled_vector_is_the_mean_of_the_token_projections(c2_model, config2_batch):
+    """The forward pools the final norm's fp32 rows and projects each sequence's mean once; the
+    reference projects every token and averages (CPUReference.swift:274-282). Both are linear, so
+    the pooled vector equals the mean of the traced per-token projections (result_embd) up to fp32
+    rounding, for texts alone and in a pack, on the skinny (short) and the tiled path."""
+    ctx = c2_model.context
+    for texts in ([config2_batch[3][:9], config2_batch[7][:50], config2_batch[2][:20]], config2_batch[:2]):
+        pooled, _ = ctx.forward(texts)
+        per_token = ctx.trace(texts, "result_embd", -1)
+        off = 0
+        for i, t in enumerate(texts):
+            mean = per_token[off:off + len(t)].astype(np.float64).mean(axis=0)
+            off += len(t)
+            err = np.abs(pooled[i] - mean).max() / np.abs(mean).max()
+            print(f"text {i} ({len(t)} tokens): pooled vs mean of projections {err:.2e}", flush=True)
+            assert err < 1e-5, i
+
+
 def test_packing_invariance_and_determinism(c2_model, config2_batch):
     batch = config2_batch[:8]
     a = c2_model.embed_tokens(batch)
