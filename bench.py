@@ -185,8 +185,8 @@ def image_embed_variant(tmp: str, text_path: str, reps: int):
 
 def reference_shapes_variant(tmp: str, reps: int):
     """The reference's own architecture at its real shapes (d 512, per-layer inputs; synthetic
-    weights) on the shapes of its published benchmarks (Apple M3 Max with the real
-    model, first run's medians: an 8 x 1024-token pack in 0.4078 s, 32 x 64 in 0.0604 s, 8 x 256
+    weights) on the shapes of its published benchmarks (benchmarks/hillclimb-2026-10-27.json, Apple M3
+    Max with the real model, first run's medians: an 8 x 1024-token pack in 0.4078 s, 32 x 64 in 0.0604 s, 8 x 256
     in 0.0686 s, a 1 x 64-token call in 6.18 ms, 12 queries of 171 tokens in all as 12 separate
     calls in 52.2 ms), through the host API: token ids in host memory -> normalised vectors, the
     reference's own boundary (COMPARISON.md:57-60)."""
