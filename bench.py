@@ -433,15 +433,27 @@ def config3_variant(model_path: str, reps: int, with_cpu: bool):
         gpu_s = sorted(gpu_s)[len(gpu_s) // 2]
     finally:
         model.close()
+    # the same texts with split-precision scores on every layer (ge_load_options.split_scores)
+    split = ge.EmbeddingModel.load(model_path, split_scores=True)
+    try:
+        svecs = np.stack([e.vector for e in split.embed(texts, opts)])
+        sctx = split.context
+        split_s = sorted(sum(sctx.forward(texts[r.start:r.stop])[1] for r in ranges) for _ in range(reps))
+        split_s = split_s[len(split_s) // 2]
+    finally:
+        split.close()
     res = {"workload": "config3: 256 texts, lengths U[8, 256], planned by token count (budget 8192), "
                        "Matryoshka 256 + L2", "tokens": tokens, "planned_batches": len(ranges),
            "host_api_pcie_inclusive_tokens_per_s": round(tokens / api_s, 1),
-           "gpu_forward_tokens_per_s": round(tokens / gpu_s, 1), "gpu_forward_ms": round(gpu_s * 1e3, 3)}
+           "gpu_forward_tokens_per_s": round(tokens / gpu_s, 1), "gpu_forward_ms": round(gpu_s * 1e3, 3),
+           "split_scores": {"gpu_forward_tokens_per_s": round(tokens / split_s, 1),
+                            "gpu_forward_ms": round(split_s * 1e3, 3)}}
     if with_cpu:
         oracle_vecs, done, secs, threads = oracle_sample(model_path, texts, 6.0, "config 3")
         res["cpu_oracle"] = {"tokens_per_s": round(done / secs, 1), "cores": threads, "kind": "port",
                              "sample": f"{len(oracle_vecs)} of the 256 texts ({done} tokens), {secs:.2f} s"}
         res["parity"] = parity(vecs, oracle_vecs, dims=256)
+        res["split_scores"]["parity"] = parity(svecs, oracle_vecs, dims=256)
     return res
 
 

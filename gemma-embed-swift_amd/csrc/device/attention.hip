@@ -848,7 +848,8 @@ hipError_t launch_attention_v2(hipStream_t s, const uint16_t* q, const uint16_t*
 // and its 16 x 512 output accumulators take 256 registers, so a SIMD runs one wave. LDS holds
 // K_hi and K_lo of a 32-key block in two stages (block it + 1 copies while block it is used)
 // and V^T of one block in one buffer, refilled after the P.V product while the next block's
-// scores are computed: 2 x 64 KB + 32 KB at head dim 512.
+// scores are computed: 2 x 64 KB + 32 KB at head dim 512, 2 x 32 KB + 16 KB at head dim 256 (three
+// query heads per KV head there, for contexts that ask for split scores on every layer).
 namespace attns {
 constexpr int BKV = 32;  // keys per block
 }  // namespace attns
@@ -869,8 +870,11 @@ __global__ __launch_bounds__(G * 64) void attention_split_kernel(const uint16_t*
     constexpr int K_BYTES = BKV * HD * 2;  // one plane (K_hi or K_lo) of a block
     constexpr int KCH = K_BYTES / 1024;    // its chunks (ks, m)
     constexpr int KSTAGE = 2 * K_BYTES;    // K_hi, then K_lo
-    constexpr int KPW = 2 * KCH / G, VPW = DT / G;  // copies per wave per block: K planes, V^T
-    static_assert(KCH == 2 * KS && (2 * KCH) % G == 0 && DT % G == 0, "chunk counts");
+    // copies per wave per block (K planes, V^T), rounded up: where G does not divide the chunk
+    // count, a wave past the last chunk repeats its own previous chunk (same data, same wave), so
+    // every wave issues the same number of copies and the vmcnt waits below hold for each
+    constexpr int KPW = (2 * KCH + G - 1) / G, VPW = (DT + G - 1) / G;
+    static_assert(KCH == 2 * KS && 2 * KCH >= G && DT >= G, "chunk counts");
     static_assert(KPW + VPW < 64 && KS * 2 + KPW + VPW < 64, "outstanding copies fit the vmcnt counter");
     extern __shared__ __attribute__((aligned(1024))) unsigned char ldss[];
     unsigned char* const vbuf = ldss + 2 * KSTAGE;
@@ -913,7 +917,7 @@ __global__ __launch_bounds__(G * 64) void attention_split_kernel(const uint16_t*
 #define AS_KISSUE(kb, b)                                                                                   \
     do {                                                                                                   \
         _Pragma("unroll") for (int i = 0; i < KPW; i++) {                                                  \
-            const int c = wave + i * G, pl = c / KCH, cc = c % KCH;                                        \
+            const int c0 = wave + i * G, c = c0 < 2 * KCH ? c0 : c0 - G, pl = c / KCH, cc = c % KCH;       \
             lds_copy16(pl ? klr : kr, ldss + (b) * KSTAGE + pl * K_BYTES + cc * 1024,                      \
                        klane + uint32_t(((kb) + 4 * (cc & 1)) * kvStride * 2 + (cc >> 1) * 64), 0);        \
         }                                                                                                  \
@@ -921,7 +925,7 @@ __global__ __launch_bounds__(G * 64) void attention_split_kernel(const uint16_t*
 #define AS_VISSUE(kb)                                                                                      \
     do {                                                                                                   \
         _Pragma("unroll") for (int i = 0; i < VPW; i++) {                                                  \
-            const int c = wave + i * G;                                                                    \
+            const int c0 = wave + i * G, c = c0 < DT ? c0 : c0 - G;                                        \
             lds_copy16(vr, vbuf + c * 1024, vlane + uint32_t(c * 16 * vt_cols * 2 + (kb) * 2), 0);        \
         }                                                                                                  \
     } while (0)
@@ -1066,7 +1070,9 @@ __global__ __launch_bounds__(G * 64) void attention_split_kernel(const uint16_t*
     }
 }
 
-bool attention_split_supported(int hd, int H, int KV) { return hd == 512 && KV > 0 && H == 4 * KV; }
+bool attention_split_supported(int hd, int H, int KV) {
+    return KV > 0 && ((hd == 512 && H == 4 * KV) || (hd == 256 && H == 3 * KV));
+}
 
 hipError_t launch_attention_split(hipStream_t s, const uint16_t* q, const uint16_t* q_lo, const uint16_t* k,
                                   const uint16_t* k_lo, const uint16_t* vt, int vt_cols, uint16_t* o, const AttnWork* work,
@@ -1077,8 +1083,12 @@ hipError_t launch_attention_split(hipStream_t s, const uint16_t* q, const uint16
     if (n_work == 0) return hipSuccess;
     const float scale_log2 = scale * 1.4426950408889634f;
     const dim3 grid(n_work, KV, item_queries / 16);
-    launch_kernel(attention_split_kernel<512, 4>, grid, dim3(4 * 64), uint32_t(attention_split_lds_bytes<512>()), s, q, q_lo, k,
-                  k_lo, vt, o, work, H, KV, vt_cols, half_window, scale_log2);
+    if (hd == 512)
+        launch_kernel(attention_split_kernel<512, 4>, grid, dim3(4 * 64), uint32_t(attention_split_lds_bytes<512>()), s, q, q_lo,
+                      k, k_lo, vt, o, work, H, KV, vt_cols, half_window, scale_log2);
+    else
+        launch_kernel(attention_split_kernel<256, 3>, grid, dim3(3 * 64), uint32_t(attention_split_lds_bytes<256>()), s, q, q_lo,
+                      k, k_lo, vt, o, work, H, KV, vt_cols, half_window, scale_log2);
     return hipGetLastError();
 }
 
@@ -1386,6 +1396,9 @@ hipError_t configure_kernels() {
     if (e == hipSuccess)
         e = hipFuncSetAttribute(reinterpret_cast<const void*>(&attention_split_kernel<512, 4>),
                                 hipFuncAttributeMaxDynamicSharedMemorySize, attention_split_lds_bytes<512>());
+    if (e == hipSuccess)
+        e = hipFuncSetAttribute(reinterpret_cast<const void*>(&attention_split_kernel<256, 3>),
+                                hipFuncAttributeMaxDynamicSharedMemorySize, attention_split_lds_bytes<256>());
     if (e == hipSuccess) e = attention_configure_all<256, 256>();
     if (e == hipSuccess) e = attention_configure_all<512, 256>();
     return e;

@@ -511,7 +511,7 @@ void upload(ge_ctx* c, const ge_model_desc* d, const void* base, size_t len) {
             repack_rows(q8_tensor(d, b + "attn_q.weight", D, L.qd, base, len), L.qd, D, &h, 0);
             repack_rows(q8_tensor(d, b + "attn_k.weight", D, L.kvd, base, len), L.kvd, D, &h, L.qd);
             repack_rows(q8_tensor(d, b + "attn_v.weight", D, L.kvd, base, len), L.kvd, D, &h, L.qd + L.kvd);
-            L.precise = hd >= kPreciseHeadDim && attention_split_supported(hd, m.heads, L.kv_heads);
+            L.precise = hd >= c->split_head_dim && attention_split_supported(hd, m.heads, L.kv_heads);
             // a precise layer's GEMMs read only the split copy
             L.wqkv = upload_q8(c, h, "attn_qkv", !L.precise);
             if (L.precise) L.wqkv3 = upload_split_fragments(c, h, "attn_qkv split");
@@ -1517,6 +1517,13 @@ void ge_destroy(ge_ctx* c) {
 const char* ge_last_error(const ge_ctx* c) { return c ? c->err.c_str() : "null context"; }
 const char* ge_create_error(void) { return ge::g_create_error.c_str(); }
 const char* ge_device_name(const ge_ctx* c) { return c ? c->name.c_str() : ""; }
+
+int ge_set_split_scores(ge_ctx* c, int32_t min_head_dim) {
+    return guarded(c, [&] {
+        if (min_head_dim < 0) fail(GE_ERR_INVALID, "split-score head dim %d is negative", min_head_dim);
+        c->split_head_dim = min_head_dim;
+    });
+}
 
 int ge_upload_model(ge_ctx* c, const ge_model_desc* desc, const void* base, size_t len) {
     return guarded(c, [&] {

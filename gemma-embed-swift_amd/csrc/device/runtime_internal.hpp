@@ -146,6 +146,9 @@ struct ge_q8_matrix {
 
 struct ge_ctx {
     int device = 0;
+    // Layers of at least this head dim (and a query/KV grouping attention_split_kernel supports)
+    // run the split-precision QKV projection and scores; set before ge_upload_model.
+    int split_head_dim = ge::kPreciseHeadDim;
     hipStream_t stream = nullptr;
     // Part p > 0 of a split batch runs its layers on part_stream[p] (see stage()).
     hipStream_t part_stream[ge::kMaxParts] = {};

@@ -147,7 +147,8 @@ int ge_model_load(const char* path, const ge_load_options* options, ge_model** o
     m->device_name = ge_device_name(m->ctx);
     ge::UploadDesc u;
     ge::make_upload_desc(*m->file, m->cfg, &u);
-    rc = ge_upload_model(m->ctx, &u.desc, m->file->base(), m->file->size());
+    if (opt.split_scores) rc = ge_set_split_scores(m->ctx, 0);
+    if (rc == GE_OK) rc = ge_upload_model(m->ctx, &u.desc, m->file->base(), m->file->size());
     if (rc != GE_OK) return report(rc, ge_last_error(m->ctx));
     m->budget = opt.batch_token_budget > 0 ? std::max(64, opt.batch_token_budget) : 8192;
     if (opt.warm_up) {

@@ -53,7 +53,8 @@ class ge_attention_work(C.Structure):
 
 
 class ge_load_options(C.Structure):
-    _fields_ = [("device", C.c_int32), ("batch_token_budget", C.c_int32), ("warm_up", C.c_int32)]
+    _fields_ = [("device", C.c_int32), ("batch_token_budget", C.c_int32), ("warm_up", C.c_int32),
+                ("split_scores", C.c_int32)]
 
 
 class ge_embed_options(C.Structure):
@@ -115,6 +116,7 @@ SIGNATURES = {
     "ge_create_error": (C.c_char_p, []),
     "ge_device_name": (C.c_char_p, [_P]),
     "ge_upload_model": (_I, [_P, _P, _P, C.c_size_t]),
+    "ge_set_split_scores": (_I, [_P, C.c_int32]),
     "ge_forward": (_I, [_P, _PI32, _PI32, C.c_int32, C.POINTER(ge_seq), C.c_int32, _PF, C.POINTER(C.c_double)]),
     "ge_forward_trace": (_I, [_P, _PI32, _PI32, C.c_int32, C.POINTER(ge_seq), C.c_int32, C.c_char_p, C.c_int32,
                               _PF, C.c_size_t, C.POINTER(C.c_size_t)]),
@@ -733,8 +735,11 @@ class EmbeddingModel:
         self.context = Context(lib.ge_model_context(self._h), owned=False, out_dims=info.out_dims)
 
     @classmethod
-    def load(cls, path: str, device: int = 0, batch_token_budget: int = 8192, warm_up: bool = True):
-        opt = ge_load_options(device, batch_token_budget, int(warm_up))
+    def load(cls, path: str, device: int = 0, batch_token_budget: int = 8192, warm_up: bool = True,
+             split_scores: bool = False):
+        """split_scores: hi/lo fp16 q and k (near-fp32 scores) on every layer whose query grouping
+        allows it, not only the head-dim-512 ones (ge_set_split_scores)."""
+        opt = ge_load_options(device, batch_token_budget, int(warm_up), int(split_scores))
         h = C.c_void_p()
         err = C.create_string_buffer(1024)
         rc = lib.ge_model_load(path.encode(), C.byref(opt), C.byref(h), err, 1024)

@@ -85,6 +85,15 @@ typedef struct ge_model_desc {
  * fp16 scale planes. The caller may unmap the file afterwards. */
 int ge_upload_model(ge_ctx* ctx, const ge_model_desc* desc, const void* file_base, size_t len);
 
+/* Precision of the attention scores, read by the next ge_upload_model: layers whose head dim is at
+ * least `min_head_dim` run the QKV projection on hi/lo fp16 operand pairs and score
+ * q_hi.k_hi + q_lo.k_hi + q_hi.k_lo (near-fp32 scores, as the reference's fp32 attention,
+ * Shaders/Attention.metal:172-188), where the query grouping allows it (head dim 512 with 4 query
+ * heads per KV head, 256 with 3). Default 512: the reference's global layers. 0 asks for every
+ * such layer, at about twice the QKV and score work there. No counterpart in the reference, whose
+ * GPU path is fp32 throughout; for callers that need its 1e-4 agreement on short texts. */
+int ge_set_split_scores(ge_ctx* ctx, int32_t min_head_dim);
+
 /* SequenceRange (Shaders/Common.metal:86-89): one packed sequence. */
 typedef struct ge_seq {
     uint32_t start;
@@ -314,6 +323,8 @@ typedef struct ge_load_options {
     int32_t device;              /* HIP device ordinal */
     int32_t batch_token_budget;  /* default 8192; at least 64 (EmbeddingModel.swift:110) */
     int32_t warm_up;             /* run one small forward at load (EmbeddingModel.swift:111-114) */
+    int32_t split_scores;        /* nonzero: split-precision scores on every layer that allows them
+                                    (ge_set_split_scores(ctx, 0)); no counterpart in LoadOptions */
 } ge_load_options;
 
 /* EmbedOptions (EmbedOptions.swift:35-56), minus the task prefix: prefixes and tokenization

@@ -54,7 +54,10 @@ def model_of(spec):
         KV = spec["kv_heads_swa"] if sliding else spec["kv_heads_global"]
         sl = H + 2 * KV
         L = dict(sliding=sliding, hd=hd, kv=KV, qd=H * hd, kvd=KV * hd)
-        L["precise"] = hd == 512 and H == 4 * KV  # hd >= kPreciseHeadDim and attention_split_supported
+        # hd >= ge_ctx::split_head_dim (512, or 0 after ge_set_split_scores(ctx, 0)) and
+        # attention_split_supported (attention.hip:1073)
+        split_ok = (hd == 512 and H == 4 * KV) or (hd == 256 and H == 3 * KV)
+        L["precise"] = split_ok and hd >= (0 if spec.get("split_scores") else 512)
         L["attn_v2"] = v2_supported(hd, H, KV)
         L["qkv_gn"] = hd in (128, 256) and sl in (3, 4, 5, 6, 8, 10) and KV * hd * 66 * 2 <= 64 * 1024
         L["qkv_fused"] = hd in (128, 256)

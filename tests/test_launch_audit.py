@@ -10,7 +10,9 @@ import gemma_embed as ge
 import launch_audit as la
 
 MODELS = {"tiny": ge.TINY, "tiny_ple": ge.TINY_PLE, "config2": ge.CONFIG2, "outlier_norms": ge.OUTLIER_NORMS,
-          "real_shapes": ge.REAL_SHAPES}
+          "real_shapes": ge.REAL_SHAPES,
+          # config 2 loaded with split-precision scores on every layer (ge_load_options.split_scores)
+          "config2_split_scores": dict(ge.CONFIG2, split_scores=True)}
 
 SHORT = [[1], [2], [40, 9], [63], [64], [65], [1] * 64, [5, 0, 7], [300], [1, 65], [100, 33, 7, 1]]
 LONG = [[1024] * 8, [512] * 32, [8192], [8192, 8192], [4096, 1], [1, 4096], [2048] * 8, [3000, 5000, 192],
@@ -27,7 +29,7 @@ def config3_batches():
 def cases():
     out = []
     for name in MODELS:
-        packs = SHORT + (LONG + config3_batches() if name in ("config2", "real_shapes") else [[1024] * 8, [8192]])
+        packs = SHORT + (LONG + config3_batches() if name in ("config2", "real_shapes", "config2_split_scores") else [[1024] * 8, [8192]])
         out += [(name, p) for p in packs]
     return out
 
