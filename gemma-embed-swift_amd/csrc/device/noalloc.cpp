@@ -1,6 +1,8 @@
 // The forward of one packed batch with every device buffer in a file-scope device array, for
-// callers that cannot allocate device memory (code under HIP graph capture, tight serving loops,
-// harnesses that forbid hipMalloc). No counterpart in the reference.
+// callers that cannot allocate device memory (tight serving loops, harnesses that forbid
+// hipMalloc). No counterpart in the reference. The call is synchronous like ge_forward: it clears
+// its region with hipMemsetAsync, waits for its stream and reads the pooled vectors back with a
+// blocking copy, so it is not meant to be captured into a HIP graph.
 //
 // The workspace the forward's kernels read and write (activations, the staged token ids,
 // positions, sequence ranges and attention work lists, transposed V, the pooled output) is carved
@@ -58,7 +60,7 @@ Workspace carve(const DevModel& m, const BatchPlan& b, int n, int n_seqs, Carver
     w.attn = cv.take<uint16_t>(R * m.max_qd);
     w.t = cv.take<float>(R * m.hidden);
     w.act = cv.take<uint16_t>(R * m.ff);
-    w.out = cv.take<float>(R * m.out_dims);
+    w.out = nullptr;  // only a trace of the per-token projection (result_embd) writes it; this forward never traces
     w.hn = cv.take<float>(R * m.hidden);
     w.tokens = cv.take<int32_t>(R);
     w.positions = cv.take<int32_t>(R);
@@ -80,8 +82,9 @@ Workspace carve(const DevModel& m, const BatchPlan& b, int n, int n_seqs, Carver
     w.seqs = cv.take<SeqRange>(size_t(n_seqs));
     w.pooled = cv.take<float>(size_t(n_seqs) * m.out_dims);
     w.pooled_n = cv.take<float>(size_t(n_seqs) * m.hidden);
-    w.work_cap = std::max(int(b.work.size()), 1);
-    w.work = cv.take<AttnWork>(size_t(w.work_cap));
+    // the producer-wave attention's work list, read only by layers off the LDS-copy attention
+    w.work_cap = m.all_v2 ? 0 : std::max(int(b.work.size()), 1);
+    w.work = m.all_v2 ? nullptr : cv.take<AttnWork>(size_t(w.work_cap));
     if (m.any_v2) {
         w.work2_cap = std::max(int(b.work2.size()), 1);
         w.work2 = cv.take<AttnWork>(size_t(w.work2_cap));
@@ -96,8 +99,9 @@ void forward_noalloc(ge_ctx* c, const int32_t* tokens, const int32_t* positions,
     if (!pooled) fail(GE_ERR_INVALID, "null output");
     if (!c->scratch) fail(GE_ERR_STATE, "the no-allocation scratch of device %d is not set up", c->device);
     if (c->prof) fail(GE_ERR_STATE, "the no-allocation forward does not run while profiling is enabled");
+    if (n >= kSplitMinTokens) fail(GE_ERR_INVALID, "the no-allocation forward takes packs below %d tokens", kSplitMinTokens);
     const BatchPlan b = plan_batch(c, tokens, positions, n, seqs, n_seqs, own_vectors(c), own_vector_rows(c));
-    if (b.n_parts != 1) fail(GE_ERR_INVALID, "the no-allocation forward takes packs below %d tokens", kSplitMinTokens);
+    if (b.n_parts != 1) fail(GE_ERR_STATE, "a pack below %d tokens was split into parts", kSplitMinTokens);
     Carver count{nullptr};
     carve(c->model, b, n, n_seqs, count);
     if (count.used > kScratchBytes)
@@ -112,7 +116,8 @@ void forward_noalloc(ge_ctx* c, const int32_t* tokens, const int32_t* positions,
     hip_check(hipMemcpyAsync(w.tokens, tokens, size_t(n) * 4, hipMemcpyHostToDevice, s), "upload tokens");
     hip_check(hipMemcpyAsync(w.positions, positions, size_t(n) * 4, hipMemcpyHostToDevice, s), "upload positions");
     hip_check(hipMemcpyAsync(w.seqs, b.sr.data(), b.sr.size() * sizeof(SeqRange), hipMemcpyHostToDevice, s), "upload");
-    hip_check(hipMemcpyAsync(w.work, b.work.data(), b.work.size() * sizeof(AttnWork), hipMemcpyHostToDevice, s), "upload");
+    if (w.work)
+        hip_check(hipMemcpyAsync(w.work, b.work.data(), b.work.size() * sizeof(AttnWork), hipMemcpyHostToDevice, s), "upload");
     if (!b.work2.empty()) {
         hip_check(hipMemcpyAsync(w.work2, b.work2.data(), b.work2.size() * sizeof(AttnWork), hipMemcpyHostToDevice, s),
                   "upload");

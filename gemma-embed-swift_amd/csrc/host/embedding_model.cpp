@@ -19,6 +19,7 @@ struct ge_model {
     ge::ModelConfig cfg;
     ge_ctx* ctx = nullptr;
     int budget = 8192;
+    int64_t pack_tokens = 8192;  // largest device pack: the budget unless the load options raise it
     std::string err;
     std::string device_name;
     ~ge_model() {
@@ -67,9 +68,6 @@ void finish(const float* v, int dims, bool normalise, float* out) {
             for (int i = 0; i < dims; i++) out[i] /= norm;
     }
 }
-
-// Largest device pack that consecutive planned batches are merged into (tokens).
-constexpr int64_t kRunTokens = 32768;
 
 int model_fail(ge_model* m, int code, const std::string& msg) {
     m->err = msg;
@@ -133,14 +131,18 @@ int ge_model_load(const char* path, const ge_load_options* options, ge_model** o
     };
     if (!path || !out) return report(GE_ERR_INVALID, "null argument");
     *out = nullptr;
-    ge_load_options opt{0, 8192, 1};
+    ge_load_options opt{0, 8192, 1, 0, 0};
     if (options) opt = *options;
+    if (opt.pack_tokens < 0) return report(GE_ERR_OPTIONS, "invalid options: pack_tokens must not be negative");
     std::unique_ptr<ge_model> m(new ge_model);
     try {
         m->file.reset(new ge::GGUFFile(path));
         m->cfg = ge::read_config(*m->file);
     } catch (const ge::Error& e) {
         return report(e.code, e.what());
+    } catch (const std::exception& e) {
+        // no C++ exception crosses the C boundary (a corrupt file must not terminate the caller)
+        return report(GE_ERR_GGUF, std::string("invalid GGUF file: ") + e.what());
     }
     int rc = ge_create(opt.device, &m->ctx);
     if (rc != GE_OK) return report(rc, ge_create_error());
@@ -151,6 +153,7 @@ int ge_model_load(const char* path, const ge_load_options* options, ge_model** o
     if (rc == GE_OK) rc = ge_upload_model(m->ctx, &u.desc, m->file->base(), m->file->size());
     if (rc != GE_OK) return report(rc, ge_last_error(m->ctx));
     m->budget = opt.batch_token_budget > 0 ? std::max(64, opt.batch_token_budget) : 8192;
+    m->pack_tokens = std::max<int64_t>(m->budget, opt.pack_tokens);
     if (opt.warm_up) {
         // EmbeddingModel.swift:111-114: one small forward before the first request.
         std::vector<std::vector<int32_t>> warm{{m->cfg.bos_id, 2 < m->cfg.vocab ? 2 : 0, m->cfg.eos_id}};
@@ -191,6 +194,9 @@ int ge_gguf_open(const char* path, ge_gguf** out, char* err, size_t errlen) {
     } catch (const ge::Error& e) {
         if (err && errlen) std::snprintf(err, errlen, "%s", e.what());
         return e.code;
+    } catch (const std::exception& e) {
+        if (err && errlen) std::snprintf(err, errlen, "invalid GGUF file: %s", e.what());
+        return GE_ERR_GGUF;
     }
 }
 
@@ -227,6 +233,9 @@ int ge_gguf_text_config(const ge_gguf* g, ge_model_info* info, char* err, size_t
     } catch (const ge::Error& e) {
         if (err && errlen) std::snprintf(err, errlen, "%s", e.what());
         return e.code;
+    } catch (const std::exception& e) {
+        if (err && errlen) std::snprintf(err, errlen, "invalid GGUF file: %s", e.what());
+        return GE_ERR_GGUF;
     }
 }
 
@@ -290,15 +299,16 @@ int ge_model_embed(ge_model* m, const int32_t* tokens, const int32_t* lengths, i
         for (int i = starts[r]; i < starts[r + 1]; i++) t += costs[size_t(i)];
         return t;
     };
-    // Consecutive planned batches run on the device as one pack of up to kRunTokens tokens. A
-    // text's vector does not depend on the pack around it (every kernel gives the same bits for
-    // its rows whatever the pack), so only the time changes: an 8192-token pack (the default
-    // budget) uses the GPU less well than a larger one. Progress and cancellation still follow
-    // the planned batches.
+    // By default each planned batch is one forward (EmbeddingModel.swift:157-172), so the budget
+    // bounds every pack and a cancel returned after a batch stops before the next batch's GPU
+    // work. With pack_tokens above the budget, consecutive planned batches run as one device pack
+    // of up to pack_tokens tokens. A text's vector does not depend on the pack around it (every
+    // kernel gives the same bits for its rows whatever the pack), so only the time changes;
+    // progress still follows the planned batches, and a cancel takes effect at the next pack.
     for (size_t r = 0; r + 1 < starts.size();) {
         size_t r_end = r + 1;
         int64_t tok = batch_tokens(r);
-        while (r_end + 1 < starts.size() && tok + batch_tokens(r_end) <= ge::kRunTokens) tok += batch_tokens(r_end++);
+        while (r_end + 1 < starts.size() && tok + batch_tokens(r_end) <= m->pack_tokens) tok += batch_tokens(r_end++);
         std::vector<std::vector<int32_t>> pack(prepared.begin() + starts[r], prepared.begin() + starts[r_end]);
         int rc = ge::run_batch(m, pack, &pooled);
         if (rc != GE_OK) return rc;

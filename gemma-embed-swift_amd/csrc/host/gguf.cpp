@@ -47,8 +47,14 @@ struct Cursor {
     size_t pos = 0;
 
     void need(size_t k) {
-        if (pos + k > n || pos + k < pos)
+        if (k > n - pos)
             throw Error(GE_ERR_GGUF, "invalid GGUF file: truncated header at byte " + std::to_string(pos));
+    }
+    // `count` elements of `es` bytes each, checked without forming count * es (which can wrap).
+    void need_elements(uint64_t count, size_t es) {
+        if (es == 0 || count > (n - pos) / es)
+            throw Error(GE_ERR_GGUF, "invalid GGUF file: array of " + std::to_string(count) +
+                                         " elements past the end of the header at byte " + std::to_string(pos));
     }
     template <typename T>
     T read() {
@@ -114,12 +120,11 @@ GGUFValue read_value(Cursor& c, int type) {
         if (v.arr_type == 8) {
             for (uint64_t i = 0; i < count; i++) c.skip_str();
         } else if (v.arr_type == 6 || v.arr_type == 12) {
-            size_t es = scalar_size(v.arr_type);
-            c.need(count * es);
+            c.need_elements(count, scalar_size(v.arr_type));
             v.floats.reserve(count);
             for (uint64_t i = 0; i < count; i++) v.floats.push_back(v.arr_type == 6 ? c.read<float>() : c.read<double>());
         } else if (scalar_size(v.arr_type) > 0) {
-            c.need(count * scalar_size(v.arr_type));
+            c.need_elements(count, scalar_size(v.arr_type));
             v.ints.reserve(count);
             for (uint64_t i = 0; i < count; i++) v.ints.push_back(read_int(c, v.arr_type));
         } else {
@@ -177,6 +182,15 @@ GGUFFile::GGUFFile(const std::string& path) {
             t.type = int(c.read<uint32_t>());
             if (type_block_bytes(t.type) == 0)
                 throw Error(GE_ERR_MODEL, "tensor " + t.name + " uses unsupported storage type " + std::to_string(t.type));
+            // Every dimension positive and the element count representable, so that elements(),
+            // rows() and bytes() below cannot wrap; a Q8_0 row is whole blocks.
+            int64_t elems = 1;
+            for (int64_t d : t.shape) {
+                if (d <= 0 || __builtin_mul_overflow(elems, d, &elems) || elems > (int64_t(1) << 56))
+                    throw Error(GE_ERR_GGUF, "invalid GGUF file: tensor " + t.name + " has an invalid shape");
+            }
+            if (t.columns() % int64_t(type_block_size(t.type)) != 0)
+                throw Error(GE_ERR_GGUF, "invalid GGUF file: tensor " + t.name + " has rows of partial blocks");
             t.offset = c.read<uint64_t>();
             index_[t.name] = tensors_.size();
             tensors_.push_back(std::move(t));
@@ -184,8 +198,10 @@ GGUFFile::GGUFFile(const std::string& path) {
         uint64_t alignment = 32;
         if (auto* a = meta("general.alignment"); a && a->is_int() && a->i > 0) alignment = uint64_t(a->i);
         data_offset_ = (c.pos + alignment - 1) / alignment * alignment;
+        if (data_offset_ > size_) throw Error(GE_ERR_GGUF, "invalid GGUF file: data section past the end of the file");
         for (const auto& t : tensors_) {
-            if (data_offset_ + t.offset + t.bytes() > size_)
+            const uint64_t room = size_ - data_offset_;
+            if (t.offset > room || t.bytes() > room - t.offset)
                 throw Error(GE_ERR_GGUF, "invalid GGUF file: tensor " + t.name + " extends past the end of the file");
         }
     } catch (...) {

@@ -54,7 +54,7 @@ class ge_attention_work(C.Structure):
 
 class ge_load_options(C.Structure):
     _fields_ = [("device", C.c_int32), ("batch_token_budget", C.c_int32), ("warm_up", C.c_int32),
-                ("split_scores", C.c_int32)]
+                ("split_scores", C.c_int32), ("pack_tokens", C.c_int32)]
 
 
 class ge_embed_options(C.Structure):
@@ -736,10 +736,11 @@ class EmbeddingModel:
 
     @classmethod
     def load(cls, path: str, device: int = 0, batch_token_budget: int = 8192, warm_up: bool = True,
-             split_scores: bool = False):
+             split_scores: bool = False, pack_tokens: int = 0):
         """split_scores: hi/lo fp16 q and k (near-fp32 scores) on every layer whose query grouping
-        allows it, not only the head-dim-512 ones (ge_set_split_scores)."""
-        opt = ge_load_options(device, batch_token_budget, int(warm_up), int(split_scores))
+        allows it, not only the head-dim-512 ones (ge_set_split_scores). pack_tokens: largest
+        device pack of embed(); 0 = the batch budget (one forward per planned batch)."""
+        opt = ge_load_options(device, batch_token_budget, int(warm_up), int(split_scores), int(pack_tokens))
         h = C.c_void_p()
         err = C.create_string_buffer(1024)
         rc = lib.ge_model_load(path.encode(), C.byref(opt), C.byref(h), err, 1024)

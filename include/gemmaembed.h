@@ -110,15 +110,17 @@ int ge_forward(ge_ctx* ctx, const int32_t* tokens, const int32_t* positions, int
                int32_t n_seqs, float* pooled_out, double* gpu_seconds);
 
 /* ge_forward with no device allocation: no counterpart in the reference; for callers that cannot
- * allocate device memory (code under HIP graph capture, tight serving loops, harnesses that forbid
- * hipMalloc). Same arguments, results bitwise those of ge_forward. The forward's workspace
- * (activations, staged ids and work lists, V^T, pooled output) lives in a 64 MiB device array of
- * the library, one per GPU, held until the process ends; its address is taken at ge_create. A pack
- * whose workspace does not fit (above about 2300 tokens for config 2's model, 380 for the
- * reference's architecture with its per-layer inputs) or of 4096 tokens or
- * more is refused with GE_ERR_INVALID, as is a call while profiling is enabled. Calls on one GPU
- * share the array: calls that overlap (two contexts of one GPU used from two threads) race. The
- * context's own staged batch and workspace are left as they were. */
+ * allocate device memory (tight serving loops, harnesses that forbid hipMalloc). Same arguments,
+ * results bitwise those of ge_forward. The forward's workspace (activations, staged ids and work
+ * lists, V^T, pooled output) lives in a 64 MiB device array of the library, one per GPU, held
+ * until the process ends; its address is taken at ge_create. Packs of 4096 tokens or more are
+ * refused with GE_ERR_INVALID, and so is a smaller pack whose workspace does not fit (above about
+ * 2650 tokens for config 2's model, 380 for the reference's architecture with its per-layer
+ * inputs), as is a call while profiling is enabled. Synchronous like ge_forward: it clears its
+ * region with hipMemsetAsync, waits for its stream and reads back with a blocking copy, so it is
+ * not for HIP graph capture. Calls on one GPU share the array: calls that overlap (two contexts of
+ * one GPU used from two threads) race. The context's own staged batch and workspace are left as
+ * they were. */
 int ge_forward_noalloc(ge_ctx* ctx, const int32_t* tokens, const int32_t* positions, int32_t n_tokens,
                        const ge_seq* seqs, int32_t n_seqs, float* pooled_out, double* gpu_seconds);
 
@@ -325,6 +327,12 @@ typedef struct ge_load_options {
     int32_t warm_up;             /* run one small forward at load (EmbeddingModel.swift:111-114) */
     int32_t split_scores;        /* nonzero: split-precision scores on every layer that allows them
                                     (ge_set_split_scores(ctx, 0)); no counterpart in LoadOptions */
+    int32_t pack_tokens;         /* largest device pack of ge_model_embed, in tokens. 0 (default) =
+                                    batch_token_budget: one forward per planned batch, as
+                                    EmbeddingModel.swift:157-172 runs them. Larger values run
+                                    consecutive planned batches as one forward of up to this many
+                                    tokens (same vectors, better GPU use); a cancel then takes
+                                    effect at the next forward. No counterpart in LoadOptions. */
 } ge_load_options;
 
 /* EmbedOptions (EmbedOptions.swift:35-56), minus the task prefix: prefixes and tokenization

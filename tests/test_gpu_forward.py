@@ -369,6 +369,45 @@ def test_embed_batching_progress_and_cancel(c2_model, config2_batch):
     assert err.value.kind == "cancelled"
 
 
+def _forwards_run(model, texts, options, progress):
+    """Runs embed with the context's kernel profile on and returns how many forwards it launched
+    (one embedding-gather launch per forward) and what the call raised, if anything."""
+    ctx = model.context
+    ctx.profile_enable("")
+    ctx.profile_reset()
+    raised = None
+    try:
+        model.embed(texts, options, progress=progress)
+    except ge.GemmaEmbedError as e:
+        raised = e
+    finally:
+        ctx.profile_disable()
+    stats = ctx.profile_stats()
+    return sum(n for name, (n, _) in stats.items() if name.startswith("embed_norm")), raised
+
+
+def test_embed_one_forward_per_planned_batch_and_cancel(config2_gguf, config2_batch):
+    """By default each planned batch is one forward, bounded by the batch budget
+    (EmbeddingModel.swift:157-172, EmbedOptions.swift:194), and a cancel returned after the first
+    batch stops before the second batch's GPU work (Task.checkCancellation, :162)."""
+    texts = [t[:300] for t in config2_batch[:12]]  # 3600 tokens: batches of 1000 at budget 1000
+    with ge.EmbeddingModel.load(config2_gguf, batch_token_budget=1000) as m:
+        n, raised = _forwards_run(m, texts, ge.EmbedOptions(), None)
+        assert raised is None and n == 4, n
+        calls = []
+        n, raised = _forwards_run(m, texts, ge.EmbedOptions(), lambda p: calls.append(p) or True)
+        assert raised is not None and raised.kind == "cancelled"
+        assert n == 1 and len(calls) == 1 and calls[0].completed_texts == 3, (n, calls)
+        ref = m.embed(texts)
+    # merged device packs (pack_tokens above the budget): same vectors, fewer forwards
+    with ge.EmbeddingModel.load(config2_gguf, batch_token_budget=1000, pack_tokens=8192) as m:
+        n, raised = _forwards_run(m, texts, ge.EmbedOptions(), None)
+        assert raised is None and n == 1, n
+        got = m.embed(texts)
+    for a, b in zip(ref, got):
+        assert np.array_equal(a.vector, b.vector)
+
+
 def test_config3_ragged_vs_oracle(c2_model, c2_oracle):
     """256 texts, lengths U[8, 256], packed by token count, Matryoshka 256."""
     lengths = ge.synth_tokens(5, 8, 257, 256)

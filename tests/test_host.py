@@ -177,3 +177,40 @@ def test_load_rejects_missing_metadata(tmp_path, tiny_gguf):
     with pytest.raises(ge.GemmaEmbedError) as e:
         ge.EmbeddingModel.load(str(p))
     assert e.value.kind == "model" and "feed_forward_length" in e.value.message
+
+
+def _gguf_header(kv: bytes, n_kv: int, tensors: bytes = b"", n_tensors: int = 0) -> bytes:
+    return b"GGUF" + struct.pack("<IQQ", 3, n_tensors, n_kv) + kv + tensors
+
+
+def _gguf_key(name: str) -> bytes:
+    return struct.pack("<Q", len(name)) + name.encode()
+
+
+@pytest.mark.parametrize("count", [2 ** 61, 2 ** 62, 2 ** 64 - 1])
+def test_load_rejects_array_count_past_the_file(tmp_path, count):
+    """A metadata array whose element count times its element size wraps 64 bits: rejected as an
+    invalid file, not an uncaught C++ exception that would abort the caller."""
+    kv = _gguf_key("general.junk") + struct.pack("<IIQ", 9, 4, count) + b"\0" * 16
+    p = tmp_path / "count.gguf"
+    p.write_bytes(_gguf_header(kv, 1).ljust(100, b"\0"))
+    with pytest.raises(ge.GemmaEmbedError) as e:
+        ge.EmbeddingModel.load(str(p))
+    assert e.value.kind == "invalidGGUF" and "past the end of the header" in e.value.message
+
+
+@pytest.mark.parametrize("shape,offset,msg", [
+    ((2 ** 32, 2 ** 32), 0, "invalid shape"),          # element count past 2^63
+    ((2 ** 63 - 1, 2), 0, "invalid shape"),
+    ((0, 4), 0, "invalid shape"),
+    ((33, 2), 0, "partial blocks"),                     # Q8_0 rows of whole 32-blocks only
+    ((32, 2), 2 ** 64 - 32, "extends past the end"),   # offset + bytes wraps 64 bits
+])
+def test_load_rejects_tensor_extents(tmp_path, shape, offset, msg):
+    t = _gguf_key("blk.0.x.weight") + struct.pack("<I", len(shape)) + b"".join(struct.pack("<Q", d) for d in shape)
+    t += struct.pack("<IQ", 8, offset)  # Q8_0
+    p = tmp_path / "extent.gguf"
+    p.write_bytes(_gguf_header(b"", 0, t, 1).ljust(256, b"\0"))
+    with pytest.raises(ge.GemmaEmbedError) as e:
+        ge.EmbeddingModel.load(str(p))
+    assert e.value.kind == "invalidGGUF" and msg in e.value.message, e.value.message

@@ -45,12 +45,17 @@ def test_no_alloc_forward_refuses_what_does_not_fit(config2_gguf):
     m = ge.EmbeddingModel.load(config2_gguf)
     try:
         ctx = m.context
-        too_big = [ge.synth_tokens(97, 2, 262144, 3000).tolist()]  # ~70 MB of workspace at d 768
+        too_big = [ge.synth_tokens(97, 2, 262144, 3000).tolist()]  # ~72 MB of workspace at d 768
         with pytest.raises(ge.GemmaEmbedError) as e:
             ctx.forward_noalloc(too_big)
         assert e.value.code == ge.GE_ERR_INVALID and "scratch" in e.value.message
-        ok, _ = ctx.forward_noalloc([too_big[0][:500]])
-        want, _ = ctx.forward([too_big[0][:500]])
-        assert np.array_equal(ok, want)
+        split_size = [too_big[0] + too_big[0][:1096]]  # 4096 tokens: refused whatever its workspace
+        with pytest.raises(ge.GemmaEmbedError) as e:
+            ctx.forward_noalloc(split_size)
+        assert e.value.code == ge.GE_ERR_INVALID and "below 4096" in e.value.message
+        for n in (2600, 500):  # near the array's limit at config 2's widths, then a small pack
+            ok, _ = ctx.forward_noalloc([too_big[0][:n]])
+            want, _ = ctx.forward([too_big[0][:n]])
+            assert np.array_equal(ok, want), n
     finally:
         m.close()
