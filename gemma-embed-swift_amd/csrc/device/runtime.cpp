@@ -1752,7 +1752,7 @@ void op_attention(ge_ctx* c, const void* q, const void* q_lo, const void* k, con
     if (n_work < 0 || (n_work > 0 && !work)) fail(GE_ERR_INVALID, "bad attention work list");
     const bool split = q_lo || k_lo;
     if (split && (!q_lo || !k_lo || !attention_split_supported(head_dim, heads, kv_heads)))
-        fail(GE_ERR_INVALID, "split-precision attention takes q_lo and k_lo, head dim 512 and 4 query heads per KV head");
+        fail(GE_ERR_INVALID, "split-precision attention takes q_lo and k_lo, and head dim 512 with 4 query heads per KV head or 256 with 3");
     if (n_work == 0) return;
     // The ABI's work items (ge_attention_work) come in; the kernels take ge::AttnWork.
     std::vector<ge_attention_work> items(static_cast<size_t>(n_work), ge_attention_work{});

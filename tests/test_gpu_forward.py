@@ -408,20 +408,53 @@ def test_embed_one_forward_per_planned_batch_and_cancel(config2_gguf, config2_ba
         assert np.array_equal(a.vector, b.vector)
 
 
-def test_config3_ragged_vs_oracle(c2_model, c2_oracle):
-    """256 texts, lengths U[8, 256], packed by token count, Matryoshka 256."""
-    lengths = ge.synth_tokens(5, 8, 257, 256)
-    ids = ge.synth_tokens(6, 2, 262144, int(lengths.sum()))
+def config3_texts():
+    """BASELINE config 3 as the bench draws it: 256 texts, lengths U[8, 256] (SplitMix64 seed 31),
+    ids U[2, 262144) (seed 32)."""
+    lengths = ge.synth_tokens(31, 8, 257, 256)
+    ids = ge.synth_tokens(32, 2, 262144, int(lengths.sum()))
     texts, off = [], 0
     for n in lengths:
         texts.append(ids[off:off + n].tolist())
         off += n
+    return texts
+
+
+@pytest.fixture(scope="module")
+def config3_default(c2_model, c2_oracle):
+    """Config 3 through embed at the default load (fp16 scores), Matryoshka 256, and the max |d|
+    of the normalised vectors against the oracle on the 32 shortest texts plus texts 0, 77, 255."""
+    texts = config3_texts()
     out = c2_model.embed(texts, ge.EmbedOptions(dimensions=256))
     assert len(out) == 256 and all(o.vector.shape == (256,) for o in out)
-    for i in (0, 77, 255):
+    pick = sorted(range(256), key=lambda i: len(texts[i]))[:32] + [0, 77, 255]
+    worst = (0.0, -1)
+    for i in pick:
         want, _ = c2_oracle.forward(texts[i])
         w = want[:256] / np.linalg.norm(want[:256])
         assert cosine(out[i].vector, w) >= COSINE_BAR, i
+        worst = max(worst, (float(np.abs(out[i].vector - w).max()), i))
+    print(f"config 3 default: max |d| {worst[0]:.3e} (text {worst[1]}, {len(texts[worst[1]])} tokens)", flush=True)
+    return worst
+
+
+# Bound of the fp16-operand design on these texts: the float64 emulation of its roundings
+# (tests/fp16_emulation.py) gives a mean max |d| of 6.8e-5 and a worst of 9.1e-5 over 80 of
+# config 3's texts; GPU draws of the same distribution reached 1.26e-4 on one text of 44.
+FP16_DESIGN_MAX_ABS = 2e-4
+
+
+def test_config3_ragged_vs_oracle(config3_default):
+    """256 texts, lengths U[8, 256], packed by token count, Matryoshka 256:
+    cosine >= 0.99999 on every checked text, and max |d| within the fp16 design's bound."""
+    assert config3_default[0] < FP16_DESIGN_MAX_ABS, config3_default
+
+
+@pytest.mark.xfail(reason="fp16 q.k scores: config 3's worst short text reaches 1.0-1.3e-4 against the "
+                          "reference's 1e-4 (MetalForwardTests.swift:213-214); the split_scores load "
+                          "option meets it (3.2e-5), the default does not", strict=False)
+def test_config3_default_meets_the_reference_max_abs(config3_default):
+    assert config3_default[0] < 1e-4, config3_default
 
 
 def test_split_scores_meet_the_reference_bar_on_config3(config2_gguf, c2_oracle):
@@ -455,6 +488,25 @@ def test_split_scores_meet_the_reference_bar_on_config3(config2_gguf, c2_oracle)
         worst = max(worst, float(np.abs(g - w).max()))
     print(f"split scores, config 3 sample of {len(sample)} texts: max |diff| {worst:.3g}")
     assert worst < 1e-4
+
+
+def test_split_scores_texts_longer_than_the_window(config2_gguf, c2_oracle, config2_batch):
+    """split_scores on texts longer than the 512-token window (sliding layers clip their key range
+    and mask by it; global layers see every key), packed with a short one: against the oracle at
+    the reference's bars, and each text's vector the same bits alone as in the pack."""
+    texts = [config2_batch[0] + config2_batch[1][:600], config2_batch[2][:700], config2_batch[3][:40]]
+    m = ge.EmbeddingModel.load(config2_gguf, split_scores=True)
+    try:
+        pooled = m.embed_tokens(texts)
+        alone = m.embed_tokens([texts[1]])[0]
+    finally:
+        m.close()
+    assert np.array_equal(alone, pooled[1])
+    for i, t in enumerate(texts):
+        want, _ = c2_oracle.forward(t)
+        d = float(np.abs(normalised(pooled[i]) - normalised(want)).max())
+        print(f"split scores, text of {len(t)} tokens: cosine {cosine(pooled[i], want):.9f} max |diff| {d:.3g}", flush=True)
+        assert cosine(pooled[i], want) > 0.99999 and d < 1e-4, i
 
 
 @pytest.fixture(scope="module")

@@ -279,22 +279,30 @@ def rms_normed(x, w):
     return (x / np.sqrt((x * x).mean(-1, keepdims=True) + 1e-6) * w).astype(np.float32)
 
 
-SPLIT_CASES = [  # (lengths, H, KV, half_window, correlation of the rows with one shared direction)
-    ([1024, 300], 4, 1, 0, 0.0),
-    ([2048, 7, 129], 4, 1, 0, 0.95),
-    ([700, 1], 8, 2, 256, 0.5),
+SPLIT_CASES = [  # (lengths, H, KV, half_window, correlation of the rows with one shared direction, head dim)
+    ([1024, 300], 4, 1, 0, 0.0, 512),
+    ([2048, 7, 129], 4, 1, 0, 0.95, 512),
+    ([700, 1], 8, 2, 256, 0.5, 512),
+    # head dim 256 with 3 query heads per KV head (attention_split_kernel<256, 3>, config 2's layers
+    # under split_scores), sequences longer than the window so that the window's key range and its
+    # mask act, and empty-neighbour edge cases
+    ([1024, 300], 3, 1, 256, 0.5, 256),
+    ([700, 1], 3, 1, 256, 0.0, 256),
+    ([2048, 7, 129], 3, 1, 256, 0.95, 256),
+    ([2048, 7, 129], 6, 2, 0, 0.5, 256),
 ]
 
 
-@pytest.mark.parametrize("lengths,H,KV,hw,corr", SPLIT_CASES)
-def test_attention_split_normed_hd512_vs_oracle(ctx, lengths, H, KV, hw, corr):
-    """RMS-normed, weighted q and k of width 512 at attention scale 1 (the reference's global
-    layers, Model/Architecture.md:8-9, CPUReference.swift:225-233): scores of several hundred.
-    The oracle gets the fp32 q and k; the GPU gets them as split fp16 pairs. fp16 operands alone
-    put such cases at 6-8e-3 of max |want| (a near-tie between keys moves with a 0.02 score shift);
-    the split scores leave the fp16 rounding of V and P (~4e-4)."""
-    print(f"split attention lengths={lengths} H={H} KV={KV} hw={hw} corr={corr}", flush=True)
-    hd, T, slack = 512, sum(lengths), 64
+@pytest.mark.parametrize("lengths,H,KV,hw,corr,hd", SPLIT_CASES)
+def test_attention_split_normed_vs_oracle(ctx, lengths, H, KV, hw, corr, hd):
+    """RMS-normed, weighted q and k at attention scale 1 (the reference's global layers of width
+    512, Model/Architecture.md:8-9, CPUReference.swift:225-233; config 2's width 256 when split
+    scores are loaded): scores of several hundred. The oracle gets the fp32 q and k; the GPU gets
+    them as split fp16 pairs. fp16 operands alone put such cases at 6-8e-3 of max |want| (a
+    near-tie between keys moves with a 0.02 score shift); the split scores leave the fp16 rounding
+    of V and P (~4e-4)."""
+    print(f"split attention lengths={lengths} H={H} KV={KV} hw={hw} corr={corr} hd={hd}", flush=True)
+    T, slack = sum(lengths), 64
     rng = np.random.default_rng(1000 + T)
     base = rng.standard_normal(hd)
     mix = lambda shape: corr * base + np.sqrt(1 - corr * corr) * rng.standard_normal(shape)
