@@ -582,11 +582,15 @@ void upload(ge_ctx* c, const ge_model_desc* d, const void* base, size_t len) {
 
 // ---------------------------------------------------------------- workspace
 
+// A zero-filled workspace buffer. The fill is queued on the context's stream, ahead of the batch
+// copies and kernels that follow there: the context's streams are created non-blocking, so a
+// plain hipMemset (the null stream) would not be ordered before them, and a fill that landed late
+// would overwrite the staged batch with zeros.
 template <typename T>
-T* ws_alloc(size_t rows, size_t width, const char* what) {
+T* ws_alloc(hipStream_t s, size_t rows, size_t width, const char* what) {
     const size_t bytes = rows * width * sizeof(T);
     void* p = dev_alloc(bytes, what);
-    hip_check(hipMemset(p, 0, bytes), "hipMemset workspace");
+    hip_check(hipMemsetAsync(p, 0, bytes, s), "hipMemsetAsync workspace");
     return static_cast<T*>(p);
 }
 
@@ -624,32 +628,32 @@ void ensure_workspace_impl(ge_ctx* c, int tokens, int seqs, int work, int work2,
         w.seq_cap = keep_seq;
         w.work_cap = keep_work;
         w.rows = rows;
-        w.x = ws_alloc<float>(rows, m.hidden, "x");
-        w.h = ws_alloc<uint16_t>(rows, m.hidden, "h");
-        w.qkv = ws_alloc<float>(rows, m.max_qkv, "qkv");
-        w.q = ws_alloc<uint16_t>(rows, m.max_qd, "q");
-        w.k = ws_alloc<uint16_t>(rows, m.max_kvd, "k");
-        w.v = ws_alloc<uint16_t>(rows, m.max_kvd, "v");
-        w.attn = ws_alloc<uint16_t>(rows, m.max_qd, "attn");
-        w.t = ws_alloc<float>(rows, m.hidden, "t");
-        w.act = ws_alloc<uint16_t>(rows, m.ff, "act");
-        w.out = ws_alloc<float>(rows, m.out_dims, "out");
-        w.hn = ws_alloc<float>(rows, m.hidden, "final norm");
-        w.tokens = ws_alloc<int32_t>(rows, 1, "tokens");
-        w.positions = ws_alloc<int32_t>(rows, 1, "positions");
-        w.vcol = ws_alloc<int32_t>(rows, 1, "vt columns");
+        w.x = ws_alloc<float>(c->stream, rows, m.hidden, "x");
+        w.h = ws_alloc<uint16_t>(c->stream, rows, m.hidden, "h");
+        w.qkv = ws_alloc<float>(c->stream, rows, m.max_qkv, "qkv");
+        w.q = ws_alloc<uint16_t>(c->stream, rows, m.max_qd, "q");
+        w.k = ws_alloc<uint16_t>(c->stream, rows, m.max_kvd, "k");
+        w.v = ws_alloc<uint16_t>(c->stream, rows, m.max_kvd, "v");
+        w.attn = ws_alloc<uint16_t>(c->stream, rows, m.max_qd, "attn");
+        w.t = ws_alloc<float>(c->stream, rows, m.hidden, "t");
+        w.act = ws_alloc<uint16_t>(c->stream, rows, m.ff, "act");
+        w.out = ws_alloc<float>(c->stream, rows, m.out_dims, "out");
+        w.hn = ws_alloc<float>(c->stream, rows, m.hidden, "final norm");
+        w.tokens = ws_alloc<int32_t>(c->stream, rows, 1, "tokens");
+        w.positions = ws_alloc<int32_t>(c->stream, rows, 1, "positions");
+        w.vcol = ws_alloc<int32_t>(c->stream, rows, 1, "vt columns");
         if (m.any_precise) {
-            w.h3 = ws_alloc<uint16_t>(rows, 3 * size_t(m.hidden), "split-precision input");
-            w.q_lo = ws_alloc<uint16_t>(rows, m.max_qd, "q low halves");
-            w.k_lo = ws_alloc<uint16_t>(rows, m.max_kvd, "k low halves");
+            w.h3 = ws_alloc<uint16_t>(c->stream, rows, 3 * size_t(m.hidden), "split-precision input");
+            w.q_lo = ws_alloc<uint16_t>(c->stream, rows, m.max_qd, "q low halves");
+            w.k_lo = ws_alloc<uint16_t>(c->stream, rows, m.max_kvd, "k low halves");
         }
         if (m.pl > 0) {
-            w.ple = ws_alloc<float>(rows, size_t(m.layers) * m.pl, "per-layer inputs");
-            w.ple_t = ws_alloc<float>(rows, size_t(std::max(m.pl, m.hidden)), "per-layer projection");
-            w.rs = ws_alloc<float>(rows, 1, "row scales");
-            w.rs2 = ws_alloc<float>(rows, 1, "row scales");
-            w.x16 = ws_alloc<uint16_t>(rows, m.hidden, "scaled residual");
-            w.g16 = ws_alloc<uint16_t>(rows, m.pl, "per-layer gate");
+            w.ple = ws_alloc<float>(c->stream, rows, size_t(m.layers) * m.pl, "per-layer inputs");
+            w.ple_t = ws_alloc<float>(c->stream, rows, size_t(std::max(m.pl, m.hidden)), "per-layer projection");
+            w.rs = ws_alloc<float>(c->stream, rows, 1, "row scales");
+            w.rs2 = ws_alloc<float>(c->stream, rows, 1, "row scales");
+            w.x16 = ws_alloc<uint16_t>(c->stream, rows, m.hidden, "scaled residual");
+            w.g16 = ws_alloc<uint16_t>(c->stream, rows, m.pl, "per-layer gate");
         }
         w.seqs = nullptr;
         w.work = nullptr;
@@ -669,19 +673,19 @@ void ensure_workspace_impl(ge_ctx* c, int tokens, int seqs, int work, int work2,
         w.seqs = nullptr;
         w.pooled = w.pooled_n = nullptr;
         w.seq_cap = std::max(seqs, 1);
-        w.seqs = ws_alloc<SeqRange>(w.seq_cap, 1, "sequences");
-        w.pooled = ws_alloc<float>(w.seq_cap, m.out_dims, "pooled");
-        w.pooled_n = ws_alloc<float>(w.seq_cap, m.hidden, "pooled rows");
+        w.seqs = ws_alloc<SeqRange>(c->stream, w.seq_cap, 1, "sequences");
+        w.pooled = ws_alloc<float>(c->stream, w.seq_cap, m.out_dims, "pooled");
+        w.pooled_n = ws_alloc<float>(c->stream, w.seq_cap, m.hidden, "pooled rows");
     }
     if (work > w.work_cap || !w.work) {
         if (w.work) (void)hipFree(w.work);
         w.work_cap = std::max(work, 1);
-        w.work = ws_alloc<AttnWork>(w.work_cap, 1, "attention work");
+        w.work = ws_alloc<AttnWork>(c->stream, w.work_cap, 1, "attention work");
     }
     if (m.any_v2 && (work2 > w.work2_cap || !w.work2)) {
         if (w.work2) (void)hipFree(w.work2);
         w.work2_cap = std::max(work2, 1);
-        w.work2 = ws_alloc<AttnWork>(w.work2_cap, 1, "attention work");
+        w.work2 = ws_alloc<AttnWork>(c->stream, w.work2_cap, 1, "attention work");
     }
     // Zero-filled once: columns no token writes (alignment gaps, slack) stay finite, and keys
     // read from them are masked, so they contribute exact zeros.
@@ -690,7 +694,7 @@ void ensure_workspace_impl(ge_ctx* c, int tokens, int seqs, int work, int work2,
         // grow by half, in whole 64-column steps: the copies and the kernels' checks need
         // 16-byte aligned rows (a multiple of 8 columns)
         w.vt_cap = (std::max(vt_cols, w.vt_cap + w.vt_cap / 2) + 63) / 64 * 64;
-        w.vt = ws_alloc<uint16_t>(size_t(m.max_kvd), size_t(w.vt_cap), "transposed v");
+        w.vt = ws_alloc<uint16_t>(c->stream, size_t(m.max_kvd), size_t(w.vt_cap), "transposed v");
     }
 }
 
@@ -821,18 +825,6 @@ void set_staged(ge_ctx* c, const BatchPlan& b, int n, int n_seqs, const float* v
     std::copy(b.part_work, b.part_work + kMaxParts + 1, c->part_work);
 }
 
-// GE_SYNC_STAGING=1 uploads staged batches with synchronous hipMemcpy instead of asynchronous
-// copies from pinned host memory. Under rocprofv3 --pmc the asynchronous copies did not reach the
-// workspace (a staged config-2 pack read back as zeros: every pooled vector 0), so counter runs of
-// whole forwards set it; nothing else needs it.
-bool sync_staging() {
-    static const bool on = [] {
-        const char* e = std::getenv("GE_SYNC_STAGING");
-        return e && e[0] == '1';
-    }();
-    return on;
-}
-
 // Validates and uploads a packed batch into the context's workspace, grown as needed.
 void stage(ge_ctx* c, const int32_t* tokens, const int32_t* positions, int n, const ge_seq* seqs, int n_seqs,
            const float* vectors, int n_vectors) {
@@ -854,14 +846,6 @@ void stage(ge_ctx* c, const int32_t* tokens, const int32_t* positions, int n, co
                             {w.work, b.work.data(), b.work.size() * sizeof(AttnWork)},
                             {w.work2, b.work2.data(), b.work2.size() * sizeof(AttnWork)},
                             {w.vcol, b.vl.vcol.data(), b.work2.empty() ? 0 : size_t(n) * 4}};
-    if (sync_staging()) {
-        // Synchronous copies from the caller's arrays (profiling aid, see sync_staging).
-        drain(c);
-        for (const Piece& pc : pieces)
-            if (pc.bytes) hip_check(hipMemcpy(pc.dst, pc.src, pc.bytes, hipMemcpyHostToDevice), "upload batch");
-        set_staged(c, b, n, n_seqs, vectors);
-        return;
-    }
     size_t total = 0;
     for (const Piece& pc : pieces) total += (pc.bytes + 255) / 256 * 256;
     if (c->staged_copy_recorded) hip_check(hipEventSynchronize(c->staged_copy), "hipEventSynchronize");
@@ -1619,7 +1603,9 @@ void* ge_dev_alloc(ge_ctx* c, size_t bytes) {
     void* p = nullptr;
     int rc = guarded(c, [&] {
         p = ge::dev_alloc(bytes, "ge_dev_alloc");
-        ge::hip_check(hipMemset(p, 0, bytes ? bytes : 16), "hipMemset");
+        // zeroed before the pointer is returned, whichever stream the caller uses next
+        ge::hip_check(hipMemsetAsync(p, 0, bytes ? bytes : 16, c->stream), "hipMemsetAsync");
+        ge::hip_check(hipStreamSynchronize(c->stream), "hipStreamSynchronize");
     });
     return rc == GE_OK ? p : nullptr;
 }

@@ -245,15 +245,17 @@ void vision_upload(ge_ctx* c, const ge_vision_desc* d, const void* base, size_t 
 
 // ---------------------------------------------------------------- staging
 
+// A zero-filled workspace buffer, the fill queued on the context's stream (see ws_alloc): the
+// image batch's copies and the tower's kernels come after it there.
 template <typename T>
-T* vws_alloc(size_t rows, size_t width, const char* what) {
+T* vws_alloc(hipStream_t s, size_t rows, size_t width, const char* what) {
     const size_t bytes = rows * width * sizeof(T);
     void* p = dev_alloc(bytes, what);
-    hip_check(hipMemset(p, 0, bytes), "hipMemset workspace");
+    hip_check(hipMemsetAsync(p, 0, bytes, s), "hipMemsetAsync workspace");
     return static_cast<T*>(p);
 }
 
-void alloc_vision_workspace(VisionState& v, int r, int tr, int wc, int vc);
+void alloc_vision_workspace(hipStream_t s, VisionState& v, int r, int tr, int wc, int vc);
 
 void ensure_vision_workspace(ge_ctx* c, VisionState& v, int patches, int tokens, int work, int vt_cols) {
     const int rows = (patches + 63) / 64 * 64 + kRowSlack, tok_rows = (tokens + 63) / 64 * 64 + kRowSlack;
@@ -264,7 +266,7 @@ void ensure_vision_workspace(ge_ctx* c, VisionState& v, int patches, int tokens,
     const int vc = (std::max(vt_cols, v.vt_cap + v.vt_cap / 2) + 63) / 64 * 64;
     free_vision_workspace(v);
     try {
-        alloc_vision_workspace(v, r, tr, wc, vc);
+        alloc_vision_workspace(c->stream, v, r, tr, wc, vc);
     } catch (...) {
         free_vision_workspace(v);  // no capacity is recorded for buffers that do not exist
         throw;
@@ -275,29 +277,29 @@ void ensure_vision_workspace(ge_ctx* c, VisionState& v, int patches, int tokens,
     v.vt_cap = vc;
 }
 
-void alloc_vision_workspace(VisionState& v, int r, int tr, int wc, int vc) {
+void alloc_vision_workspace(hipStream_t s, VisionState& v, int r, int tr, int wc, int vc) {
     const size_t D = size_t(v.hidden), HP = size_t(v.heads) * v.hp;
-    v.patches32 = vws_alloc<float>(r, v.area, "patches");
-    v.patches16 = vws_alloc<uint16_t>(r, v.area, "patches");
-    v.x = vws_alloc<float>(r, D, "x");
-    v.t = vws_alloc<float>(r, D, "t");
-    v.h = vws_alloc<uint16_t>(r, D, "h");
+    v.patches32 = vws_alloc<float>(s, r, v.area, "patches");
+    v.patches16 = vws_alloc<uint16_t>(s, r, v.area, "patches");
+    v.x = vws_alloc<float>(s, r, D, "x");
+    v.t = vws_alloc<float>(s, r, D, "t");
+    v.h = vws_alloc<uint16_t>(s, r, D, "h");
     // q, k, v keep zeros in each head's padding columns: the epilogue never writes them
-    v.q = vws_alloc<uint16_t>(r, HP, "q");
-    v.k = vws_alloc<uint16_t>(r, HP, "k");
-    v.v = vws_alloc<uint16_t>(r, HP, "v");
-    v.vt = vws_alloc<uint16_t>(HP, size_t(vc), "transposed v");
-    v.attn = vws_alloc<uint16_t>(r, size_t(v.heads) * v.hd, "attn");
-    v.act = vws_alloc<uint16_t>(r, size_t(v.ff_pad), "act");
-    v.pooled = vws_alloc<float>(tr, D, "pooled");
-    v.pooled16 = vws_alloc<uint16_t>(tr, D, "pooled");
-    v.out = vws_alloc<float>(tr, size_t(v.proj), "vectors");
-    v.px = vws_alloc<int32_t>(r, 1, "patch x");
-    v.py = vws_alloc<int32_t>(r, 1, "patch y");
-    v.vcol = vws_alloc<int32_t>(r, 1, "vt columns");
-    v.tok_row0 = vws_alloc<int32_t>(tr, 1, "pool windows");
-    v.tok_gx = vws_alloc<int32_t>(tr, 1, "pool windows");
-    v.work = vws_alloc<AttnWork>(size_t(wc), 1, "attention work");
+    v.q = vws_alloc<uint16_t>(s, r, HP, "q");
+    v.k = vws_alloc<uint16_t>(s, r, HP, "k");
+    v.v = vws_alloc<uint16_t>(s, r, HP, "v");
+    v.vt = vws_alloc<uint16_t>(s, HP, size_t(vc), "transposed v");
+    v.attn = vws_alloc<uint16_t>(s, r, size_t(v.heads) * v.hd, "attn");
+    v.act = vws_alloc<uint16_t>(s, r, size_t(v.ff_pad), "act");
+    v.pooled = vws_alloc<float>(s, tr, D, "pooled");
+    v.pooled16 = vws_alloc<uint16_t>(s, tr, D, "pooled");
+    v.out = vws_alloc<float>(s, tr, size_t(v.proj), "vectors");
+    v.px = vws_alloc<int32_t>(s, r, 1, "patch x");
+    v.py = vws_alloc<int32_t>(s, r, 1, "patch y");
+    v.vcol = vws_alloc<int32_t>(s, r, 1, "vt columns");
+    v.tok_row0 = vws_alloc<int32_t>(s, tr, 1, "pool windows");
+    v.tok_gx = vws_alloc<int32_t>(s, tr, 1, "pool windows");
+    v.work = vws_alloc<AttnWork>(s, size_t(wc), 1, "attention work");
 }
 
 // VisionBatch.init (VisionTower.swift:17-33) and VisionTower.upload (:113-140): images back to
