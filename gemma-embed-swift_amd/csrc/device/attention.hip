@@ -1093,25 +1093,52 @@ hipError_t launch_attention_split(hipStream_t s, const uint16_t* q, const uint16
 }
 
 // The image tower's attention: one query head per KV head, no window, heads stored padded (HD
-// dims of which the first HO are real). As attention_v3_kernel (the same K/V^T ring in LDS, the
-// same MFMAs and softmax), but each wave owns QT tiles of 16 queries, so every K and V^T fragment
-// read from LDS feeds QT MFMAs: at head dim 72 the LDS reads, not the MFMAs, set the pace.
-template <int HD, int QW, int QT, int HO>
+// dims of which the first HO are real). Each wave owns 32 queries of one head on
+// v_mfma_f32_32x32x16_f16: on gfx950 the 16x16x32 form issues no faster than this one (14.3
+// against 14.8 ns per instruction per SIMD in a register-only loop), so these 32x32 tiles do twice
+// the work per MFMA cycle. S^T = K Q^T over HS dims (the real HO rounded up to 16: 80 for 72, where
+// 16x16x32 steps needed 96), O^T = V^T P^T over the stored HD dims in 32-dim tiles.
+//
+// LDS per block of 32 keys, in fragment order (1 KB chunk = one operand fragment, lane l's 16
+// bytes at 16 l):
+//   K chunk ks (16 dims): lane l holds key pi(l % 32), dims 16 ks + 8 (l / 32) + [0, 8), where pi
+//     swaps the 4s and 8s bits of the row. With that key order, register r of a lane's S^T tile
+//     holds key 16 (r / 8) + 8 (l / 32) + r % 8 of query l % 32, so registers 8 t .. 8 t + 7 are
+//     the B operand of the P.V k-step t (keys 16 t + 8 (l / 32) + [0, 8)) with no data exchange;
+//   V^T chunk (dt, t): lane l holds dim 32 dt + l % 32, keys 16 t + 8 (l / 32) + [0, 8).
+// A query's 32 scores of a block sit in lanes q and q + 32: its block max is one lane swap.
+__device__ __forceinline__ float max_over_lane_halves(float v) {
+    const auto b = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    return fmaxf(__uint_as_float(b[0]), __uint_as_float(b[1]));
+}
+
+__device__ __forceinline__ float sum_over_lane_halves(float v) {
+    const auto b = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    return __uint_as_float(b[0]) + __uint_as_float(b[1]);
+}
+
+namespace attnp {
+constexpr int NS = 2;    // key blocks in LDS
+constexpr int BKV = 32;  // keys per block
+}  // namespace attnp
+
+template <int HD, int HS>
+constexpr int attention_mq_lds_bytes() { return attnp::NS * (HS / 16 + (HD / 32) * 2) * 1024; }
+
+template <int HD, int HS, int QW, int HO>
 __global__ __launch_bounds__(QW * 64) void attention_mq_kernel(const uint16_t* __restrict__ Qg,
                                                                const uint16_t* __restrict__ Kg,
                                                                const uint16_t* __restrict__ VTg,
                                                                uint16_t* __restrict__ Og,
                                                                const AttnWork* __restrict__ work, int H, int vt_cols,
                                                                float scale_log2) {
-    using namespace attn3;
-    constexpr int NW = QW, KS = HD / 32, DT = HD / 16, DTO = (HO + 15) / 16;
-    constexpr int K_BYTES = BKV * HD * 2, STAGE = 2 * K_BYTES;
-    constexpr int KCH = K_BYTES / 1024, CH = 2 * KCH;  // K chunks (ks, m), then V^T chunks dt
-    static_assert(KCH == 2 * KS && KCH == DT, "chunk counts");
-    static_assert(HO <= HD && HO % 8 == 0, "stored head dims");
-    static_assert(NW <= CH, "a wave past the last chunk repeats its own chunk index");
-    constexpr int CPW = (CH + NW - 1) / NW;
-    extern __shared__ __attribute__((aligned(1024))) unsigned char ldsa[];
+    using namespace attnp;
+    constexpr int KSS = HS / 16, DT = HD / 32;
+    constexpr int KCH = KSS, VCH = DT * 2, CH = KCH + VCH, STAGE = CH * 1024;
+    constexpr int CPW = (CH + QW - 1) / QW;  // copies per wave per block (some waves repeat one)
+    static_assert(HO <= HS && HS <= HD && HS % 16 == 0 && HD % 32 == 0 && HO % 8 == 0, "head dims");
+    static_assert(QW <= CH, "a wave past the last chunk repeats its own chunk index");
+    extern __shared__ __attribute__((aligned(1024))) unsigned char ldsm[];
 
     const int nb = int(gridDim.x), full = nb / 8 * 8, bx = int(blockIdx.x);
     const int widx = bx < full ? (bx % 8) * (full / 8) + bx / 8 : bx;
@@ -1124,8 +1151,8 @@ __global__ __launch_bounds__(QW * 64) void attention_mq_kernel(const uint16_t* _
     const int vt_start = __builtin_amdgcn_readfirstlane(int(work[widx].vt_start));
     const int h = blockIdx.y;
     const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(int(threadIdx.x >> 6));
-    const int qbase = wq0 + wave * 16 * QT;  // tile t: queries qbase + 16 t + lane % 16
-    const int l16 = lane & 15, g4 = lane >> 4;
+    const int l32 = lane & 31, hi = lane >> 5;
+    const int q0 = wq0 + wave * 32, qi = q0 + l32;
     const int stride = H * HD;
     const int nblocks = (len + BKV - 1) / BKV;
 
@@ -1133,149 +1160,131 @@ __global__ __launch_bounds__(QW * 64) void attention_mq_kernel(const uint16_t* _
         buffer_rsrc(Kg + (size_t)seq_start * stride + h * HD, uint32_t(((len - 1) * stride + HD) * 2));
     const __amdgpu_buffer_rsrc_t vr = buffer_rsrc(VTg + (size_t)h * HD * vt_cols + vt_start,
                                                   uint32_t(((HD - 1) * vt_cols + (vt_cols - vt_start)) * 2));
-    const uint32_t klane = uint32_t(((8 * (l16 >> 2) + (lane & 3)) * stride + 8 * g4) * 2);
-    const uint32_t vlane = uint32_t((l16 * vt_cols + 8 * g4) * 2);
+    const int krow = (l32 & 16) | ((l32 & 4) << 1) | ((l32 & 8) >> 1) | (l32 & 3);  // pi(l % 32)
+    const uint32_t klane = uint32_t((krow * stride + 8 * hi) * 2);
+    const uint32_t vlane = uint32_t((l32 * vt_cols + 8 * hi) * 2);
 #define MQ_ISSUE(kb, b)                                                                                    \
     do {                                                                                                   \
         _Pragma("unroll") for (int i = 0; i < CPW; i++) {                                                  \
-            int c = wave + i * NW;                                                                         \
+            int c = wave + i * QW;                                                                         \
             if (c >= CH) c = wave;                                                                         \
-            unsigned char* dst_ = ldsa + (b) * STAGE + c * 1024;                                           \
+            unsigned char* dst_ = ldsm + (b) * STAGE + c * 1024;                                           \
             if (c < KCH) {                                                                                 \
-                const int ks_ = c >> 1, m_ = c & 1;                                                        \
-                lds_copy16(kr, dst_, klane + uint32_t(((kb) + 4 * m_) * stride * 2 + ks_ * 64), 0);        \
+                lds_copy16(kr, dst_, klane + uint32_t((kb) * stride * 2 + c * 32), 0);                      \
             } else {                                                                                       \
-                lds_copy16(vr, dst_, vlane + uint32_t((c - KCH) * 16 * vt_cols * 2 + (kb) * 2), 0);        \
+                const int vc_ = c - KCH, dt_ = vc_ >> 1, t_ = vc_ & 1;                                     \
+                lds_copy16(vr, dst_, vlane + uint32_t((dt_ * 32 * vt_cols + (kb) + 16 * t_) * 2), 0);      \
             }                                                                                              \
         }                                                                                                  \
     } while (0)
 
-    half8_t qa[QT][KS];
+    // This wave's query fragments (B operand of S^T = K Q^T): lane l: query qi (rows past the
+    // sequence re-read its last row; their outputs are never stored), dims 16 ks + 8 (l / 32).
+    half8_t qa[KSS];
     {
         const __amdgpu_buffer_rsrc_t qr =
             buffer_rsrc(Qg + (size_t)seq_start * stride + h * HD, uint32_t(((len - 1) * stride + HD) * 2));
+        const uint32_t qo = uint32_t((min(qi, len - 1) * stride + 8 * hi) * 2);
 #pragma unroll
-        for (int t = 0; t < QT; t++) {
-            const uint32_t qo = uint32_t((min(qbase + 16 * t + l16, len - 1) * stride + 8 * g4) * 2);
-#pragma unroll
-            for (int ks = 0; ks < KS; ks++)
-                qa[t][ks] = __builtin_bit_cast(half8_t, __builtin_amdgcn_raw_buffer_load_b128(qr, qo + ks * 64, 0, 0));
-        }
+        for (int ks = 0; ks < KSS; ks++)
+            qa[ks] = __builtin_bit_cast(half8_t, __builtin_amdgcn_raw_buffer_load_b128(qr, qo + ks * 32, 0, 0));
     }
-    float4_t o[QT][DTO];
-    float m_run[QT], l_run[QT];
+    float16_t o[DT];
 #pragma unroll
-    for (int t = 0; t < QT; t++) {
+    for (int i = 0; i < DT; i++)
 #pragma unroll
-        for (int i = 0; i < DTO; i++) o[t][i] = float4_t{0.0f, 0.0f, 0.0f, 0.0f};
-        m_run[t] = -INFINITY;
-        l_run[t] = 0.0f;
-    }
+        for (int r = 0; r < 16; r++) o[i][r] = 0.0f;
+    float m_run = -INFINITY, l_run = 0.0f;
 
-#pragma unroll
-    for (int s = 0; s < NS - 1; s++)
-        if (s < nblocks) MQ_ISSUE(s * BKV, s);
+    if (0 < nblocks) MQ_ISSUE(0, 0);
     int b = 0;
     for (int it = 0; it < nblocks; it++) {
         const int kb = it * BKV;
-        static_assert(NS >= 2 && NS <= 4, "the waits below cover two to four stages");
-        const int ahead = min(NS - 2, nblocks - 1 - it);
-        if (ahead >= 2)
-            wait_vmcnt<2 * CPW>();
-        else if (ahead == 1)
-            wait_vmcnt<CPW>();
-        else
-            wait_vmcnt<0>();
+        // block it has landed (every wave's copies: the barrier), and every wave is done reading
+        // the buffer the next copies overwrite
+        wait_vmcnt<0>();
         wait_lgkmcnt0();
         workgroup_barrier();
-        if (it + NS - 1 < nblocks) MQ_ISSUE((it + NS - 1) * BKV, b == 0 ? NS - 1 : b - 1);
-        const unsigned char* const kf = ldsa + b * STAGE + lane * 16;
-        const unsigned char* const vf = kf + K_BYTES;
+        if (it + 1 < nblocks) MQ_ISSUE(kb + BKV, b ^ 1);
+        const unsigned char* const kf = ldsm + b * STAGE + lane * 16;
+        const unsigned char* const vf = kf + KCH * 1024;
         constexpr int PF = 2, RING = PF + 1;
-        float4_t s[QT][2];
+        float16_t s;
 #pragma unroll
-        for (int t = 0; t < QT; t++) s[t][0] = s[t][1] = float4_t{0.0f, 0.0f, 0.0f, 0.0f};
-        half8_t ka[RING][2];
+        for (int r = 0; r < 16; r++) s[r] = 0.0f;
+        half8_t ka[RING];
 #pragma unroll
-        for (int f = 0; f < PF; f++) {
-            ka[f][0] = *reinterpret_cast<const half8_t*>(kf + (2 * f) * 1024);
-            ka[f][1] = *reinterpret_cast<const half8_t*>(kf + (2 * f + 1) * 1024);
-        }
+        for (int f = 0; f < PF && f < KSS; f++) ka[f] = *reinterpret_cast<const half8_t*>(kf + f * 1024);
 #pragma unroll
-        for (int ks = 0; ks < KS; ks++) {
-            if (ks + PF < KS) {
-                ka[(ks + PF) % RING][0] = *reinterpret_cast<const half8_t*>(kf + (2 * (ks + PF)) * 1024);
-                ka[(ks + PF) % RING][1] = *reinterpret_cast<const half8_t*>(kf + (2 * (ks + PF) + 1) * 1024);
-            }
+        for (int ks = 0; ks < KSS; ks++) {
+            if (ks + PF < KSS) ka[(ks + PF) % RING] = *reinterpret_cast<const half8_t*>(kf + (ks + PF) * 1024);
+            // keep the reads ahead of the MFMAs (the scheduler would otherwise sink them)
             __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-            for (int t = 0; t < QT; t++) {
-                s[t][0] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ka[ks % RING][0], qa[t][ks], s[t][0], 0, 0, 0);
-                s[t][1] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ka[ks % RING][1], qa[t][ks], s[t][1], 0, 0, 0);
-            }
+            s = __builtin_amdgcn_mfma_f32_32x32x16_f16(ka[ks % RING], qa[ks], s, 0, 0, 0);
         }
+        // the first V^T fragments are read while the softmax runs
         half8_t va[RING];
 #pragma unroll
         for (int f = 0; f < PF; f++) va[f] = *reinterpret_cast<const half8_t*>(vf + f * 1024);
-        const bool inside = kb + BKV <= len;
-        half8_t pb[QT];
+        // register r: key kb + 16 (r / 8) + 8 (l / 32) + r % 8 of query qi
+        float sc[16];
 #pragma unroll
-        for (int t = 0; t < QT; t++) {
-            float sc[8] = {s[t][0][0], s[t][0][1], s[t][0][2], s[t][0][3], s[t][1][0], s[t][1][1], s[t][1][2], s[t][1][3]};
-            if (!inside) {
+        for (int r = 0; r < 16; r++) sc[r] = s[r];
+        if (kb + BKV > len) {
 #pragma unroll
-                for (int e = 0; e < 8; e++) sc[e] = kb + 8 * g4 + e < len ? sc[e] : -INFINITY;
-            }
-            const float lmax =
-                fmaxf(fmaxf(fmaxf(sc[0], sc[1]), fmaxf(sc[2], sc[3])), fmaxf(fmaxf(sc[4], sc[5]), fmaxf(sc[6], sc[7])));
-            // lazy rescaling, as in attention_v3_kernel
-            if (__builtin_amdgcn_ballot_w64(lmax * scale_log2 > m_run[t] + 8.0f)) {
-                const float bmax = max_over_key_groups(lmax) * scale_log2;
-                const float m_new = fmaxf(m_run[t], bmax);
-                const float alpha = m_new == -INFINITY ? 1.0f : __builtin_amdgcn_exp2f(m_run[t] - m_new);
-                l_run[t] *= alpha;
-#pragma unroll
-                for (int i = 0; i < DTO; i++) o[t][i] *= alpha;
-                m_run[t] = m_new;
-            }
-            const float m_ref = m_run[t] == -INFINITY ? 0.0f : m_run[t];
-            float sum = 0.0f;
-#pragma unroll
-            for (int e = 0; e < 8; e++) {
-                const float p = __builtin_amdgcn_exp2f(__builtin_fmaf(sc[e], scale_log2, -m_ref));
-                sum += p;
-                pb[t][e] = _Float16(p);
-            }
-            l_run[t] += sum;
+            for (int r = 0; r < 16; r++) sc[r] = kb + 16 * (r >> 3) + 8 * hi + (r & 7) < len ? sc[r] : -INFINITY;
         }
+        float lmax = sc[0];
 #pragma unroll
-        for (int dt = 0; dt < DTO; dt++) {
-            if (dt + PF < DTO) va[(dt + PF) % RING] = *reinterpret_cast<const half8_t*>(vf + (dt + PF) * 1024);
+        for (int r = 1; r < 16; r++) lmax = fmaxf(lmax, sc[r]);
+        // lazy rescaling, as in attention_v3_kernel: the reference point moves only when a score
+        // exceeds it by more than 2^8, so P stays below 256
+        if (__builtin_amdgcn_ballot_w64(lmax * scale_log2 > m_run + 8.0f)) {
+            const float bmax = max_over_lane_halves(lmax) * scale_log2;
+            const float m_new = fmaxf(m_run, bmax);
+            const float alpha = m_new == -INFINITY ? 1.0f : __builtin_amdgcn_exp2f(m_run - m_new);
+            l_run *= alpha;
+#pragma unroll
+            for (int i = 0; i < DT; i++) o[i] *= alpha;
+            m_run = m_new;
+        }
+        const float m_ref = m_run == -INFINITY ? 0.0f : m_run;
+        float sum = 0.0f;
+        half8_t pb[2];
+#pragma unroll
+        for (int r = 0; r < 16; r++) {
+            const float p = __builtin_amdgcn_exp2f(__builtin_fmaf(sc[r], scale_log2, -m_ref));
+            sum += p;
+            pb[r >> 3][r & 7] = _Float16(p);
+        }
+        l_run += sum;  // this lane's keys only; the two lane halves are summed once, at the end
+        // O^T += V^T P^T: 32-dim tiles dt, the block's keys as two k-steps t of 16
+#pragma unroll
+        for (int f = 0; f < DT * 2; f++) {
+            const int dt = f >> 1, t = f & 1;
+            if (f + PF < DT * 2) va[(f + PF) % RING] = *reinterpret_cast<const half8_t*>(vf + (f + PF) * 1024);
             __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-            for (int t = 0; t < QT; t++) o[t][dt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(va[dt % RING], pb[t], o[t][dt], 0, 0, 0);
+            o[dt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(va[f % RING], pb[t], o[dt], 0, 0, 0);
         }
-        b = b + 1 == NS ? 0 : b + 1;
+        b ^= 1;
     }
 #undef MQ_ISSUE
     wait_vmcnt<0>();
+    l_run = sum_over_lane_halves(l_run);
+    if (qi >= len) return;
+    const float inv = l_run > 0.0f ? 1.0f / l_run : 0.0f;
+    // o[dt] register 4 g + e: dim 32 dt + 8 g + 4 (l / 32) + e of query qi; outputs [rows][H][HO]
+    _Float16* op = reinterpret_cast<_Float16*>(Og) + (size_t)(seq_start + qi) * (H * HO) + h * HO + 4 * hi;
 #pragma unroll
-    for (int t = 0; t < QT; t++) l_run[t] = sum_over_key_groups(l_run[t]);
+    for (int dt = 0; dt < DT; dt++)
 #pragma unroll
-    for (int t = 0; t < QT; t++) {
-        const int qi = qbase + 16 * t + l16;
-        if (qi >= len) continue;
-        const float inv = l_run[t] > 0.0f ? 1.0f / l_run[t] : 0.0f;
-        _Float16* op = reinterpret_cast<_Float16*>(Og) + (size_t)(seq_start + qi) * (H * HO) + h * HO + 4 * g4;
-#pragma unroll
-        for (int dt = 0; dt < DTO; dt++) {
-            if (HO < HD && 16 * dt + 4 * g4 >= HO) continue;
+        for (int g = 0; g < 4; g++) {
+            if (32 * dt + 8 * g >= HO) continue;
             half4_t v4;
 #pragma unroll
-            for (int r = 0; r < 4; r++) v4[r] = _Float16(o[t][dt][r] * inv);
-            *reinterpret_cast<half4_t*>(op + dt * 16) = v4;
+            for (int e = 0; e < 4; e++) v4[e] = _Float16(o[dt][4 * g + e] * inv);
+            *reinterpret_cast<half4_t*>(op + 32 * dt + 8 * g) = v4;
         }
-    }
 }
 
 bool attention_padded_supported(int hp, int hd, int H, int KV) { return hp == 96 && hd == 72 && H > 0 && KV == H; }
@@ -1288,13 +1297,15 @@ hipError_t launch_attention_padded(hipStream_t s, const uint16_t* q, const uint1
         return hipErrorInvalidValue;
     if (n_work == 0) return hipSuccess;
     const float scale_log2 = scale * 1.4426950408889634f;
-    // 256-query items: eight waves of two 16-query tiles share each K/V block copied into LDS
+    // 256-query items: eight waves of 32 queries share each K/V block copied into LDS; 64-query
+    // items (small batches): two
+    constexpr uint32_t lds = uint32_t(attention_mq_lds_bytes<96, 80>());
     if (item_queries == 256)
-        launch_kernel(attention_mq_kernel<96, 8, 2, 72>, dim3(n_work, KV), dim3(8 * 64), uint32_t(attention_v3_lds_bytes<96>()),
-                      s, q, k, vt, o, work, H, vt_cols, scale_log2);
+        launch_kernel(attention_mq_kernel<96, 80, 8, 72>, dim3(n_work, KV), dim3(8 * 64), lds, s, q, k, vt, o, work, H, vt_cols,
+                      scale_log2);
     else
-        launch_kernel(attention_mq_kernel<96, 4, 1, 72>, dim3(n_work, KV), dim3(4 * 64), uint32_t(attention_v3_lds_bytes<96>()),
-                      s, q, k, vt, o, work, H, vt_cols, scale_log2);
+        launch_kernel(attention_mq_kernel<96, 80, 2, 72>, dim3(n_work, KV), dim3(2 * 64), lds, s, q, k, vt, o, work, H, vt_cols,
+                      scale_log2);
     return hipGetLastError();
 }
 
