@@ -99,6 +99,18 @@ def test_config2_pooled_vs_oracle(c2_model, c2_oracle, config2_batch):
     assert worst_abs < 1e-4
 
 
+def test_1500_token_text_vs_oracle(c2_model, c2_oracle, config2_batch):
+    """The reference's GPU-vs-oracle check at its size (MetalForwardTests.swift:198-215): one
+    1500-token text, cosine > 0.99999 and max |d| < 1e-4 of the normalised vectors, here on the
+    config-2 model at default precision (sliding layers clip to their 512-token window)."""
+    text = (config2_batch[5] + config2_batch[6] + config2_batch[7])[:1500]
+    got = c2_model.embed_tokens([text])[0]
+    want, _ = c2_oracle.forward(text)
+    d = float(np.abs(normalised(got) - normalised(want)).max())
+    print(f"1500 tokens: cosine {cosine(got, want):.9f}, max |d| {d:.3g}", flush=True)
+    assert cosine(got, want) > 0.99999 and d < 1e-4
+
+
 def test_config2_per_layer_vs_oracle(c2_model, c2_oracle, config2_batch):
     names = [("l_out", l) for l in range(24)] + [("Qcur_pos", 0), ("Kcur_pos", 5), ("Vcur_normed", 5),
                                                   ("kqv_out", 0), ("kqv_out", 5), ("ffn_geglu", 3),

@@ -99,6 +99,24 @@ def test_gemm_f16_output_and_row_independence(ctx, c2):
     assert np.array_equal(y32[131:140], y_part)
 
 
+@pytest.mark.parametrize("name", ["blk.2.attn_output.weight", "blk.2.ffn_down.weight"])
+def test_gemm_row_boundaries_bitwise(ctx, c2, name):
+    """The reference's batch-register GEMM check (BatchRegisterGemmTests.swift:81-137): a row's
+    result is the same bits at every batch size. The 768-wide projections change kernel and tile
+    with the row count (skinny up to 512, 128 x 128 below 6144, 128 x 256 below 12288, 256 x 256
+    above); each batch below is compared with the same rows of a 16384-row launch."""
+    shape, _, _ = c2.tensors[name]
+    cols, rows = shape
+    raw = np.asarray(c2.raw(name))
+    x16 = f16_round(RNG.standard_normal((16384, cols)))
+    full = run_gemm(ctx, raw, rows, cols, x16, y_f16=True)
+    for M in (1, 63, 64, 65, 511, 512, 513, 2047, 2048, 2049, 6143, 6144, 8192, 12287, 12288, 12289):
+        lo = min(777, 16384 - M)
+        print(f"{name}: rows [{lo}, {lo + M}) against the 16384-row launch", flush=True)
+        part = run_gemm(ctx, raw, rows, cols, x16[lo:lo + M].copy(), y_f16=True)
+        assert np.array_equal(full[lo:lo + M], part), M
+
+
 @pytest.mark.parametrize("name,y_f16", [("blk.1.attn_q.weight", False), ("blk.1.ffn_down.weight", True),
                                          ("output.weight", False)])
 def test_gemm_short_batches_match_tiled_rows(ctx, c2, name, y_f16):
