@@ -1099,13 +1099,19 @@ hipError_t launch_attention_split(hipStream_t s, const uint16_t* q, const uint16
 // the work per MFMA cycle. S^T = K Q^T over HS dims (the real HO rounded up to 16: 80 for 72, where
 // 16x16x32 steps needed 96), O^T = V^T P^T over the stored HD dims in 32-dim tiles.
 //
-// LDS per block of 32 keys, in fragment order (1 KB chunk = one operand fragment, lane l's 16
-// bytes at 16 l):
-//   K chunk ks (16 dims): lane l holds key pi(l % 32), dims 16 ks + 8 (l / 32) + [0, 8), where pi
-//     swaps the 4s and 8s bits of the row. With that key order, register r of a lane's S^T tile
-//     holds key 16 (r / 8) + 8 (l / 32) + r % 8 of query l % 32, so registers 8 t .. 8 t + 7 are
-//     the B operand of the P.V k-step t (keys 16 t + 8 (l / 32) + [0, 8)) with no data exchange;
-//   V^T chunk (dt, t): lane l holds dim 32 dt + l % 32, keys 16 t + 8 (l / 32) + [0, 8).
+// LDS per block of 32 keys, filled by coalesced copies (each copy instruction reads whole key rows
+// of K and whole key runs of V^T, not one 16-byte piece of 64 rows; with 16-byte pieces per row the
+// texture units' return path was busy 78% of the kernel):
+//   K: key-major rows of HS / 8 + 1 16-byte pieces (the last a pad, never read; the odd row
+//     stride makes the fragment reads conflict-free). The S^T MFMA's A operand for k-step ks is
+//     lane l: key pi(l % 32), piece 2 ks + l / 32, where pi swaps the 4s and 8s bits of the row.
+//     With that key order, register r of a lane's S^T tile holds key 16 (r / 8) + 8 (l / 32) + r % 8
+//     of query l % 32, so registers 8 t .. 8 t + 7 are the B operand of the P.V k-step t (keys
+//     16 t + 8 (l / 32) + [0, 8)) with no data exchange;
+//   V^T: dim-major rows of 5 pieces (32 keys, a pad) for the HO real dims. The P.V MFMA's A operand
+//     (dt, t) is lane l: dim 32 dt + l % 32, piece 2 t + l / 32. Dims HO .. HD - 1 come from a
+//     constant area written once: zeros, except dim HO, all ones, so that row HO of O^T is the sum
+//     of the fp16 P the products used, the softmax denominator, with no VALU additions.
 // A query's 32 scores of a block sit in lanes q and q + 32: its block max is one lane swap.
 __device__ __forceinline__ float max_over_lane_halves(float v) {
     const auto b = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
@@ -1122,8 +1128,15 @@ constexpr int NS = 2;    // key blocks in LDS
 constexpr int BKV = 32;  // keys per block
 }  // namespace attnp
 
-template <int HD, int HS>
-constexpr int attention_mq_lds_bytes() { return attnp::NS * (HS / 16 + (HD / 32) * 2) * 1024; }
+// Pieces per K row and per V^T row, and the 1 KB chunks a block's copies fill.
+template <int HS>
+constexpr int mq_k_chunks() { return (attnp::BKV * (HS / 8 + 1) + 63) / 64; }
+template <int HO>
+constexpr int mq_v_chunks() { return (HO * (attnp::BKV / 8 + 1) + 63) / 64; }
+template <int HD, int HS, int HO>
+constexpr int attention_mq_lds_bytes() {
+    return attnp::NS * (mq_k_chunks<HS>() + mq_v_chunks<HO>()) * 1024 + (HD - HO) * (attnp::BKV / 8 + 1) * 16;
+}
 
 template <int HD, int HS, int QW, int HO>
 __global__ __launch_bounds__(QW * 64) void attention_mq_kernel(const uint16_t* __restrict__ Qg,
@@ -1134,9 +1147,12 @@ __global__ __launch_bounds__(QW * 64) void attention_mq_kernel(const uint16_t* _
                                                                float scale_log2) {
     using namespace attnp;
     constexpr int KSS = HS / 16, DT = HD / 32;
-    constexpr int KCH = KSS, VCH = DT * 2, CH = KCH + VCH, STAGE = CH * 1024;
+    constexpr int KP = HS / 8 + 1, KPIECES = BKV * KP, KCH = mq_k_chunks<HS>();
+    constexpr int VP = BKV / 8 + 1, VPIECES = HO * VP, VCH = mq_v_chunks<HO>();
+    constexpr int CH = KCH + VCH, STAGE = CH * 1024, VOFF = KCH * 1024;
     constexpr int CPW = (CH + QW - 1) / QW;  // copies per wave per block (some waves repeat one)
-    static_assert(HO <= HS && HS <= HD && HS % 16 == 0 && HD % 32 == 0 && HO % 8 == 0, "head dims");
+    constexpr int CONST_OFF = NS * STAGE, CONST_BYTES = (HD - HO) * VP * 16;
+    static_assert(HO <= HS && HS <= HD && HS % 16 == 0 && HD % 32 == 0 && HO % 32 == 8, "head dims (row sum in register 4)");
     static_assert(QW <= CH, "a wave past the last chunk repeats its own chunk index");
     extern __shared__ __attribute__((aligned(1024))) unsigned char ldsm[];
 
@@ -1156,27 +1172,42 @@ __global__ __launch_bounds__(QW * 64) void attention_mq_kernel(const uint16_t* _
     const int stride = H * HD;
     const int nblocks = (len + BKV - 1) / BKV;
 
+    // Keys past the sequence read as zeros (the resource ends at its last row); their scores are
+    // masked below.
     const __amdgpu_buffer_rsrc_t kr =
         buffer_rsrc(Kg + (size_t)seq_start * stride + h * HD, uint32_t(((len - 1) * stride + HD) * 2));
     const __amdgpu_buffer_rsrc_t vr = buffer_rsrc(VTg + (size_t)h * HD * vt_cols + vt_start,
                                                   uint32_t(((HD - 1) * vt_cols + (vt_cols - vt_start)) * 2));
-    const int krow = (l32 & 16) | ((l32 & 4) << 1) | ((l32 & 8) >> 1) | (l32 & 3);  // pi(l % 32)
-    const uint32_t klane = uint32_t((krow * stride + 8 * hi) * 2);
-    const uint32_t vlane = uint32_t((l32 * vt_cols + 8 * hi) * 2);
+    // This wave's chunks and each lane's source at block 0: piece p of the block's K rows or V^T
+    // rows; a pad piece (and a lane past the last piece) re-reads its row's first piece into a
+    // place no fragment read touches.
+    uint32_t src[CPW];
+    int chk[CPW];
+#pragma unroll
+    for (int i = 0; i < CPW; i++) {
+        int c = wave + i * QW;
+        if (c >= CH) c = wave;
+        chk[i] = c;
+        if (c < KCH) {
+            const int pz = c * 64 + lane, key = pz < KPIECES ? pz / KP : 0, pc = pz < KPIECES ? pz % KP : 0;
+            src[i] = uint32_t((key * stride + 8 * (pc < KP - 1 ? pc : 0)) * 2);
+        } else {
+            const int pz = (c - KCH) * 64 + lane, dim = pz < VPIECES ? pz / VP : 0, pc = pz < VPIECES ? pz % VP : 0;
+            src[i] = uint32_t((dim * vt_cols + 8 * (pc < VP - 1 ? pc : 0)) * 2);
+        }
+    }
 #define MQ_ISSUE(kb, b)                                                                                    \
     do {                                                                                                   \
         _Pragma("unroll") for (int i = 0; i < CPW; i++) {                                                  \
-            int c = wave + i * QW;                                                                         \
-            if (c >= CH) c = wave;                                                                         \
-            unsigned char* dst_ = ldsm + (b) * STAGE + c * 1024;                                           \
-            if (c < KCH) {                                                                                 \
-                lds_copy16(kr, dst_, klane + uint32_t((kb) * stride * 2 + c * 32), 0);                      \
-            } else {                                                                                       \
-                const int vc_ = c - KCH, dt_ = vc_ >> 1, t_ = vc_ & 1;                                     \
-                lds_copy16(vr, dst_, vlane + uint32_t((dt_ * 32 * vt_cols + (kb) + 16 * t_) * 2), 0);      \
-            }                                                                                              \
+            unsigned char* dst_ = ldsm + (b) * STAGE + chk[i] * 1024;                                      \
+            if (chk[i] < KCH) lds_copy16(kr, dst_, src[i] + uint32_t((kb) * stride * 2), 0);               \
+            else lds_copy16(vr, dst_, src[i] + uint32_t((kb) * 2), 0);                                     \
         }                                                                                                  \
     } while (0)
+
+    // the constant V^T rows HO .. HD - 1 (ones in row HO, keys and pad), read after the first barrier
+    for (int i = int(threadIdx.x); i < CONST_BYTES / 4; i += QW * 64)
+        reinterpret_cast<uint32_t*>(ldsm + CONST_OFF)[i] = i < VP * 4 ? 0x3c003c00u : 0u;
 
     // This wave's query fragments (B operand of S^T = K Q^T): lane l: query qi (rows past the
     // sequence re-read its last row; their outputs are never stored), dims 16 ks + 8 (l / 32).
@@ -1189,14 +1220,26 @@ __global__ __launch_bounds__(QW * 64) void attention_mq_kernel(const uint16_t* _
         for (int ks = 0; ks < KSS; ks++)
             qa[ks] = __builtin_bit_cast(half8_t, __builtin_amdgcn_raw_buffer_load_b128(qr, qo + ks * 32, 0, 0));
     }
+    // fragment offsets in a block's buffer: K (key pi(l % 32), piece hi), V^T (dim 32 dt + l % 32,
+    // piece hi; dims past HO in the constant area, offsets from the start of LDS)
+    const int krow = (l32 & 16) | ((l32 & 4) << 1) | ((l32 & 8) >> 1) | (l32 & 3);  // pi(l % 32)
+    const int koff = (krow * KP + hi) * 16;
+    int voff[DT];
+    bool vconst[DT];
+#pragma unroll
+    for (int dt = 0; dt < DT; dt++) {
+        const int dim = 32 * dt + l32;
+        vconst[dt] = dim >= HO;
+        voff[dt] = dim < HO ? VOFF + (dim * VP + hi) * 16 : CONST_OFF + ((dim - HO) * VP + hi) * 16;
+    }
     float16_t o[DT];
 #pragma unroll
     for (int i = 0; i < DT; i++)
 #pragma unroll
         for (int r = 0; r < 16; r++) o[i][r] = 0.0f;
-    float m_run = -INFINITY, l_run = 0.0f;
+    float m_run = -INFINITY;
 
-    if (0 < nblocks) MQ_ISSUE(0, 0);
+    MQ_ISSUE(0, 0);
     int b = 0;
     for (int it = 0; it < nblocks; it++) {
         const int kb = it * BKV;
@@ -1206,26 +1249,26 @@ __global__ __launch_bounds__(QW * 64) void attention_mq_kernel(const uint16_t* _
         wait_lgkmcnt0();
         workgroup_barrier();
         if (it + 1 < nblocks) MQ_ISSUE(kb + BKV, b ^ 1);
-        const unsigned char* const kf = ldsm + b * STAGE + lane * 16;
-        const unsigned char* const vf = kf + KCH * 1024;
-        constexpr int PF = 2, RING = PF + 1;
+        const unsigned char* const kb_lds = ldsm + b * STAGE;
         float16_t s;
 #pragma unroll
         for (int r = 0; r < 16; r++) s[r] = 0.0f;
-        half8_t ka[RING];
+        half8_t ka[KSS];
 #pragma unroll
-        for (int f = 0; f < PF && f < KSS; f++) ka[f] = *reinterpret_cast<const half8_t*>(kf + f * 1024);
+        for (int f = 0; f < KSS; f++) ka[f] = *reinterpret_cast<const half8_t*>(kb_lds + koff + f * 32);
 #pragma unroll
         for (int ks = 0; ks < KSS; ks++) {
-            if (ks + PF < KSS) ka[(ks + PF) % RING] = *reinterpret_cast<const half8_t*>(kf + (ks + PF) * 1024);
             // keep the reads ahead of the MFMAs (the scheduler would otherwise sink them)
             __builtin_amdgcn_sched_barrier(0);
-            s = __builtin_amdgcn_mfma_f32_32x32x16_f16(ka[ks % RING], qa[ks], s, 0, 0, 0);
+            s = __builtin_amdgcn_mfma_f32_32x32x16_f16(ka[ks], qa[ks], s, 0, 0, 0);
         }
-        // the first V^T fragments are read while the softmax runs
-        half8_t va[RING];
+        // the V^T fragments are read while the softmax runs
+        half8_t va[DT * 2];
 #pragma unroll
-        for (int f = 0; f < PF; f++) va[f] = *reinterpret_cast<const half8_t*>(vf + f * 1024);
+        for (int f = 0; f < DT * 2; f++) {
+            const int dt = f >> 1, t = f & 1;
+            va[f] = *reinterpret_cast<const half8_t*>((vconst[dt] ? ldsm : kb_lds) + voff[dt] + t * 32);
+        }
         // register r: key kb + 16 (r / 8) + 8 (l / 32) + r % 8 of query qi
         float sc[16];
 #pragma unroll
@@ -1238,42 +1281,37 @@ __global__ __launch_bounds__(QW * 64) void attention_mq_kernel(const uint16_t* _
 #pragma unroll
         for (int r = 1; r < 16; r++) lmax = fmaxf(lmax, sc[r]);
         // lazy rescaling, as in attention_v3_kernel: the reference point moves only when a score
-        // exceeds it by more than 2^8, so P stays below 256
+        // exceeds it by more than 2^8, so P stays below 256; rescaling O^T rescales its row-sum row
         if (__builtin_amdgcn_ballot_w64(lmax * scale_log2 > m_run + 8.0f)) {
             const float bmax = max_over_lane_halves(lmax) * scale_log2;
             const float m_new = fmaxf(m_run, bmax);
             const float alpha = m_new == -INFINITY ? 1.0f : __builtin_amdgcn_exp2f(m_run - m_new);
-            l_run *= alpha;
 #pragma unroll
             for (int i = 0; i < DT; i++) o[i] *= alpha;
             m_run = m_new;
         }
         const float m_ref = m_run == -INFINITY ? 0.0f : m_run;
-        float sum = 0.0f;
         half8_t pb[2];
 #pragma unroll
-        for (int r = 0; r < 16; r++) {
-            const float p = __builtin_amdgcn_exp2f(__builtin_fmaf(sc[r], scale_log2, -m_ref));
-            sum += p;
-            pb[r >> 3][r & 7] = _Float16(p);
-        }
-        l_run += sum;  // this lane's keys only; the two lane halves are summed once, at the end
+        for (int r = 0; r < 16; r++)
+            pb[r >> 3][r & 7] = _Float16(__builtin_amdgcn_exp2f(__builtin_fmaf(sc[r], scale_log2, -m_ref)));
         // O^T += V^T P^T: 32-dim tiles dt, the block's keys as two k-steps t of 16
 #pragma unroll
         for (int f = 0; f < DT * 2; f++) {
             const int dt = f >> 1, t = f & 1;
-            if (f + PF < DT * 2) va[(f + PF) % RING] = *reinterpret_cast<const half8_t*>(vf + (f + PF) * 1024);
             __builtin_amdgcn_sched_barrier(0);
-            o[dt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(va[f % RING], pb[t], o[dt], 0, 0, 0);
+            o[dt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(va[f], pb[t], o[dt], 0, 0, 0);
         }
         b ^= 1;
     }
 #undef MQ_ISSUE
     wait_vmcnt<0>();
-    l_run = sum_over_lane_halves(l_run);
+    // o[dt] register 4 g + e: dim 32 dt + 8 g + 4 (l / 32) + e of query qi, so the row sum (dim HO,
+    // register 4 of tile HO / 32) sits in lane qi % 32
+    const float lsum = __shfl(o[HO / 32][4], l32, 64);
     if (qi >= len) return;
-    const float inv = l_run > 0.0f ? 1.0f / l_run : 0.0f;
-    // o[dt] register 4 g + e: dim 32 dt + 8 g + 4 (l / 32) + e of query qi; outputs [rows][H][HO]
+    const float inv = lsum > 0.0f ? 1.0f / lsum : 0.0f;
+    // outputs [rows][H][HO]
     _Float16* op = reinterpret_cast<_Float16*>(Og) + (size_t)(seq_start + qi) * (H * HO) + h * HO + 4 * hi;
 #pragma unroll
     for (int dt = 0; dt < DT; dt++)
@@ -1299,7 +1337,7 @@ hipError_t launch_attention_padded(hipStream_t s, const uint16_t* q, const uint1
     const float scale_log2 = scale * 1.4426950408889634f;
     // 256-query items: eight waves of 32 queries share each K/V block copied into LDS; 64-query
     // items (small batches): two
-    constexpr uint32_t lds = uint32_t(attention_mq_lds_bytes<96, 80>());
+    constexpr uint32_t lds = uint32_t(attention_mq_lds_bytes<96, 80, 72>());
     if (item_queries == 256)
         launch_kernel(attention_mq_kernel<96, 80, 8, 72>, dim3(n_work, KV), dim3(8 * 64), lds, s, q, k, vt, o, work, H, vt_cols,
                       scale_log2);
