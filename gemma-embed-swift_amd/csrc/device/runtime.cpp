@@ -1230,6 +1230,17 @@ constexpr size_t kMaxGraphs = 32;
 // the second captures the launches (encode) into a graph, which that run and every later one
 // replays with one launch. The key holds everything the launches' arguments depend on besides
 // the workspace and model addresses, and every graph is dropped when those change.
+// GE_NO_GRAPHS=1 in the environment runs short packs eagerly, launch by launch, as on their
+// first run: the same kernels and bits, for tools that trace kernel dispatches but not graph
+// launches.
+static bool graphs_disabled() {
+    static const bool off = [] {
+        const char* v = std::getenv("GE_NO_GRAPHS");
+        return v && *v && std::strcmp(v, "0") != 0;
+    }();
+    return off;
+}
+
 void run_graph(ge_ctx* c) {
     const int key[6] = {c->staged_tokens, c->staged_seqs, c->staged_work, c->staged_work2, c->ws.vt_cap, c->attn_items};
     ShortGraph* g = nullptr;
@@ -1237,7 +1248,12 @@ void run_graph(ge_ctx* c) {
         if (std::equal(key, key + 6, x.key)) g = &x;
     if (!g) {
         if (c->graphs.size() >= kMaxGraphs) {
-            if (c->graphs.front().exec) (void)hipGraphExecDestroy(c->graphs.front().exec);
+            // a launch of the oldest graph may still be queued (ge_batch_run returns before the
+            // GPU is done): its executable is destroyed only once the streams are idle
+            if (c->graphs.front().exec) {
+                drain(c);
+                (void)hipGraphExecDestroy(c->graphs.front().exec);
+            }
             c->graphs.erase(c->graphs.begin());
         }
         ShortGraph n;
@@ -1299,7 +1315,7 @@ void run_forward(ge_ctx* c, double* gpu_seconds, bool record_start) {
     if (record_start) hip_check(hipEventRecord(c->ev_start, c->stream), "hipEventRecord");
     if (c->n_parts > 1 && !c->prof)
         encode_split(c);
-    else if (!c->prof && c->staged_tokens <= kGraphMaxTokens && !c->staged_vectors)  // graphs hold no vector source
+    else if (!c->prof && !graphs_disabled() && c->staged_tokens <= kGraphMaxTokens && !c->staged_vectors)  // graphs hold no vector source
         run_graph(c);
     else
         encode(c, nullptr);
