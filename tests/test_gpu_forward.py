@@ -337,6 +337,40 @@ def test_short_pack_graph_replays_match_eager(c2_model, config2_batch, c2_oracle
     assert cosine(replayed[0], want) >= COSINE_BAR
 
 
+def test_short_pack_graph_cache_eviction(config2_gguf, config2_batch):
+    """A context keeps the graphs of at most 32 short-pack shapes; a 33rd shape evicts the oldest.
+    Here the oldest graph's replay is still queued (ge_batch_run returns before the GPU is done)
+    when the new shape evicts it: the eviction waits for the streams, and every result equals
+    the shape's eager run bitwise. A fresh model, so that the cache starts empty and the 32 shapes
+    below fill it in order."""
+    m = ge.EmbeddingModel.load(config2_gguf, batch_token_budget=8192)
+    try:
+        _graph_cache_eviction(m.context, config2_batch[21])
+    finally:
+        m.close()
+
+
+def _graph_cache_eviction(ctx, text):
+    lengths = list(range(64, 32, -1))  # 32 shapes, the largest first (the workspace never grows)
+    first = {}
+    for n in lengths:
+        first[n], _ = ctx.forward([text[:n]])  # eager: records the shape
+        again, _ = ctx.forward([text[:n]])  # captured, then replayed
+        assert np.array_equal(again, first[n]), n
+    oldest, new = lengths[0], 32
+    ctx.batch_stage([text[:oldest]])
+    ctx.batch_run()  # replays the oldest graph; not waited for
+    ctx.batch_stage([text[:new]])
+    ctx.batch_run()  # a 33rd shape: evicts the oldest graph, then runs eagerly
+    got_new = ctx.batch_read()
+    want_new, _ = ctx.forward([text[:new]])  # the same shape again: captured and replayed
+    assert np.array_equal(got_new, want_new)
+    for n in (oldest, oldest, oldest, 40):
+        got, _ = ctx.forward([text[:n]])  # the evicted shape is recorded, captured and replayed again
+        assert np.array_equal(got, first[n]), n
+    print("33 short-pack shapes: eviction of a queued graph, all runs bitwise equal", flush=True)
+
+
 def test_embed_api_options(c2_model, config2_batch):
     texts = [t[: 20 + 37 * i] for i, t in enumerate(config2_batch[:10])]
     full = c2_model.embed(texts, ge.EmbedOptions(normalise=False))
