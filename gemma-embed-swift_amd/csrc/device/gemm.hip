@@ -136,6 +136,10 @@ struct GemmCfg {
 using GemmWide = GemmCfg<128, 256, 2, 4, 32, 3>;
 using GemmSquare = GemmCfg<256, 256, 4, 4, 64, 2>;
 using GemmSmall = GemmCfg<128, 128, 2, 2, 64, 2>;
+// 256 x 192 tiles of 4 x 2 waves of 64 x 96 (three column fragments, so no GeGLU pairs), K in
+// stages of 64, two stages (112 KB): the 768-wide projections over many rows (768 = 4 x 192:
+// 256 tiles at 16384 rows, one per CU).
+using GemmNarrow = GemmCfg<256, 192, 4, 2, 64, 2>;
 
 // Workgroup b's tile: workgroups are dealt to the 8 XCDs round robin (b runs on XCD b % 8), and
 // tile (b % 8) * (T / 8) + b / 8 gives each XCD a contiguous, M-major run of tiles.
@@ -602,7 +606,8 @@ hipError_t gemm_configure_shape() {
     if constexpr (C::LDS <= 65536) return hipSuccess;
     hipError_t e = set_lds_limit(gemm_kernel<C, kEpiF32>, C::LDS);
     if (e == hipSuccess) e = set_lds_limit(gemm_kernel<C, kEpiF16>, C::LDS);
-    if (e == hipSuccess) e = set_lds_limit(gemm_kernel<C, kEpiGeglu>, C::LDS);
+    if constexpr (C::FN % 2 == 0)
+        if (e == hipSuccess) e = set_lds_limit(gemm_kernel<C, kEpiGeglu>, C::LDS);
     if (e == hipSuccess) e = set_lds_limit(gemm_kernel<C, kEpiGeluBias>, C::LDS);
     if (e == hipSuccess) e = set_lds_limit(gemm_kernel<C, kEpiHeads>, C::LDS);
     return e;
@@ -612,6 +617,7 @@ hipError_t gemm_configure() {
     hipError_t e = gemm_configure_shape<GemmWide>();
     if (e == hipSuccess) e = gemm_configure_shape<GemmSquare>();
     if (e == hipSuccess) e = gemm_configure_shape<GemmSmall>();
+    if (e == hipSuccess) e = gemm_configure_shape<GemmNarrow>();
     if (e == hipSuccess) e = set_lds_limit(gemm_qkv_kernel<128>, GemmWide::LDS);
     if (e == hipSuccess) e = set_lds_limit(gemm_qkv_kernel<256>, GemmWide::LDS);
     return e;
@@ -631,7 +637,10 @@ hipError_t gemm_launch(hipStream_t s, const Q8Dev& w, const uint16_t* x, int M, 
         launch_kernel(gemm_kernel<C, kEpiF16>, grid, block, C::LDS, s, x, w.fh, y, M, N, K, out_scale, tiles_n, tiles, ea);
         break;
     case kEpiGeglu:
-        launch_kernel(gemm_kernel<C, kEpiGeglu>, grid, block, C::LDS, s, x, w.fh, y, M, N, K, out_scale, tiles_n, tiles, ea);
+        if constexpr (C::FN % 2 == 0)
+            launch_kernel(gemm_kernel<C, kEpiGeglu>, grid, block, C::LDS, s, x, w.fh, y, M, N, K, out_scale, tiles_n, tiles, ea);
+        else
+            return hipErrorInvalidValue;  // the GeGLU epilogue pairs column fragments
         break;
     case kEpiGeluBias:
         launch_kernel(gemm_kernel<C, kEpiGeluBias>, grid, block, C::LDS, s, x, w.fh, y, M, N, K, out_scale, tiles_n, tiles, ea);
@@ -718,14 +727,21 @@ hipError_t launch_gemm_q8(hipStream_t s, const Q8Dev& w, const uint16_t* x, int 
         default: return hipErrorInvalidValue;
         }
     }
-    // The 768-wide projections (o, down, output) by batch rows, from a sweep of the tile shapes
-    // (the timed config-2 forward launches them at M = 8192, two at a time): 256 x 256 tiles from
-    // 12288 rows, 128 x 256 from 6144, 128 x 128 (K in stages of 64) below. The tile shape does
-    // not change the results: every shape runs the same MFMA over the same k order.
-    // The widest projections (the image tower's QKV, 3456 outputs, and MLP up, 4352) at 8 x 2304
-    // patch rows: 256 x 256 tiles 8-10% faster than 128 x 256 (142.7 against 155.8 us and 174.9
-    // against 193.7 us); 2304-wide gate/up stays on 128 x 256 (67.2 against 71.5 us).
+    // Tile shapes by projection and batch rows, from sweeps of the shapes (20 launches back to
+    // back, one box). The tile shape does not change the results: every shape runs the same MFMA
+    // over the same k order. The 768-wide projections (o, down): 128 x 128 tiles (K in stages of
+    // 64) below 6144 rows, 128 x 256 from 6144 (the config-2 forward's four parts launch them at
+    // 4096 rows each). From 12288 rows the fp16-output projections whose width 192 divides
+    // (768: o and down) take 256 x 192 tiles: at 16384 rows o 22.6 against 23.2 us (256 x 256),
+    // down 30.0 against 31.0. With fp32 outputs (the image tower's o and down, 1152 wide, into
+    // the residual stream) they lost inside the tower, o 72.1 against 63.2 us and down 228.7
+    // against 203.3 (128 x 256): a 256 x 192 workgroup holds a whole CU, so its twice larger
+    // stores overlap no other workgroup's main loop. The widest projections (the tower's QKV,
+    // 3456 outputs, and MLP up, 4352) take 256 x 256 tiles: 139.1 against 151.1 us and 190.4
+    // against 203.9. The 2304-wide gate/up stays on 128 x 256 (65.0 against 69.9 us).
     if (w.cols % GemmSquare::BK == 0) {
+        if (M >= 12288 && w.rows <= 1152 && w.rows % GemmNarrow::BN == 0 && epi == kEpiF16)
+            return gemm_launch<GemmNarrow>(s, w, x, M, y, epi, out_scale, ea);
         if (w.rows <= 1024 && M >= 12288) return gemm_launch<GemmSquare>(s, w, x, M, y, epi, out_scale, ea);
         if (w.rows <= 1024 && M < 6144) return gemm_launch<GemmSmall>(s, w, x, M, y, epi, out_scale, ea);
         if (w.rows >= 3072 && M >= 12288) return gemm_launch<GemmSquare>(s, w, x, M, y, epi, out_scale, ea);
