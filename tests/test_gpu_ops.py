@@ -103,8 +103,8 @@ def test_gemm_f16_output_and_row_independence(ctx, c2):
 def test_gemm_row_boundaries_bitwise(ctx, c2, name):
     """The reference's batch-register GEMM check (BatchRegisterGemmTests.swift:81-137): a row's
     result is the same bits at every batch size. The 768-wide projections change kernel and tile
-    with the row count (skinny up to 512, 128 x 128 below 6144, 128 x 256 below 12288, 256 x 256
-    above); each batch below is compared with the same rows of a 16384-row launch."""
+    with the row count (skinny up to 512, 128 x 128 below 6144, 128 x 256 below 12288, 256 x 192
+    from there); each batch below is compared with the same rows of a 16384-row launch."""
     shape, _, _ = c2.tensors[name]
     cols, rows = shape
     raw = np.asarray(c2.raw(name))
