@@ -211,6 +211,33 @@ def test_gemm_geglu_short_batch_matches_tiled_rows(ctx, c2):
         ctx.q8_destroy(u)
 
 
+def test_gemm_geglu_row_boundaries_bitwise(ctx, c2):
+    """Gate/up rows at every batch size against a 16384-row launch. Launches whose 128 x 256 tiles
+    leave a last partial round of workgroup slots run those tiles as 128 x 128 halves (16384 rows:
+    1024 whole tiles and 256 halves; 8192: 512 and 128); a row's bits must not depend on which."""
+    x16 = f16_round(RNG.standard_normal((16384, 768)) * 0.05)
+    g = ctx.q8_create(np.asarray(c2.raw("blk.3.ffn_gate.weight")), 1152, 768)
+    u = ctx.q8_create(np.asarray(c2.raw("blk.3.ffn_up.weight")), 1152, 768)
+
+    def geglu(x):
+        dx, da = ctx.alloc(x.nbytes), ctx.alloc(x.shape[0] * 1152 * 2)
+        try:
+            ctx.upload(dx, x)
+            ctx.gemm_q8_geglu(g, u, dx, x.shape[0], da)
+            return ctx.download(da, (x.shape[0], 1152), np.float16)
+        finally:
+            ctx.free(dx)
+            ctx.free(da)
+    try:
+        full = geglu(x16)
+        for M, lo in ((16383, 1), (8192, 8187), (9000, 7000), (4096, 12288), (600, 15784), (64, 16320)):
+            print(f"gate/up rows [{lo}, {lo + M}) against the 16384-row launch", flush=True)
+            assert np.array_equal(full[lo:lo + M], geglu(x16[lo:lo + M].copy())), (M, lo)
+    finally:
+        ctx.q8_destroy(g)
+        ctx.q8_destroy(u)
+
+
 def test_gemm_geglu_vs_oracle(ctx, c2):
     M = 333
     x16 = f16_round(RNG.standard_normal((M, 768)) * 0.05)
