@@ -124,7 +124,9 @@ struct StopPoint {
 // (head dim 512) at 1.1e-2 max relative error against the fp32 oracle.
 constexpr int kPreciseHeadDim = 512;
 
-constexpr int kMaxParts = 4;  // streams a large batch is split over (measured 2, 3, 4: 5.93, 5.93, 5.85 ms at config 2)
+// Streams a large batch is split over (measured 2, 3, 4: 5.93, 5.93, 5.85 ms at config 2; with
+// 8192-row parts' gate/up launches ending in half tiles, 2 parts 6.18 against 4 parts 6.15 ms).
+constexpr int kMaxParts = 4;
 
 // A short pack's forward captured as a HIP graph, keyed by everything its launches' arguments
 // depend on (see run_graph); exec is null while the shape has been seen only once.
