@@ -170,6 +170,20 @@ def test_config5_batch_of_eight_bitwise(config5):
         assert np.array_equal(alone, batch[i * 256:(i + 1) * 256]), i
 
 
+def test_config5_three_images_bitwise(config5):
+    """Three images (6912 patch rows): the QKV (head-padded epilogue) and MLP-up (GELU and bias)
+    launches take 128 x 256 tiles whose last partial round runs as half tiles; each image's
+    vectors must equal its own single-image run, which has no partial round to split."""
+    c, o = config5
+    grids = [(48, 48)] * 3
+    patches = ge.image_patches(33, grids, o.area)
+    batch, _ = c.vision_encode(patches, grids, o.proj_dims)
+    assert batch.shape == (3 * 256, 768) and np.all(np.isfinite(batch))
+    for i in range(3):
+        alone, _ = c.vision_encode(patches[i * 2304:(i + 1) * 2304], [(48, 48)], o.proj_dims)
+        assert np.array_equal(alone, batch[i * 256:(i + 1) * 256]), i
+
+
 def test_tower_with_128_wide_heads_and_q8_down(tmp_path):
     """The other head path (head dim 128 through the text path's LDS-copy attention, no padding)
     and a Q8_0 ffn_down, on a small tower with a 2 x 2 merge."""
