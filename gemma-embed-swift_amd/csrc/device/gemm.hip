@@ -6,6 +6,7 @@
 #include "common.hpp"
 #include "kernels.hpp"
 
+#include <atomic>
 #include <type_traits>
 
 namespace ge {
@@ -647,14 +648,15 @@ hipError_t gemm_configure_shape() {
     return e;
 }
 
-// Workgroup slots of a GemmWide launch: two workgroups per CU.
-static int g_wide_slots = 512;
+// Workgroup slots of a GemmWide launch: two workgroups per CU (contexts may be created from
+// several threads; they all store the same device's count).
+static std::atomic<int> g_wide_slots{512};
 
 hipError_t gemm_configure() {
     int dev = 0, cus = 0;
     hipError_t e = hipGetDevice(&dev);
     if (e == hipSuccess) e = hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev);
-    if (e == hipSuccess && cus > 0) g_wide_slots = 2 * cus;
+    if (e == hipSuccess && cus > 0) g_wide_slots.store(2 * cus, std::memory_order_relaxed);
     if (e == hipSuccess) e = gemm_configure_shape<GemmWide>();
     if (e == hipSuccess) e = gemm_configure_shape<GemmSquare>();
     if (e == hipSuccess) e = gemm_configure_shape<GemmSmall>();
@@ -672,7 +674,8 @@ hipError_t gemm_launch(hipStream_t s, const Q8Dev& w, const uint16_t* x, int M, 
     // n_full: the tiles taken whole; a last partial round of slots runs as half tiles (HalfTile)
     int n_full = tiles;
     if constexpr (!std::is_void_v<typename HalfTile<C>::type>)
-        if (tiles > g_wide_slots && tiles % g_wide_slots != 0) n_full = tiles - tiles % g_wide_slots;
+        if (const int slots = g_wide_slots.load(std::memory_order_relaxed); tiles > slots && tiles % slots != 0)
+            n_full = tiles - tiles % slots;
     const dim3 grid(n_full + 2 * (tiles - n_full)), block(C::NT);
     switch (epi) {
     case kEpiF32:
