@@ -212,10 +212,11 @@ def test_gemm_geglu_short_batch_matches_tiled_rows(ctx, c2):
 
 
 def test_gemm_geglu_row_boundaries_bitwise(ctx, c2):
-    """Gate/up rows at every batch size against a 16384-row launch. Launches whose 128 x 256 tiles
-    leave a last partial round of workgroup slots run those tiles as 128 x 128 halves (16384 rows:
-    1024 whole tiles and 256 halves; 8192: 512 and 128); a row's bits must not depend on which."""
-    x16 = f16_round(RNG.standard_normal((16384, 768)) * 0.05)
+    """Gate/up rows at every batch size against a 20000-row launch. Launches whose 128 x 256 tiles
+    leave a last partial round of workgroup slots run those tiles as 128 x 128 halves (20000 rows:
+    1024 whole tiles and 778 halves, more than a round of them; 16384: 1024 and 256; 8192: 512 and
+    128); a row's bits must not depend on which."""
+    x16 = f16_round(RNG.standard_normal((20000, 768)) * 0.05)
     g = ctx.q8_create(np.asarray(c2.raw("blk.3.ffn_gate.weight")), 1152, 768)
     u = ctx.q8_create(np.asarray(c2.raw("blk.3.ffn_up.weight")), 1152, 768)
 
@@ -230,8 +231,8 @@ def test_gemm_geglu_row_boundaries_bitwise(ctx, c2):
             ctx.free(da)
     try:
         full = geglu(x16)
-        for M, lo in ((16383, 1), (8192, 8187), (9000, 7000), (4096, 12288), (600, 15784), (64, 16320)):
-            print(f"gate/up rows [{lo}, {lo + M}) against the 16384-row launch", flush=True)
+        for M, lo in ((16384, 3616), (16383, 1), (8192, 8187), (9000, 7000), (4096, 12288), (600, 19400), (64, 16320)):
+            print(f"gate/up rows [{lo}, {lo + M}) against the 20000-row launch", flush=True)
             assert np.array_equal(full[lo:lo + M], geglu(x16[lo:lo + M].copy())), (M, lo)
     finally:
         ctx.q8_destroy(g)
