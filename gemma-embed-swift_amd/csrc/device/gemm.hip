@@ -145,11 +145,12 @@ using GemmSmall = GemmCfg<128, 128, 2, 2, 64, 2>;
 using GemmNarrow = GemmCfg<256, 192, 4, 2, 64, 2>;
 
 // The half-width tile of GemmWide: the same 8 waves as 4 x 2 blocks of 32 x 64 (so GeGLU pairs
-// stay in one wave) over 128 x 128. A launch whose tiles leave a last partial round of the
-// workgroup slots (two per CU) runs those last tiles as twice as many half tiles: the CUs the
-// partial round would leave idle take the other halves. Every output still comes from the same
-// MFMA over the same k order, so the bits do not change (gate/up at 16384 rows: 68.3 -> 65.5 us,
-// at 8192: 39.4 -> 36.3 us).
+// stay in one wave) over 128 x 128. A launch whose tiles leave a last partial round of at most a
+// quarter of the workgroup slots (two per CU) runs those last tiles as twice as many half tiles:
+// the CUs the partial round would leave idle take the other halves. Every output still comes from
+// the same MFMA over the same k order, so the bits do not change (gate/up at 16384 rows, a quarter
+// round: 65.9 -> 62.9 us; at 8192, an eighth: 39.4 -> 36.3 us). Larger partial rounds lost:
+// 40.6 -> 42.5 us at 10000 rows (0.39 of a round), 54.9 -> 63.1 us at 14000 (0.93).
 template <class C>
 struct HalfTile {
     using type = void;
@@ -674,7 +675,8 @@ hipError_t gemm_launch(hipStream_t s, const Q8Dev& w, const uint16_t* x, int M, 
     // n_full: the tiles taken whole; a last partial round of slots runs as half tiles (HalfTile)
     int n_full = tiles;
     if constexpr (!std::is_void_v<typename HalfTile<C>::type>)
-        if (const int slots = g_wide_slots.load(std::memory_order_relaxed); tiles > slots && tiles % slots != 0)
+        if (const int slots = g_wide_slots.load(std::memory_order_relaxed);
+            tiles > slots && tiles % slots != 0 && tiles % slots <= slots / 4)
             n_full = tiles - tiles % slots;
     const dim3 grid(n_full + 2 * (tiles - n_full)), block(C::NT);
     switch (epi) {

@@ -213,9 +213,9 @@ def test_gemm_geglu_short_batch_matches_tiled_rows(ctx, c2):
 
 def test_gemm_geglu_row_boundaries_bitwise(ctx, c2):
     """Gate/up rows at every batch size against a 20000-row launch. Launches whose 128 x 256 tiles
-    leave a last partial round of workgroup slots run those tiles as 128 x 128 halves (20000 rows:
-    1024 whole tiles and 778 halves, more than a round of them; 16384: 1024 and 256; 8192: 512 and
-    128); a row's bits must not depend on which."""
+    leave a last partial round of at most a quarter of the workgroup slots run those tiles as
+    128 x 128 halves (16384 rows: 1024 whole tiles and 256 halves; 8192: 512 and 128; 20000 rows,
+    0.76 of a round, whole tiles only); a row's bits must not depend on which."""
     x16 = f16_round(RNG.standard_normal((20000, 768)) * 0.05)
     g = ctx.q8_create(np.asarray(c2.raw("blk.3.ffn_gate.weight")), 1152, 768)
     u = ctx.q8_create(np.asarray(c2.raw("blk.3.ffn_up.weight")), 1152, 768)

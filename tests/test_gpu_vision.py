@@ -170,18 +170,24 @@ def test_config5_batch_of_eight_bitwise(config5):
         assert np.array_equal(alone, batch[i * 256:(i + 1) * 256]), i
 
 
-def test_config5_three_images_bitwise(config5):
-    """Three images (6912 patch rows): the QKV (head-padded epilogue) and MLP-up (GELU and bias)
-    launches take 128 x 256 tiles whose last partial round runs as half tiles; each image's
-    vectors must equal its own single-image run, which has no partial round to split."""
+@pytest.mark.parametrize("grids", [
+    [(48, 48)] * 2,                # 4608 rows: the MLP-up launch (GELU and bias) ends in half tiles
+    [(48, 48)] * 2 + [(24, 24)],   # 5184 rows: the QKV launch (head-padded outputs) ends in half tiles
+    [(48, 48)] * 6,                # 13824 rows: the fp32 o and down launches end in half tiles, the
+                                   # right half of their last column tile past the 1152 outputs
+])
+def test_config5_half_tile_batches_bitwise(config5, grids):
+    """Batches whose 128 x 256 GEMM launches leave a small last partial round of workgroup slots,
+    which then runs as 128 x 128 half tiles: each image's vectors must equal its own run alone."""
     c, o = config5
-    grids = [(48, 48)] * 3
     patches = ge.image_patches(33, grids, o.area)
     batch, _ = c.vision_encode(patches, grids, o.proj_dims)
-    assert batch.shape == (3 * 256, 768) and np.all(np.isfinite(batch))
-    for i in range(3):
-        alone, _ = c.vision_encode(patches[i * 2304:(i + 1) * 2304], [(48, 48)], o.proj_dims)
-        assert np.array_equal(alone, batch[i * 256:(i + 1) * 256]), i
+    rows = split_rows(batch, [(gx // 3) * (gy // 3) for gx, gy in grids])
+    pats = split_rows(patches, [gx * gy for gx, gy in grids])
+    assert np.all(np.isfinite(batch))
+    for i in sorted({0, len(grids) - 1}):
+        alone, _ = c.vision_encode(pats[i], [grids[i]], o.proj_dims)
+        assert np.array_equal(alone, rows[i]), i
 
 
 def test_tower_with_128_wide_heads_and_q8_down(tmp_path):
