@@ -101,27 +101,49 @@ hipError_t launch_embed_norm(hipStream_t s, const Q8Dev& table, const int32_t* t
 // x = (x + rmsnorm(t) * w) * out_scale, then optionally h = rmsnorm(x) * next_w in fp16: the
 // post-attention / post-FFN norm, the residual add and the next block's pre-norm in one pass
 // (reference Shaders/Elementwise.metal:260-354; Model/CPUReference.swift:240-245, :254-257, :269).
-template <int CH, bool F32OUT>
+//
+// Modes (the layer's two residual steps without storing x in between):
+//   kResStore  x = (x + rmsnorm(t) w) s stored; h = rmsnorm(x) next_w when next_w is given.
+//   kResNoX    the same h; x is left as it was. The caller later runs kResTwo on the same x and t.
+//   kResTwo    x1 = (x + rmsnorm(t) w) s as above, then x = (x1 + rmsnorm(t2) w2) s2 stored and
+//              h = rmsnorm(x) next_w: the attention residual (t the o projection) recomputed
+//              beside the FFN residual (t2 the down projection). x1 is formed by residual_add in
+//              every mode, so it is the same number whether it was stored or recomputed.
+// The sums of squares are fused multiply-adds in lane order, then a wave butterfly.
+enum ResMode { kResStore = 0, kResNoX = 1, kResTwo = 2 };
+
+__device__ __forceinline__ float residual_add(float x, float t, float inv, float w, float s) {
+    return __builtin_fmaf(t * inv, w, x) * s;
+}
+
+template <int CH, bool F32OUT, int MODE>
 __global__ __launch_bounds__(256) void residual_norm_kernel(float* __restrict__ x, const uint16_t* __restrict__ t16,
                                                             float t_eps, const float* __restrict__ w, float out_scale,
+                                                            const uint16_t* __restrict__ t2_16, float t2_eps,
+                                                            const float* __restrict__ w2, float out_scale2,
                                                             const float* __restrict__ next_w, float eps, int T, int d,
                                                             uint16_t* __restrict__ h, float* __restrict__ h32) {
+#pragma clang fp contract(off)
     const int row = blockIdx.x * 4 + (threadIdx.x >> 6), lane = threadIdx.x & 63;
     if (row >= T) return;
-    // t arrives as fp16 t * c (c a power of two) with t_eps = eps * c^2: the RMSNorm of the
-    // stored values with t_eps is the RMSNorm of t.
-    float tv[CH][4], xv[CH][4];
-    float ss = 0.0f;
-    // Both inputs' chunks are loaded before any is used (a lane past d reads chunk d - 4 and
+    // t (and t2) arrive as fp16 t * c (c a power of two) with t_eps = eps * c^2: the RMSNorm of
+    // the stored values with t_eps is the RMSNorm of t.
+    float tv[CH][4], t2v[CH][4], xv[CH][4];
+    float ss = 0.0f, ss_t2 = 0.0f;
+    // Every input's chunks are loaded before any is used (a lane past d reads chunk d - 4 and
     // discards it): the row's loads are in flight together.
-    half4_t ta[CH];
-    float4 xa4[CH], wa[CH], nwa[CH];
+    half4_t ta[CH], t2a[CH];
+    float4 xa4[CH], wa[CH], w2a[CH], nwa[CH];
 #pragma unroll
     for (int c = 0; c < CH; c++) {
         const int ec = min(c * 256 + lane * 4, d - 4);
         ta[c] = *reinterpret_cast<const half4_t*>(t16 + (size_t)row * d + ec);
         xa4[c] = *reinterpret_cast<const float4*>(x + (size_t)row * d + ec);
         wa[c] = *reinterpret_cast<const float4*>(w + ec);
+        if constexpr (MODE == kResTwo) {
+            t2a[c] = *reinterpret_cast<const half4_t*>(t2_16 + (size_t)row * d + ec);
+            w2a[c] = *reinterpret_cast<const float4*>(w2 + ec);
+        }
         if (next_w) nwa[c] = *reinterpret_cast<const float4*>(next_w + ec);
     }
 #pragma unroll
@@ -131,12 +153,18 @@ __global__ __launch_bounds__(256) void residual_norm_kernel(float* __restrict__ 
 #pragma unroll
             for (int j = 0; j < 4; j++) {
                 tv[c][j] = float(ta[c][j]);
-                ss += tv[c][j] * tv[c][j];
+                ss = __builtin_fmaf(tv[c][j], tv[c][j], ss);
+                if constexpr (MODE == kResTwo) {
+                    t2v[c][j] = float(t2a[c][j]);
+                    ss_t2 = __builtin_fmaf(t2v[c][j], t2v[c][j], ss_t2);
+                }
             }
         }
     }
     ss = wave_sum(ss);
+    if constexpr (MODE == kResTwo) ss_t2 = wave_sum(ss_t2);
     const float inv = 1.0f / sqrtf(ss / float(d) + t_eps);
+    const float inv_t2 = MODE == kResTwo ? 1.0f / sqrtf(ss_t2 / float(d) + t2_eps) : 0.0f;
     float ss2 = 0.0f;
 #pragma unroll
     for (int c = 0; c < CH; c++) {
@@ -146,10 +174,15 @@ __global__ __launch_bounds__(256) void residual_norm_kernel(float* __restrict__ 
             const float wv[4] = {wa[c].x, wa[c].y, wa[c].z, wa[c].w};
 #pragma unroll
             for (int j = 0; j < 4; j++) {
-                xv[c][j] = (xa[j] + tv[c][j] * inv * wv[j]) * out_scale;
-                ss2 += xv[c][j] * xv[c][j];
+                xv[c][j] = residual_add(xa[j], tv[c][j], inv, wv[j], out_scale);
+                if constexpr (MODE == kResTwo) {
+                    const float w2v[4] = {w2a[c].x, w2a[c].y, w2a[c].z, w2a[c].w};
+                    xv[c][j] = residual_add(xv[c][j], t2v[c][j], inv_t2, w2v[j], out_scale2);
+                }
+                ss2 = __builtin_fmaf(xv[c][j], xv[c][j], ss2);
             }
-            *reinterpret_cast<float4*>(x + (size_t)row * d + e) = make_float4(xv[c][0], xv[c][1], xv[c][2], xv[c][3]);
+            if constexpr (MODE != kResNoX)
+                *reinterpret_cast<float4*>(x + (size_t)row * d + e) = make_float4(xv[c][0], xv[c][1], xv[c][2], xv[c][3]);
         }
     }
     if (!next_w) return;
@@ -173,15 +206,20 @@ __global__ __launch_bounds__(256) void residual_norm_kernel(float* __restrict__ 
     }
 }
 
-hipError_t launch_residual_norm(hipStream_t s, float* x, const uint16_t* t16, float t_eps, const float* w,
-                                float out_scale, const float* next_w, float eps, int T, int d, uint16_t* h, float* h32) {
-    if (T < 0 || d <= 0 || d % 4 != 0 || d > 1024 || (next_w && !h && !h32) || !t16) return hipErrorInvalidValue;
+namespace {
+template <int MODE>
+hipError_t residual_norm_dispatch(hipStream_t s, float* x, const uint16_t* t16, float t_eps, const float* w,
+                                  float out_scale, const uint16_t* t2_16, float t2_eps, const float* w2, float out_scale2,
+                                  const float* next_w, float eps, int T, int d, uint16_t* h, float* h32) {
+    if (T < 0 || d <= 0 || d % 4 != 0 || d > 1024 || (next_w && !h && !h32) || !t16 || !x || !w) return hipErrorInvalidValue;
     if (T == 0) return hipSuccess;
     const int blocks = (T + 3) / 4, CH = (d + 255) / 256;
     // the fp32 output is a separate instantiation, so the fp16 one compiles as on its own
 #define RN_LAUNCH(C)                                                                                              \
-    (h32 ? launch_kernel(residual_norm_kernel<C, true>, blocks, 256, 0, s, x, t16, t_eps, w, out_scale, next_w, eps, T, d, h, h32) \
-         : launch_kernel(residual_norm_kernel<C, false>, blocks, 256, 0, s, x, t16, t_eps, w, out_scale, next_w, eps, T, d, h, h32))
+    (h32 ? launch_kernel(residual_norm_kernel<C, true, MODE>, blocks, 256, 0, s, x, t16, t_eps, w, out_scale, t2_16, \
+                         t2_eps, w2, out_scale2, next_w, eps, T, d, h, h32)                                       \
+         : launch_kernel(residual_norm_kernel<C, false, MODE>, blocks, 256, 0, s, x, t16, t_eps, w, out_scale, t2_16, \
+                         t2_eps, w2, out_scale2, next_w, eps, T, d, h, h32))
     switch (CH) {
     case 1: RN_LAUNCH(1); break;
     case 2: RN_LAUNCH(2); break;
@@ -190,6 +228,29 @@ hipError_t launch_residual_norm(hipStream_t s, float* x, const uint16_t* t16, fl
     }
 #undef RN_LAUNCH
     return hipGetLastError();
+}
+}  // namespace
+
+hipError_t launch_residual_norm(hipStream_t s, float* x, const uint16_t* t16, float t_eps, const float* w,
+                                float out_scale, const float* next_w, float eps, int T, int d, uint16_t* h, float* h32) {
+    return residual_norm_dispatch<kResStore>(s, x, t16, t_eps, w, out_scale, nullptr, 0.0f, nullptr, 0.0f, next_w, eps,
+                                             T, d, h, h32);
+}
+
+hipError_t launch_residual_norm_h(hipStream_t s, const float* x, const uint16_t* t16, float t_eps, const float* w,
+                                  float out_scale, const float* next_w, float eps, int T, int d, uint16_t* h) {
+    if (!next_w || !h) return hipErrorInvalidValue;
+    return residual_norm_dispatch<kResNoX>(s, const_cast<float*>(x), t16, t_eps, w, out_scale, nullptr, 0.0f, nullptr,
+                                           0.0f, next_w, eps, T, d, h, nullptr);
+}
+
+hipError_t launch_residual_norm_two(hipStream_t s, float* x, const uint16_t* t16, float t_eps, const float* w,
+                                    float out_scale, const uint16_t* t2_16, float t2_eps, const float* w2,
+                                    float out_scale2, const float* next_w, float eps, int T, int d, uint16_t* h,
+                                    float* h32) {
+    if (!t2_16 || !w2) return hipErrorInvalidValue;
+    return residual_norm_dispatch<kResTwo>(s, x, t16, t_eps, w, out_scale, t2_16, t2_eps, w2, out_scale2, next_w, eps, T,
+                                           d, h, h32);
 }
 
 // ============================================================================ split-precision norm

@@ -111,6 +111,18 @@ hipError_t launch_residual_norm(hipStream_t s, float* x, const uint16_t* t16, fl
                                 float out_scale, const float* next_w, float eps, int T, int d, uint16_t* h,
                                 float* h32 = nullptr);
 
+// The layer's two residual steps with x stored once. launch_residual_norm_h writes only
+// h = rmsnorm((x + rmsnorm(t) * w) * out_scale) * next_w and leaves x as it was;
+// launch_residual_norm_two then stores x = ((x + rmsnorm(t) * w) * out_scale + rmsnorm(t2) * w2) *
+// out_scale2 and h = rmsnorm(x) * next_w (or h32) from the same x and t. The sum x + rmsnorm(t) * w
+// has the bits launch_residual_norm would have stored.
+hipError_t launch_residual_norm_h(hipStream_t s, const float* x, const uint16_t* t16, float t_eps, const float* w,
+                                  float out_scale, const float* next_w, float eps, int T, int d, uint16_t* h);
+hipError_t launch_residual_norm_two(hipStream_t s, float* x, const uint16_t* t16, float t_eps, const float* w,
+                                    float out_scale, const uint16_t* t2_16, float t2_eps, const float* w2,
+                                    float out_scale2, const float* next_w, float eps, int T, int d, uint16_t* h,
+                                    float* h32 = nullptr);
+
 // h3 fp16 [T][3 d] = [hi | lo | hi] of y = rmsnorm(x) * w (hi = fp16(y), lo = fp16(y - hi)): the
 // input of a split-precision GEMM against [W_hi | W_hi | W_lo]. d a multiple of 4, at most 1024.
 hipError_t launch_norm_split(hipStream_t s, const float* x, const float* w, float eps, int T, int d, uint16_t* h3);

@@ -983,11 +983,22 @@ void encode(ge_ctx* c, StopPoint* sp) {
             });
         }
         if (at(sp, "kqv_out", l)) return;
+        // t (fp32 [T][D]) holds two fp16 [T][D] halves: the o projection in the second, the down
+        // projection in the first. Without the per-layer-input branch x is stored once per layer:
+        // the attention residual's kernel writes only the FFN input h, and the FFN residual's
+        // kernel sums both residuals into x (the sum after attention is stored only for its trace).
         uint16_t* t16 = reinterpret_cast<uint16_t*>(w.t);
-        launch(c, "gemm_o", [&] { return launch_gemm_q8(s, L.wo, w.attn, T, t16, kEpiF16, L.o_c); });
-        launch(c, "residual_norm", [&] {
-            return launch_residual_norm(s, w.x, t16, m.eps * L.o_c * L.o_c, L.post_attn, 1.0f, L.ffn_norm, m.eps, T, D, w.h);
-        });
+        uint16_t* const o16 = t16 + size_t(T) * D;
+        const bool x_once = m.pl == 0 && !(sp && !sp->hit && sp->layer == l && sp->name == "attn_out");
+        launch(c, "gemm_o", [&] { return launch_gemm_q8(s, L.wo, w.attn, T, o16, kEpiF16, L.o_c); });
+        if (x_once)
+            launch(c, "residual_norm_h", [&] {
+                return launch_residual_norm_h(s, w.x, o16, m.eps * L.o_c * L.o_c, L.post_attn, 1.0f, L.ffn_norm, m.eps, T, D, w.h);
+            });
+        else
+            launch(c, "residual_norm", [&] {
+                return launch_residual_norm(s, w.x, o16, m.eps * L.o_c * L.o_c, L.post_attn, 1.0f, L.ffn_norm, m.eps, T, D, w.h);
+            });
         if (at(sp, "attn_out", l) || at(sp, "ffn_norm", l)) return;
         launch(c, "gemm_gate_up", [&] { return launch_gemm_q8(s, L.wgu, w.h, T, w.act, kEpiGeglu, L.act_scale); });
         if (at(sp, "ffn_geglu", l)) return;
@@ -1012,10 +1023,17 @@ void encode(ge_ctx* c, StopPoint* sp) {
             if (at(sp, "l_out", l) || at(sp, "attn_norm", l + 1)) return;
             continue;
         }
-        launch(c, "residual_norm", [&] {
-            return launch_residual_norm(s, w.x, t16, m.eps * L.down_c * L.down_c, L.post_ffw, L.out_scale, next, m.eps, T, D,
-                                        w.h, h32);
-        });
+        if (x_once)
+            launch(c, "residual_norm_two", [&] {
+                return launch_residual_norm_two(s, w.x, o16, m.eps * L.o_c * L.o_c, L.post_attn, 1.0f, t16,
+                                                m.eps * L.down_c * L.down_c, L.post_ffw, L.out_scale, next, m.eps, T, D, w.h,
+                                                h32);
+            });
+        else
+            launch(c, "residual_norm", [&] {
+                return launch_residual_norm(s, w.x, t16, m.eps * L.down_c * L.down_c, L.post_ffw, L.out_scale, next, m.eps, T, D,
+                                            w.h, h32);
+            });
         if (at(sp, "pe_in", l) || at(sp, "l_out", l) || at(sp, "attn_norm", l + 1)) return;
     }
     if (at(sp, "result_norm", -1)) return;
@@ -1157,15 +1175,26 @@ void encode_split(ge_ctx* c) {
                                            w.vt, w.vt_cap, part_base(w.attn, H.r0, L.qd, m.max_qd), H.work, H.n_work, m.heads, L.kv_heads,
                                            L.head_dim, hw, 1.0f, c->attn_items);
             });
+        // a part's rows of t hold its down projection (fp16) in their first half and its o
+        // projection in the second, as encode() lays them out for the whole pack
+        auto o16 = [&](const Half& H) { return rows(t16, H.r0, 2 * size_t(D)) + size_t(H.T) * D; };
+        const bool x_once = m.pl == 0;
         for (const Half& H : halves)
             launch(c, "gemm_o", [&] {
-                return launch_gemm_q8(H.s, L.wo, rows(w.attn, H.r0, m.max_qd), H.T, rows(t16, H.r0, 2 * size_t(D)), kEpiF16, L.o_c);
+                return launch_gemm_q8(H.s, L.wo, rows(w.attn, H.r0, m.max_qd), H.T, o16(H), kEpiF16, L.o_c);
             });
-        for (const Half& H : halves)
-            launch(c, "residual_norm", [&] {
-                return launch_residual_norm(H.s, rows(w.x, H.r0, D), rows(t16, H.r0, 2 * size_t(D)), m.eps * L.o_c * L.o_c, L.post_attn,
-                                            1.0f, L.ffn_norm, m.eps, H.T, D, rows(w.h, H.r0, D));
-            });
+        for (const Half& H : halves) {
+            if (x_once)
+                launch(c, "residual_norm_h", [&] {
+                    return launch_residual_norm_h(H.s, rows(w.x, H.r0, D), o16(H), m.eps * L.o_c * L.o_c, L.post_attn, 1.0f,
+                                                  L.ffn_norm, m.eps, H.T, D, rows(w.h, H.r0, D));
+                });
+            else
+                launch(c, "residual_norm", [&] {
+                    return launch_residual_norm(H.s, rows(w.x, H.r0, D), o16(H), m.eps * L.o_c * L.o_c, L.post_attn, 1.0f,
+                                                L.ffn_norm, m.eps, H.T, D, rows(w.h, H.r0, D));
+                });
+        }
         for (const Half& H : halves)
             launch(c, "gemm_gate_up", [&] {
                 return launch_gemm_q8(H.s, L.wgu, rows(w.h, H.r0, D), H.T, rows(w.act, H.r0, m.ff), kEpiGeglu, L.act_scale);
@@ -1206,10 +1235,11 @@ void encode_split(ge_ctx* c) {
             continue;
         }
         for (const Half& H : halves)
-            launch(c, "residual_norm", [&] {
-                return launch_residual_norm(H.s, rows(w.x, H.r0, D), rows(t16, H.r0, 2 * size_t(D)), m.eps * L.down_c * L.down_c,
-                                            L.post_ffw, L.out_scale, next, m.eps, H.T, D, rows(w.h, H.r0, D),
-                                            last ? rows(w.hn, H.r0, D) : nullptr);
+            launch(c, "residual_norm_two", [&] {
+                return launch_residual_norm_two(H.s, rows(w.x, H.r0, D), o16(H), m.eps * L.o_c * L.o_c, L.post_attn, 1.0f,
+                                                rows(t16, H.r0, 2 * size_t(D)), m.eps * L.down_c * L.down_c, L.post_ffw,
+                                                L.out_scale, next, m.eps, H.T, D, rows(w.h, H.r0, D),
+                                                last ? rows(w.hn, H.r0, D) : nullptr);
             });
     }
     for (int p = 0; p < c->n_parts; p++)

@@ -193,8 +193,8 @@ def at(ptr, nbytes):
 # ---------------------------------------------------------------- kernels
 
 def row_kernel(a, kernel, T, spans):
-    """The one-wave-per-row kernels (embed_norm_kernel elementwise.hip:15, residual_norm_kernel :105,
-    norm_split_kernel :198, the ple_*_kernel family ple.hip:30-218): row < T; loads of chunk
+    """The one-wave-per-row kernels (embed_norm_kernel elementwise.hip:15, residual_norm_kernel :120,
+    norm_split_kernel :264, the ple_*_kernel family ple.hip:30-218): row < T; loads of chunk
     min(e, width - 4) and stores of element e = c * 256 + 4 lane + j < width. spans: (pointer, bytes
     per row of the access)."""
     for ptr, row_bytes in spans:
@@ -215,7 +215,7 @@ def norm_split(a, T, D, x, h3):
 
 
 def qk_norm_rope(a, T, H, KV, HD, qkv, positions, q, k, v, q_lo=None, k_lo=None, pos=None, table_rows=8192):
-    """qk_norm_rope_kernel (elementwise.hip:261): item = (t, slot) < T (H + 2 KV); reads
+    """qk_norm_rope_kernel (elementwise.hip:327): item = (t, slot) < T (H + 2 KV); reads
     qkv[t][slot][0, HD), the RoPE row positions[t]; writes q / k / v (and the low halves)."""
     S = H + 2 * KV
     a.span("qk_norm_rope", qkv, 0, T * S * HD * F32)
@@ -237,7 +237,7 @@ def vt_rows(a, kernel, vt, rows, vt_cols, vcol_used):
 
 
 def qkv_norm_rope_vt(a, T, H, KV, HD, qkv16, positions, q, k, v, vcol, vt_cols, vt, vc):
-    """qkv_norm_rope_vt_kernel (elementwise.hip:351): token t = 64 blockIdx + 4 wave + i < T; V^T rows
+    """qkv_norm_rope_vt_kernel (elementwise.hip:417): token t = 64 blockIdx + 4 wave + i < T; V^T rows
     r < KV HD at column vcol[t] for t < T."""
     S = H + 2 * KV
     a.span("qkv_norm_rope_vt", qkv16, 0, T * S * HD * F16)
@@ -338,14 +338,14 @@ def attention_legacy(a, work, H, KV, HD, hw, q, k, v, o, rows_alloc_k):
 
 
 def pooled_projection(a, n_rows, width, n_out, x, out):
-    """pooled_projection_kernel (elementwise.hip:569): rows r < n_rows of x [*][width] (16-byte loads
+    """pooled_projection_kernel (elementwise.hip:630): rows r < n_rows of x [*][width] (16-byte loads
     of columns clamped to width - 4), out[r][n] for n < n_out. The weight planes are the model's."""
     a.span("pooled_projection", x, 0, n_rows * width * F32)
     a.span("pooled_projection", out, 0, n_rows * n_out * F32)
 
 
 def mean_pool(a, seqs, width, x, seq_ptr, pooled):
-    """mean_pool_kernel (elementwise.hip:501): rows start .. start + len - 1 of each sequence, 16-byte
+    """mean_pool_kernel (elementwise.hip:562): rows start .. start + len - 1 of each sequence, 16-byte
     loads of columns c .. c + 3 < width."""
     a.span("mean_pool", seq_ptr, 0, len(seqs) * SEQ_BYTES)
     a.span("mean_pool", pooled, 0, len(seqs) * width * F32)
@@ -445,9 +445,13 @@ def replay(m, b, positions=None):
             else:
                 assert not split
                 attention_legacy(a, w1, H, KV, hd, hw, ("q", 0), ("k", 0), ("v", 0), ("attn", 0), None)
+            # the part's rows of t (fp32) hold two fp16 [T][D] halves: down's output in the first,
+            # o's in the second (runtime.cpp encode / encode_split)
             t16 = rows("t", r0, 2 * D, F16)
-            gemm(a, "gemm_o", T, D, qd, rows("attn", r0, m["max_qd"], F16), t16, "f16")
-            residual_norm(a, T, D, rows("x", r0, D, F32), t16, rows("h", r0, D, F16))
+            o16 = (t16[0], t16[1] + T * D * F16)
+            gemm(a, "gemm_o", T, D, qd, rows("attn", r0, m["max_qd"], F16), o16, "f16")
+            # residual_norm, or residual_norm_h (the same reads, h only) without the per-layer inputs
+            residual_norm(a, T, D, rows("x", r0, D, F32), o16, rows("h", r0, D, F16))
             gemm(a, "gemm_gate_up", T, 2 * m["ff"], D, rows("h", r0, D, F16), rows("act", r0, m["ff"], F16), "geglu")
             gemm(a, "gemm_down", T, D, m["ff"], rows("act", r0, m["ff"], F16), t16, "f16")
             if m["pl"] > 0:
@@ -468,8 +472,8 @@ def replay(m, b, positions=None):
                 row_kernel(a, "ple_residual_norm", T, [(rows("x", r0, D, F32), D * F32), (rows("t", r0, D, F32), D * F32),
                                                        (rows("rs2", r0, 1, F32), F32), hout])
             else:
-                row_kernel(a, "residual_norm", T, [(rows("x", r0, D, F32), D * F32), (t16, D * F16),
-                                                   (rows("hn", r0, D, F32), D * F32) if last else (rows("h", r0, D, F16), D * F16)])
+                row_kernel(a, "residual_norm_two", T, [(rows("x", r0, D, F32), D * F32), (o16, D * F16), (t16, D * F16),
+                                                       (rows("hn", r0, D, F32), D * F32) if last else (rows("h", r0, D, F16), D * F16)])
     mean_pool(a, b["seqs"], D, ("hn", 0), ("seqs", 0), ("pooled_n", 0))
     pooled_projection(a, len(b["seqs"]), D, m["out_dims"], ("pooled_n", 0), ("pooled", 0))
     return a
