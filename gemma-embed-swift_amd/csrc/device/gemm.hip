@@ -781,16 +781,17 @@ hipError_t launch_gemm_q8(hipStream_t s, const Q8Dev& w, const uint16_t* x, int 
     // back, one box). The tile shape does not change the results: every shape runs the same MFMA
     // over the same k order. The 768-wide projections (o, down): 128 x 128 tiles (K in stages of
     // 64) below 6144 rows, 128 x 256 from 6144 (the config-2 forward's four parts launch them at
-    // 4096 rows each). From 12288 rows the fp16-output projections whose width 192 divides
-    // (768: o and down) take 256 x 192 tiles: at 16384 rows o 22.6 against 23.2 us (256 x 256),
-    // down 30.0 against 31.0. With fp32 outputs (the image tower's o and down, 1152 wide, into
-    // the residual stream) they lost inside the tower, o 72.1 against 63.2 us and down 228.7
-    // against 203.3 (128 x 256): a 256 x 192 workgroup holds a whole CU, so its twice larger
-    // stores overlap no other workgroup's main loop. The widest projections (the tower's QKV,
+    // 4096 rows each). From 12288 rows the fp16-output projections of at most 1024 outputs whose
+    // width 192 divides (768: o and down) take 256 x 192 tiles: at 16384 rows o 22.6 against
+    // 23.2 us (256 x 256), down 30.0 against 31.0. The image tower's 1152-wide o and down stay on
+    // 128 x 256 inside the tower: with fp32 outputs 256 x 192 lost (o 72.1 against 63.2 us, down
+    // 228.7 against 203.3), and with the fp16 o output the tower ran 16.03-16.04 against
+    // 15.95 ms per batch (a 256 x 192 workgroup holds a whole CU, so its stores overlap no other
+    // workgroup's main loop). The widest projections (the tower's QKV,
     // 3456 outputs, and MLP up, 4352) take 256 x 256 tiles: 139.1 against 151.1 us and 190.4
     // against 203.9. The 2304-wide gate/up stays on 128 x 256 (65.0 against 69.9 us).
     if (w.cols % GemmSquare::BK == 0) {
-        if (M >= 12288 && w.rows <= 1152 && w.rows % GemmNarrow::BN == 0 && epi == kEpiF16)
+        if (M >= 12288 && w.rows <= 1024 && w.rows % GemmNarrow::BN == 0 && epi == kEpiF16)
             return gemm_launch<GemmNarrow>(s, w, x, M, y, epi, out_scale, ea);
         if (w.rows <= 1024 && M >= 12288) return gemm_launch<GemmSquare>(s, w, x, M, y, epi, out_scale, ea);
         if (w.rows <= 1024 && M < 6144) return gemm_launch<GemmSmall>(s, w, x, M, y, epi, out_scale, ea);

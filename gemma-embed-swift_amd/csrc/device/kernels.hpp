@@ -216,6 +216,13 @@ hipError_t launch_vit_embed(hipStream_t s, const float* t, const float* bias, co
 // x = x + (t + bias); if w: h = LayerNorm(x) * w + b (fp16).
 hipError_t launch_vit_residual_ln(hipStream_t s, float* x, const float* t, const float* bias, const float* w,
                                   const float* b, float eps, int T, int d, uint16_t* h);
+// The layer's two residual steps with x stored once; o16 is the attention output in fp16 times
+// 1 / o_inv (a power of two). mode 0: h = LayerNorm(x + (o o_inv + bo)) * w + b, x unchanged;
+// mode 1: the same, and x = x + (o o_inv + bo) stored; mode 2: x = (x + (o o_inv + bo)) + (t + bt)
+// stored and, with w, h = LayerNorm(x) * w + b.
+hipError_t launch_vit_residual2_ln(hipStream_t s, int mode, float* x, const uint16_t* o16, float o_inv, const float* bo,
+                                   const float* t, const float* bt, const float* w, const float* b, float eps, int T,
+                                   int d, uint16_t* h);
 // Token i: the mean of LayerNorm(x) * pw + pb over rows row0[i] + dy gx[i] + dx (dy, dx < merge)
 // into pooled (fp32 [n][d]), and RMSNorm(mean) * nw into out (fp16 [n][d]).
 hipError_t launch_vit_pool(hipStream_t s, const float* x, const int32_t* row0, const int32_t* gx, int n_tokens, int merge,

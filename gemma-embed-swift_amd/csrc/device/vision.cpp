@@ -20,9 +20,10 @@ struct VitLayer {
     Q8Dev wqkv, wo, wup, wdown;  // wup rows padded to ff_pad; wdown columns padded to ff_pad
     float *ln1_w = nullptr, *ln1_b = nullptr, *bqkv = nullptr, *bo = nullptr;
     float *ln2_w = nullptr, *ln2_b = nullptr, *bup = nullptr, *bdown = nullptr;
-    // q, k, v are stored in fp16 times qkv_c, the MLP activation times act_c (powers of two from
-    // load-time bounds, so the values stay inside fp16's range; their consumers divide back).
-    float qkv_c = 1, act_c = 1;
+    // q, k, v are stored in fp16 times qkv_c, the MLP activation times act_c and the attention
+    // output projection times o_c (powers of two from load-time bounds, so the values stay inside
+    // fp16's range; their consumers divide back).
+    float qkv_c = 1, act_c = 1, o_c = 1;
 };
 
 struct VisionState {
@@ -37,7 +38,7 @@ struct VisionState {
     int rows = 0, tok_rows = 0, work_cap = 0, vt_cap = 0;
     float *patches32 = nullptr, *x = nullptr, *t = nullptr, *pooled = nullptr, *out = nullptr;
     uint16_t *patches16 = nullptr, *h = nullptr, *q = nullptr, *k = nullptr, *v = nullptr, *vt = nullptr;
-    uint16_t *attn = nullptr, *act = nullptr, *pooled16 = nullptr;
+    uint16_t *attn = nullptr, *act = nullptr, *pooled16 = nullptr, *o16 = nullptr;
     int32_t *px = nullptr, *py = nullptr, *vcol = nullptr, *tok_row0 = nullptr, *tok_gx = nullptr;
     AttnWork* work = nullptr;
     // staged batch
@@ -57,11 +58,11 @@ VisionState& vision_of(ge_ctx* c) {
 
 void free_vision_workspace(VisionState& v) {
     void* ps[] = {v.patches32, v.x, v.t, v.pooled, v.out, v.patches16, v.h, v.q, v.k, v.v, v.vt, v.attn, v.act,
-                  v.pooled16, v.px, v.py, v.vcol, v.tok_row0, v.tok_gx, v.work};
+                  v.pooled16, v.o16, v.px, v.py, v.vcol, v.tok_row0, v.tok_gx, v.work};
     for (void* p : ps)
         if (p) (void)hipFree(p);
     v.patches32 = v.x = v.t = v.pooled = v.out = nullptr;
-    v.patches16 = v.h = v.q = v.k = v.v = v.vt = v.attn = v.act = v.pooled16 = nullptr;
+    v.patches16 = v.h = v.q = v.k = v.v = v.vt = v.attn = v.act = v.pooled16 = v.o16 = nullptr;
     v.px = v.py = v.vcol = v.tok_row0 = v.tok_gx = nullptr;
     v.work = nullptr;
     v.rows = v.tok_rows = v.work_cap = v.vt_cap = 0;
@@ -192,6 +193,7 @@ void vision_upload(ge_ctx* c, const ge_vision_desc* d, const void* base, size_t 
             const auto ln1w = f32_vector(d, b + "ln1.weight", D, base, len), ln1b = f32_vector(d, b + "ln1.bias", D, base, len);
             const auto ln2w = f32_vector(d, b + "ln2.weight", D, base, len), ln2b = f32_vector(d, b + "ln2.bias", D, base, len);
             const double hn1 = ln_bounds(ln1w, ln1b, b + "ln1"), hn2 = ln_bounds(ln2w, ln2b, b + "ln2");
+            double qkv_bound = 0;
             {
                 HostQ8 h = host_q8(3 * D, D);
                 const char* parts[3] = {"attn_q", "attn_k", "attn_v"};
@@ -206,9 +208,16 @@ void vision_upload(ge_ctx* c, const ge_vision_desc* d, const void* base, size_t 
                 L.wqkv = upload_vision_q8(c, v, h, "v.attn_qkv");
                 L.bqkv = upload_floats(v, bias, "v.attn_qkv.bias");
                 // |q_j| <= ||h|| ||W_j|| + |b_j|
-                L.qkv_c = fp16_range_scale(hn1 * max_row_norm(h) + max_abs(bias));
+                qkv_bound = hn1 * max_row_norm(h) + max_abs(bias);
+                L.qkv_c = fp16_range_scale(qkv_bound);
             }
-            L.wo = upload_vision_q8(c, v, q8_rows(d, b + "attn_out.weight", D, D, base, len, D), "v.attn_out");
+            {
+                // an attention output row mixes v rows (|a_e| <= the v bound), so
+                // |o_j| <= sqrt(heads hd) * bound * ||W_o,j||
+                const HostQ8 h = q8_rows(d, b + "attn_out.weight", D, D, base, len, D);
+                L.o_c = fp16_range_scale(std::sqrt(double(D)) * qkv_bound * max_row_norm(h));
+                L.wo = upload_vision_q8(c, v, h, "v.attn_out");
+            }
             L.bo = upload_floats(v, f32_vector(d, b + "attn_out.bias", D, base, len), "v.attn_out.bias");
             {
                 const HostQ8 h = q8_rows(d, b + "ffn_up.weight", D, v.ff, base, len, v.ff_pad);
@@ -284,6 +293,7 @@ void alloc_vision_workspace(hipStream_t s, VisionState& v, int r, int tr, int wc
     v.x = vws_alloc<float>(s, r, D, "x");
     v.t = vws_alloc<float>(s, r, D, "t");
     v.h = vws_alloc<uint16_t>(s, r, D, "h");
+    v.o16 = vws_alloc<uint16_t>(s, r, D, "attention output");
     // q, k, v keep zeros in each head's padding columns: the epilogue never writes them
     v.q = vws_alloc<uint16_t>(s, r, HP, "q");
     v.k = vws_alloc<uint16_t>(s, r, HP, "k");
@@ -421,10 +431,15 @@ void vision_encode(ge_ctx* c, VitStop* sp) {
                                        sc);
         });
         if (stop("kqv_out", l)) return;
-        launch(c, "vit_gemm_o", [&] { return launch_gemm_q8(s, L.wo, v.attn, P, v.t, kEpiF32, 1.0f / L.qkv_c); });
+        // The attention output in fp16 (times o_c). x is stored once per layer: the attention
+        // residual's launch writes only the MLP input h (and x only when a trace wants the sum after
+        // attention), and the MLP residual's launch recomputes that sum beside its own.
+        launch(c, "vit_gemm_o", [&] { return launch_gemm_q8(s, L.wo, v.attn, P, v.o16, kEpiF16, L.o_c / L.qkv_c); });
         if (stop("attn_out", l)) return;
+        const bool store_sum = sp && !sp->hit && sp->layer == l && sp->name == "ffn_inp";
         launch(c, "vit_residual_ln", [&] {
-            return launch_vit_residual_ln(s, v.x, v.t, L.bo, L.ln2_w, L.ln2_b, v.eps, P, D, v.h);
+            return launch_vit_residual2_ln(s, store_sum ? 1 : 0, v.x, v.o16, 1.0f / L.o_c, L.bo, nullptr, nullptr, L.ln2_w,
+                                           L.ln2_b, v.eps, P, D, v.h);
         });
         if (stop("ffn_inp", l) || stop("ffn_inp_normed", l)) return;
         launch(c, "vit_gemm_up", [&] {
@@ -436,10 +451,10 @@ void vision_encode(ge_ctx* c, VitStop* sp) {
         launch(c, "vit_gemm_down", [&] { return launch_gemm_q8(s, L.wdown, v.act, P, v.t, kEpiF32, 1.0f / L.act_c); });
         if (stop("ffn_out", l)) return;
         const bool last = l + 1 == v.layers;
-        launch(c, "vit_residual_ln", [&] {
+        launch(c, "vit_residual2_ln", [&] {
             const VitLayer* N = last ? nullptr : &v.layer[size_t(l) + 1];
-            return launch_vit_residual_ln(s, v.x, v.t, L.bdown, N ? N->ln1_w : nullptr, N ? N->ln1_b : nullptr, v.eps, P, D,
-                                          v.h);
+            return launch_vit_residual2_ln(s, 2, v.x, v.o16, 1.0f / L.o_c, L.bo, v.t, L.bdown, N ? N->ln1_w : nullptr,
+                                           N ? N->ln1_b : nullptr, v.eps, P, D, v.h);
         });
         if (stop("layer_out", l) || stop("layer_inp_normed", l + 1)) return;
     }
@@ -473,7 +488,9 @@ void vision_trace(ge_ctx* c, const char* name, int layer, float* out, size_t cap
     bool f16 = false, heads = false;
     int rows = P, stride = D, width = D;
     float unscale = 1;
-    if (n == "inp" || n == "attn_out" || n == "ffn_out") {
+    if (n == "attn_out") {
+        buf = v.o16; f16 = true; unscale = 1.0f / L->o_c;
+    } else if (n == "inp" || n == "ffn_out") {
         buf = v.t;
     } else if (n == "pos_embd" || n == "ffn_inp" || n == "layer_out") {
         buf = v.x;
