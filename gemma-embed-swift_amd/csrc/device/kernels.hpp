@@ -213,9 +213,6 @@ constexpr int kVitMaxWidth = 2048;
 hipError_t launch_vit_embed(hipStream_t s, const float* t, const float* bias, const float* pos, int npos,
                             const int32_t* px, const int32_t* py, int T, int d, const float* w, const float* b, float eps,
                             float* x, uint16_t* h);
-// x = x + (t + bias); if w: h = LayerNorm(x) * w + b (fp16).
-hipError_t launch_vit_residual_ln(hipStream_t s, float* x, const float* t, const float* bias, const float* w,
-                                  const float* b, float eps, int T, int d, uint16_t* h);
 // The layer's two residual steps with x stored once; o16 is the attention output in fp16 times
 // 1 / o_inv (a power of two). mode 0: h = LayerNorm(x + (o o_inv + bo)) * w + b, x unchanged;
 // mode 1: the same, and x = x + (o o_inv + bo) stored; mode 2: x = (x + (o o_inv + bo)) + (t + bt)

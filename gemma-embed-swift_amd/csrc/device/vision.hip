@@ -104,42 +104,6 @@ __global__ __launch_bounds__(256) void vit_embed_kernel(const float* __restrict_
     vit_ln_store<CH>(v, d, lane, mean, rstd, wa, lb, h + (size_t)row * d);
 }
 
-// x = x + (t + bias); with w: h = LayerNorm(x) * w + b (fp16), the next block's pre-norm.
-template <int CH>
-__global__ __launch_bounds__(256) void vit_residual_ln_kernel(float* __restrict__ x, const float* __restrict__ t,
-                                                              const float* __restrict__ bias,
-                                                              const float* __restrict__ w, const float* __restrict__ b,
-                                                              float eps, int T, int d, uint16_t* __restrict__ h) {
-    const int row = blockIdx.x * 4 + (threadIdx.x >> 6), lane = threadIdx.x & 63;
-    if (row >= T) return;
-    float v[CH][4];
-    float4 xa[CH], ta[CH], ba[CH], wa[CH], lb[CH];
-    vit_load_chunks<CH>(x + (size_t)row * d, d, lane, xa);
-    vit_load_chunks<CH>(t + (size_t)row * d, d, lane, ta);
-    vit_load_chunks<CH>(bias, d, lane, ba);
-    if (w) {
-        vit_load_chunks<CH>(w, d, lane, wa);
-        vit_load_chunks<CH>(b, d, lane, lb);
-    }
-#pragma unroll
-    for (int c = 0; c < CH; c++) {
-        const int e = c * 256 + lane * 4;
-        if (e < d) {
-            float4* xp = reinterpret_cast<float4*>(x + (size_t)row * d + e);
-            const float4 xv = xa[c], tv = ta[c], bv = ba[c];
-            v[c][0] = xv.x + (tv.x + bv.x);
-            v[c][1] = xv.y + (tv.y + bv.y);
-            v[c][2] = xv.z + (tv.z + bv.z);
-            v[c][3] = xv.w + (tv.w + bv.w);
-            *xp = make_float4(v[c][0], v[c][1], v[c][2], v[c][3]);
-        }
-    }
-    if (!w) return;
-    float mean, rstd;
-    vit_ln_stats<CH>(v, d, lane, eps, mean, rstd);
-    vit_ln_store<CH>(v, d, lane, mean, rstd, wa, lb, h + (size_t)row * d);
-}
-
 // The layer's two residual steps with x stored once (the attention output o in fp16, times a
 // power of two o_c, so o_inv = 1 / o_c scales it back exactly):
 //   kVitResH      v = x + (o o_inv + bo); h = LayerNorm(v) * w + b; x is left as it was.
@@ -303,15 +267,6 @@ hipError_t launch_vit_embed(hipStream_t s, const float* t, const float* bias, co
     if (T == 0) return hipSuccess;
     const int CH = (d + 255) / 256;
     VIT_DISPATCH(vit_embed_kernel, CH, dim3((T + 3) / 4), dim3(256), 0, s, t, bias, pos, npos, px, py, T, d, w, b, eps, x, h)
-    return hipGetLastError();
-}
-
-hipError_t launch_vit_residual_ln(hipStream_t s, float* x, const float* t, const float* bias, const float* w,
-                                  const float* b, float eps, int T, int d, uint16_t* h) {
-    if (T < 0 || !vit_width_ok(d) || !x || !t || !bias || (w && (!b || !h))) return hipErrorInvalidValue;
-    if (T == 0) return hipSuccess;
-    const int CH = (d + 255) / 256;
-    VIT_DISPATCH(vit_residual_ln_kernel, CH, dim3((T + 3) / 4), dim3(256), 0, s, x, t, bias, w, b, eps, T, d, h)
     return hipGetLastError();
 }
 
