@@ -213,13 +213,14 @@ constexpr int kVitMaxWidth = 2048;
 hipError_t launch_vit_embed(hipStream_t s, const float* t, const float* bias, const float* pos, int npos,
                             const int32_t* px, const int32_t* py, int T, int d, const float* w, const float* b, float eps,
                             float* x, uint16_t* h);
-// The layer's two residual steps with x stored once; o16 is the attention output in fp16 times
-// 1 / o_inv (a power of two). mode 0: h = LayerNorm(x + (o o_inv + bo)) * w + b, x unchanged;
-// mode 1: the same, and x = x + (o o_inv + bo) stored; mode 2: x = (x + (o o_inv + bo)) + (t + bt)
-// stored and, with w, h = LayerNorm(x) * w + b.
+// The layer's two residual steps with x stored once; o16 (the attention output) and t16 (the
+// down projection) are fp16 times 1 / o_inv and 1 / t_inv (powers of two). mode 0:
+// h = LayerNorm(x + (o o_inv + bo)) * w + b, x unchanged; mode 1: the same, and
+// x = x + (o o_inv + bo) stored; mode 2: x = (x + (o o_inv + bo)) + (t t_inv + bt) stored and,
+// with w, h = LayerNorm(x) * w + b.
 hipError_t launch_vit_residual2_ln(hipStream_t s, int mode, float* x, const uint16_t* o16, float o_inv, const float* bo,
-                                   const float* t, const float* bt, const float* w, const float* b, float eps, int T,
-                                   int d, uint16_t* h);
+                                   const uint16_t* t16, float t_inv, const float* bt, const float* w, const float* b,
+                                   float eps, int T, int d, uint16_t* h);
 // Token i: the mean of LayerNorm(x) * pw + pb over rows row0[i] + dy gx[i] + dx (dy, dx < merge)
 // into pooled (fp32 [n][d]), and RMSNorm(mean) * nw into out (fp16 [n][d]).
 hipError_t launch_vit_pool(hipStream_t s, const float* x, const int32_t* row0, const int32_t* gx, int n_tokens, int merge,

@@ -222,12 +222,13 @@ Q8Dev upload_dense_fragments(const std::vector<uint16_t>& dense, int rows, int c
 // columns zero-padded to cols_pad: values are rounded to fp16 once (Q8_0: fp16 of q * d, as the
 // device dequantisation does; F16 as stored; F32 and BF16 rounded to nearest even).
 Q8Dev upload_fragments(const ge_tensor_desc* t, int64_t cols, int64_t rows, int cols_pad, const void* base, size_t len,
-                       std::vector<void*>& allocs) {
+                       std::vector<void*>& allocs, double* row_norm) {
     check_shape(t, cols, rows);
     if (rows % 32 || cols_pad % 32 || cols_pad < cols) fail(GE_ERR_MODEL, "tensor %s: shape does not tile", t->name);
     const uint8_t* p = tensor_ptr(t, base, len);
     std::vector<float> row(size_t(cols), 0.0f);
     std::vector<uint16_t> dense(size_t(rows) * cols_pad, 0);
+    if (row_norm) *row_norm = 0;
     for (int64_t r = 0; r < rows; r++) {
         switch (t->type) {
         case GE_TYPE_F32: std::memcpy(row.data(), p + size_t(r) * cols * 4, size_t(cols) * 4); break;
@@ -257,8 +258,13 @@ Q8Dev upload_fragments(const ge_tensor_desc* t, int64_t cols, int64_t rows, int 
         }
         default: fail(GE_ERR_MODEL, "tensor %s uses unsupported storage type %d", t->name, t->type);
         }
-        for (int64_t i = 0; i < cols; i++)
-            dense[size_t(r) * cols_pad + i] = __builtin_bit_cast(uint16_t, _Float16(row[size_t(i)]));
+        double ss = 0;
+        for (int64_t i = 0; i < cols; i++) {
+            const _Float16 w = _Float16(row[size_t(i)]);
+            dense[size_t(r) * cols_pad + i] = __builtin_bit_cast(uint16_t, w);
+            ss += double(w) * double(w);
+        }
+        if (row_norm) *row_norm = std::max(*row_norm, std::sqrt(ss));
     }
     return upload_dense_fragments(dense, int(rows), cols_pad, t->name, allocs);
 }

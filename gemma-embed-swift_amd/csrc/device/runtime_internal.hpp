@@ -262,9 +262,9 @@ HostQ8 host_q8(int rows, int cols);
 Q8Dev upload_q8(ge_ctx* c, const HostQ8& h, const char* what, bool gemm_weight = true);
 // A [cols, rows] weight tensor of any accepted type (F32, F16, BF16, Q8_0) as fp16 MFMA fragments
 // (Q8Dev::fh order only, no quant planes), columns zero-padded to cols_pad; the allocation is
-// appended to allocs.
+// appended to allocs. With row_norm, *row_norm = max_j ||W_j||_2 of the fp16 rows uploaded.
 Q8Dev upload_fragments(const ge_tensor_desc* t, int64_t cols, int64_t rows, int cols_pad, const void* base, size_t len,
-                       std::vector<void*>& allocs);
+                       std::vector<void*>& allocs, double* row_norm = nullptr);
 // max_j ||W_j||_2 of repacked Q8_0 rows.
 double max_row_norm(const HostQ8& h);
 // The power of two c <= 1 that brings `bound` under 2^15 (half of fp16's largest finite value).

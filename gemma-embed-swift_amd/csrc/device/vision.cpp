@@ -20,10 +20,10 @@ struct VitLayer {
     Q8Dev wqkv, wo, wup, wdown;  // wup rows padded to ff_pad; wdown columns padded to ff_pad
     float *ln1_w = nullptr, *ln1_b = nullptr, *bqkv = nullptr, *bo = nullptr;
     float *ln2_w = nullptr, *ln2_b = nullptr, *bup = nullptr, *bdown = nullptr;
-    // q, k, v are stored in fp16 times qkv_c, the MLP activation times act_c and the attention
-    // output projection times o_c (powers of two from load-time bounds, so the values stay inside
-    // fp16's range; their consumers divide back).
-    float qkv_c = 1, act_c = 1, o_c = 1;
+    // q, k, v are stored in fp16 times qkv_c, the MLP activation times act_c, the attention
+    // output projection times o_c and the MLP down projection times down_c (powers of two from
+    // load-time bounds, so the values stay inside fp16's range; their consumers divide back).
+    float qkv_c = 1, act_c = 1, o_c = 1, down_c = 1;
 };
 
 struct VisionState {
@@ -121,8 +121,8 @@ HostQ8 q8_rows(const ge_vision_desc* d, const std::string& name, int64_t cols, i
 
 // A [cols, rows] weight of any accepted type as fp16 MFMA fragments, columns zero-padded.
 Q8Dev fragments_any(VisionState& v, const ge_vision_desc* d, const std::string& name, int64_t cols, int64_t rows,
-                    int cols_pad, const void* base, size_t len) {
-    return upload_fragments(vfind(d, name), cols, rows, cols_pad, base, len, v.weights);
+                    int cols_pad, const void* base, size_t len, double* row_norm = nullptr) {
+    return upload_fragments(vfind(d, name), cols, rows, cols_pad, base, len, v.weights, row_norm);
 }
 
 Q8Dev upload_vision_q8(ge_ctx* c, VisionState& v, const HostQ8& h, const char* what) {
@@ -193,7 +193,7 @@ void vision_upload(ge_ctx* c, const ge_vision_desc* d, const void* base, size_t 
             const auto ln1w = f32_vector(d, b + "ln1.weight", D, base, len), ln1b = f32_vector(d, b + "ln1.bias", D, base, len);
             const auto ln2w = f32_vector(d, b + "ln2.weight", D, base, len), ln2b = f32_vector(d, b + "ln2.bias", D, base, len);
             const double hn1 = ln_bounds(ln1w, ln1b, b + "ln1"), hn2 = ln_bounds(ln2w, ln2b, b + "ln2");
-            double qkv_bound = 0;
+            double qkv_bound = 0, act_bound = 0;
             {
                 HostQ8 h = host_q8(3 * D, D);
                 const char* parts[3] = {"attn_q", "attn_k", "attn_v"};
@@ -225,9 +225,15 @@ void vision_upload(ge_ctx* c, const ge_vision_desc* d, const void* base, size_t 
                 const auto bu = f32_vector(d, b + "ffn_up.bias", v.ff, base, len, v.ff_pad);
                 L.bup = upload_floats(v, bu, "v.ffn_up.bias");
                 // |gelu(z)| <= |z| and |z_j| <= ||h|| ||W_j|| + |b_j|
-                L.act_c = fp16_range_scale(hn2 * max_row_norm(h) + max_abs(bu));
+                act_bound = hn2 * max_row_norm(h) + max_abs(bu);
+                L.act_c = fp16_range_scale(act_bound);
             }
-            L.wdown = fragments_any(v, d, b + "ffn_down.weight", v.ff, D, v.ff_pad, base, len);
+            {
+                // |d_j| <= ||a|| ||W_down,j|| with every activation a_e within the bound above
+                double wn = 0;
+                L.wdown = fragments_any(v, d, b + "ffn_down.weight", v.ff, D, v.ff_pad, base, len, &wn);
+                L.down_c = fp16_range_scale(std::sqrt(double(v.ff)) * act_bound * wn);
+            }
             L.bdown = upload_floats(v, f32_vector(d, b + "ffn_down.bias", D, base, len), "v.ffn_down.bias");
             L.ln1_w = upload_floats(v, ln1w, "v.ln1");
             L.ln1_b = upload_floats(v, ln1b, "v.ln1");
@@ -438,8 +444,8 @@ void vision_encode(ge_ctx* c, VitStop* sp) {
         if (stop("attn_out", l)) return;
         const bool store_sum = sp && !sp->hit && sp->layer == l && sp->name == "ffn_inp";
         launch(c, "vit_residual_ln", [&] {
-            return launch_vit_residual2_ln(s, store_sum ? 1 : 0, v.x, v.o16, 1.0f / L.o_c, L.bo, nullptr, nullptr, L.ln2_w,
-                                           L.ln2_b, v.eps, P, D, v.h);
+            return launch_vit_residual2_ln(s, store_sum ? 1 : 0, v.x, v.o16, 1.0f / L.o_c, L.bo, nullptr, 1.0f, nullptr,
+                                           L.ln2_w, L.ln2_b, v.eps, P, D, v.h);
         });
         if (stop("ffn_inp", l) || stop("ffn_inp_normed", l)) return;
         launch(c, "vit_gemm_up", [&] {
@@ -448,13 +454,15 @@ void vision_encode(ge_ctx* c, VitStop* sp) {
             return launch_gemm_q8(s, L.wup, v.h, P, v.act, kEpiGeluBias, L.act_c, &ea);
         });
         if (stop("ffn_gelu", l)) return;
-        launch(c, "vit_gemm_down", [&] { return launch_gemm_q8(s, L.wdown, v.act, P, v.t, kEpiF32, 1.0f / L.act_c); });
+        // the down projection in fp16 (times down_c) over the start of t
+        uint16_t* const d16 = reinterpret_cast<uint16_t*>(v.t);
+        launch(c, "vit_gemm_down", [&] { return launch_gemm_q8(s, L.wdown, v.act, P, d16, kEpiF16, L.down_c / L.act_c); });
         if (stop("ffn_out", l)) return;
         const bool last = l + 1 == v.layers;
         launch(c, "vit_residual2_ln", [&] {
             const VitLayer* N = last ? nullptr : &v.layer[size_t(l) + 1];
-            return launch_vit_residual2_ln(s, 2, v.x, v.o16, 1.0f / L.o_c, L.bo, v.t, L.bdown, N ? N->ln1_w : nullptr,
-                                           N ? N->ln1_b : nullptr, v.eps, P, D, v.h);
+            return launch_vit_residual2_ln(s, 2, v.x, v.o16, 1.0f / L.o_c, L.bo, d16, 1.0f / L.down_c, L.bdown,
+                                           N ? N->ln1_w : nullptr, N ? N->ln1_b : nullptr, v.eps, P, D, v.h);
         });
         if (stop("layer_out", l) || stop("layer_inp_normed", l + 1)) return;
     }
@@ -490,7 +498,9 @@ void vision_trace(ge_ctx* c, const char* name, int layer, float* out, size_t cap
     float unscale = 1;
     if (n == "attn_out") {
         buf = v.o16; f16 = true; unscale = 1.0f / L->o_c;
-    } else if (n == "inp" || n == "ffn_out") {
+    } else if (n == "ffn_out") {
+        buf = v.t; f16 = true; unscale = 1.0f / L->down_c;
+    } else if (n == "inp") {
         buf = v.t;
     } else if (n == "pos_embd" || n == "ffn_inp" || n == "layer_out") {
         buf = v.x;

@@ -104,32 +104,34 @@ __global__ __launch_bounds__(256) void vit_embed_kernel(const float* __restrict_
     vit_ln_store<CH>(v, d, lane, mean, rstd, wa, lb, h + (size_t)row * d);
 }
 
-// The layer's two residual steps with x stored once (the attention output o in fp16, times a
-// power of two o_c, so o_inv = 1 / o_c scales it back exactly):
+// The layer's two residual steps with x stored once (the attention output o and the down
+// projection t in fp16, times powers of two, so o_inv and t_inv scale them back exactly):
 //   kVitResH      v = x + (o o_inv + bo); h = LayerNorm(v) * w + b; x is left as it was.
 //   kVitResStore  the same v and h, and x = v stored (a trace of the sum after attention).
-//   kVitResTwo    v = x + (o o_inv + bo) as above, then x = v + (t + bt) stored and, with w,
-//                 h = LayerNorm(x) * w + b: the MLP residual (t the down projection) beside the
-//                 attention residual it recomputes, so the sum after attention is never stored.
+//   kVitResTwo    v = x + (o o_inv + bo) as above, then x = v + (t t_inv + bt) stored and, with w,
+//                 h = LayerNorm(x) * w + b: the MLP residual beside the attention residual it
+//                 recomputes, so the sum after attention is never stored.
 enum VitResMode { kVitResH = 0, kVitResStore = 1, kVitResTwo = 2 };
 
 template <int CH, int MODE>
 __global__ __launch_bounds__(256) void vit_residual2_ln_kernel(float* __restrict__ x, const uint16_t* __restrict__ o16,
                                                                float o_inv, const float* __restrict__ bo,
-                                                               const float* __restrict__ t, const float* __restrict__ bt,
+                                                               const uint16_t* __restrict__ t16, float t_inv,
+                                                               const float* __restrict__ bt,
                                                                const float* __restrict__ w, const float* __restrict__ b,
                                                                float eps, int T, int d, uint16_t* __restrict__ h) {
     const int row = blockIdx.x * 4 + (threadIdx.x >> 6), lane = threadIdx.x & 63;
     if (row >= T) return;
     float v[CH][4];
-    float4 xa[CH], ba[CH], ta[CH], bta[CH], wa[CH], lb[CH];
-    half4_t oa[CH];
+    float4 xa[CH], ba[CH], bta[CH], wa[CH], lb[CH];
+    half4_t oa[CH], ta[CH];
     vit_load_chunks<CH>(x + (size_t)row * d, d, lane, xa);
 #pragma unroll
     for (int c = 0; c < CH; c++) oa[c] = *reinterpret_cast<const half4_t*>(o16 + (size_t)row * d + min(c * 256 + lane * 4, d - 4));
     vit_load_chunks<CH>(bo, d, lane, ba);
     if constexpr (MODE == kVitResTwo) {
-        vit_load_chunks<CH>(t + (size_t)row * d, d, lane, ta);
+#pragma unroll
+        for (int c = 0; c < CH; c++) ta[c] = *reinterpret_cast<const half4_t*>(t16 + (size_t)row * d + min(c * 256 + lane * 4, d - 4));
         vit_load_chunks<CH>(bt, d, lane, bta);
     }
     if (w) {
@@ -144,9 +146,9 @@ __global__ __launch_bounds__(256) void vit_residual2_ln_kernel(float* __restrict
 #pragma unroll
             for (int j = 0; j < 4; j++) v[c][j] = xv[j] + (float(oa[c][j]) * o_inv + bv[j]);
             if constexpr (MODE == kVitResTwo) {
-                const float tv[4] = {ta[c].x, ta[c].y, ta[c].z, ta[c].w}, btv[4] = {bta[c].x, bta[c].y, bta[c].z, bta[c].w};
+                const float btv[4] = {bta[c].x, bta[c].y, bta[c].z, bta[c].w};
 #pragma unroll
-                for (int j = 0; j < 4; j++) v[c][j] = v[c][j] + (tv[j] + btv[j]);
+                for (int j = 0; j < 4; j++) v[c][j] = v[c][j] + (float(ta[c][j]) * t_inv + btv[j]);
             }
             if constexpr (MODE != kVitResH)
                 *reinterpret_cast<float4*>(x + (size_t)row * d + e) = make_float4(v[c][0], v[c][1], v[c][2], v[c][3]);
@@ -271,19 +273,19 @@ hipError_t launch_vit_embed(hipStream_t s, const float* t, const float* bias, co
 }
 
 hipError_t launch_vit_residual2_ln(hipStream_t s, int mode, float* x, const uint16_t* o16, float o_inv, const float* bo,
-                                   const float* t, const float* bt, const float* w, const float* b, float eps, int T,
-                                   int d, uint16_t* h) {
+                                   const uint16_t* t16, float t_inv, const float* bt, const float* w, const float* b,
+                                   float eps, int T, int d, uint16_t* h) {
     if (T < 0 || !vit_width_ok(d) || !x || !o16 || !bo || (w && (!b || !h)) || mode < kVitResH || mode > kVitResTwo ||
-        (mode == kVitResTwo && (!t || !bt)) || (mode != kVitResTwo && !w))
+        (mode == kVitResTwo && (!t16 || !bt)) || (mode != kVitResTwo && !w))
         return hipErrorInvalidValue;
     if (T == 0) return hipSuccess;
     const int CH = (d + 255) / 256;
     if (mode == kVitResH)
-        VIT_DISPATCH(vit_residual2_ln_kernel_h, CH, dim3((T + 3) / 4), dim3(256), 0, s, x, o16, o_inv, bo, t, bt, w, b, eps, T, d, h)
+        VIT_DISPATCH(vit_residual2_ln_kernel_h, CH, dim3((T + 3) / 4), dim3(256), 0, s, x, o16, o_inv, bo, t16, t_inv, bt, w, b, eps, T, d, h)
     else if (mode == kVitResStore)
-        VIT_DISPATCH(vit_residual2_ln_kernel_store, CH, dim3((T + 3) / 4), dim3(256), 0, s, x, o16, o_inv, bo, t, bt, w, b, eps, T, d, h)
+        VIT_DISPATCH(vit_residual2_ln_kernel_store, CH, dim3((T + 3) / 4), dim3(256), 0, s, x, o16, o_inv, bo, t16, t_inv, bt, w, b, eps, T, d, h)
     else
-        VIT_DISPATCH(vit_residual2_ln_kernel_two, CH, dim3((T + 3) / 4), dim3(256), 0, s, x, o16, o_inv, bo, t, bt, w, b, eps, T, d, h)
+        VIT_DISPATCH(vit_residual2_ln_kernel_two, CH, dim3((T + 3) / 4), dim3(256), 0, s, x, o16, o_inv, bo, t16, t_inv, bt, w, b, eps, T, d, h)
     return hipGetLastError();
 }
 

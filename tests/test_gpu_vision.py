@@ -173,8 +173,8 @@ def test_config5_batch_of_eight_bitwise(config5):
 @pytest.mark.parametrize("grids", [
     [(48, 48)] * 2,                # 4608 rows: the MLP-up launch (GELU and bias) ends in half tiles
     [(48, 48)] * 2 + [(24, 24)],   # 5184 rows: the QKV launch (head-padded outputs) ends in half tiles
-    [(48, 48)] * 6,                # 13824 rows: the o (fp16) and down (fp32) launches end in half
-                                   # tiles, the right half of their last column tile past the 1152 outputs
+    [(48, 48)] * 6,                # 13824 rows: the o and down launches end in half tiles, the
+                                   # right half of their last column tile past the 1152 outputs
 ])
 def test_config5_half_tile_batches_bitwise(config5, grids):
     """Batches whose 128 x 256 GEMM launches leave a small last partial round of workgroup slots,
