@@ -443,7 +443,7 @@ void vision_encode(ge_ctx* c, VitStop* sp) {
         launch(c, "vit_gemm_o", [&] { return launch_gemm_q8(s, L.wo, v.attn, P, v.o16, kEpiF16, L.o_c / L.qkv_c); });
         if (stop("attn_out", l)) return;
         const bool store_sum = sp && !sp->hit && sp->layer == l && sp->name == "ffn_inp";
-        launch(c, "vit_residual_ln", [&] {
+        launch(c, "vit_residual_ln_h", [&] {
             return launch_vit_residual2_ln(s, store_sum ? 1 : 0, v.x, v.o16, 1.0f / L.o_c, L.bo, nullptr, 1.0f, nullptr,
                                            L.ln2_w, L.ln2_b, v.eps, P, D, v.h);
         });
@@ -459,7 +459,7 @@ void vision_encode(ge_ctx* c, VitStop* sp) {
         launch(c, "vit_gemm_down", [&] { return launch_gemm_q8(s, L.wdown, v.act, P, d16, kEpiF16, L.down_c / L.act_c); });
         if (stop("ffn_out", l)) return;
         const bool last = l + 1 == v.layers;
-        launch(c, "vit_residual2_ln", [&] {
+        launch(c, "vit_residual_ln_two", [&] {
             const VitLayer* N = last ? nullptr : &v.layer[size_t(l) + 1];
             return launch_vit_residual2_ln(s, 2, v.x, v.o16, 1.0f / L.o_c, L.bo, d16, 1.0f / L.down_c, L.bdown,
                                            N ? N->ln1_w : nullptr, N ? N->ln1_b : nullptr, v.eps, P, D, v.h);
